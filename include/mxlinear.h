@@ -1,0 +1,137 @@
+/*
+ * mxlinear.h -- C ABI of the MI355X (gfx950) quantized-linear library
+ * (libmxlinear.so).  Plain pointers and sizes; every device pointer is HIP
+ * device memory and every call enqueues on `stream` (a hipStream_t, may be 0).
+ *
+ * Status-returning entry points return 0 on success and a negative code on
+ * failure (MXL_EINVAL -1: bad argument, nothing launched; MXL_EHIP -2: a HIP
+ * launch failed); mxl_last_error() then describes the failure (thread-local).
+ *
+ * Formats:  fmt 0 = E4M3 (8-bit codes), 2 = E2M3, 3 = E3M2 (FP6 packed four
+ * values per three bytes, little-endian 6-bit fields: value i of a group in
+ * bits [6i, 6i+6)).  Scales are E8M0 bytes (2^(s-127)), one per 32 along K.
+ * rule 0 = floor_carry175 (the reference quantizer quantize_block,
+ * src/vllm_mach/mxfp8/reconstruct_model.py:34-50), rule 1 = ceil_div448
+ * (src/vllm_mach/mxfp6/mxfp8_mlp.py:100-105).
+ *
+ * Each declaration cites the reference interface (troycheng/vllm-mach
+ * v0.4.0) it replaces.
+ */
+#ifndef MXLINEAR_H
+#define MXLINEAR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXL_OK 0
+#define MXL_EINVAL -1
+#define MXL_EHIP -2
+#define MXL_EUNSUPPORTED -3
+
+/* Library identity and error text.  Counterpart of the reference's ABI/schema
+ * verification (src/vllm_mach/mxfp8/native_backend.py:76-97). */
+int mxl_version(void);
+const char* mxl_last_error(void);
+
+/* 1 if `device` is gfx950, 0 if not, <0 if HIP cannot be queried.  Replaces
+ * the SM120 capability gate (src/vllm_mach/mxfp6/dense.py:83-110). */
+int mxl_device_supported(int device);
+
+/* Dynamic MXFP8 activation quantization: bf16 x [M, K] (row stride ldx
+ * elements) -> E4M3 codes [M, K] + E8M0 scales [M, K/32], row-major.
+ * K % 32 == 0.  Replaces torch.ops.mxfp6.quantize_mxfp8 / quantize_mxfp8_logical
+ * (src/vllm_mach/mxfp6/dense_mxfp8.py:40, src/vllm_mach/mxfp6/moe_utils.py:172-202). */
+int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t ldx, int rule,
+                       void* codes, void* scales, void* stream);
+
+/* Bytes of the swizzled scale buffer for [M, K] (mxfp8_mlp.py:122). */
+int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K);
+
+/* SwiGLU -> MXFP8 producer: gate_up bf16 [M, 2K] (gate = cols [0, K), up =
+ * [K, 2K)) -> codes [M, K] + scales, logical [M, K/32] (swizzled = 0) or the
+ * reference's swizzled layout (swizzled = 1, padding zeroed).  Replaces
+ * _silu_quant / _triton_quantize (src/vllm_mach/mxfp6/mxfp8_mlp.py:87-127). */
+int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int rule, int swizzled,
+                     void* codes, void* scales, void* stream);
+
+/* Per-token group-128 FP8 quantization: bf16 x [M, K] -> E4M3 q [M, K] +
+ * fp32 scales column-major s[g * M + m].  Replaces _quantize_kernel.quantize_out
+ * (src/vllm_mach/fp8/_quantize_kernel.py:7-25). */
+int mxl_quantize_block_fp8(const void* x, int64_t M, int64_t K, void* q, void* s_colmajor,
+                           void* stream);
+
+/* SiLU(gate)*up -> block-FP8: bf16 input [rows, 2H] -> E4M3 q [rows, H] +
+ * fp32 scales [rows, H/128] (transposed = 1: s[g * rows + r]).  Replaces
+ * mach_fp8_activation::run (native/fp8_activation/activation.cu:62-104). */
+int mxl_silu_mul_block_fp8(const void* input, int64_t rows, int64_t H, int transposed,
+                           void* q, void* scales, void* stream);
+
+/* Sizes of the MFMA-tiled weight layout (16-row x 512-K tiles). */
+int64_t mxl_tiled_weight_bytes(int64_t N, int64_t K, int fmt);
+int64_t mxl_tiled_scale_bytes(int64_t N, int64_t K);
+
+/* Load-time repack of a logical weight (E4M3 [N, K] or packed FP6 [N, 3K/4])
+ * and its E8M0 scales [N, K/32] (may be NULL: block-FP8) into the tiled
+ * layout.  K % 128 == 0.  Replaces pack_scales at process_weights_after_loading
+ * (src/vllm_mach/mxfp6/dense_mxfp8.py:150-151, src/vllm_mach/mxfp6/dense.py:185-188,
+ * src/vllm_mach/mxfp6/moe_utils.py:162-169). */
+int mxl_pack_weight(const void* codes, const void* scales, int64_t N, int64_t K, int fmt,
+                    void* tiled_codes, void* tiled_scales, void* stream);
+
+/* Scratch bytes the GEMMs may use for split-K partials at (M, N, K); with a
+ * smaller workspace they run unsplit. */
+int64_t mxl_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* MX block-scaled GEMM: y[M, N] (bf16, row stride ldc) = A . W^T, A = E4M3
+ * codes [M, K] + E8M0 [M, K/32]; W tiled (fmt 0/2/3); bias bf16 [N] or NULL
+ * (added after the bf16 rounding, as y + bias in bf16).  Replaces
+ * mxfp8_sm120::gemm (src/vllm_mach/mxfp6/dense_mxfp8.py:86,
+ * src/vllm_mach/mxfp8/native_backend.py:77-89) and mxfp6::gemm_w6a8_pdl
+ * (src/vllm_mach/mxfp6/ar_norm.py:144-147). */
+int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,
+                int64_t N, int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc,
+                void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Block-FP8 GEMM: y[m, n] = sum_g sa[g*M + m] * sb[(n/128) * (K/128) + g] *
+ * (A_g . W_g) with fp32 FMA per K128 block, bf16 out.  A E4M3 [M, K]; W tiled
+ * E4M3 (fmt 0, no scales); sb fp32 [ceil(N/128), K/128].  Replaces
+ * vllm_mach_block_fp8::mm / the ordered route / cutlass_scaled_mm
+ * (src/vllm_mach/fp8/linear.py:65-81, src/vllm_mach/fp8/ordered.py:8-64,
+ * native/block_fp8/block_fp8.cu:229-255). */
+int mxl_block_fp8_gemm(const void* a, const void* sa_colmajor, int64_t M, const void* w_tiled,
+                       const void* sb, int64_t N, int64_t K, const void* bias, void* out, int64_t ldc,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Grouped MX GEMM over experts: output row p (bf16 [routed_rows, N]) of expert
+ * e, expert_offsets[e] <= p < expert_offsets[e+1], is A[row_index[p] / row_div]
+ * . W[e]^T (A[p] when row_index is NULL).  W: num_experts tiled weights laid
+ * out back to back.  Replaces grouped_gemm_w6a8_out
+ * (src/vllm_mach/mxfp6/moe_utils.py:320-380, src/vllm_mach/mxfp6/moe.py:671-696). */
+int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index, int row_div,
+                     const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
+                     const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
+                     void* out, void* stream);
+
+/* Token sort by expert (stable): topk_ids int32 [T, topk] -> sorted_routes
+ * int32 [T*topk], expert_offsets int64 [E+1], inverse int32 [T*topk] (-1 for
+ * ids outside [0, E)).  Replaces route_mxfp8_out's routing outputs
+ * (src/vllm_mach/mxfp6/moe_utils.py:205-255, src/vllm_mach/mxfp6/moe.py:651-669). */
+int64_t mxl_moe_route_workspace_bytes(int64_t T, int64_t topk, int64_t E);
+int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_routes,
+                  int64_t* expert_offsets, int32_t* inverse, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
+/* Weighted combine: out[t, h] = bf16(sum_k y[inverse[t*topk+k], h] * w[t, k])
+ * in fp32, k ascending.  Replaces moe_reduce_out
+ * (src/vllm_mach/mxfp6/moe.py:697-702, src/vllm_mach/mxfp6/moe_utils.py:445-488). */
+int mxl_moe_reduce(const void* routed_output, const float* topk_weights, const int32_t* inverse, int64_t T,
+                   int64_t topk, int64_t H, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXLINEAR_H */

@@ -1,0 +1,178 @@
+"""GPU parity of the block-scaled GEMMs against the oracle's dequantize-then-matmul.
+
+Bar: relative Frobenius error <= 1e-3 and max elementwise
+error <= 1e-2 * max|ref| against the fp32-accumulated reference.  Activations are
+quantized on the GPU and checked bit-exact first, so the GEMM comparison isolates
+the contraction.  Full-size configurations (c1..c4 shapes) run through the same
+checks with the reference computed by torch (fp32 dequant + matmul on the GPU).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+REL_FRO, MAX_ELEM = 1e-3, 1e-2
+
+
+def _check(got: np.ndarray, ref: np.ndarray):
+    err = got.astype(np.float64) - ref.astype(np.float64)
+    scale = max(np.linalg.norm(ref), 1e-30)
+    rel = np.linalg.norm(err) / scale
+    mx = np.abs(err).max() / max(np.abs(ref).max(), 1e-30)
+    assert rel <= REL_FRO and mx <= MAX_ELEM, (rel, mx)
+    return rel, mx
+
+
+def _act(M, K, seed, magnitude=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g) * magnitude
+    x[:, torch.randperm(K, generator=g)[: max(1, K // 100)]] *= 20
+    return x.bfloat16()
+
+
+def _weights(oracle_mod, N, K, fmt, std, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(N, K, generator=g) * std).bfloat16()
+    if fmt == 0:
+        codes, scales = oracle_mod.quant_mxfp8(w, 0)
+        stored = codes
+    else:
+        codes, scales = oracle_mod.quant_mxfp6(w, fmt)
+        stored = oracle_mod.pack_fp6(codes)
+    return codes, scales, stored
+
+
+@pytest.mark.parametrize("fmt", [0, 2, 3])
+@pytest.mark.parametrize("M", [1, 5, 16, 33, 64, 130])
+@pytest.mark.parametrize("N,K", [(256, 512), (384, 2560), (2048, 2048)])
+def test_mx_gemm_matches_oracle(pkg, oracle_mod, dev, fmt, M, N, K):
+    ops = pkg.ops
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 17 + N + K)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    x = _act(M, K, 29 + M)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    assert np.array_equal(a.view(torch.uint8).cpu().numpy(), rc)
+    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, None)
+    ref = oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)
+    ref_bf = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref))
+    _check(y.float().cpu().numpy(), ref_bf)
+
+
+def test_mx_gemm_bias_and_k_tail(pkg, oracle_mod, dev):
+    """K % 512 != 0 (a partial last super-tile) and a bf16 bias added after rounding."""
+    ops = pkg.ops
+    M, N, K = 9, 200, 384
+    wc, ws, stored = _weights(oracle_mod, N, K, 0, 0.05, 3)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), 0)
+    x = _act(M, K, 4)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(1)).bfloat16()
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, 0, bias.to(dev))
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    ref = torch.from_numpy(oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws))))
+    ref = (ref.bfloat16() + bias).float().numpy()
+    _check(y.float().cpu().numpy(), ref)
+
+
+def test_mx_gemm_zero_and_empty(pkg, dev):
+    ops = pkg.ops
+    N, K = 128, 256
+    codes = torch.zeros(N, K, dtype=torch.uint8, device=dev)
+    scales = torch.full((N, K // 32), 127, dtype=torch.uint8, device=dev)
+    tiled, tiled_s = ops.pack_weight(codes, scales, 0)
+    x = torch.zeros(3, K, dtype=torch.bfloat16, device=dev)
+    y = ops.mx_gemm_from_float(x, tiled, tiled_s, N, 0)
+    assert torch.count_nonzero(y) == 0
+    e = ops.mx_gemm_from_float(x[:0], tiled, tiled_s, N, 0)
+    assert tuple(e.shape) == (0, N)
+
+
+def _torch_dequant(codes_u8: torch.Tensor, scales_u8: torch.Tensor, fmt: int, oracle_mod) -> torch.Tensor:
+    if fmt == 0:
+        v = codes_u8.view(torch.float8_e4m3fn).float()
+    else:
+        lut = torch.from_numpy(oracle_mod.fp6_to_f32(np.arange(64, dtype=np.uint8), fmt)).to(codes_u8.device)
+        v = lut[codes_u8.long()]
+    return v * torch.exp2(scales_u8.float() - 127).repeat_interleave(32, dim=1)
+
+
+@pytest.mark.parametrize("name,M,N,K,fmt,std", [
+    ("c1", 16, 2048, 2048, 0, 0.02),
+    ("c2", 512, 2560, 9216, 0, 0.02),
+    ("c4", 16, 17408, 5120, 2, 0.015),
+    ("c4", 256, 17408, 5120, 2, 0.015),
+])
+def test_full_size_configs(pkg, oracle_mod, dev, name, M, N, K, fmt, std):
+    """BASELINE shapes: GPU GEMM vs a torch fp32 dequant-matmul of the same codes."""
+    ops = pkg.ops
+    g = torch.Generator(device=dev).manual_seed(7)
+    w = (torch.randn(N, K, generator=g, device=dev) * std).bfloat16()
+    if fmt == 0:
+        wc, ws = torch.ops.mach_amd.quantize_mxfp8(w, 0)
+        wc = wc.view(torch.uint8)
+        stored = wc
+    else:
+        c, s = oracle_mod.quant_mxfp6(w.cpu(), fmt)
+        wc, ws = torch.from_numpy(c).to(dev), torch.from_numpy(s).to(dev)
+        stored = torch.from_numpy(oracle_mod.pack_fp6(c)).to(dev)
+    tiled, tiled_s = ops.pack_weight(stored, ws, fmt)
+    x = (torch.randn(M, K, generator=g, device=dev)).bfloat16()
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x, 0)
+    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, None)
+    ref = (_torch_dequant(a.view(torch.uint8), sa, 0, oracle_mod) @ _torch_dequant(wc, ws, fmt, oracle_mod).T)
+    ref = ref.bfloat16().float()
+    _check(y.float().cpu().numpy(), ref.cpu().numpy())
+    del w, tiled, tiled_s
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("M", [1, 3, 16, 64, 130, 512])
+@pytest.mark.parametrize("N,K", [(256, 512), (18432, 2560), (2560, 9216)])
+def test_block_fp8_gemm_matches_oracle(pkg, oracle_mod, dev, M, N, K):
+    if N * K > 10_000_000 and M > 64:
+        pytest.skip("covered at smaller M; keeps the CPU reference within seconds")
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(173 + M + K)
+    w = (torch.randn(N, K, generator=g) * 0.02)
+    wb = w.reshape(N // 128, 128, K // 128, 128)
+    sb = (wb.abs().amax(dim=(1, 3)) / 448.0).float()
+    wq = (wb / sb[:, None, :, None]).reshape(N, K).to(torch.float8_e4m3fn)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    tiled, _ = ops.pack_weight(wq.to(dev), None, 0)
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x.to(dev))
+    y = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, None)
+    rq, rs = oracle_mod.quant_block_fp8(x)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), rq)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.block_fp8_gemm_ref(rq, rs, wq.view(torch.uint8).numpy(), sb.numpy()))
+    _check(y.float().cpu().numpy(), ref)
+
+
+def test_graph_replay_with_changing_inputs(pkg, oracle_mod, dev):
+    """Capture one MXFP8 linear call, replay with new inputs (x.normal_(), zero), as
+    tests/native_mxfp6/test_mxfp8_sm120.py:40-58 does."""
+    ops = pkg.ops
+    M, N, K = 16, 512, 1024
+    wc, ws, stored = _weights(oracle_mod, N, K, 0, 0.02, 5)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), 0)
+    x = torch.randn(M, K, device=dev).bfloat16()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        ops.mx_gemm_from_float(x, tiled, tiled_s, N, 0)  # warm the per-stream workspace
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y = ops.mx_gemm_from_float(x, tiled, tiled_s, N, 0)
+        for zero in (False, False, True):
+            x.zero_() if zero else x.normal_()
+            graph.replay()
+            stream.synchronize()
+            rc, rs = oracle_mod.quant_mxfp8(x.cpu(), 0)
+            ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws)))
+            got = y.float().cpu().numpy()
+            if zero:
+                assert not got.any()
+            else:
+                _check(got, ref)
+    torch.cuda.current_stream().wait_stream(stream)

@@ -1,0 +1,96 @@
+"""GPU parity: quantizers and producers are bit-exact against the CPU oracle.
+
+Shapes and magnitude sweeps follow the reference's GPU checks
+(tests/test_mxfp8_swiglu_quant.py:86-109: M in {1,4,16,24,32,64}, K in {6144,9216},
+magnitudes [1, 0, 1e-15, 50]; tests/test_fp8_activation_gpu.py:51-64: rows, seed 1729+rows).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _u8(t):
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def _inputs(M, K, magnitude, seed, outliers=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g) * magnitude
+    if outliers and K >= 100:
+        x[:, torch.randperm(K, generator=g)[: max(1, K // 100)]] *= 20
+    return x.bfloat16()
+
+
+@pytest.mark.parametrize("rule", [0, 1])
+@pytest.mark.parametrize("M,K", [(1, 32), (7, 128), (16, 2048), (33, 5120), (130, 2560)])
+@pytest.mark.parametrize("magnitude", [1.0, 0.0, 1e-15, 50.0])
+def test_quantize_mxfp8_bit_exact(pkg, oracle_mod, dev, rule, M, K, magnitude):
+    x = _inputs(M, K, magnitude, 29 + M + K)
+    codes, scales = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), rule)
+    rc, rs = oracle_mod.quant_mxfp8(x, rule)
+    assert np.array_equal(_u8(scales), rs)
+    assert np.array_equal(_u8(codes), rc)
+
+
+def test_quantize_mxfp8_strided_rows(pkg, oracle_mod, dev):
+    base = _inputs(12, 1024, 1.0, 3)
+    x = base.to(dev)[:, 256:768]  # row stride 1024, K = 512
+    codes, scales = torch.ops.mach_amd.quantize_mxfp8(x, 0)
+    rc, rs = oracle_mod.quant_mxfp8(base[:, 256:768].contiguous(), 0)
+    assert np.array_equal(_u8(codes), rc) and np.array_equal(_u8(scales), rs)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 24, 32, 64])
+@pytest.mark.parametrize("K", [6144, 9216])
+def test_swiglu_mxfp8_bit_exact(pkg, oracle_mod, dev, M, K):
+    for magnitude in [1.0, 0.0, 1e-15, 50.0]:
+        gu = _inputs(M, 2 * K, magnitude, 71 + M, outliers=False)
+        codes, scales = torch.ops.mach_amd.swiglu_mxfp8(gu.to(dev), 1, False)
+        rc, rs = oracle_mod.swiglu_mxfp8(gu, 1)
+        assert np.array_equal(_u8(codes), rc), magnitude
+        assert np.array_equal(_u8(scales), rs), magnitude
+
+
+@pytest.mark.parametrize("M,K", [(1, 9216), (130, 6144), (200, 128)])
+def test_swiglu_mxfp8_swizzled_layout(pkg, oracle_mod, dev, M, K):
+    gu = _inputs(M, 2 * K, 1.0, 5, outliers=False)
+    codes, scales = torch.ops.mach_amd.swiglu_mxfp8(gu.to(dev), 1, True)
+    rc, rs = oracle_mod.swiglu_mxfp8(gu, 1)
+    assert np.array_equal(_u8(codes), rc)
+    assert np.array_equal(_u8(scales), oracle_mod.swizzle_scales(rs, K))
+
+
+def test_swiglu_rule_floor_carry175(pkg, oracle_mod, dev):
+    gu = _inputs(16, 2 * 2048, 3.0, 9, outliers=False)
+    codes, scales = torch.ops.mach_amd.swiglu_mxfp8(gu.to(dev), 0, False)
+    rc, rs = oracle_mod.swiglu_mxfp8(gu, 0)
+    assert np.array_equal(_u8(codes), rc) and np.array_equal(_u8(scales), rs)
+
+
+@pytest.mark.parametrize("M,K", [(1, 2560), (9, 4096), (512, 2560)])
+def test_quantize_block_fp8_bit_exact(pkg, oracle_mod, dev, M, K):
+    x = _inputs(M, K, 1.0, 173 + M + K)
+    x[0, :128] = 0
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x.to(dev))
+    rq, rsc = oracle_mod.quant_block_fp8(x)
+    assert s.stride() == (1, M) or M == 1
+    assert np.array_equal(_u8(q), rq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), np.ascontiguousarray(rsc).view(np.uint32))
+
+
+@pytest.mark.parametrize("rows", [1, 7, 128, 2048])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_silu_mul_block_fp8_bit_exact(pkg, oracle_mod, dev, rows, transposed):
+    g = torch.Generator().manual_seed(1729 + rows)
+    x = (torch.randn(rows, 18432, generator=g) * 3).bfloat16()
+    out = torch.empty(rows, 9216, dtype=torch.float8_e4m3fn, device=dev)
+    if transposed:
+        scales = torch.empty(72, rows, dtype=torch.float32, device=dev).t()
+    else:
+        scales = torch.empty(rows, 72, dtype=torch.float32, device=dev)
+    torch.ops.mach_amd.silu_and_mul_per_block_quant(out, x.to(dev), scales, transposed)
+    rq, rs = oracle_mod.silu_mul_block_fp8(x, transposed)
+    assert np.array_equal(_u8(out), rq)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), np.ascontiguousarray(rs).view(np.uint32))

@@ -1,0 +1,24 @@
+"""MI355X-native (gfx950) quantized-linear hot path for vllm-mach.
+
+Dynamic MXFP8 activation quantization, the SwiGLU -> MXFP8 producer, and the
+block-scaled GEMMs for MXFP8, packed MXFP6 (W6A8) and block-FP8, dense and
+MoE-grouped, as hand-written HIP kernels behind a C ABI (``include/mxlinear.h``,
+``libmxlinear.so``) and vLLM's quantization-method surface (``linear``, ``moe``).
+
+Importing the package registers the ``torch.ops.mach_amd`` operators; it does
+not touch the GPU or load the HIP library (that happens on first use).
+"""
+from . import ops  # noqa: F401  (registers torch.ops.mach_amd.*)
+from .linear import (  # noqa: F401
+    BlockFp8LinearKernel,
+    Mxfp6LinearKernel,
+    Mxfp8LinearKernel,
+    MxLinearLayerConfig,
+    MxLinearMethod,
+    is_mi355x_available,
+    register_kernels,
+    swiglu_mxfp8_down,
+)
+from .moe import Mxfp6Experts, select_experts  # noqa: F401
+
+__version__ = "0.1.0"

@@ -1,0 +1,89 @@
+"""ctypes binding of the C ABI in ``include/mxlinear.h`` (``libmxlinear.so``).
+
+The library is loaded lazily on first use, after ``import torch``, so that its
+``libamdhip64.so.7`` dependency resolves to the HIP runtime torch already
+loaded and HIP stream handles are shared.  There is no fallback: a missing
+library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the library load; see module docstring)
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("MXLINEAR_LIBRARY_PATH", HERE / "libmxlinear.so"))
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+
+# name -> (restype, argtypes); mirrors include/mxlinear.h
+SIGNATURES = {
+    "mxl_version": (_I, []),
+    "mxl_last_error": (ctypes.c_char_p, []),
+    "mxl_device_supported": (_I, [_I]),
+    "mxl_quantize_mxfp8": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "mxl_swizzled_scale_bytes": (_I64, [_I64, _I64]),
+    "mxl_swiglu_mxfp8": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P]),
+    "mxl_quantize_block_fp8": (_I, [_P, _I64, _I64, _P, _P, _P]),
+    "mxl_silu_mul_block_fp8": (_I, [_P, _I64, _I64, _I, _P, _P, _P]),
+    "mxl_tiled_weight_bytes": (_I64, [_I64, _I64, _I]),
+    "mxl_tiled_scale_bytes": (_I64, [_I64, _I64]),
+    "mxl_pack_weight": (_I, [_P, _P, _I64, _I64, _I, _P, _P, _P]),
+    "mxl_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "mxl_mx_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P]),
+    "mxl_block_fp8_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
+    "mxl_grouped_gemm": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P]),
+    "mxl_moe_route_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "mxl_moe_route": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+    "mxl_moe_reduce": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class MxlError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.is_file():
+                    raise ImportError(
+                        f"libmxlinear.so not found at {LIB_PATH}: build it with "
+                        "`python vllm-mach_amd/build.py` (there is no CPU fallback)")
+                L = ctypes.CDLL(str(LIB_PATH))
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(L, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = L
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke a status-returning entry point; raise MxlError with its message on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().mxl_last_error().decode(errors="replace")
+        raise MxlError(f"{name} failed ({rc}): {msg}")
+
+
+def query(name: str, *args):
+    return getattr(lib(), name)(*args)
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

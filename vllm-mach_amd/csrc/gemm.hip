@@ -1,0 +1,549 @@
+// Block-scaled GEMMs on CDNA4 scaled MFMA (v_mfma_scale_f32_16x16x128_f8f6f4).
+//
+// y[m, n] = sum_k a[m, k] * w[n, k] with
+//   MX (MXFP8 / MXFP6): a = E4M3 codes * 2^(sa - 127) per 32 along K,
+//                       w = E4M3 | E2M3 | E3M2 codes * 2^(sw - 127) per 32;
+//                       the E8M0 scales are applied inside the MFMA.
+//   block-FP8:          a = E4M3 * sa[m, k/128] (fp32), w = E4M3 * sb[n/128, k/128];
+//                       each K128 block is one unscaled MFMA whose fp32 result is
+//                       folded into the accumulator with fma(raw, sa*sb, acc).
+//
+// Weights live in an MFMA-tiled layout written once at load time:
+//   tile (nt, kt) = weight rows [16nt, 16nt+16) x K [512kt, 512kt+512)
+//   CH 1 KiB chunks (CH = 8 for 8-bit codes, 6 for FP6); lane l's 16 bytes of
+//   chunk c are at c*1024 + 16l, so one 16-byte load per lane moves 1 KiB of
+//   contiguous memory per wavefront.  Lane l = 16q + r (r = row in tile,
+//   q = 0..3) concatenates, for MFMA j = 0..3, the 32 values
+//   K[512kt + 128j + 32q, +32) of row r: 32 bytes (E4M3) or 24 bytes (FP6,
+//   little-endian 6-bit fields).  The MX scale tile is 256 bytes: lane l's
+//   dword holds, in byte j, the E8M0 of block 16kt + 4j + q of row r, so the
+//   MFMA takes it with op_sel = j.  Tiles are ordered (nt, kt) with kt fastest,
+//   so a wave walking K streams one contiguous region.
+//
+// Activations stay row-major (the producers' natural layout and the gather
+// layout the MoE path needs): lane l loads row r's 32 bytes at K offset
+// 512kt + 128j + 32q for MFMA j -- the operand layout of the 16x16x128 MFMA
+// (A: row = lane % 16, K block = lane / 16; C: row = 4(lane/16) + i,
+// col = lane % 16).
+//
+// Work split: a workgroup of KW wavefronts owns an MT x NT grid of 16x16
+// output tiles; its waves take interleaved 512-wide K super-tiles and their
+// fp32 partials are summed in LDS in wave order.  When the tile grid alone
+// cannot fill 256 CUs, S workgroups split K further and write fp32 partials
+// that a second kernel sums in split order: both orders are fixed, so every
+// result is deterministic.
+#include "mx_common.h"
+
+namespace mxl {
+
+constexpr int kTileK = 512;
+
+template <int FMT>
+struct FmtTraits;
+template <>
+struct FmtTraits<kE4M3> { static constexpr int CH = 8; static constexpr int RUN = 32; };
+template <>
+struct FmtTraits<kE2M3> { static constexpr int CH = 6; static constexpr int RUN = 24; };
+template <>
+struct FmtTraits<kE3M2> { static constexpr int CH = 6; static constexpr int RUN = 24; };
+
+__host__ __device__ inline int tile_chunks(int fmt) { return fmt == kE4M3 ? 8 : 6; }
+
+// ------------------------------------------------------------ weight packing
+
+// One thread writes one 16-byte (chunk, lane) piece of one tile.
+__global__ void pack_weight_kernel(const uint8_t* __restrict__ src, int64_t ld_src, uint8_t* __restrict__ dst,
+                                   int64_t N, int64_t K, int64_t KT, int CH, int fp6, int64_t total) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  const int64_t c = (id >> 6) % CH;
+  const int64_t tile = (id >> 6) / CH;
+  const int64_t nt = tile / KT, kt = tile - nt * KT;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t row = nt * 16 + r;
+  uint8_t out[16];
+  if (!fp6) {
+    const int j = (int)(c >> 1), half = (int)(c & 1);
+    const int64_t k0 = kt * kTileK + 128 * j + 32 * q;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < N && k0 < K) v = *reinterpret_cast<const uint4*>(src + row * ld_src + k0 + 16 * half);
+    *reinterpret_cast<uint4*>(dst + tile * (CH * 1024) + c * 1024 + lane * 16) = v;
+    return;
+  }
+#pragma unroll
+  for (int b = 0; b < 16; ++b) {
+    const int cb = (int)c * 16 + b;          // byte within the lane's 96-byte run
+    const int j = cb / 24, o = cb % 24;
+    const int64_t k0 = kt * kTileK + 128 * j + 32 * q;
+    uint8_t v = 0;
+    if (row < N && k0 < K) v = src[row * ld_src + k0 * 3 / 4 + o];
+    out[b] = v;
+  }
+  uint4 w;
+  w.x = out[0] | (out[1] << 8) | (out[2] << 16) | ((uint32_t)out[3] << 24);
+  w.y = out[4] | (out[5] << 8) | (out[6] << 16) | ((uint32_t)out[7] << 24);
+  w.z = out[8] | (out[9] << 8) | (out[10] << 16) | ((uint32_t)out[11] << 24);
+  w.w = out[12] | (out[13] << 8) | (out[14] << 16) | ((uint32_t)out[15] << 24);
+  *reinterpret_cast<uint4*>(dst + tile * (CH * 1024) + c * 1024 + lane * 16) = w;
+}
+
+// One thread writes one lane's scale dword of one tile.
+__global__ void pack_scale_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t N,
+                                  int64_t K, int64_t KT, int64_t total) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int lane = (int)(id & 63);
+  const int64_t tile = id >> 6;
+  const int64_t nt = tile / KT, kt = tile - nt * KT;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t row = nt * 16 + r;
+  uint32_t w = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t blk = kt * 16 + 4 * j + q;
+    if (row < N && blk * 32 < K) w |= (uint32_t)src[row * (K / 32) + blk] << (8 * j);
+  }
+  *reinterpret_cast<uint32_t*>(dst + tile * 256 + lane * 4) = w;
+}
+
+// ------------------------------------------------------------- GEMM kernel
+
+struct GemmParams {
+  const uint8_t* a;      // activation codes, row-major
+  const void* sa;        // MX: E8M0 [rows, K/32]; block-FP8: fp32 column-major [K/128, M]
+  const uint8_t* w;      // tiled weight codes (expert 0)
+  const void* sw;        // MX: tiled scales; block-FP8: fp32 [ceil(N/128), K/128]
+  const uint16_t* bias;  // bf16 [N] or null
+  uint16_t* out;         // bf16, row stride ldc
+  float* partial;        // [S, rows, N] when split
+  const int32_t* row_index;     // grouped: sorted_routes (A row = row_index[r] / row_div)
+  const int64_t* expert_offsets;
+  int64_t lda, ldc, M, N, K, KT, a_rows;
+  int64_t w_expert_stride, sw_expert_stride;
+  int row_div, S;
+};
+
+template <int MT>
+struct ATile {
+  v8i d[MT][4];
+  uint32_t s[MT][4];
+};
+
+// Load the activation operands of one super-tile for MT 16-row tiles.
+template <int MT, bool BLOCK>
+__device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow)[MT], int64_t kt, int q,
+                                       ATile<MT>& t) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint8_t* base = p.a + arow[mt] * p.lda;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t k0 = kt * kTileK + 128 * j + 32 * q;
+      if (k0 < p.K) {
+        const uint4* src = reinterpret_cast<const uint4*>(base + k0);
+        uint4 lo = src[0], hi = src[1];
+        t.d[mt][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      } else {
+        t.d[mt][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+      if (!BLOCK) {
+        const int64_t kb = kt * 16 + 4 * j;  // first 32-block of this MFMA's 128 columns
+        uint32_t sv = 0;
+        if (kb * 32 < p.K) sv = *reinterpret_cast<const uint32_t*>(
+                                   static_cast<const uint8_t*>(p.sa) + arow[mt] * (p.K / 32) + kb);
+        t.s[mt][j] = (sv >> (8 * q)) & 0xFFu;
+      }
+    }
+  }
+}
+
+template <int FMT, int NT>
+struct BTile {
+  uint4 c[NT][FmtTraits<FMT>::CH];
+  uint32_t s[NT];
+};
+
+template <int FMT>
+__device__ __forceinline__ v8i b_operand(const uint4* c, int j) {
+  if (FMT == kE4M3) {
+    const uint4 lo = c[2 * j], hi = c[2 * j + 1];
+    return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  } else {
+    // the lane's 24 dwords; MFMA j takes dwords [6j, 6j + 6)
+    uint32_t d[24];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      d[4 * i] = c[i].x; d[4 * i + 1] = c[i].y; d[4 * i + 2] = c[i].z; d[4 * i + 3] = c[i].w;
+    }
+    return v8i{(int)d[6 * j], (int)d[6 * j + 1], (int)d[6 * j + 2], (int)d[6 * j + 3],
+               (int)d[6 * j + 4], (int)d[6 * j + 5], 0, 0};
+  }
+}
+
+template <int FMT, int NT, bool BLOCK>
+__device__ __forceinline__ void load_b(const GemmParams& p, const uint8_t* w, const uint8_t* sw,
+                                       const int64_t (&ntile)[NT], int64_t kt, int lane, BTile<FMT, NT>& t) {
+  constexpr int CH = FmtTraits<FMT>::CH;
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const uint8_t* base = w + (ntile[n] * p.KT + kt) * (CH * 1024) + lane * 16;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) t.c[n][c] = *reinterpret_cast<const uint4*>(base + c * 1024);
+    if (!BLOCK) t.s[n] = *reinterpret_cast<const uint32_t*>(sw + (ntile[n] * p.KT + kt) * 256 + lane * 4);
+  }
+}
+
+// The B-format and op_sel operands must be immediates.
+template <int FMT, int J>
+__device__ __forceinline__ v4f mfma_step(v8i a, v8i b, v4f c, uint32_t sa, uint32_t sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, kE4M3, FMT, 0, (int)sa, J, (int)sb);
+}
+
+template <int FMT>
+__device__ __forceinline__ v4f mfma_raw(v8i a, v8i b) {
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, kE4M3, FMT, 0, 127, 0, 127);
+}
+
+// Accumulate one super-tile into acc[MT][NT].
+template <int FMT, int MT, int NT, bool BLOCK>
+__device__ __forceinline__ void compute_tile(const GemmParams& p, const ATile<MT>& A, const BTile<FMT, NT>& B,
+                                             v4f (&acc)[MT][NT], int64_t kt, const int64_t (&r4)[MT],
+                                             int64_t hi, const int64_t (&ntile)[NT], const float* sb_rows) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const v8i b = b_operand<FMT>(B.c[n], j);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (!BLOCK) {
+          const uint32_t sb = B.s[n];
+          if (j == 0) acc[mt][n] = mfma_step<FMT, 0>(A.d[mt][j], b, acc[mt][n], A.s[mt][j], sb);
+          if (j == 1) acc[mt][n] = mfma_step<FMT, 1>(A.d[mt][j], b, acc[mt][n], A.s[mt][j], sb);
+          if (j == 2) acc[mt][n] = mfma_step<FMT, 2>(A.d[mt][j], b, acc[mt][n], A.s[mt][j], sb);
+          if (j == 3) acc[mt][n] = mfma_step<FMT, 3>(A.d[mt][j], b, acc[mt][n], A.s[mt][j], sb);
+        } else {
+          const int64_t g = kt * 4 + j;
+          if (g * 128 >= p.K) continue;
+          const v4f raw = mfma_raw<FMT>(A.d[mt][j], b);
+          const float sbv = sb_rows[(ntile[n] * 16 / 128) * (p.K / 128) + g];
+          const float* sa = static_cast<const float*>(p.sa) + g * p.M;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int64_t row = r4[mt] + i < hi ? r4[mt] + i : hi - 1;  // padding rows: any valid scale
+            const float f = sa[row] * sbv;
+            acc[mt][n][i] = __builtin_fmaf(raw[i], f, acc[mt][n][i]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Write one 16x16 fp32 tile (lane holds rows 4q+i, col r) to bf16 output or fp32 partials.
+__device__ __forceinline__ void store_tile(const GemmParams& p, v4f v, int64_t row0, int64_t row_hi,
+                                           int64_t col, int64_t split) {
+  if (col >= p.N) return;
+  float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = row0 + i;
+    if (row >= row_hi) continue;
+    if (p.S > 1) {
+      p.partial[(split * p.a_rows + row) * p.N + col] = v[i];
+    } else {
+      float y = bf16_round(v[i]);
+      if (p.bias) y = y + bias;
+      p.out[row * p.ldc + col] = f32_to_bf16(y);
+    }
+  }
+}
+
+// Dense: grid (n_groups, m_groups, S), KW waves per workgroup.
+// Grouped: grid (n_groups, experts, 1); the workgroup walks its expert's rows.
+template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED>
+__global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
+  extern __shared__ float red[];  // [KW][MT][NT][4][64] when KW > 1
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, KW = blockDim.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t split = blockIdx.z;
+
+  const int64_t ntiles_total = (p.N + 15) / 16;
+  int64_t ntile[NT], ntile_ld[NT];  // ntile_ld stays inside the packed buffer for a ragged last group
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    ntile[n] = (int64_t)blockIdx.x * NT + n;
+    ntile_ld[n] = ntile[n] < ntiles_total ? ntile[n] : ntiles_total - 1;
+  }
+
+  int64_t lo = 0, hi = p.M;
+  const uint8_t* w = p.w;
+  const uint8_t* sw = static_cast<const uint8_t*>(p.sw);
+  if (GROUPED) {
+    const int64_t e = blockIdx.y;
+    lo = p.expert_offsets[e];
+    hi = p.expert_offsets[e + 1];
+    if (lo >= hi) return;  // experts without routed rows read no weights
+    w += e * p.w_expert_stride;
+    sw += e * p.sw_expert_stride;
+  }
+  const int64_t mg_begin = GROUPED ? 0 : (int64_t)blockIdx.y;
+  const int64_t mg_end = GROUPED ? (hi - lo + 16 * MT - 1) / (16 * MT) : mg_begin + 1;
+
+  for (int64_t mg = mg_begin; mg < mg_end; ++mg) {
+    const int64_t rowbase = lo + mg * 16 * MT;
+    int64_t arow[MT], r4[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      int64_t row = rowbase + mt * 16 + r;
+      if (row >= hi) row = hi - 1;  // padding rows reuse a valid row; their outputs are not stored
+      arow[mt] = (GROUPED && p.row_index) ? (int64_t)(p.row_index[row] / p.row_div) : row;
+      r4[mt] = rowbase + mt * 16 + 4 * q;  // first output row held by this lane
+    }
+    v4f acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[mt][n] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t kstride = (int64_t)p.S * KW;
+    for (int64_t kt = split * KW + wv; kt < p.KT; kt += kstride) {
+      BTile<FMT, NT> B;
+      ATile<MT> A;
+      load_b<FMT, NT, BLOCK>(p, w, sw, ntile_ld, kt, lane, B);
+      load_a<MT, BLOCK>(p, arow, kt, q, A);
+      compute_tile<FMT, MT, NT, BLOCK>(p, A, B, acc, kt, r4, hi, ntile_ld,
+                                       BLOCK ? static_cast<const float*>(p.sw) : nullptr);
+    }
+
+    if (KW > 1) {
+      float* mine = red + (size_t)wv * (MT * NT * 4 * 64);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mine[((mt * NT + n) * 4 + i) * 64 + lane] = acc[mt][n][i];
+      __syncthreads();
+      const int elems = MT * NT * 4 * 64;
+      for (int e = threadIdx.x; e < elems; e += blockDim.x) {
+        float s = red[e];
+        for (int v = 1; v < KW; ++v) s += red[(size_t)v * elems + e];
+        const int l = e & 63, i = (e >> 6) & 3, tn = (e >> 8);
+        const int n = tn % NT, mt = tn / NT;
+        const int64_t row = rowbase + mt * 16 + 4 * (l >> 4) + i;
+        const int64_t col = ntile[n] * 16 + (l & 15);
+        if (col < p.N && row < hi && ntile[n] < ntiles_total) {
+          if (p.S > 1) {
+            p.partial[(split * p.a_rows + row) * p.N + col] = s;
+          } else {
+            float y = bf16_round(s);
+            if (p.bias) y = y + bf16_to_f32(p.bias[col]);
+            p.out[row * p.ldc + col] = f32_to_bf16(y);
+          }
+        }
+      }
+      __syncthreads();
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          if (ntile[n] < ntiles_total)
+            store_tile(p, acc[mt][n], rowbase + mt * 16 + 4 * q, hi, ntile[n] * 16 + r, split);
+    }
+  }
+}
+
+// Sum split-K partials in split order, round to bf16, add bias in bf16.
+__global__ void splitk_reduce_kernel(const float* __restrict__ partial, const uint16_t* __restrict__ bias,
+                                     uint16_t* __restrict__ out, int64_t M, int64_t N, int64_t ldc, int S) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= M * N) return;
+  const int64_t m = id / N, n = id - m * N;
+  float s = partial[id];
+  for (int k = 1; k < S; ++k) s += partial[(int64_t)k * M * N + id];
+  float y = bf16_round(s);
+  if (bias) y = y + bf16_to_f32(bias[n]);
+  out[m * ldc + n] = f32_to_bf16(y);
+}
+
+// ------------------------------------------------------------ configuration
+
+struct GemmConfig {
+  int MT, NT, KW, S;
+};
+
+// Choose the wave tile and K split for an (M, N, K) problem so that the
+// launch carries enough wavefronts to keep 256 CUs' memory pipes busy.
+static GemmConfig choose_config(int64_t M, int64_t N, int64_t K) {
+  GemmConfig c;
+  const int64_t KT = (K + kTileK - 1) / kTileK;
+  c.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  c.NT = M > 64 ? 1 : 1;
+  if (M > 32 && M <= 64) { c.MT = 2; c.NT = 2; }
+  const int64_t n_groups = ((N + 15) / 16 + c.NT - 1) / c.NT;
+  const int64_t m_groups = (M + 16 * c.MT - 1) / (16 * c.MT);
+  const int64_t tiles = n_groups * m_groups;
+  c.KW = (int)(KT >= 4 ? 4 : KT);
+  const int64_t target_waves = 4096;
+  int64_t S = (target_waves + tiles * c.KW - 1) / (tiles * c.KW);
+  const int64_t max_s = (KT + c.KW - 1) / c.KW;
+  if (S > max_s) S = max_s;
+  if (S < 1) S = 1;
+  c.S = (int)S;
+  return c;
+}
+
+template <int FMT, bool BLOCK, bool GROUPED>
+static hipError_t launch_gemm(const GemmConfig& c, dim3 grid, const GemmParams& p, hipStream_t stream) {
+  const size_t shmem = c.KW > 1 ? (size_t)c.KW * c.MT * c.NT * 4 * 64 * sizeof(float) : 0;
+  dim3 block(64 * c.KW);
+#define MXL_LAUNCH(MT_, NT_)                                                                        \
+  if (c.MT == MT_ && c.NT == NT_) {                                                                 \
+    hipLaunchKernelGGL((gemm_kernel<FMT, MT_, NT_, BLOCK, GROUPED>), grid, block, shmem, stream, p); \
+    return hipGetLastError();                                                                       \
+  }
+  MXL_LAUNCH(1, 1)
+  MXL_LAUNCH(2, 1)
+  MXL_LAUNCH(4, 1)
+  MXL_LAUNCH(2, 2)
+#undef MXL_LAUNCH
+  return hipErrorInvalidValue;
+}
+
+template <bool BLOCK, bool GROUPED>
+static hipError_t dispatch_fmt(int fmt, const GemmConfig& c, dim3 grid, const GemmParams& p, hipStream_t s) {
+  if (fmt == kE4M3) return launch_gemm<kE4M3, BLOCK, GROUPED>(c, grid, p, s);
+  if (BLOCK) return hipErrorInvalidValue;
+  if (fmt == kE2M3) return launch_gemm<kE2M3, false, GROUPED>(c, grid, p, s);
+  if (fmt == kE3M2) return launch_gemm<kE3M2, false, GROUPED>(c, grid, p, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mxl
+
+// ------------------------------------------------------------------- C ABI
+
+using namespace mxl;
+
+static bool valid_wfmt(int f) { return f == kE4M3 || f == kE2M3 || f == kE3M2; }
+
+extern "C" int64_t mxl_tiled_weight_bytes(int64_t N, int64_t K, int fmt) {
+  const int64_t NTl = (N + 15) / 16, KT = (K + kTileK - 1) / kTileK;
+  return NTl * KT * tile_chunks(fmt) * 1024;
+}
+
+extern "C" int64_t mxl_tiled_scale_bytes(int64_t N, int64_t K) {
+  const int64_t NTl = (N + 15) / 16, KT = (K + kTileK - 1) / kTileK;
+  return NTl * KT * 256;
+}
+
+extern "C" int mxl_pack_weight(const void* codes, const void* scales, int64_t N, int64_t K, int fmt,
+                               void* tiled_codes, void* tiled_scales, void* stream) {
+  MXL_CHECK_ARG(valid_wfmt(fmt), "mxl_pack_weight: unknown weight format %d", fmt);
+  MXL_CHECK_ARG(N > 0 && K > 0 && K % 128 == 0, "mxl_pack_weight: need N > 0 and K %% 128 == 0 (N=%lld K=%lld)",
+                (long long)N, (long long)K);
+  MXL_CHECK_ARG(((uintptr_t)codes & 15) == 0 && ((uintptr_t)tiled_codes & 15) == 0,
+                "mxl_pack_weight: codes must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t NTl = (N + 15) / 16, KT = (K + kTileK - 1) / kTileK;
+  const int CH = tile_chunks(fmt);
+  const int64_t total = NTl * KT * CH * 64;
+  const int64_t ld = fmt == kE4M3 ? K : K * 3 / 4;
+  pack_weight_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, s>>>(
+      (const uint8_t*)codes, ld, (uint8_t*)tiled_codes, N, K, KT, CH, fmt != kE4M3, total);
+  MXL_CHECK_LAUNCH("mxl_pack_weight(codes)");
+  if (scales) {
+    const int64_t ts = NTl * KT * 64;
+    pack_scale_kernel<<<dim3((unsigned)((ts + 255) / 256)), 256, 0, s>>>((const uint8_t*)scales,
+                                                                         (uint8_t*)tiled_scales, N, K, KT, ts);
+    MXL_CHECK_LAUNCH("mxl_pack_weight(scales)");
+  }
+  return MXL_OK;
+}
+
+static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw, int64_t N,
+                       int64_t K, int fmt, bool block, const void* bias, void* out, int64_t ldc, void* workspace,
+                       int64_t workspace_bytes, void* stream, const char* who) {
+  MXL_CHECK_ARG(M >= 0 && N > 0 && K > 0 && K % 128 == 0, "%s: need N > 0, K %% 128 == 0 (M=%lld N=%lld K=%lld)", who,
+                (long long)M, (long long)N, (long long)K);
+  MXL_CHECK_ARG(ldc >= N, "%s: ldc < N", who);
+  MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0, "%s: a and w must be 16-byte aligned", who);
+  if (M == 0) return MXL_OK;
+  GemmConfig c = choose_config(M, N, K);
+  const int64_t need = c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
+  if (need > workspace_bytes || (need > 0 && workspace == nullptr)) c.S = 1;  // no room: skip the K split
+  GemmParams p{};
+  p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw;
+  p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out; p.partial = (float*)workspace;
+  p.lda = K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
+  p.row_div = 1; p.S = c.S;
+  const int64_t n_groups = ((N + 15) / 16 + c.NT - 1) / c.NT;
+  const int64_t m_groups = (M + 16 * c.MT - 1) / (16 * c.MT);
+  dim3 grid((unsigned)n_groups, (unsigned)m_groups, (unsigned)c.S);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = block ? dispatch_fmt<true, false>(fmt, c, grid, p, s) : dispatch_fmt<false, false>(fmt, c, grid, p, s);
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", who, hipGetErrorString(e));
+    return MXL_EHIP;
+  }
+  if (c.S > 1) {
+    splitk_reduce_kernel<<<dim3((unsigned)((M * N + 255) / 256)), 256, 0, s>>>(
+        (const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, c.S);
+    MXL_CHECK_LAUNCH(who);
+  }
+  return MXL_OK;
+}
+
+extern "C" int64_t mxl_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0) return 0;
+  GemmConfig c = choose_config(M, N, K);
+  return c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
+}
+
+extern "C" int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,
+                           int64_t N, int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm: unknown weight format %d", w_fmt);
+  return gemm_common(a, sa, M, w_tiled, sw_tiled, N, K, w_fmt, false, bias, out, ldc, workspace, workspace_bytes,
+                     stream, "mxl_mx_gemm");
+}
+
+extern "C" int mxl_block_fp8_gemm(const void* a, const void* sa_colmajor, int64_t M, const void* w_tiled,
+                                  const void* sb, int64_t N, int64_t K, const void* bias, void* out, int64_t ldc,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemm_common(a, sa_colmajor, M, w_tiled, sb, N, K, kE4M3, true, bias, out, ldc, workspace, workspace_bytes,
+                     stream, "mxl_block_fp8_gemm");
+}
+
+extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index, int row_div,
+                                const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
+                                const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
+                                void* out, void* stream) {
+  MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_grouped_gemm: unknown weight format %d", w_fmt);
+  MXL_CHECK_ARG(N > 0 && K > 0 && K % 128 == 0 && num_experts > 0 && row_div >= 1,
+                "mxl_grouped_gemm: need N > 0, K %% 128 == 0, experts > 0");
+  MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0, "mxl_grouped_gemm: misaligned operands");
+  if (routed_rows == 0) return MXL_OK;
+  GemmConfig c;
+  const int64_t KT = (K + kTileK - 1) / kTileK;
+  c.MT = 1; c.NT = 1; c.S = 1;
+  c.KW = (int)(KT >= 4 ? 4 : KT);
+  GemmParams p{};
+  p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;
+  p.out = (uint16_t*)out; p.row_index = row_index; p.expert_offsets = expert_offsets;
+  p.lda = K; p.ldc = N; p.M = routed_rows; p.N = N; p.K = K; p.KT = KT; p.a_rows = a_rows;
+  p.w_expert_stride = mxl_tiled_weight_bytes(N, K, w_fmt);
+  p.sw_expert_stride = mxl_tiled_scale_bytes(N, K);
+  p.row_div = row_div; p.S = 1;
+  dim3 grid((unsigned)((N + 15) / 16), (unsigned)num_experts, 1);
+  hipError_t e = dispatch_fmt<false, true>(w_fmt, c, grid, p, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    set_error("mxl_grouped_gemm: launch failed: %s", hipGetErrorString(e));
+    return MXL_EHIP;
+  }
+  return MXL_OK;
+}

@@ -1,0 +1,181 @@
+// MoE token sort and weighted combine for gfx950.
+//
+// Token sort: routes r = t * topk + k are grouped by expert id, keeping
+// ascending r inside each expert (a stable counting sort), which yields
+//   expert_offsets[E + 1]  exclusive prefix of per-expert route counts
+//   sorted_routes[pos]     route at each sorted position
+//   inverse[r]             sorted position of each route (-1 if dropped)
+// Three passes over 1024-route chunks: per-chunk histograms (LDS atomics,
+// order free), one workgroup scanning chunks and experts, then a pass that
+// ranks each route inside its chunk (shuffle count inside the wavefront plus
+// an LDS prefix over the chunk's 16 wavefronts) and scatters.
+//
+// Combine: out[t, h] = bf16(sum_k y[inverse[t*topk + k], h] * w[t, k]),
+// each product rounded to binary32 and added in ascending k from zero.
+#include "mx_common.h"
+
+namespace mxl {
+
+constexpr int kChunk = 1024;
+
+__global__ __launch_bounds__(kChunk) void route_hist_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
+                                                           int32_t* __restrict__ chunk_counts) {
+  extern __shared__ int32_t hist[];
+  const int64_t c = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+  __syncthreads();
+  const int64_t r = c * kChunk + threadIdx.x;
+  if (r < R) {
+    const int32_t e = ids[r];
+    if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) chunk_counts[c * E + e] = hist[e];
+}
+
+// One workgroup: chunk bases per expert (in place) and expert offsets.
+__global__ __launch_bounds__(1024) void route_scan_kernel(int32_t* __restrict__ chunk_counts, int64_t C, int E,
+                                                         int64_t* __restrict__ expert_offsets) {
+  extern __shared__ int64_t tot[];  // [2][E]
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int64_t run = 0;
+    for (int64_t c = 0; c < C; ++c) {
+      const int32_t v = chunk_counts[c * E + e];
+      chunk_counts[c * E + e] = (int32_t)run;
+      run += v;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+  // inclusive Hillis-Steele scan over E values (ping-pong buffers)
+  int src = 0;
+  for (int d = 1; d < E; d <<= 1) {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      int64_t v = tot[src * E + e];
+      if (e >= d) v += tot[src * E + e - d];
+      tot[(1 - src) * E + e] = v;
+    }
+    __syncthreads();
+    src = 1 - src;
+  }
+  for (int e = threadIdx.x; e < E; e += blockDim.x) expert_offsets[e + 1] = tot[src * E + e];
+  if (threadIdx.x == 0) expert_offsets[0] = 0;
+}
+
+__global__ __launch_bounds__(kChunk) void route_scatter_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
+                                                              const int32_t* __restrict__ chunk_base,
+                                                              const int64_t* __restrict__ expert_offsets,
+                                                              int32_t* __restrict__ sorted_routes,
+                                                              int32_t* __restrict__ inverse) {
+  extern __shared__ int32_t whist[];  // [kChunk / 64][E]
+  const int64_t c = blockIdx.x;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  constexpr int W = kChunk / 64;
+  for (int i = t; i < W * E; i += blockDim.x) whist[i] = 0;
+  const int64_t r = c * kChunk + t;
+  const int32_t e = r < R ? ids[r] : -1;
+  const bool valid = e >= 0 && e < E;
+  int rank = 0;  // routes of the same expert in earlier lanes of this wavefront
+  for (int l = 0; l < 64; ++l) {
+    const int32_t el = __shfl(e, l);
+    rank += (l < lane && el == e) ? 1 : 0;
+  }
+  __syncthreads();
+  if (valid) atomicAdd(&whist[w * E + e], 1);
+  __syncthreads();
+  for (int x = t; x < E; x += blockDim.x) {
+    int32_t run = 0;
+    for (int v = 0; v < W; ++v) {
+      const int32_t n = whist[v * E + x];
+      whist[v * E + x] = run;
+      run += n;
+    }
+  }
+  __syncthreads();
+  if (r >= R) return;
+  if (!valid) {
+    inverse[r] = -1;
+    return;
+  }
+  const int64_t pos = expert_offsets[e] + chunk_base[c * E + e] + whist[w * E + e] + rank;
+  sorted_routes[pos] = (int32_t)r;
+  inverse[r] = (int32_t)pos;
+}
+
+// One thread: 8 consecutive hidden columns of one token.
+__global__ __launch_bounds__(256) void moe_reduce_kernel(const uint16_t* __restrict__ y,
+                                                         const float* __restrict__ topk_weights,
+                                                         const int32_t* __restrict__ inverse, int64_t T, int topk,
+                                                         int64_t H, uint16_t* __restrict__ out) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_row = H / 8;
+  if (id >= T * per_row) return;
+  const int64_t t = id / per_row, h0 = (id - t * per_row) * 8;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int k = 0; k < topk; ++k) {
+    const int32_t p = inverse[t * topk + k];
+    if (p < 0) continue;
+    const float wk = topk_weights[t * topk + k];
+    float v[8];
+    bf16x8_to_f32(*reinterpret_cast<const uint4*>(y + (int64_t)p * H + h0), v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float term = v[i] * wk;
+      acc[i] = acc[i] + term;
+    }
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (uint32_t)f32_to_bf16(acc[2 * i]) | ((uint32_t)f32_to_bf16(acc[2 * i + 1]) << 16);
+  *reinterpret_cast<uint4*>(out + t * H + h0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+}  // namespace mxl
+
+using namespace mxl;
+
+extern "C" int64_t mxl_moe_route_workspace_bytes(int64_t T, int64_t topk, int64_t E) {
+  const int64_t R = T * topk;
+  const int64_t C = (R + kChunk - 1) / kChunk;
+  return C * E * (int64_t)sizeof(int32_t);
+}
+
+extern "C" int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_routes,
+                             int64_t* expert_offsets, int32_t* inverse, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  MXL_CHECK_ARG(T >= 0 && topk > 0 && E > 0, "mxl_moe_route: need T >= 0, topk > 0, E > 0");
+  MXL_CHECK_ARG(E <= 4096, "mxl_moe_route: at most 4096 experts (E=%lld)", (long long)E);
+  const int64_t R = T * topk;
+  const int64_t C = (R + kChunk - 1) / kChunk;
+  MXL_CHECK_ARG(workspace_bytes >= mxl_moe_route_workspace_bytes(T, topk, E) && (C == 0 || workspace),
+                "mxl_moe_route: workspace too small (%lld < %lld bytes)", (long long)workspace_bytes,
+                (long long)mxl_moe_route_workspace_bytes(T, topk, E));
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* counts = (int32_t*)workspace;
+  if (C > 0) {
+    route_hist_kernel<<<dim3((unsigned)C), kChunk, E * sizeof(int32_t), s>>>(topk_ids, R, (int)E, counts);
+    MXL_CHECK_LAUNCH("mxl_moe_route(hist)");
+  }
+  route_scan_kernel<<<1, 1024, 2 * E * sizeof(int64_t), s>>>(counts, C, (int)E, expert_offsets);
+  MXL_CHECK_LAUNCH("mxl_moe_route(scan)");
+  if (C > 0) {
+    route_scatter_kernel<<<dim3((unsigned)C), kChunk, (kChunk / 64) * E * sizeof(int32_t), s>>>(
+        topk_ids, R, (int)E, counts, expert_offsets, sorted_routes, inverse);
+    MXL_CHECK_LAUNCH("mxl_moe_route(scatter)");
+  }
+  return MXL_OK;
+}
+
+extern "C" int mxl_moe_reduce(const void* routed_output, const float* topk_weights, const int32_t* inverse, int64_t T,
+                              int64_t topk, int64_t H, void* out, void* stream) {
+  MXL_CHECK_ARG(T >= 0 && topk > 0 && H > 0 && H % 8 == 0, "mxl_moe_reduce: need H %% 8 == 0 (H=%lld)", (long long)H);
+  MXL_CHECK_ARG(((uintptr_t)routed_output & 15) == 0 && ((uintptr_t)out & 15) == 0, "mxl_moe_reduce: misaligned");
+  if (T == 0) return MXL_OK;
+  const int64_t n = T * (H / 8);
+  moe_reduce_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)routed_output, topk_weights, inverse, T, (int)topk, H, (uint16_t*)out);
+  MXL_CHECK_LAUNCH("mxl_moe_reduce");
+  return MXL_OK;
+}

@@ -1,0 +1,151 @@
+// Shared device helpers for the MI355X (gfx950) quantized-linear library.
+//
+// Every conversion here is a binary32 / integer operation sequence with
+// round-to-nearest-even and no contraction (the library is compiled with
+// -ffp-contract=off; fused steps call __builtin_fmaf explicitly), so codes
+// and scales are bit-identical to a CPU evaluation of the same sequence.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxl {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// element formats understood by the scaled MFMA (cbsz / blgp operand)
+enum Fmt : int { kE4M3 = 0, kE5M2 = 1, kE2M3 = 2, kE3M2 = 3 };
+
+// E8M0 scale rules
+enum Rule : int { kFloorCarry175 = 0, kCeilDiv448 = 1 };
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+// round-to-nearest-even binary32 -> bf16, NaN -> 0x7FC0
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// binary32 -> E4M3 ("fn") with torch's cast semantics: RNE onto the E4M3
+// grid; magnitudes that round past 448, or are >= 480, give the NaN code.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  uint32_t u = f2u(f);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  if (a >= 0x43F00000u) return sign | 0x7Fu;
+  if (a < 0x3C800000u) return sign | (uint32_t)__builtin_rintf(u2f(a) * 512.0f);
+  uint32_t odd = (a >> 20) & 1u;
+  return sign | ((a - (120u << 23) + 0x7FFFFu + odd) >> 20);
+}
+
+// E8M0 code of the floor_carry175 rule from the bf16 bits of the block amax
+__device__ __forceinline__ uint32_t scale_floor_carry175(uint32_t amax_bf16) {
+  uint32_t e = (((amax_bf16 + 32u) & 0xFF80u) >> 7) & 0xFFu;
+  return e == 0 ? 0u : (uint32_t)((int)e - 8) & 0xFFu;
+}
+
+// power-of-two bits (exponent field only) of the ceil_div448 rule
+__device__ __forceinline__ uint32_t pow2_ceil_div448(float amax) {
+  float raw = amax / 448.0f;
+  if (!(raw >= 1.0e-30f)) raw = 1.0e-30f;
+  return (f2u(raw) + 0x007FFFFFu) & 0x7F800000u;
+}
+
+// exp() with a fixed binary32 operation sequence: Cody-Waite reduction by ln2
+// and the Cephes expf minimax polynomial (S. L. Moshier), explicit FMAs.
+__device__ __forceinline__ float mx_exp(float x) {
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.0f) return __builtin_inff();
+  float n = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(n, -0.693359375f, x);
+  r = __builtin_fmaf(n, 2.12194440e-4f, r);
+  float p = 1.9875691500e-4f;
+  p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+  p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+  p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+  p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+  p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+  float r2 = r * r;
+  float y = __builtin_fmaf(p, r2, r) + 1.0f;
+  return __builtin_ldexpf(y, (int)n);
+}
+
+// Quantize 32 values (each exactly a bf16) held by one thread: returns the
+// E8M0 code and writes 8 dwords of packed E4M3 codes (byte i = value i).
+template <int RULE>
+__device__ __forceinline__ uint32_t quant32(const float* v, uint32_t* packed) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+  uint32_t s;
+  float mul;
+  int e2 = 0;
+  if (RULE == kFloorCarry175) {
+    s = scale_floor_carry175(f2u(amax) >> 16);
+    e2 = 127 - (int)s;
+  } else {
+    uint32_t bits = pow2_ceil_div448(amax);
+    s = bits >> 23;
+    mul = 1.0f / u2f(bits);
+  }
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      float x = v[d * 4 + b];
+      float y = RULE == kFloorCarry175 ? __builtin_ldexpf(x, e2) : x * mul;
+      w |= f32_to_e4m3(y) << (8 * b);
+    }
+    packed[d] = w;
+  }
+  return s;
+}
+
+// Unpack 8 bf16 from a 16-byte vector into floats
+__device__ __forceinline__ void bf16x8_to_f32(uint4 q, float* f) {
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = u2f(w[i] << 16);
+    f[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
+  }
+}
+
+}  // namespace mxl
+
+// ---------------------------------------------------------------- host side
+
+#define MXL_OK 0
+#define MXL_EINVAL -1
+#define MXL_EHIP -2
+#define MXL_EUNSUPPORTED -3
+
+namespace mxl {
+void set_error(const char* fmt, ...);
+}
+
+#define MXL_CHECK_ARG(cond, ...)           \
+  do {                                     \
+    if (!(cond)) {                         \
+      ::mxl::set_error(__VA_ARGS__);       \
+      return MXL_EINVAL;                   \
+    }                                      \
+  } while (0)
+
+#define MXL_CHECK_LAUNCH(what)                                                       \
+  do {                                                                               \
+    hipError_t e_ = hipGetLastError();                                               \
+    if (e_ != hipSuccess) {                                                          \
+      ::mxl::set_error("%s: launch failed: %s", what, hipGetErrorString(e_));       \
+      return MXL_EHIP;                                                               \
+    }                                                                                \
+  } while (0)

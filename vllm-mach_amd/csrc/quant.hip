@@ -1,0 +1,253 @@
+// Activation quantizers and fused producers for gfx950.
+//
+//  * MXFP8 dynamic quantization (E4M3 codes, E8M0 scale per 32 along K)
+//  * SwiGLU -> MXFP8 producer (bf16 SiLU, bf16 product, ceil_div448 scales)
+//  * block-FP8 per-token group-128 quantization (fp32 scales, column-major)
+//  * SiLU*up -> block-FP8 producer
+//
+// All four are HBM-bound elementwise passes: one thread owns one 32-element
+// MX block (so the amax needs no cross-lane traffic) or 16 lanes own one
+// 128-element group (amax by xor-shuffle inside the 16-lane row).  Loads and
+// stores are 16-byte vectors; consecutive threads walk consecutive blocks of
+// a row so every wavefront access is one contiguous span.
+#include "mx_common.h"
+
+namespace mxl {
+
+// --------------------------------------------------------------- MXFP8 quant
+
+template <int RULE>
+__global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                          uint8_t* __restrict__ codes,
+                                                          uint8_t* __restrict__ scales, int64_t M,
+                                                          int64_t K) {
+  const int64_t blocks_per_row = K / 32;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= M * blocks_per_row) return;
+  const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
+  const uint4* src = reinterpret_cast<const uint4*>(x + row * ldx + blk * 32);
+  float v[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) bf16x8_to_f32(src[q], v + 8 * q);
+  uint32_t packed[8];
+  uint32_t s = quant32<RULE>(v, packed);
+  uint4* dst = reinterpret_cast<uint4*>(codes + row * K + blk * 32);
+  dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  scales[row * blocks_per_row + blk] = (uint8_t)s;
+}
+
+// ------------------------------------------------------------ SwiGLU -> MXFP8
+
+__device__ __forceinline__ int64_t swizzle_offset(int64_t r, int64_t g, int64_t K) {
+  const int64_t T = (K / 32 + 3) / 4;
+  return (((r / 128 * T + g / 4) * 32 + r % 32) * 4 + (r % 128) / 32) * 4 + g % 4;
+}
+
+template <int RULE, bool SWIZZLED>
+__global__ __launch_bounds__(256) void swiglu_mxfp8_kernel(const uint16_t* __restrict__ gate_up,
+                                                           uint8_t* __restrict__ codes,
+                                                           uint8_t* __restrict__ scales, int64_t M,
+                                                           int64_t K) {
+  const int64_t blocks_per_row = K / 32;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= M * blocks_per_row) return;
+  const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
+  const uint4* g4 = reinterpret_cast<const uint4*>(gate_up + row * 2 * K + blk * 32);
+  const uint4* u4 = reinterpret_cast<const uint4*>(gate_up + row * 2 * K + K + blk * 32);
+  float g[32], u[32], v[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    bf16x8_to_f32(g4[q], g + 8 * q);
+    bf16x8_to_f32(u4[q], u + 8 * q);
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    float act = bf16_round(g[i] / (1.0f + mx_exp(-g[i])));
+    v[i] = bf16_round(act * u[i]);
+  }
+  uint32_t packed[8];
+  uint32_t s = quant32<RULE>(v, packed);
+  uint4* dst = reinterpret_cast<uint4*>(codes + row * K + blk * 32);
+  dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  if (SWIZZLED)
+    scales[swizzle_offset(row, blk, K)] = (uint8_t)s;
+  else
+    scales[row * blocks_per_row + blk] = (uint8_t)s;
+}
+
+// Zero the padding bytes of a swizzled scale buffer (rows beyond M inside the
+// last 128-row tile and groups beyond K/32 inside the last 4-group tile), so
+// the buffer content is a pure function of the input.
+__global__ void swizzle_pad_kernel(uint8_t* __restrict__ scales, int64_t M, int64_t K, int64_t total) {
+  const int64_t off = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (off >= total) return;
+  // invert the map: off = (((rt*T + gt)*32 + r32)*4 + r4)*4 + g4
+  const int64_t T = (K / 32 + 3) / 4;
+  int64_t t = off;
+  const int64_t g4 = t % 4; t /= 4;
+  const int64_t r4 = t % 4; t /= 4;
+  const int64_t r32 = t % 32; t /= 32;
+  const int64_t gt = t % T, rt = t / T;
+  const int64_t r = rt * 128 + r4 * 32 + r32, g = gt * 4 + g4;
+  if (r >= M || g >= K / 32) scales[off] = 0;
+}
+
+// ------------------------------------------------------- block-FP8 quantizer
+
+// 16 lanes own one 128-element group; each lane holds 8 consecutive values.
+__device__ __forceinline__ float group16_amax(float m) {
+#pragma unroll
+  for (int d = 8; d >= 1; d >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, d, 16));
+  return m;
+}
+
+__global__ __launch_bounds__(256) void quant_block_fp8_kernel(const uint16_t* __restrict__ x,
+                                                              uint8_t* __restrict__ q,
+                                                              float* __restrict__ s_colmajor,
+                                                              int64_t M, int64_t K) {
+  const int64_t groups = M * (K / 128);
+  const int64_t gid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 16;
+  const int sub = threadIdx.x & 15;
+  const bool live = gid < groups;
+  const int64_t g = live ? gid : groups - 1;  // keep every lane in the shuffle
+  const int64_t row = g / (K / 128), col = g - row * (K / 128);
+  float v[8];
+  bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * K + col * 128 + sub * 8), v);
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+  m = group16_amax(m);
+  m = __builtin_fmaxf(m, 1e-10f);
+  const float scale = m / 448.0f;
+  uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float y = v[i] / scale;
+    y = __builtin_fminf(__builtin_fmaxf(y, -448.0f), 448.0f);
+    uint32_t c = f32_to_e4m3(y);
+    if (i < 4) w0 |= c << (8 * i); else w1 |= c << (8 * (i - 4));
+  }
+  if (!live) return;
+  *reinterpret_cast<uint2*>(q + row * K + col * 128 + sub * 8) = make_uint2(w0, w1);
+  if (sub == 0) s_colmajor[col * M + row] = scale;
+}
+
+template <bool TRANSPOSED>
+__global__ __launch_bounds__(256) void silu_mul_block_fp8_kernel(const uint16_t* __restrict__ in,
+                                                                 uint8_t* __restrict__ q,
+                                                                 float* __restrict__ scales,
+                                                                 int64_t rows, int64_t H) {
+  const int64_t groups = rows * (H / 128);
+  const int64_t gid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 16;
+  const int sub = threadIdx.x & 15;
+  const bool live = gid < groups;
+  const int64_t g = live ? gid : groups - 1;
+  const int64_t row = g / (H / 128), col = g - row * (H / 128);
+  float gt[8], up[8], v[8];
+  bf16x8_to_f32(*reinterpret_cast<const uint4*>(in + row * 2 * H + col * 128 + sub * 8), gt);
+  bf16x8_to_f32(*reinterpret_cast<const uint4*>(in + row * 2 * H + H + col * 128 + sub * 8), up);
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float sig = 1.0f / (1.0f + mx_exp(-gt[i]));
+    v[i] = (gt[i] * sig) * up[i];
+    m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+  }
+  m = group16_amax(m);
+  const float scale = __builtin_fmaxf(m / 448.0f, 1.0f / (448.0f * 512.0f));
+  uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float y = __builtin_fmaxf(-448.0f, __builtin_fminf(v[i] / scale, 448.0f));
+    uint32_t c = f32_to_e4m3(y);
+    if (i < 4) w0 |= c << (8 * i); else w1 |= c << (8 * (i - 4));
+  }
+  if (!live) return;
+  *reinterpret_cast<uint2*>(q + row * H + col * 128 + sub * 8) = make_uint2(w0, w1);
+  if (sub == 0) scales[TRANSPOSED ? col * rows + row : row * (H / 128) + col] = scale;
+}
+
+}  // namespace mxl
+
+// ------------------------------------------------------------------- C ABI
+
+using namespace mxl;
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t ldx, int rule,
+                                  void* codes, void* scales, void* stream) {
+  MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_quantize_mxfp8: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
+  MXL_CHECK_ARG(ldx >= K && ldx % 8 == 0, "mxl_quantize_mxfp8: ldx must be >= K and a multiple of 8");
+  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_quantize_mxfp8: unknown rule %d", rule);
+  MXL_CHECK_ARG(aligned16(x) && aligned16(codes), "mxl_quantize_mxfp8: x and codes must be 16-byte aligned");
+  if (M == 0) return MXL_OK;
+  const int64_t n = M * (K / 32);
+  dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (rule == kFloorCarry175)
+    quant_mxfp8_kernel<kFloorCarry175><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)codes, (uint8_t*)scales, M, K);
+  else
+    quant_mxfp8_kernel<kCeilDiv448><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)codes, (uint8_t*)scales, M, K);
+  MXL_CHECK_LAUNCH("mxl_quantize_mxfp8");
+  return MXL_OK;
+}
+
+extern "C" int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K) {
+  return (M + 127) / 128 * 128 * ((K / 32 + 3) / 4) * 4;
+}
+
+extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int rule, int swizzled,
+                                void* codes, void* scales, void* stream) {
+  MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_swiglu_mxfp8: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
+  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_swiglu_mxfp8: unknown rule %d", rule);
+  MXL_CHECK_ARG(aligned16(gate_up) && aligned16(codes), "mxl_swiglu_mxfp8: gate_up and codes must be 16-byte aligned");
+  if (M == 0) return MXL_OK;
+  const int64_t n = M * (K / 32);
+  dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  const uint16_t* in = (const uint16_t*)gate_up;
+  uint8_t* c = (uint8_t*)codes;
+  uint8_t* sc = (uint8_t*)scales;
+  if (swizzled) {
+    const int64_t total = mxl_swizzled_scale_bytes(M, K);
+    swizzle_pad_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, s>>>(sc, M, K, total);
+    if (rule == kFloorCarry175) swiglu_mxfp8_kernel<kFloorCarry175, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+    else swiglu_mxfp8_kernel<kCeilDiv448, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+  } else {
+    if (rule == kFloorCarry175) swiglu_mxfp8_kernel<kFloorCarry175, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+    else swiglu_mxfp8_kernel<kCeilDiv448, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+  }
+  MXL_CHECK_LAUNCH("mxl_swiglu_mxfp8");
+  return MXL_OK;
+}
+
+extern "C" int mxl_quantize_block_fp8(const void* x, int64_t M, int64_t K, void* q, void* s_colmajor,
+                                      void* stream) {
+  MXL_CHECK_ARG(M >= 0 && K > 0 && K % 128 == 0, "mxl_quantize_block_fp8: need K %% 128 == 0 (K=%lld)", (long long)K);
+  MXL_CHECK_ARG(aligned16(x) && ((uintptr_t)q & 7) == 0, "mxl_quantize_block_fp8: misaligned buffers");
+  if (M == 0) return MXL_OK;
+  const int64_t threads = M * (K / 128) * 16;
+  quant_block_fp8_kernel<<<dim3((unsigned)((threads + 255) / 256)), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x, (uint8_t*)q, (float*)s_colmajor, M, K);
+  MXL_CHECK_LAUNCH("mxl_quantize_block_fp8");
+  return MXL_OK;
+}
+
+extern "C" int mxl_silu_mul_block_fp8(const void* input, int64_t rows, int64_t H, int transposed, void* q,
+                                      void* scales, void* stream) {
+  MXL_CHECK_ARG(rows >= 0 && H > 0 && H % 128 == 0, "mxl_silu_mul_block_fp8: need H %% 128 == 0 (H=%lld)", (long long)H);
+  MXL_CHECK_ARG(aligned16(input) && ((uintptr_t)q & 7) == 0, "mxl_silu_mul_block_fp8: misaligned buffers");
+  if (rows == 0) return MXL_OK;
+  const int64_t threads = rows * (H / 128) * 16;
+  dim3 grid((unsigned)((threads + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (transposed)
+    silu_mul_block_fp8_kernel<true><<<grid, 256, 0, s>>>((const uint16_t*)input, (uint8_t*)q, (float*)scales, rows, H);
+  else
+    silu_mul_block_fp8_kernel<false><<<grid, 256, 0, s>>>((const uint16_t*)input, (uint8_t*)q, (float*)scales, rows, H);
+  MXL_CHECK_LAUNCH("mxl_silu_mul_block_fp8");
+  return MXL_OK;
+}

@@ -1,0 +1,395 @@
+"""Torch-facing operators over the gfx950 C ABI.
+
+Every operator enqueues on the current HIP stream of its input's device,
+allocates a fresh output per call, and is registered as a ``torch.library``
+custom op whose fake implementation keeps the row count symbolic (the
+contract of the reference's ``direct_register_custom_op`` ops, e.g.
+src/vllm_mach/mxfp6/dense_mxfp8.py:99-111 and mxfp8/native_backend.py:208-220).
+Scratch memory (split-K partials, routing counts) lives in per-(device, stream)
+workspaces that grow outside graph capture and raise inside it when a shape
+was not warmed (mxfp8/native_backend.py:159-189).
+"""
+from __future__ import annotations
+
+import threading
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, query, stream_handle
+
+E4M3, E2M3, E3M2 = 0, 2, 3
+FLOOR_CARRY175, CEIL_DIV448 = 0, 1
+FORMATS = {"e4m3": E4M3, "e2m3": E2M3, "e3m2": E3M2}
+
+_ws_lock = threading.RLock()
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_COUNTS: dict[str, int] = {}
+
+
+def _count(key: str) -> None:
+    _COUNTS[key] = _COUNTS.get(key, 0) + 1
+
+
+def inspect() -> dict:
+    """Call counters (eager/capture invocations, not graph replays) and workspace sizes."""
+    with _ws_lock:
+        return {"counts": dict(_COUNTS),
+                "workspaces": {f"{d}:{s:#x}": t.numel() for (d, s), t in _workspaces.items()}}
+
+
+def workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
+    """Per-(device, stream) scratch of at least ``nbytes``; never reallocated during capture."""
+    if nbytes <= 0:
+        return None
+    key = (device.index, stream_handle(device))
+    with _ws_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    f"mach_amd workspace for stream {key[1]:#x} holds "
+                    f"{0 if buf is None else buf.numel()} bytes but this shape needs {nbytes}; "
+                    "run the shape once (warmup) before graph capture")
+            size = max(nbytes, 0 if buf is None else 2 * buf.numel())
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            _workspaces[key] = buf
+        return buf
+
+
+def _u8(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.uint8 else t.view(torch.uint8)
+
+
+def _check_cuda(*ts) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("mach_amd operators need tensors on a HIP device")
+
+
+# -------------------------------------------------------------- quantizers
+
+@torch.library.custom_op("mach_amd::quantize_mxfp8", mutates_args=())
+def quantize_mxfp8(x: torch.Tensor, rule: int = FLOOR_CARRY175) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 [M, K] -> (E4M3 codes [M, K], E8M0 scales u8 [M, K/32]).
+
+    Replaces ``torch.ops.mxfp6.quantize_mxfp8`` / ``quantize_mxfp8_logical``
+    (src/vllm_mach/mxfp6/dense_mxfp8.py:40, mxfp6/moe_utils.py:172-202).
+    """
+    _check_cuda(x)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.shape[1] % 32:
+        raise ValueError("quantize_mxfp8 needs a 2-D bf16 tensor with K % 32 == 0")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M, K = x.shape
+    codes = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
+    scales = torch.empty((M, K // 32), dtype=torch.uint8, device=x.device)
+    if M:
+        call("mxl_quantize_mxfp8", ptr(x), M, K, x.stride(0), rule, ptr(codes), ptr(scales),
+             stream_handle(x.device))
+    _count("quantize_mxfp8")
+    return codes, scales
+
+
+@quantize_mxfp8.register_fake
+def _(x, rule=FLOOR_CARRY175):
+    return (x.new_empty(x.shape, dtype=torch.float8_e4m3fn),
+            x.new_empty((x.shape[0], x.shape[1] // 32), dtype=torch.uint8))
+
+
+@torch.library.custom_op("mach_amd::swiglu_mxfp8", mutates_args=())
+def swiglu_mxfp8(gate_up: torch.Tensor, rule: int = CEIL_DIV448,
+                 swizzled: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """SwiGLU -> MXFP8 producer, gate_up bf16 [M, 2K] -> (E4M3 [M, K], scales).
+
+    Replaces ``_triton_quantize`` (src/vllm_mach/mxfp6/mxfp8_mlp.py:113-127);
+    ``swizzled=True`` writes the reference's swizzled scale buffer
+    (mxfp8_mlp.py:107-110,122), otherwise logical [M, K/32].
+    """
+    _check_cuda(gate_up)
+    if gate_up.dtype != torch.bfloat16 or gate_up.ndim != 2 or gate_up.shape[1] % 64:
+        raise ValueError("swiglu_mxfp8 needs bf16 [M, 2K] with K % 32 == 0")
+    gate_up = gate_up.contiguous()
+    M, K = gate_up.shape[0], gate_up.shape[1] // 2
+    codes = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=gate_up.device)
+    if swizzled:
+        scales = torch.empty((query("mxl_swizzled_scale_bytes", M, K),), dtype=torch.uint8, device=gate_up.device)
+    else:
+        scales = torch.empty((M, K // 32), dtype=torch.uint8, device=gate_up.device)
+    if M:
+        call("mxl_swiglu_mxfp8", ptr(gate_up), M, K, rule, int(swizzled), ptr(codes), ptr(scales),
+             stream_handle(gate_up.device))
+    _count("swiglu_mxfp8")
+    return codes, scales
+
+
+@swiglu_mxfp8.register_fake
+def _(gate_up, rule=CEIL_DIV448, swizzled=False):
+    M, K = gate_up.shape[0], gate_up.shape[1] // 2
+    codes = gate_up.new_empty((M, K), dtype=torch.float8_e4m3fn)
+    if swizzled:
+        rows = (M + 127) // 128 * 128
+        return codes, gate_up.new_empty((rows * ((K // 32 + 3) // 4) * 4,), dtype=torch.uint8)
+    return codes, gate_up.new_empty((M, K // 32), dtype=torch.uint8)
+
+
+@torch.library.custom_op("mach_amd::quantize_block_fp8", mutates_args=())
+def quantize_block_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-token group-128 FP8 quantization -> (E4M3 [M, K], fp32 [M, K/128] stride (1, M)).
+
+    Replaces ``_quantize_kernel.quantize_out`` (src/vllm_mach/fp8/_quantize_kernel.py:20-25).
+    """
+    _check_cuda(x)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.shape[1] % 128:
+        raise ValueError("quantize_block_fp8 needs bf16 [M, K] with K % 128 == 0")
+    x = x.contiguous()
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty((K // 128, M), dtype=torch.float32, device=x.device).t()
+    if M:
+        call("mxl_quantize_block_fp8", ptr(x), M, K, ptr(q), ptr(s), stream_handle(x.device))
+    _count("quantize_block_fp8")
+    return q, s
+
+
+@quantize_block_fp8.register_fake
+def _(x):
+    M, K = x.shape
+    return (x.new_empty((M, K), dtype=torch.float8_e4m3fn),
+            x.new_empty((K // 128, M), dtype=torch.float32).t())
+
+
+@torch.library.custom_op("mach_amd::silu_and_mul_per_block_quant", mutates_args=("out", "scales"))
+def silu_and_mul_per_block_quant(out: torch.Tensor, input: torch.Tensor, scales: torch.Tensor,
+                                 is_scale_transposed: bool) -> None:
+    """SiLU(gate)*up -> block-FP8, in place; the contract of ``mach_fp8_activation::run``
+    (native/fp8_activation/activation.cu:62-104): input bf16 [rows, 2H], out E4M3 [rows, H],
+    scales fp32 [rows, H/128] contiguous or with stride (1, rows)."""
+    _check_cuda(out, input, scales)
+    rows, H2 = input.shape
+    H = H2 // 2
+    if (input.dtype != torch.bfloat16 or out.dtype != torch.float8_e4m3fn or scales.dtype != torch.float32
+            or tuple(out.shape) != (rows, H) or tuple(scales.shape) != (rows, H // 128) or H % 128
+            or not input.is_contiguous() or not out.is_contiguous()):
+        raise ValueError("silu_and_mul_per_block_quant: unexpected dtype/shape/layout")
+    if is_scale_transposed:
+        if rows > 1 and scales.stride() != (1, rows):
+            raise ValueError("transposed scales need stride (1, rows)")
+    elif not scales.is_contiguous():
+        raise ValueError("scales must be contiguous")
+    if rows:
+        call("mxl_silu_mul_block_fp8", ptr(input), rows, H, int(is_scale_transposed), ptr(out), ptr(scales),
+             stream_handle(input.device))
+    _count("silu_and_mul_per_block_quant")
+
+
+@silu_and_mul_per_block_quant.register_fake
+def _(out, input, scales, is_scale_transposed):
+    return None
+
+
+# ------------------------------------------------------------ weight layout
+
+def pack_weight(codes: torch.Tensor, scales: Optional[torch.Tensor], fmt: int) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Logical checkpoint layout -> MFMA-tiled layout (load time, replaces ``pack_scales``,
+    src/vllm_mach/mxfp6/dense_mxfp8.py:150-151 and dense.py:185-188).
+
+    codes: E4M3 [N, K] (fmt 0) or packed FP6 u8 [N, 3K/4]; scales: E8M0 u8 [N, K/32] or None.
+    Batched [E, N, ...] inputs are packed per expert into one contiguous buffer.
+    """
+    _check_cuda(codes, scales)
+    if codes.ndim == 3:
+        parts = [pack_weight(codes[e], None if scales is None else scales[e], fmt) for e in range(codes.shape[0])]
+        w = torch.stack([p[0] for p in parts])
+        s = None if scales is None else torch.stack([p[1] for p in parts])
+        return w, s
+    c = _u8(codes).contiguous()
+    N = c.shape[0]
+    K = c.shape[1] if fmt == E4M3 else c.shape[1] * 4 // 3
+    tiled = torch.empty(query("mxl_tiled_weight_bytes", N, K, fmt), dtype=torch.uint8, device=c.device)
+    tiled_s = None
+    if scales is not None:
+        s = _u8(scales).contiguous()
+        if tuple(s.shape) != (N, K // 32):
+            raise ValueError(f"scales must be [N, K/32] = [{N}, {K // 32}], got {tuple(s.shape)}")
+        tiled_s = torch.empty(query("mxl_tiled_scale_bytes", N, K), dtype=torch.uint8, device=c.device)
+    call("mxl_pack_weight", ptr(c), ptr(s) if scales is not None else None, N, K, fmt, ptr(tiled), ptr(tiled_s),
+         stream_handle(c.device))
+    return tiled, tiled_s
+
+
+# -------------------------------------------------------------------- GEMMs
+
+def _gemm_ws(device, M, N, K):
+    nbytes = query("mxl_gemm_workspace_bytes", M, N, K)
+    buf = workspace(device, nbytes)
+    return (ptr(buf), nbytes) if buf is not None else (None, 0)
+
+
+@torch.library.custom_op("mach_amd::mx_gemm", mutates_args=())
+def mx_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, k: int,
+            w_fmt: int, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block-scaled MX GEMM on pre-quantized MXFP8 activations: y = A * W^T, bf16 [M, N].
+
+    Replaces ``torch.ops.mxfp8_sm120.gemm(a, b, sa, sb)`` (src/vllm_mach/mxfp6/dense_mxfp8.py:86)
+    and ``mxfp6::gemm_w6a8_pdl`` (src/vllm_mach/mxfp6/ar_norm.py:144-147).  a: E4M3 [M, K] row-major,
+    sa: E8M0 [M, K/32]; w / sw: tiled weight (``pack_weight``).
+    """
+    _check_cuda(a, sa, w, sw, bias)
+    a8 = _u8(a)
+    if a8.ndim != 2 or a8.shape[1] != k or a8.stride(1) != 1 or a8.stride(0) != k:
+        a8 = a8.contiguous()
+        if a8.shape[1] != k:
+            raise ValueError(f"activation K={a8.shape[1]} does not match weight K={k}")
+    M = a8.shape[0]
+    sa8 = _u8(sa).contiguous()
+    if tuple(sa8.shape) != (M, k // 32):
+        raise ValueError(f"activation scales must be [M, K/32] = [{M}, {k // 32}]")
+    out = torch.empty((M, n), dtype=torch.bfloat16, device=a.device)
+    if M:
+        ws, wsb = _gemm_ws(a.device, M, n, k)
+        call("mxl_mx_gemm", ptr(a8), ptr(sa8), M, ptr(w), ptr(sw), n, k, w_fmt, ptr(bias), ptr(out), n,
+             ws, wsb, stream_handle(a.device))
+    _count("mx_gemm")
+    return out
+
+
+@mx_gemm.register_fake
+def _(a, sa, w, sw, n, k, w_fmt, bias=None):
+    return a.new_empty((a.shape[0], n), dtype=torch.bfloat16)
+
+
+def mx_gemm_from_float(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
+                       rule: int = FLOOR_CARRY175, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Quantize bf16 activations to MXFP8 and run the MX GEMM.
+
+    Replaces ``mxfp8_sm120::gemm_from_float`` / ``mxfp6::gemm_from_float``
+    (src/vllm_mach/mxfp6/dense_mxfp8.py:96, src/vllm_mach/mxfp6/dense.py:122-129).
+    """
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x, rule)
+    return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, x.shape[1], w_fmt, bias)
+
+
+def swiglu_mx_down(gate_up: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int = E4M3,
+                   rule: int = CEIL_DIV448) -> torch.Tensor:
+    """SwiGLU -> MXFP8 producer then the down-projection GEMM (``mach_swiglu_mxfp8_down``,
+    src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22)."""
+    if gate_up.shape[0] == 0:
+        return gate_up.new_empty((0, n))
+    a, sa = torch.ops.mach_amd.swiglu_mxfp8(gate_up, rule, False)
+    return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, gate_up.shape[1] // 2, w_fmt, None)
+
+
+@torch.library.custom_op("mach_amd::block_fp8_gemm", mutates_args=())
+def block_fp8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sb: torch.Tensor, n: int, k: int,
+                   bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block-FP8 GEMM: y[m, n] = sum_g sa[m, g] sb[n/128, g] (A_g . W_g), bf16 out.
+
+    Replaces ``vllm_mach_block_fp8::mm`` and the ``cutlass_scaled_mm`` route
+    (src/vllm_mach/fp8/linear.py:65-81).  a E4M3 [M, K]; sa fp32 [M, K/128] with stride (1, M);
+    w tiled (``pack_weight`` fmt 0, no scales); sb fp32 [ceil(N/128), K/128].
+    """
+    _check_cuda(a, sa, w, sb, bias)
+    a8 = _u8(a).contiguous()
+    M = a8.shape[0]
+    if a8.shape[1] != k:
+        raise ValueError("activation K does not match weight K")
+    if tuple(sa.shape) != (M, k // 128) or sa.dtype != torch.float32:
+        raise ValueError("sa must be fp32 [M, K/128]")
+    if M > 1 and sa.stride() != (1, M):
+        sa = sa.t().contiguous().t()
+    sb = sb.contiguous()
+    out = torch.empty((M, n), dtype=torch.bfloat16, device=a.device)
+    if M:
+        ws, wsb = _gemm_ws(a.device, M, n, k)
+        call("mxl_block_fp8_gemm", ptr(a8), ptr(sa), M, ptr(w), ptr(sb), n, k, ptr(bias), ptr(out), n, ws, wsb,
+             stream_handle(a.device))
+    _count("block_fp8_gemm")
+    return out
+
+
+@block_fp8_gemm.register_fake
+def _(a, sa, w, sb, n, k, bias=None):
+    return a.new_empty((a.shape[0], n), dtype=torch.bfloat16)
+
+
+# ---------------------------------------------------------------------- MoE
+
+@torch.library.custom_op("mach_amd::moe_route", mutates_args=())
+def moe_route(topk_ids: torch.Tensor, num_experts: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Stable token sort by expert -> (sorted_routes i32 [R], expert_offsets i64 [E+1], inverse i32 [R]).
+
+    The routing contract of ``route_mxfp8_out`` (src/vllm_mach/mxfp6/moe_utils.py:205-255):
+    expert_offsets, inverse_permutation; ids outside [0, E) are dropped (inverse -1).
+    """
+    _check_cuda(topk_ids)
+    ids = topk_ids.to(torch.int32).contiguous()
+    T, topk = ids.shape
+    R = T * topk
+    dev = ids.device
+    sorted_routes = torch.empty(R, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int64, device=dev)
+    inverse = torch.empty(R, dtype=torch.int32, device=dev)
+    nbytes = query("mxl_moe_route_workspace_bytes", T, topk, num_experts)
+    buf = workspace(dev, nbytes)
+    call("mxl_moe_route", ptr(ids), T, topk, num_experts, ptr(sorted_routes), ptr(offsets), ptr(inverse),
+         ptr(buf), nbytes, stream_handle(dev))
+    _count("moe_route")
+    return sorted_routes, offsets, inverse
+
+
+@moe_route.register_fake
+def _(topk_ids, num_experts):
+    R = topk_ids.shape[0] * topk_ids.shape[1]
+    return (topk_ids.new_empty((R,), dtype=torch.int32),
+            topk_ids.new_empty((num_experts + 1,), dtype=torch.int64),
+            topk_ids.new_empty((R,), dtype=torch.int32))
+
+
+@torch.library.custom_op("mach_amd::grouped_gemm", mutates_args=())
+def grouped_gemm(a: torch.Tensor, sa: torch.Tensor, row_index: Optional[torch.Tensor], row_div: int,
+                 expert_offsets: torch.Tensor, routed_rows: int, w: torch.Tensor, sw: torch.Tensor,
+                 n: int, k: int, w_fmt: int) -> torch.Tensor:
+    """Grouped MX GEMM over experts (``grouped_gemm_w6a8_out``, src/vllm_mach/mxfp6/moe_utils.py:320-380).
+
+    Output row p (sorted order) of expert e (expert_offsets[e] <= p < expert_offsets[e+1]) is
+    A[row_index[p] // row_div] . W[e]^T, or A[p] . W[e]^T when row_index is None.
+    Rows past expert_offsets[E] are left unwritten.
+    """
+    _check_cuda(a, sa, row_index, expert_offsets, w, sw)
+    a8 = _u8(a).contiguous()
+    sa8 = _u8(sa).contiguous()
+    E = expert_offsets.shape[0] - 1
+    out = torch.empty((routed_rows, n), dtype=torch.bfloat16, device=a.device)
+    if routed_rows:
+        call("mxl_grouped_gemm", ptr(a8), ptr(sa8), a8.shape[0], ptr(row_index), row_div, ptr(expert_offsets), E,
+             routed_rows, ptr(w), ptr(sw), n, k, w_fmt, ptr(out), stream_handle(a.device))
+    _count("grouped_gemm")
+    return out
+
+
+@grouped_gemm.register_fake
+def _(a, sa, row_index, row_div, expert_offsets, routed_rows, w, sw, n, k, w_fmt):
+    return a.new_empty((routed_rows, n), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("mach_amd::moe_reduce", mutates_args=("output",))
+def moe_reduce(output: torch.Tensor, routed_output: torch.Tensor, topk_weights: torch.Tensor,
+               inverse: torch.Tensor) -> None:
+    """Weighted combine into ``output`` bf16 [T, H] (``moe_reduce_out``, src/vllm_mach/mxfp6/moe.py:697-702)."""
+    _check_cuda(output, routed_output, topk_weights, inverse)
+    T, H = output.shape
+    topk = topk_weights.shape[1]
+    if not output.is_contiguous():
+        raise ValueError("moe_reduce needs a contiguous output")
+    w = topk_weights.to(torch.float32).contiguous()
+    y = routed_output.contiguous()
+    inv = inverse.contiguous()
+    call("mxl_moe_reduce", ptr(y), ptr(w), ptr(inv), T, topk, H, ptr(output), stream_handle(output.device))
+    _count("moe_reduce")
+
+
+@moe_reduce.register_fake
+def _(output, routed_output, topk_weights, inverse):
+    return None
