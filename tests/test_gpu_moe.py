@@ -58,26 +58,67 @@ def _moe_case(oracle_mod, E, H, I, T, topk, seed, fmt=2, std=0.1):
     return c13, s13, c2, s2, x, wts, ids.int()
 
 
+def _check_gemm(got, ref):
+    err = got.astype(np.float64) - ref
+    rel = np.linalg.norm(err) / max(np.linalg.norm(ref), 1e-30)
+    mx = np.abs(err).max() / max(np.abs(ref).max(), 1e-30)
+    assert rel <= 1e-3 and mx <= 1e-2, (rel, mx)
+
+
 @pytest.mark.parametrize("E,H,I,T,topk,fmt", [
     (4, 256, 128, 7, 2, 2),
     (4, 256, 128, 7, 2, 3),
     (32, 2048, 512, 128, 8, 2),
+    (16, 2048, 512, 512, 8, 3),
 ])
 def test_moe_layer_matches_oracle(pkg, oracle_mod, dev, E, H, I, T, topk, fmt):
+    """Each stage against the oracle on the GPU's own inputs to that stage (quantizers and
+    routing bit-exact, grouped GEMMs to the GEMM bar), then the whole layer."""
     c13, s13, c2, s2, x, wts, ids = _moe_case(oracle_mod, E, H, I, T, topk, 12035, fmt)
     experts = pkg.Mxfp6Experts(fmt=fmt)
     w1, w2 = experts.process_weights_after_loading(
         torch.from_numpy(oracle_mod.pack_fp6(c13)).to(dev), torch.from_numpy(s13).to(dev),
         torch.from_numpy(oracle_mod.pack_fp6(c2)).to(dev), torch.from_numpy(s2).to(dev))
+    xd, wd, idd = x.to(dev), wts.to(dev), ids.to(dev)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-    experts.apply(out, x.to(dev), w1, w2, wts.to(dev), ids.to(dev), "silu", E, None,
-                  None, None, None, None, None, False)
+    experts.apply(out, xd, w1, w2, wd, idd, "silu", E, None, None, None, None, None, None, False)
+
+    # stage by stage, each fed with the GPU's own output of the previous stage
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(xd, 0)
+    ac, as_ = oracle_mod.quant_mxfp8(x, 0)
+    assert np.array_equal(a.view(torch.uint8).cpu().numpy(), ac)
+    sr, off, inv = torch.ops.mach_amd.moe_route(idd, E)
+    rs, ro, rinv = oracle_mod.moe_route(ids.numpy(), E)
+    assert np.array_equal(sr.cpu().numpy(), rs) and np.array_equal(off.cpu().numpy(), ro)
+    gu = torch.ops.mach_amd.grouped_gemm(a, sa, sr, topk, off, T * topk, w1, experts.w1_scale, 2 * I, H, fmt)
+    a2, sa2 = torch.ops.mach_amd.swiglu_mxfp8(gu, 1, False)
+    y = torch.ops.mach_amd.grouped_gemm(a2, sa2, None, 1, off, T * topk, w2, experts.w2_scale, H, I, fmt)
+    gu_h, a2_h, sa2_h, y_h = (gu.float().cpu().numpy(), a2.view(torch.uint8).cpu().numpy(),
+                              sa2.cpu().numpy(), y.float().cpu().numpy())
+    mc, ms = oracle_mod.swiglu_mxfp8(oracle_mod.bf16_bits(gu.cpu()), 1)
+    assert np.array_equal(a2_h, mc) and np.array_equal(sa2_h, ms)
+    for e in range(E):
+        lo, hi = int(ro[e]), int(ro[e + 1])
+        if lo == hi:
+            continue
+        toks = rs[lo:hi] // topk
+        ref1 = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(
+            oracle_mod.mx_gemm_ref(ac[toks], as_[toks], c13[e], s13[e], fmt)))
+        _check_gemm(gu_h[lo:hi], ref1)
+        ref2 = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(
+            oracle_mod.mx_gemm_ref(a2_h[lo:hi], sa2_h[lo:hi], c2[e], s2[e], fmt)))
+        _check_gemm(y_h[lo:hi], ref2)
+    red = oracle_mod.moe_reduce(oracle_mod.bf16_bits(y.cpu()), wts.numpy(), rinv)
+    assert np.array_equal(oracle_mod.bf16_bits(out), red)
+
+    # whole layer against the per-expert dense reference: bf16 rounding of the gate_up
+    # intermediate flips a few MXFP8 codes, so the bar is the reference's relative one
     ref = oracle_mod.bf16_to_f32(oracle_mod.moe_ref(x, c13, s13, c2, s2, wts.numpy(), ids.numpy(), fmt))
     got = out.float().cpu().numpy()
-    # the reference's tolerance (test_moe.py:248) and the relative Frobenius bar
-    np.testing.assert_allclose(got, ref, rtol=0.03, atol=0.03)
     rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert rel < 1e-2, rel
+    if H <= 256:
+        np.testing.assert_allclose(got, ref, rtol=0.03, atol=0.03)  # tests/native_mxfp6/test_moe.py:248
 
 
 def test_moe_graph_replay_changing_routes(pkg, oracle_mod, dev):

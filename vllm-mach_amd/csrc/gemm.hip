@@ -8,23 +8,28 @@
 //                       each K128 block is one unscaled MFMA whose fp32 result is
 //                       folded into the accumulator with fma(raw, sa*sb, acc).
 //
+// Operand layout of the 16x16x128 scaled MFMA (measured on gfx950): lane
+// l = 16q + r supplies row r of A (column r of B).  For 8-bit codes its 32
+// bytes are K [16q, 16q+16) followed by K [64+16q, 64+16q+16); for FP6 its 32
+// values (24 bytes, little-endian 6-bit fields) are K [32q, 32q+32).  The E8M0
+// scale of K block b = [32b, 32b+32) is taken from lane group q = b (op_sel
+// picks the byte).  C: lane l holds rows 4q + i, column r.
+//
 // Weights live in an MFMA-tiled layout written once at load time:
 //   tile (nt, kt) = weight rows [16nt, 16nt+16) x K [512kt, 512kt+512)
 //   CH 1 KiB chunks (CH = 8 for 8-bit codes, 6 for FP6); lane l's 16 bytes of
 //   chunk c are at c*1024 + 16l, so one 16-byte load per lane moves 1 KiB of
-//   contiguous memory per wavefront.  Lane l = 16q + r (r = row in tile,
-//   q = 0..3) concatenates, for MFMA j = 0..3, the 32 values
-//   K[512kt + 128j + 32q, +32) of row r: 32 bytes (E4M3) or 24 bytes (FP6,
-//   little-endian 6-bit fields).  The MX scale tile is 256 bytes: lane l's
-//   dword holds, in byte j, the E8M0 of block 16kt + 4j + q of row r, so the
-//   MFMA takes it with op_sel = j.  Tiles are ordered (nt, kt) with kt fastest,
-//   so a wave walking K streams one contiguous region.
+//   contiguous memory per wavefront.  Lane l concatenates its operand bytes for
+//   MFMA j = 0..3 (K [512kt + 128j, +128)): 32 bytes (E4M3) or 24 bytes (FP6).
+//   The MX scale tile is 256 bytes: lane l's dword holds, in byte j, the E8M0
+//   of block 16kt + 4j + q of row r, so the MFMA takes it with op_sel = j.
+//   Tiles are ordered (nt, kt) with kt fastest, so a wave walking K streams one
+//   contiguous region.
 //
 // Activations stay row-major (the producers' natural layout and the gather
-// layout the MoE path needs): lane l loads row r's 32 bytes at K offset
-// 512kt + 128j + 32q for MFMA j -- the operand layout of the 16x16x128 MFMA
-// (A: row = lane % 16, K block = lane / 16; C: row = 4(lane/16) + i,
-// col = lane % 16).
+// layout the MoE path needs): for MFMA j lane l loads row r's two 16-byte
+// pieces at K 512kt + 128j + 16q and + 64, and the dword of four E8M0 bytes
+// at block 16kt + 4j, keeping byte q.
 //
 // Work split: a workgroup of KW wavefronts owns an MT x NT grid of 16x16
 // output tiles; its waves take interleaved 512-wide K super-tiles and their
@@ -65,9 +70,9 @@ __global__ void pack_weight_kernel(const uint8_t* __restrict__ src, int64_t ld_s
   uint8_t out[16];
   if (!fp6) {
     const int j = (int)(c >> 1), half = (int)(c & 1);
-    const int64_t k0 = kt * kTileK + 128 * j + 32 * q;
+    const int64_t base = kt * kTileK + 128 * j;
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (row < N && k0 < K) v = *reinterpret_cast<const uint4*>(src + row * ld_src + k0 + 16 * half);
+    if (row < N && base < K) v = *reinterpret_cast<const uint4*>(src + row * ld_src + base + 16 * q + 64 * half);
     *reinterpret_cast<uint4*>(dst + tile * (CH * 1024) + c * 1024 + lane * 16) = v;
     return;
   }
@@ -139,10 +144,10 @@ __device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow
     const uint8_t* base = p.a + arow[mt] * p.lda;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int64_t k0 = kt * kTileK + 128 * j + 32 * q;
+      const int64_t k0 = kt * kTileK + 128 * j;
       if (k0 < p.K) {
-        const uint4* src = reinterpret_cast<const uint4*>(base + k0);
-        uint4 lo = src[0], hi = src[1];
+        const uint4 lo = *reinterpret_cast<const uint4*>(base + k0 + 16 * q);
+        const uint4 hi = *reinterpret_cast<const uint4*>(base + k0 + 64 + 16 * q);
         t.d[mt][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
       } else {
         t.d[mt][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
