@@ -23,6 +23,8 @@ FLAGS = [
     "-ffp-contract=off",
     # keep the compiler from forming packed-FP32 ops
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep register staging arrays in VGPRs (the LDS budget belongs to the GEMM tiles)
+    "-mllvm", "-disable-promote-alloca-to-lds",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 

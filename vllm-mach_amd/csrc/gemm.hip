@@ -37,22 +37,9 @@
 // cannot fill 256 CUs, S workgroups split K further and write fp32 partials
 // that a second kernel sums in split order: both orders are fixed, so every
 // result is deterministic.
-#include "mx_common.h"
+#include "gemm_common.h"
 
 namespace mxl {
-
-constexpr int kTileK = 512;
-
-template <int FMT>
-struct FmtTraits;
-template <>
-struct FmtTraits<kE4M3> { static constexpr int CH = 8; static constexpr int RUN = 32; };
-template <>
-struct FmtTraits<kE2M3> { static constexpr int CH = 6; static constexpr int RUN = 24; };
-template <>
-struct FmtTraits<kE3M2> { static constexpr int CH = 6; static constexpr int RUN = 24; };
-
-__host__ __device__ inline int tile_chunks(int fmt) { return fmt == kE4M3 ? 8 : 6; }
 
 // ------------------------------------------------------------ weight packing
 
@@ -114,103 +101,6 @@ __global__ void pack_scale_kernel(const uint8_t* __restrict__ src, uint8_t* __re
 
 // ------------------------------------------------------------- GEMM kernel
 
-struct GemmParams {
-  const uint8_t* a;      // activation codes, row-major
-  const void* sa;        // MX: E8M0 [rows, K/32]; block-FP8: fp32 column-major [K/128, M]
-  const uint8_t* w;      // tiled weight codes (expert 0)
-  const void* sw;        // MX: tiled scales; block-FP8: fp32 [ceil(N/128), K/128]
-  const uint16_t* bias;  // bf16 [N] or null
-  uint16_t* out;         // bf16, row stride ldc
-  float* partial;        // [S, rows, N] when split
-  const int32_t* row_index;     // grouped: sorted_routes (A row = row_index[r] / row_div)
-  const int64_t* expert_offsets;
-  int64_t lda, ldc, M, N, K, KT, a_rows;
-  int64_t w_expert_stride, sw_expert_stride;
-  int row_div, S;
-};
-
-template <int MT>
-struct ATile {
-  v8i d[MT][4];
-  uint32_t s[MT][4];
-};
-
-// Load the activation operands of one super-tile for MT 16-row tiles.
-template <int MT, bool BLOCK>
-__device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow)[MT], int64_t kt, int q,
-                                       ATile<MT>& t) {
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const uint8_t* base = p.a + arow[mt] * p.lda;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t k0 = kt * kTileK + 128 * j;
-      if (k0 < p.K) {
-        const uint4 lo = *reinterpret_cast<const uint4*>(base + k0 + 16 * q);
-        const uint4 hi = *reinterpret_cast<const uint4*>(base + k0 + 64 + 16 * q);
-        t.d[mt][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-      } else {
-        t.d[mt][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-      if (!BLOCK) {
-        const int64_t kb = kt * 16 + 4 * j;  // first 32-block of this MFMA's 128 columns
-        uint32_t sv = 0;
-        if (kb * 32 < p.K) sv = *reinterpret_cast<const uint32_t*>(
-                                   static_cast<const uint8_t*>(p.sa) + arow[mt] * (p.K / 32) + kb);
-        t.s[mt][j] = (sv >> (8 * q)) & 0xFFu;
-      }
-    }
-  }
-}
-
-template <int FMT, int NT>
-struct BTile {
-  uint4 c[NT][FmtTraits<FMT>::CH];
-  uint32_t s[NT];
-};
-
-template <int FMT>
-__device__ __forceinline__ v8i b_operand(const uint4* c, int j) {
-  if (FMT == kE4M3) {
-    const uint4 lo = c[2 * j], hi = c[2 * j + 1];
-    return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-  } else {
-    // the lane's 24 dwords; MFMA j takes dwords [6j, 6j + 6)
-    uint32_t d[24];
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      d[4 * i] = c[i].x; d[4 * i + 1] = c[i].y; d[4 * i + 2] = c[i].z; d[4 * i + 3] = c[i].w;
-    }
-    return v8i{(int)d[6 * j], (int)d[6 * j + 1], (int)d[6 * j + 2], (int)d[6 * j + 3],
-               (int)d[6 * j + 4], (int)d[6 * j + 5], 0, 0};
-  }
-}
-
-template <int FMT, int NT, bool BLOCK>
-__device__ __forceinline__ void load_b(const GemmParams& p, const uint8_t* w, const uint8_t* sw,
-                                       const int64_t (&ntile)[NT], int64_t kt, int lane, BTile<FMT, NT>& t) {
-  constexpr int CH = FmtTraits<FMT>::CH;
-#pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    const uint8_t* base = w + (ntile[n] * p.KT + kt) * (CH * 1024) + lane * 16;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) t.c[n][c] = *reinterpret_cast<const uint4*>(base + c * 1024);
-    if (!BLOCK) t.s[n] = *reinterpret_cast<const uint32_t*>(sw + (ntile[n] * p.KT + kt) * 256 + lane * 4);
-  }
-}
-
-// The B-format and op_sel operands must be immediates.
-template <int FMT, int J>
-__device__ __forceinline__ v4f mfma_step(v8i a, v8i b, v4f c, uint32_t sa, uint32_t sb) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, kE4M3, FMT, 0, (int)sa, J, (int)sb);
-}
-
-template <int FMT>
-__device__ __forceinline__ v4f mfma_raw(v8i a, v8i b) {
-  const v4f z = {0.f, 0.f, 0.f, 0.f};
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, kE4M3, FMT, 0, 127, 0, 127);
-}
-
 // Accumulate one super-tile into acc[MT][NT].
 template <int FMT, int MT, int NT, bool BLOCK>
 __device__ __forceinline__ void compute_tile(const GemmParams& p, const ATile<MT>& A, const BTile<FMT, NT>& B,
@@ -269,7 +159,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, v4f v, int64_t r
 // Dense: grid (n_groups, m_groups, S), KW waves per workgroup.
 // Grouped: grid (n_groups, experts, 1); the workgroup walks its expert's rows.
 template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED>
-__global__ __launch_bounds__(512) void gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(MT == 1 && NT == 1 ? 1024 : 512) void gemm_kernel(GemmParams p) {
   extern __shared__ float red[];  // [KW][MT][NT][4][64] when KW > 1
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, KW = blockDim.x >> 6;
   const int r = lane & 15, q = lane >> 4;
@@ -381,23 +271,27 @@ struct GemmConfig {
   int MT, NT, KW, S;
 };
 
-// Choose the wave tile and K split for an (M, N, K) problem so that the
-// launch carries enough wavefronts to keep 256 CUs' memory pipes busy.
+// Choose the wave tile and the K split for an (M, N, K) problem.  Waves of a
+// workgroup split K (summed in LDS); workgroups split K further only when the
+// output-tile grid alone cannot cover the 256 CUs, since that split costs a
+// second launch and an fp32 round trip.
 static GemmConfig choose_config(int64_t M, int64_t N, int64_t K) {
   GemmConfig c;
   const int64_t KT = (K + kTileK - 1) / kTileK;
   c.MT = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  c.NT = M > 64 ? 1 : 1;
+  c.NT = 1;
   if (M > 32 && M <= 64) { c.MT = 2; c.NT = 2; }
   const int64_t n_groups = ((N + 15) / 16 + c.NT - 1) / c.NT;
   const int64_t m_groups = (M + 16 * c.MT - 1) / (16 * c.MT);
   const int64_t tiles = n_groups * m_groups;
-  c.KW = (int)(KT >= 4 ? 4 : KT);
-  const int64_t target_waves = 4096;
-  int64_t S = (target_waves + tiles * c.KW - 1) / (tiles * c.KW);
-  const int64_t max_s = (KT + c.KW - 1) / c.KW;
-  if (S > max_s) S = max_s;
-  if (S < 1) S = 1;
+  const int64_t max_kw = (c.MT == 1 && c.NT == 1) ? 16 : 8;
+  c.KW = (int)(KT < max_kw ? KT : max_kw);
+  int64_t S = 1;
+  if (tiles < 128) {
+    S = (256 + tiles - 1) / tiles;
+    const int64_t max_s = (KT + c.KW - 1) / c.KW;
+    if (S > max_s) S = max_s;
+  }
   c.S = (int)S;
   return c;
 }
@@ -478,26 +372,35 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
   MXL_CHECK_ARG(ldc >= N, "%s: ldc < N", who);
   MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0, "%s: a and w must be 16-byte aligned", who);
   if (M == 0) return MXL_OK;
-  GemmConfig c = choose_config(M, N, K);
-  const int64_t need = c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
-  if (need > workspace_bytes || (need > 0 && workspace == nullptr)) c.S = 1;  // no room: skip the K split
   GemmParams p{};
   p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw;
   p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out; p.partial = (float*)workspace;
   p.lda = K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
-  p.row_div = 1; p.S = c.S;
-  const int64_t n_groups = ((N + 15) / 16 + c.NT - 1) / c.NT;
-  const int64_t m_groups = (M + 16 * c.MT - 1) / (16 * c.MT);
-  dim3 grid((unsigned)n_groups, (unsigned)m_groups, (unsigned)c.S);
+  p.row_div = 1;
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = block ? dispatch_fmt<true, false>(fmt, c, grid, p, s) : dispatch_fmt<false, false>(fmt, c, grid, p, s);
+  hipError_t e;
+  if (lds_gemm_eligible(M, N, K, fmt, block)) {
+    int S = lds_gemm_splits(M, N, K);
+    if ((int64_t)S * M * N * 4 > workspace_bytes || workspace == nullptr) S = 1;  // no room: skip the K split
+    p.S = S;
+    e = launch_gemm_lds(fmt, p, S, s);
+  } else {
+    GemmConfig c = choose_config(M, N, K);
+    const int64_t need = c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
+    if (need > workspace_bytes || (need > 0 && workspace == nullptr)) c.S = 1;
+    p.S = c.S;
+    const int64_t n_groups = ((N + 15) / 16 + c.NT - 1) / c.NT;
+    const int64_t m_groups = (M + 16 * c.MT - 1) / (16 * c.MT);
+    dim3 grid((unsigned)n_groups, (unsigned)m_groups, (unsigned)c.S);
+    e = block ? dispatch_fmt<true, false>(fmt, c, grid, p, s) : dispatch_fmt<false, false>(fmt, c, grid, p, s);
+  }
   if (e != hipSuccess) {
     set_error("%s: launch failed: %s", who, hipGetErrorString(e));
     return MXL_EHIP;
   }
-  if (c.S > 1) {
+  if (p.S > 1) {
     splitk_reduce_kernel<<<dim3((unsigned)((M * N + 255) / 256)), 256, 0, s>>>(
-        (const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, c.S);
+        (const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, p.S);
     MXL_CHECK_LAUNCH(who);
   }
   return MXL_OK;
@@ -505,8 +408,12 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
 
 extern "C" int64_t mxl_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0) return 0;
-  GemmConfig c = choose_config(M, N, K);
-  return c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
+  int S = choose_config(M, N, K).S;
+  if (lds_gemm_eligible(M, N, K, kE4M3, false)) {
+    const int S2 = lds_gemm_splits(M, N, K);
+    if (S2 > S) S = S2;
+  }
+  return S > 1 ? (int64_t)S * M * N * 4 : 0;
 }
 
 extern "C" int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,

@@ -1,0 +1,123 @@
+// Declarations shared by the GEMM kernels (gemm.hip, gemm_lds.hip).
+#pragma once
+
+#include "mx_common.h"
+
+namespace mxl {
+
+constexpr int kTileK = 512;
+
+template <int FMT>
+struct FmtTraits;
+template <>
+struct FmtTraits<kE4M3> { static constexpr int CH = 8; static constexpr int RUN = 32; };
+template <>
+struct FmtTraits<kE2M3> { static constexpr int CH = 6; static constexpr int RUN = 24; };
+template <>
+struct FmtTraits<kE3M2> { static constexpr int CH = 6; static constexpr int RUN = 24; };
+
+__host__ __device__ inline int tile_chunks(int fmt) { return fmt == kE4M3 ? 8 : 6; }
+
+struct GemmParams {
+  const uint8_t* a;      // activation codes, row-major
+  const void* sa;        // MX: E8M0 [rows, K/32]; block-FP8: fp32 column-major [K/128, M]
+  const uint8_t* w;      // tiled weight codes (expert 0)
+  const void* sw;        // MX: tiled scales; block-FP8: fp32 [ceil(N/128), K/128]
+  const uint16_t* bias;  // bf16 [N] or null
+  uint16_t* out;         // bf16, row stride ldc
+  float* partial;        // [S, rows, N] when split
+  const int32_t* row_index;     // grouped: sorted_routes (A row = row_index[r] / row_div)
+  const int64_t* expert_offsets;
+  int64_t lda, ldc, M, N, K, KT, a_rows;
+  int64_t w_expert_stride, sw_expert_stride;
+  int row_div, S;
+};
+
+template <int MT>
+struct ATile {
+  v8i d[MT][4];
+  uint32_t s[MT][4];
+};
+
+// Load the activation operands of one super-tile for MT 16-row tiles.
+template <int MT, bool BLOCK>
+__device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow)[MT], int64_t kt, int q,
+                                       ATile<MT>& t) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint8_t* base = p.a + arow[mt] * p.lda;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t k0 = kt * kTileK + 128 * j;
+      if (k0 < p.K) {
+        const uint4 lo = *reinterpret_cast<const uint4*>(base + k0 + 16 * q);
+        const uint4 hi = *reinterpret_cast<const uint4*>(base + k0 + 64 + 16 * q);
+        t.d[mt][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      } else {
+        t.d[mt][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+      if (!BLOCK) {
+        const int64_t kb = kt * 16 + 4 * j;  // first 32-block of this MFMA's 128 columns
+        uint32_t sv = 0;
+        if (kb * 32 < p.K) sv = *reinterpret_cast<const uint32_t*>(
+                                   static_cast<const uint8_t*>(p.sa) + arow[mt] * (p.K / 32) + kb);
+        t.s[mt][j] = (sv >> (8 * q)) & 0xFFu;
+      }
+    }
+  }
+}
+
+template <int FMT, int NT>
+struct BTile {
+  uint4 c[NT][FmtTraits<FMT>::CH];
+  uint32_t s[NT];
+};
+
+template <int FMT>
+__device__ __forceinline__ v8i b_operand(const uint4* c, int j) {
+  if (FMT == kE4M3) {
+    const uint4 lo = c[2 * j], hi = c[2 * j + 1];
+    return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  } else {
+    // the lane's 24 dwords; MFMA j takes dwords [6j, 6j + 6)
+    uint32_t d[24];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      d[4 * i] = c[i].x; d[4 * i + 1] = c[i].y; d[4 * i + 2] = c[i].z; d[4 * i + 3] = c[i].w;
+    }
+    return v8i{(int)d[6 * j], (int)d[6 * j + 1], (int)d[6 * j + 2], (int)d[6 * j + 3],
+               (int)d[6 * j + 4], (int)d[6 * j + 5], 0, 0};
+  }
+}
+
+template <int FMT, int NT, bool BLOCK>
+__device__ __forceinline__ void load_b(const GemmParams& p, const uint8_t* w, const uint8_t* sw,
+                                       const int64_t (&ntile)[NT], int64_t kt, int lane, BTile<FMT, NT>& t) {
+  constexpr int CH = FmtTraits<FMT>::CH;
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const uint8_t* base = w + (ntile[n] * p.KT + kt) * (CH * 1024) + lane * 16;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) t.c[n][c] = *reinterpret_cast<const uint4*>(base + c * 1024);
+    if (!BLOCK) t.s[n] = *reinterpret_cast<const uint32_t*>(sw + (ntile[n] * p.KT + kt) * 256 + lane * 4);
+  }
+}
+
+// The B-format and op_sel operands must be immediates.
+template <int FMT, int J>
+__device__ __forceinline__ v4f mfma_step(v8i a, v8i b, v4f c, uint32_t sa, uint32_t sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, kE4M3, FMT, 0, (int)sa, J, (int)sb);
+}
+
+template <int FMT>
+__device__ __forceinline__ v4f mfma_raw(v8i a, v8i b) {
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, kE4M3, FMT, 0, 127, 0, 127);
+}
+
+// LDS-staged kernel for prefill-sized M (gemm_lds.hip).
+bool lds_gemm_eligible(int64_t M, int64_t N, int64_t K, int fmt, bool block);
+int lds_gemm_splits(int64_t M, int64_t N, int64_t K);
+hipError_t launch_gemm_lds(int fmt, const GemmParams& p, int S, hipStream_t stream);
+
+}  // namespace mxl

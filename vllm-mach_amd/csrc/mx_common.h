@@ -78,15 +78,20 @@ __device__ __forceinline__ float mx_exp(float x) {
   return __builtin_ldexpf(y, (int)n);
 }
 
-// Quantize 32 values (each exactly a bf16) held by one thread: returns the
-// E8M0 code and writes 8 dwords of packed E4M3 codes (byte i = value i).
+// Quantize one 32-element block held by 4 consecutive lanes (8 values each,
+// lane (tid & 3) owns elements [8 (tid & 3), +8)).  The block amax is an
+// xor-shuffle max over the 4 lanes (order-free, so identical to a serial max).
+// Returns the E8M0 code (valid in every lane) and the lane's 8 codes packed
+// into two dwords.
 template <int RULE>
-__device__ __forceinline__ uint32_t quant32(const float* v, uint32_t* packed) {
+__device__ __forceinline__ uint32_t quant8x4(const float* v, uint32_t* packed) {
   float amax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+  for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+  amax = __builtin_fmaxf(amax, __shfl_xor(amax, 1, 4));
+  amax = __builtin_fmaxf(amax, __shfl_xor(amax, 2, 4));
   uint32_t s;
-  float mul;
+  float mul = 1.0f;
   int e2 = 0;
   if (RULE == kFloorCarry175) {
     s = scale_floor_carry175(f2u(amax) >> 16);
@@ -97,7 +102,7 @@ __device__ __forceinline__ uint32_t quant32(const float* v, uint32_t* packed) {
     mul = 1.0f / u2f(bits);
   }
 #pragma unroll
-  for (int d = 0; d < 8; ++d) {
+  for (int d = 0; d < 2; ++d) {
     uint32_t w = 0;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {

@@ -5,9 +5,9 @@
 //  * block-FP8 per-token group-128 quantization (fp32 scales, column-major)
 //  * SiLU*up -> block-FP8 producer
 //
-// All four are HBM-bound elementwise passes: one thread owns one 32-element
-// MX block (so the amax needs no cross-lane traffic) or 16 lanes own one
-// 128-element group (amax by xor-shuffle inside the 16-lane row).  Loads and
+// All four are HBM-bound elementwise passes: four lanes own one 32-element MX
+// block and 16 lanes own one 128-element group, each lane holding 8 values
+// from one 16-byte load; the amax is an xor-shuffle max inside the group.  Loads and
 // stores are 16-byte vectors; consecutive threads walk consecutive blocks of
 // a row so every wavefront access is one contiguous span.
 #include "mx_common.h"
@@ -16,25 +16,27 @@ namespace mxl {
 
 // --------------------------------------------------------------- MXFP8 quant
 
+// Four lanes own one 32-element block (8 values, one 16-byte load each), so a
+// decode-sized launch still spreads over enough lanes to hide latency.
 template <int RULE>
 __global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                           uint8_t* __restrict__ codes,
                                                           uint8_t* __restrict__ scales, int64_t M,
                                                           int64_t K) {
   const int64_t blocks_per_row = K / 32;
-  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= M * blocks_per_row) return;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int sub = (int)(tid & 3);
+  const int64_t total = M * blocks_per_row;
+  const bool live = (tid >> 2) < total;
+  const int64_t id = live ? (tid >> 2) : total - 1;  // dead lanes shadow a live block for the shuffle
   const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
-  const uint4* src = reinterpret_cast<const uint4*>(x + row * ldx + blk * 32);
-  float v[32];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) bf16x8_to_f32(src[q], v + 8 * q);
-  uint32_t packed[8];
-  uint32_t s = quant32<RULE>(v, packed);
-  uint4* dst = reinterpret_cast<uint4*>(codes + row * K + blk * 32);
-  dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-  dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-  scales[row * blocks_per_row + blk] = (uint8_t)s;
+  float v[8];
+  bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * ldx + blk * 32 + sub * 8), v);
+  uint32_t packed[2];
+  const uint32_t s = quant8x4<RULE>(v, packed);
+  if (!live) return;
+  *reinterpret_cast<uint2*>(codes + row * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
+  if (sub == 0) scales[row * blocks_per_row + blk] = (uint8_t)s;
 }
 
 // ------------------------------------------------------------ SwiGLU -> MXFP8
@@ -50,31 +52,31 @@ __global__ __launch_bounds__(256) void swiglu_mxfp8_kernel(const uint16_t* __res
                                                            uint8_t* __restrict__ scales, int64_t M,
                                                            int64_t K) {
   const int64_t blocks_per_row = K / 32;
-  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= M * blocks_per_row) return;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int sub = (int)(tid & 3);
+  const int64_t total = M * blocks_per_row;
+  const bool live = (tid >> 2) < total;
+  const int64_t id = live ? (tid >> 2) : total - 1;
   const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
-  const uint4* g4 = reinterpret_cast<const uint4*>(gate_up + row * 2 * K + blk * 32);
-  const uint4* u4 = reinterpret_cast<const uint4*>(gate_up + row * 2 * K + K + blk * 32);
-  float g[32], u[32], v[32];
+  const int64_t off = row * 2 * K + blk * 32 + sub * 8;
+  float g[8], u[8], v[8];
+  bf16x8_to_f32(*reinterpret_cast<const uint4*>(gate_up + off), g);
+  bf16x8_to_f32(*reinterpret_cast<const uint4*>(gate_up + off + K), u);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    bf16x8_to_f32(g4[q], g + 8 * q);
-    bf16x8_to_f32(u4[q], u + 8 * q);
-  }
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
+  for (int i = 0; i < 8; ++i) {
     float act = bf16_round(g[i] / (1.0f + mx_exp(-g[i])));
     v[i] = bf16_round(act * u[i]);
   }
-  uint32_t packed[8];
-  uint32_t s = quant32<RULE>(v, packed);
-  uint4* dst = reinterpret_cast<uint4*>(codes + row * K + blk * 32);
-  dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-  dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-  if (SWIZZLED)
-    scales[swizzle_offset(row, blk, K)] = (uint8_t)s;
-  else
-    scales[row * blocks_per_row + blk] = (uint8_t)s;
+  uint32_t packed[2];
+  const uint32_t s = quant8x4<RULE>(v, packed);
+  if (!live) return;
+  *reinterpret_cast<uint2*>(codes + row * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
+  if (sub == 0) {
+    if (SWIZZLED)
+      scales[swizzle_offset(row, blk, K)] = (uint8_t)s;
+    else
+      scales[row * blocks_per_row + blk] = (uint8_t)s;
+  }
 }
 
 // Zero the padding bytes of a swizzled scale buffer (rows beyond M inside the
@@ -184,7 +186,7 @@ extern "C" int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t l
   MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_quantize_mxfp8: unknown rule %d", rule);
   MXL_CHECK_ARG(aligned16(x) && aligned16(codes), "mxl_quantize_mxfp8: x and codes must be 16-byte aligned");
   if (M == 0) return MXL_OK;
-  const int64_t n = M * (K / 32);
+  const int64_t n = M * (K / 32) * 4;
   dim3 grid((unsigned)((n + 255) / 256));
   hipStream_t s = (hipStream_t)stream;
   if (rule == kFloorCarry175)
@@ -205,7 +207,7 @@ extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int r
   MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_swiglu_mxfp8: unknown rule %d", rule);
   MXL_CHECK_ARG(aligned16(gate_up) && aligned16(codes), "mxl_swiglu_mxfp8: gate_up and codes must be 16-byte aligned");
   if (M == 0) return MXL_OK;
-  const int64_t n = M * (K / 32);
+  const int64_t n = M * (K / 32) * 4;
   dim3 grid((unsigned)((n + 255) / 256));
   hipStream_t s = (hipStream_t)stream;
   const uint16_t* in = (const uint16_t*)gate_up;
