@@ -60,18 +60,19 @@ def test_mx_gemm_matches_oracle(pkg, oracle_mod, dev, fmt, M, N, K):
     _check(y.float().cpu().numpy(), ref_bf)
 
 
-def test_mx_gemm_bias_and_k_tail(pkg, oracle_mod, dev):
-    """K % 512 != 0 (a partial last super-tile) and a bf16 bias added after rounding."""
+@pytest.mark.parametrize("M,N,K,fmt", [(9, 200, 384, 0), (100, 200, 384, 0), (100, 200, 384, 2), (257, 136, 1152, 3)])
+def test_mx_gemm_bias_and_ragged_shapes(pkg, oracle_mod, dev, M, N, K, fmt):
+    """K % 512 != 0 (a partial last super-tile), N not a multiple of the tile width, and a
+    bf16 bias added after rounding, on both the decode and the LDS-staged kernels."""
     ops = pkg.ops
-    M, N, K = 9, 200, 384
-    wc, ws, stored = _weights(oracle_mod, N, K, 0, 0.05, 3)
-    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), 0)
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.05, 3)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
     x = _act(M, K, 4)
     bias = torch.randn(N, generator=torch.Generator().manual_seed(1)).bfloat16()
     a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
-    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, 0, bias.to(dev))
+    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, bias.to(dev))
     rc, rs = oracle_mod.quant_mxfp8(x, 0)
-    ref = torch.from_numpy(oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws))))
+    ref = torch.from_numpy(oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt))))
     ref = (ref.bfloat16() + bias).float().numpy()
     _check(y.float().cpu().numpy(), ref)
 

@@ -104,7 +104,7 @@ __global__ void pack_scale_kernel(const uint8_t* __restrict__ src, uint8_t* __re
 // Accumulate one super-tile into acc[MT][NT].
 template <int FMT, int MT, int NT, bool BLOCK>
 __device__ __forceinline__ void compute_tile(const GemmParams& p, const ATile<MT>& A, const BTile<FMT, NT>& B,
-                                             v4f (&acc)[MT][NT], int64_t kt, const int64_t (&r4)[MT],
+                                             v4f (&acc)[MT][NT], int64_t kt, int q, const int64_t (&r4)[MT],
                                              int64_t hi, const int64_t (&ntile)[NT], const float* sb_rows) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -115,10 +115,11 @@ __device__ __forceinline__ void compute_tile(const GemmParams& p, const ATile<MT
       for (int mt = 0; mt < MT; ++mt) {
         if (!BLOCK) {
           const uint32_t sb = B.s[n];
-          if (j == 0) acc[mt][n] = mfma_step<FMT, 0>(A.d[mt][j], b, acc[mt][n], A.s[mt][j], sb);
-          if (j == 1) acc[mt][n] = mfma_step<FMT, 1>(A.d[mt][j], b, acc[mt][n], A.s[mt][j], sb);
-          if (j == 2) acc[mt][n] = mfma_step<FMT, 2>(A.d[mt][j], b, acc[mt][n], A.s[mt][j], sb);
-          if (j == 3) acc[mt][n] = mfma_step<FMT, 3>(A.d[mt][j], b, acc[mt][n], A.s[mt][j], sb);
+          const uint32_t sa = (A.s[mt][j] >> (8 * q)) & 0xFFu;
+          if (j == 0) acc[mt][n] = mfma_step<FMT, 0>(A.d[mt][j], b, acc[mt][n], sa, sb);
+          if (j == 1) acc[mt][n] = mfma_step<FMT, 1>(A.d[mt][j], b, acc[mt][n], sa, sb);
+          if (j == 2) acc[mt][n] = mfma_step<FMT, 2>(A.d[mt][j], b, acc[mt][n], sa, sb);
+          if (j == 3) acc[mt][n] = mfma_step<FMT, 3>(A.d[mt][j], b, acc[mt][n], sa, sb);
         } else {
           const int64_t g = kt * 4 + j;
           if (g * 128 >= p.K) continue;
@@ -203,13 +204,15 @@ __global__ __launch_bounds__(MT == 1 && NT == 1 ? 1024 : 512) void gemm_kernel(G
 #pragma unroll
       for (int n = 0; n < NT; ++n) acc[mt][n] = v4f{0.f, 0.f, 0.f, 0.f};
 
+    // waves take interleaved super-tiles; each super-tile's loads are all issued
+    // before its MFMAs wait on them (enough waves per CU keep HBM busy)
     const int64_t kstride = (int64_t)p.S * KW;
     for (int64_t kt = split * KW + wv; kt < p.KT; kt += kstride) {
       BTile<FMT, NT> B;
       ATile<MT> A;
       load_b<FMT, NT, BLOCK>(p, w, sw, ntile_ld, kt, lane, B);
       load_a<MT, BLOCK>(p, arow, kt, q, A);
-      compute_tile<FMT, MT, NT, BLOCK>(p, A, B, acc, kt, r4, hi, ntile_ld,
+      compute_tile<FMT, MT, NT, BLOCK>(p, A, B, acc, kt, q, r4, hi, ntile_ld,
                                        BLOCK ? static_cast<const float*>(p.sw) : nullptr);
     }
 

@@ -36,32 +36,31 @@ struct GemmParams {
 template <int MT>
 struct ATile {
   v8i d[MT][4];
-  uint32_t s[MT][4];
+  uint32_t s[MT][4];  // MX: raw scale dword of MFMA j; the lane uses byte q (extracted at use)
 };
 
-// Load the activation operands of one super-tile for MT 16-row tiles.
+// Load the activation operands of one super-tile for MT 16-row tiles.  A
+// super-tile wholly inside K takes a branch-free path (a uniform condition),
+// so the loads are not waited on before the MFMAs that consume them.
 template <int MT, bool BLOCK>
 __device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow)[MT], int64_t kt, int q,
                                        ATile<MT>& t) {
+  const bool full = (kt + 1) * kTileK <= p.K;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const uint8_t* base = p.a + arow[mt] * p.lda;
+    const uint8_t* sbase = static_cast<const uint8_t*>(p.sa) + arow[mt] * (p.K / 32);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t k0 = kt * kTileK + 128 * j;
-      if (k0 < p.K) {
+      if (full || k0 < p.K) {
         const uint4 lo = *reinterpret_cast<const uint4*>(base + k0 + 16 * q);
         const uint4 hi = *reinterpret_cast<const uint4*>(base + k0 + 64 + 16 * q);
         t.d[mt][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        if (!BLOCK) t.s[mt][j] = *reinterpret_cast<const uint32_t*>(sbase + kt * 16 + 4 * j);
       } else {
         t.d[mt][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-      if (!BLOCK) {
-        const int64_t kb = kt * 16 + 4 * j;  // first 32-block of this MFMA's 128 columns
-        uint32_t sv = 0;
-        if (kb * 32 < p.K) sv = *reinterpret_cast<const uint32_t*>(
-                                   static_cast<const uint8_t*>(p.sa) + arow[mt] * (p.K / 32) + kb);
-        t.s[mt][j] = (sv >> (8 * q)) & 0xFFu;
+        t.s[mt][j] = 0;
       }
     }
   }

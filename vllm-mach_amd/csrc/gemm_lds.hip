@@ -1,24 +1,27 @@
 // LDS-staged MX GEMM for prefill-sized M on gfx950.
 //
 // Workgroup tile 128 (M) x 128 (N), four wavefronts in a 2 x 2 grid, each
-// owning 64 x 64 = 4 x 4 MFMA tiles of 16 x 16.  K advances in steps of 256
-// (half of a 512-wide weight super-tile), double-buffered in LDS:
+// owning 64 x 64 = 4 x 4 MFMA tiles of 16 x 16.  K advances in stages of 256
+// (half of a 512-wide weight super-tile), double-buffered in LDS, filled by
+// direct global->LDS loads (global_load_lds_dwordx4: lane i of a wave writes
+// 16 bytes at LDS base + 16 i, no staging registers):
 //
-//   A (row-major activations) is scattered on the way in so that the LDS image
-//     is in MFMA fragment order: m-tile mt, piece g = 2 jj + half holds, at
-//     lane l = 16q + r, the 16 bytes K [128 jj + 64 half + 16 q, +16) of row
-//     16 mt + r.  Wave w copies m-tiles 2w and 2w+1: lane l reads 64
-//     contiguous bytes per row across 4 lanes and writes 1 KiB contiguous, so
-//     both the global read and the LDS write are conflict-free.
-//   B (weights) is copied verbatim from the MFMA-tiled layout: the half
-//     super-tile of each n-tile is contiguous (4 KiB E4M3, 3 KiB FP6).
+//   A (row-major activations): the LDS image is in MFMA fragment order.
+//     Piece g = 2 jj + half of m-tile mt holds, at lane l = 16q + r, the 16
+//     bytes K [128 jj + 64 half + 16 q, +16) of row 16 mt + r -- so the wave
+//     that copies (mt, g) reads 64 contiguous bytes per row (4 lanes) and the
+//     DMA writes 1 KiB contiguous.  Wave w copies m-tiles 2w and 2w + 1.
+//   B (weights): the half super-tile of each n-tile is contiguous in the
+//     MFMA-tiled layout (4 KiB E4M3, 3 KiB FP6) and is copied verbatim.
 //
-// Each step: issue the next step's global loads, run 2 x 16 MFMAs per wave
-// from LDS (fragment reads are lane-contiguous 16-byte loads), write the
-// staged registers into the other LDS buffer, one barrier.  E8M0 scales are
-// read per wave straight from global memory (row-major activation scales,
-// tiled weight scales), one step ahead.  When the tile grid cannot cover the
-// GPU, S workgroups split K and write fp32 partials reduced in split order.
+// A loop iteration covers one super-tile (two stages), so the MFMA op_sel
+// immediates (which byte of each E8M0 dword) are static.  Per stage: start the
+// next stage's DMA, run 2 x 16 MFMAs per wave from lane-contiguous LDS
+// fragment reads, wait for the DMA, one barrier.  E8M0 scales come straight
+// from global memory one super-tile ahead (a 16-byte load per m-tile row of
+// activation scales, a dword per n-tile of tiled weight scales).  When the tile
+// grid cannot cover the GPU, S workgroups split K on super-tile boundaries
+// and write fp32 partials that a second kernel reduces in split order.
 #include "gemm_common.h"
 
 namespace mxl {
@@ -28,83 +31,123 @@ constexpr int kBM = 128, kBN = 128;
 template <int FMT>
 struct LdsCfg {
   static constexpr int CH = FmtTraits<FMT>::CH;
-  static constexpr int BCH = CH / 2;                 // 1 KiB B chunks per n-tile per step
+  static constexpr int BCH = CH / 2;  // 1 KiB B chunks per n-tile per stage
   static constexpr int A_BYTES = (kBM / 16) * 4 * 1024;
   static constexpr int B_BYTES = (kBN / 16) * BCH * 1024;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int B_LOADS = (kBN / 16) * BCH * 64 / 256;  // 16-byte pieces per thread
+  static constexpr int B_WAVE_COPIES = (kBN / 16) * BCH / 4;  // 1 KiB copies per wave
 };
 
-struct StepScales {
-  uint32_t a[4][2];  // byte q of the activation scale dword, per m-tile and MFMA of the step
-  uint32_t b[4];     // tiled weight scale dword per n-tile (byte j = MFMA j)
-};
+typedef __attribute__((address_space(1))) const void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
 
-template <int FMT, int J>
-__device__ __forceinline__ void mfma_tile(const v8i (&af)[4], const v8i (&bf)[4], const StepScales& sc, int jj,
-                                          v4f (&acc)[4][4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int n = 0; n < 4; ++n) acc[i][n] = mfma_step<FMT, J>(af[i], bf[n], acc[i][n], sc.a[i][jj], sc.b[n]);
+__device__ __forceinline__ void dma16(const void* src, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)lds_wave_base, 16, 0, 0);
 }
 
+struct SuperScales {
+  uint4 a[4];     // activation E8M0 bytes of blocks 16kt .. 16kt+15 of each fragment row
+  uint32_t b[4];  // tiled weight scale dword per n-tile (byte j = MFMA j)
+};
+
+// DMA one stage (super-tile kt, half h) into LDS buffer L.
 template <int FMT>
-__device__ __forceinline__ void lds_load_step(const GemmParams& p, int64_t st, int t, int lane, int q, int64_t nt0,
-                                              int64_t ntiles_total, const int64_t (&copy_row)[2],
-                                              const int64_t (&frag_row)[4], const int64_t (&ntile_ld)[4],
-                                              uint4 (&ra)[8], uint4 (&rb)[LdsCfg<FMT>::B_LOADS],
-                                              StepScales& sc) {
+__device__ __forceinline__ void stage_copy(const GemmParams& p, uint8_t* L, int64_t kt, int h, int wv, int lane,
+                                           int q, int64_t nt0, int64_t ntiles_total,
+                                           const int64_t (&copy_row)[2]) {
   using C = LdsCfg<FMT>;
-  const int64_t kt = st >> 1, h = st & 1;
   const int64_t kbase = kt * kTileK + 256 * h;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int g = i & 3;
-    const int64_t k = kbase + 64 * g + 16 * q;
-    ra[i] = k < p.K ? *reinterpret_cast<const uint4*>(p.a + copy_row[i >> 2] * p.lda + k) : make_uint4(0, 0, 0, 0);
+    const int mt = 2 * wv + (i >> 2), g = i & 3;
+    dma16(p.a + copy_row[i >> 2] * p.lda + kbase + 64 * g + 16 * q, L + (mt * 4 + g) * 1024);
   }
 #pragma unroll
-  for (int i = 0; i < C::B_LOADS; ++i) {
-    const int piece = i * 256 + t;
+  for (int i = 0; i < C::B_WAVE_COPIES; ++i) {
+    const int piece = (i * 4 + wv) * 64 + lane;  // 16-byte piece of the stage's B image
     const int nt = piece / (C::BCH * 64), off = piece % (C::BCH * 64);
     int64_t ntile = nt0 + nt;
     if (ntile >= ntiles_total) ntile = ntiles_total - 1;
-    rb[i] = *reinterpret_cast<const uint4*>(p.w + (ntile * p.KT + kt) * (C::CH * 1024) + h * (C::BCH * 1024) + off * 16);
+    dma16(p.w + (ntile * p.KT + kt) * (C::CH * 1024) + h * (C::BCH * 1024) + off * 16,
+          L + C::A_BYTES + (i * 4 + wv) * 1024);
   }
-  const uint8_t* sa_base = static_cast<const uint8_t*>(p.sa);
-  const uint8_t* sw_base = static_cast<const uint8_t*>(p.sw);
+}
+
+__device__ __forceinline__ void load_scales(const GemmParams& p, int64_t kt, int lane,
+                                            const int64_t (&frag_row)[4], const int64_t (&ntile_ld)[4],
+                                            SuperScales& sc) {
+  const uint8_t* sa = static_cast<const uint8_t*>(p.sa);
+  const uint8_t* sw = static_cast<const uint8_t*>(p.sw);
+  // rows are 8-byte aligned (K % 256 == 0); a half last super-tile has 8 scale bytes
+  const bool full = (kt + 1) * kTileK <= p.K;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
+    const uint8_t* rowp = sa + frag_row[i] * (p.K / 32) + kt * 16;
+    const uint2 lo = *reinterpret_cast<const uint2*>(rowp);
+    const uint2 hi = full ? *reinterpret_cast<const uint2*>(rowp + 8) : make_uint2(0, 0);
+    sc.a[i] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int64_t kb = kt * 16 + 4 * (2 * h + jj);
-      uint32_t v = 0;
-      if (kb * 32 < p.K) v = *reinterpret_cast<const uint32_t*>(sa_base + frag_row[i] * (p.K / 32) + kb);
-      sc.a[i][jj] = (v >> (8 * q)) & 0xFFu;
+  for (int n = 0; n < 4; ++n) sc.b[n] = *reinterpret_cast<const uint32_t*>(sw + (ntile_ld[n] * p.KT + kt) * 256 + lane * 4);
+}
+
+__device__ __forceinline__ uint32_t dword_of(const uint4& v, int j) {
+  return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
+}
+
+// 16 MFMAs of one 128-wide K slice (MFMA index J of the super-tile) from LDS stage L.
+template <int FMT, int J>
+__device__ __forceinline__ void stage_mfma(const uint8_t* L, int wm, int wn, int lane, int q,
+                                           const SuperScales& sc, v4f (&acc)[4][4]) {
+  using C = LdsCfg<FMT>;
+  constexpr int jj = J & 1;
+  v8i af[4], bf[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint8_t* base = L + ((wm * 4 + i) * 4 + 2 * jj) * 1024 + lane * 16;
+    const uint4 lo = *reinterpret_cast<const uint4*>(base);
+    const uint4 hi = *reinterpret_cast<const uint4*>(base + 1024);
+    af[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  }
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const uint8_t* base = L + C::A_BYTES + (wn * 4 + n) * (C::BCH * 1024) + lane * 16;
+    if (FMT == kE4M3) {
+      const uint4 lo = *reinterpret_cast<const uint4*>(base + 2 * jj * 1024);
+      const uint4 hi = *reinterpret_cast<const uint4*>(base + (2 * jj + 1) * 1024);
+      bf[n] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    } else if (jj == 0) {  // FP6: the lane's 12 dwords of the stage; slice jj takes [6jj, 6jj + 6)
+      const uint4 c0 = *reinterpret_cast<const uint4*>(base);
+      const uint2 c1 = *reinterpret_cast<const uint2*>(base + 1024);
+      bf[n] = v8i{(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w, (int)c1.x, (int)c1.y, 0, 0};
+    } else {
+      const uint2 c1 = *reinterpret_cast<const uint2*>(base + 1024 + 8);
+      const uint4 c2 = *reinterpret_cast<const uint4*>(base + 2048);
+      bf[n] = v8i{(int)c1.x, (int)c1.y, (int)c2.x, (int)c2.y, (int)c2.z, (int)c2.w, 0, 0};
     }
-#pragma unroll
-  for (int n = 0; n < 4; ++n)
-    sc.b[n] = *reinterpret_cast<const uint32_t*>(sw_base + (ntile_ld[n] * p.KT + kt) * 256 + lane * 4);
-}
-
-template <int FMT>
-__device__ __forceinline__ void lds_store_step(uint8_t* L, int t, int lane, int wv, const uint4 (&ra)[8],
-                                               const uint4 (&rb)[LdsCfg<FMT>::B_LOADS]) {
-  using C = LdsCfg<FMT>;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int mt = 2 * wv + (i >> 2), g = i & 3;
-    *reinterpret_cast<uint4*>(L + (mt * 4 + g) * 1024 + lane * 16) = ra[i];
   }
 #pragma unroll
-  for (int i = 0; i < C::B_LOADS; ++i) *reinterpret_cast<uint4*>(L + C::A_BYTES + (i * 256 + t) * 16) = rb[i];
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t sa = (dword_of(sc.a[i], J) >> (8 * q)) & 0xFFu;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[i][n] = mfma_step<FMT, J>(af[i], bf[n], acc[i][n], sa, sc.b[n]);
+  }
+}
+
+// The DMA writes LDS asynchronously and is counted by vmcnt: every wave drains
+// its own copies before the barrier that hands the stage to all waves.
+__device__ __forceinline__ void dma_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 }
 
 template <int FMT>
-__global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p, int steps_per_split) {
+__global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p, int64_t kt_per_split) {
   using C = LdsCfg<FMT>;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][C::STAGE];
+  // two distinct objects (not one [2][...] array) so the compiler can tell the
+  // DMA target stage from the stage being read and need not drain the DMA first
+  __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int r = lane & 15, q = lane >> 4;
   const int wm = wv >> 1, wn = wv & 1;
@@ -112,11 +155,12 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p, int steps_p
   const int64_t nt0 = (int64_t)blockIdx.x * (kBN / 16);
   const int64_t ntiles_total = (p.N + 15) / 16;
   const int64_t split = blockIdx.z;
-  const int64_t total_steps = 2 * p.KT;
-  const int64_t s_begin = split * steps_per_split;
-  const int64_t s_end = s_begin + steps_per_split < total_steps ? s_begin + steps_per_split : total_steps;
-  // rows this thread copies (A staging) and rows its fragments cover (scales)
-  int64_t copy_row[2], frag_row[4];
+  const int64_t kt_begin = split * kt_per_split;
+  const int64_t kt_end = kt_begin + kt_per_split < p.KT ? kt_begin + kt_per_split : p.KT;
+  // the last super-tile may hold only its first 256 columns (K % 512 == 256)
+  const bool half_last = (p.K % kTileK) != 0;
+
+  int64_t copy_row[2], frag_row[4], ntile_ld[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int64_t row = row0 + (2 * wv + i) * 16 + r;
@@ -127,73 +171,42 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p, int steps_p
     const int64_t row = row0 + (wm * 4 + i) * 16 + r;
     frag_row[i] = row < p.M ? row : p.M - 1;
   }
-  int64_t ntile_ld[4];
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     const int64_t nt = nt0 + wn * 4 + n;
     ntile_ld[n] = nt < ntiles_total ? nt : ntiles_total - 1;
   }
 
-  uint4 ra[8], rb[C::B_LOADS];
-  StepScales sc_next, sc_cur;
   v4f acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int n = 0; n < 4; ++n) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  if (s_begin < s_end) {
-    lds_load_step<FMT>(p, s_begin, t, lane, q, nt0, ntiles_total, copy_row, frag_row, ntile_ld, ra, rb, sc_next);
-    lds_store_step<FMT>(lds[0], t, lane, wv, ra, rb);
-    sc_cur = sc_next;
-    __syncthreads();
-    for (int64_t st = s_begin; st < s_end; ++st) {
-      const int buf = (int)((st - s_begin) & 1);
-      if (st + 1 < s_end)
-        lds_load_step<FMT>(p, st + 1, t, lane, q, nt0, ntiles_total, copy_row, frag_row, ntile_ld, ra, rb, sc_next);
-      const uint8_t* L = lds[buf];
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        v8i af[4], bf[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint8_t* base = L + ((wm * 4 + i) * 4 + 2 * jj) * 1024 + lane * 16;
-          const uint4 lo = *reinterpret_cast<const uint4*>(base);
-          const uint4 hi = *reinterpret_cast<const uint4*>(base + 1024);
-          af[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const uint8_t* base = L + C::A_BYTES + (wn * 4 + n) * (C::BCH * 1024) + lane * 16;
-          if (FMT == kE4M3) {
-            const uint4 lo = *reinterpret_cast<const uint4*>(base + 2 * jj * 1024);
-            const uint4 hi = *reinterpret_cast<const uint4*>(base + (2 * jj + 1) * 1024);
-            bf[n] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-          } else {
-            // the lane's 12 dwords of this step; MFMA jj takes dwords [6jj, 6jj + 6)
-            if (jj == 0) {
-              const uint4 c0 = *reinterpret_cast<const uint4*>(base);
-              const uint2 c1 = *reinterpret_cast<const uint2*>(base + 1024);
-              bf[n] = v8i{(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w, (int)c1.x, (int)c1.y, 0, 0};
-            } else {
-              const uint2 c1 = *reinterpret_cast<const uint2*>(base + 1024 + 8);
-              const uint4 c2 = *reinterpret_cast<const uint4*>(base + 2048);
-              bf[n] = v8i{(int)c1.x, (int)c1.y, (int)c2.x, (int)c2.y, (int)c2.z, (int)c2.w, 0, 0};
-            }
-          }
-        }
-        const bool h1 = (st & 1) != 0;
-        if (jj == 0) {
-          if (h1) mfma_tile<FMT, 2>(af, bf, sc_cur, 0, acc); else mfma_tile<FMT, 0>(af, bf, sc_cur, 0, acc);
-        } else {
-          if (h1) mfma_tile<FMT, 3>(af, bf, sc_cur, 1, acc); else mfma_tile<FMT, 1>(af, bf, sc_cur, 1, acc);
-        }
-      }
-      if (st + 1 < s_end) {
-        lds_store_step<FMT>(lds[buf ^ 1], t, lane, wv, ra, rb);
-        sc_cur = sc_next;
-      }
-      __syncthreads();
+  // super-tiles [kt_begin, kt_full) are whole; a K % 512 == 256 tail is peeled
+  const int64_t kt_full = (half_last && kt_end == p.KT) ? kt_end - 1 : kt_end;
+  if (kt_begin < kt_end) {
+    SuperScales sc, sc_next;
+    stage_copy<FMT>(p, lds0, kt_begin, 0, wv, lane, q, nt0, ntiles_total, copy_row);
+    load_scales(p, kt_begin, lane, frag_row, ntile_ld, sc);
+    dma_wait_barrier();
+    for (int64_t kt = kt_begin; kt < kt_full; ++kt) {
+      // stage (kt, 0) is in lds0; fetch (kt, 1) into lds1 and the next scales
+      stage_copy<FMT>(p, lds1, kt, 1, wv, lane, q, nt0, ntiles_total, copy_row);
+      load_scales(p, kt + 1 < p.KT ? kt + 1 : kt, lane, frag_row, ntile_ld, sc_next);
+      stage_mfma<FMT, 0>(lds0, wm, wn, lane, q, sc, acc);
+      stage_mfma<FMT, 1>(lds0, wm, wn, lane, q, sc, acc);
+      dma_wait_barrier();
+      // stage (kt, 1) is in lds1; fetch (kt + 1, 0) into lds0
+      if (kt + 1 < kt_end) stage_copy<FMT>(p, lds0, kt + 1, 0, wv, lane, q, nt0, ntiles_total, copy_row);
+      stage_mfma<FMT, 2>(lds1, wm, wn, lane, q, sc, acc);
+      stage_mfma<FMT, 3>(lds1, wm, wn, lane, q, sc, acc);
+      dma_wait_barrier();
+      sc = sc_next;
+    }
+    if (kt_full < kt_end) {  // the half super-tile: stage (kt_full, 0) is in lds0
+      stage_mfma<FMT, 0>(lds0, wm, wn, lane, q, sc, acc);
+      stage_mfma<FMT, 1>(lds0, wm, wn, lane, q, sc, acc);
     }
   }
 
@@ -222,29 +235,29 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p, int steps_p
 }
 
 bool lds_gemm_eligible(int64_t M, int64_t N, int64_t K, int fmt, bool block) {
-  return !block && M >= 64 && (fmt == kE4M3 || fmt == kE2M3 || fmt == kE3M2);
+  return !block && M >= 64 && K % 256 == 0 && (fmt == kE4M3 || fmt == kE2M3 || fmt == kE3M2);
 }
 
-// K splits so that the tile grid covers the 256 CUs; every split gets >= 2 steps.
+// K splits (on super-tile boundaries) so that the tile grid covers the 256 CUs.
 int lds_gemm_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
-  const int64_t steps = 2 * ((K + kTileK - 1) / kTileK);
+  const int64_t KT = (K + kTileK - 1) / kTileK;
   int64_t S = 1;
   if (tiles < 192) {
     S = (256 + tiles - 1) / tiles;
-    if (S > steps / 2) S = steps / 2;
-    if (S < 1) S = 1;
+    if (S > KT) S = KT;
+    const int64_t per = (KT + S - 1) / S;
+    S = (KT + per - 1) / per;  // no empty splits
   }
   return (int)S;
 }
 
 hipError_t launch_gemm_lds(int fmt, const GemmParams& p, int S, hipStream_t stream) {
-  const int64_t steps = 2 * p.KT;
-  const int steps_per_split = (int)((steps + S - 1) / S);
+  const int64_t kt_per_split = (p.KT + S - 1) / S;
   dim3 grid((unsigned)((p.N + kBN - 1) / kBN), (unsigned)((p.M + kBM - 1) / kBM), (unsigned)S);
-  if (fmt == kE4M3) hipLaunchKernelGGL(gemm_lds_kernel<kE4M3>, grid, dim3(256), 0, stream, p, steps_per_split);
-  else if (fmt == kE2M3) hipLaunchKernelGGL(gemm_lds_kernel<kE2M3>, grid, dim3(256), 0, stream, p, steps_per_split);
-  else if (fmt == kE3M2) hipLaunchKernelGGL(gemm_lds_kernel<kE3M2>, grid, dim3(256), 0, stream, p, steps_per_split);
+  if (fmt == kE4M3) hipLaunchKernelGGL(gemm_lds_kernel<kE4M3>, grid, dim3(256), 0, stream, p, kt_per_split);
+  else if (fmt == kE2M3) hipLaunchKernelGGL(gemm_lds_kernel<kE2M3>, grid, dim3(256), 0, stream, p, kt_per_split);
+  else if (fmt == kE3M2) hipLaunchKernelGGL(gemm_lds_kernel<kE3M2>, grid, dim3(256), 0, stream, p, kt_per_split);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
