@@ -96,12 +96,66 @@ def cpu_baseline(budget_s: float = 15.0):
                       f"({threads} threads) + bf16, weights pre-dequantized, {n} runs x {dt * 1e3:.1f} ms"}
 
 
+def kernel_only(pkg, args):
+    """Launch one kernel `iters` times (weights rotated as in the step) and print its
+    event-timed average, for rocprofv3 kernel-trace and counter runs."""
+    ops = pkg.ops
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if args.kernel_only == "copy":
+        # calibration for HBM byte counters: a plain device copy of known size
+        nbytes = 256 << 20
+        src = torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(generator=gen)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(args.iters):
+            dst.copy_(src)
+        e.record()
+        e.synchronize()
+        us = s.elapsed_time(e) * 1000 / args.iters
+        print(json.dumps({"kernel": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "us": round(us, 2),
+                          "GBs": round(2 * nbytes / us / 1e3, 1)}))
+        return
+    w = (torch.randn(N_OUT, K_IN, generator=gen, device=dev) * 0.02).bfloat16()
+    wc, ws = torch.ops.mach_amd.quantize_mxfp8(w, 0)
+    tiled, tiled_s = ops.pack_weight(wc, ws, ops.E4M3)
+    copies = [(tiled.clone(), tiled_s.clone()) for _ in range(WEIGHT_COPIES)]
+    gate_up = torch.randn(args.m, 2 * K_IN, generator=gen, device=dev).bfloat16()
+    a, sa = torch.ops.mach_amd.swiglu_mxfp8(gate_up, ops.CEIL_DIV448, False)
+    if args.kernel_only == "producer":
+        fn = lambda i: torch.ops.mach_amd.swiglu_mxfp8(gate_up, ops.CEIL_DIV448, False)
+    else:
+        fn = lambda i: torch.ops.mach_amd.mx_gemm(a, sa, copies[i % WEIGHT_COPIES][0],
+                                                  copies[i % WEIGHT_COPIES][1], N_OUT, K_IN, ops.E4M3, None)
+    for i in range(WEIGHT_COPIES):
+        fn(i)
+    torch.cuda.synchronize()
+    s.record()
+    for i in range(args.iters):
+        fn(i)
+    e.record()
+    e.synchronize()
+    us = s.elapsed_time(e) * 1000 / args.iters
+    flops, bytes_, gemm_bytes = algorithmic(args.m)
+    print(json.dumps({"kernel": args.kernel_only, "M": args.m, "N": N_OUT, "K": K_IN, "us_eager": round(us, 2),
+                      "algorithmic_bytes": int(gemm_bytes if args.kernel_only == "gemm" else args.m * K_IN * 5 + args.m * K_IN // 32),
+                      "flops": flops}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-only", choices=["gemm", "producer", "copy"],
+                    help="profiling mode: launch one kernel back to back (for rocprofv3)")
+    ap.add_argument("--m", type=int, default=512, help="rows for --kernel-only")
+    ap.add_argument("--iters", type=int, default=64, help="launches for --kernel-only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -110,6 +164,9 @@ def main():
 
     import __graft_entry__
     pkg = __graft_entry__.load_package()
+    if args.kernel_only:
+        kernel_only(pkg, args)
+        return
     ops = pkg.ops
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

@@ -95,20 +95,16 @@ __device__ __forceinline__ uint32_t dword_of(const uint4& v, int j) {
   return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
 }
 
-// 16 MFMAs of one 128-wide K slice (MFMA index J of the super-tile) from LDS stage L.
+// 16 MFMAs of one 128-wide K slice (MFMA index J of the super-tile) from LDS
+// stage L.  The four B fragments are read once; A fragments stream one m-tile
+// at a time so each LDS read overlaps the previous m-tile's MFMAs and only
+// 48 fragment registers are live.
 template <int FMT, int J>
 __device__ __forceinline__ void stage_mfma(const uint8_t* L, int wm, int wn, int lane, int q,
                                            const SuperScales& sc, v4f (&acc)[4][4]) {
   using C = LdsCfg<FMT>;
   constexpr int jj = J & 1;
-  v8i af[4], bf[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint8_t* base = L + ((wm * 4 + i) * 4 + 2 * jj) * 1024 + lane * 16;
-    const uint4 lo = *reinterpret_cast<const uint4*>(base);
-    const uint4 hi = *reinterpret_cast<const uint4*>(base + 1024);
-    af[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-  }
+  v8i bf[4];
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     const uint8_t* base = L + C::A_BYTES + (wn * 4 + n) * (C::BCH * 1024) + lane * 16;
@@ -128,9 +124,13 @@ __device__ __forceinline__ void stage_mfma(const uint8_t* L, int wm, int wn, int
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    const uint8_t* base = L + ((wm * 4 + i) * 4 + 2 * jj) * 1024 + lane * 16;
+    const uint4 lo = *reinterpret_cast<const uint4*>(base);
+    const uint4 hi = *reinterpret_cast<const uint4*>(base + 1024);
+    const v8i af = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     const uint32_t sa = (dword_of(sc.a[i], J) >> (8 * q)) & 0xFFu;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc[i][n] = mfma_step<FMT, J>(af[i], bf[n], acc[i][n], sa, sc.b[n]);
+    for (int n = 0; n < 4; ++n) acc[i][n] = mfma_step<FMT, J>(af, bf[n], acc[i][n], sa, sc.b[n]);
   }
 }
 
