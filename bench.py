@@ -1,17 +1,23 @@
 """Benchmark of the quantized-linear hot path on one MI355X.
 
-Workload ("c2"): fused SwiGLU -> MXFP8 producer + MXFP8
+Default workload ("c2"): fused SwiGLU -> MXFP8 producer + MXFP8
 down projection, gate_up bf16 [M, 2 x 9216] ~ N(0, 1), weights [2560, 9216] ~ N(0, 0.02)
 pre-quantized to MXFP8 (E4M3 + E8M0 per 32), bf16 out, for M in {1, 16, 128, 512}.
 One step = the producer + GEMM at each of the four M.  Weights rotate over enough
 copies to exceed the 256 MB Infinity Cache, so every step streams them from HBM.
 
+``--config`` selects the other BASELINE.json configurations (same JSON line format):
+c1 (MXFP8 linear M=16, 2048x2048), c3 (block-FP8 linear, N=18432 K=2560), c4 (MXFP6
+E2M3 dense N=17408 K=5120), c5 (MXFP6 MoE, 256 experts, top-8, hidden 2048, T in
+{128, 2048}).
+
 Timing: each step is one hipGraph (the reference's protocol, tools/benchmark_nvfp4_lm_head.py:17-40:
 warm, capture, replay, event-timed).  `value` = total algorithmic TFLOP over the step
 / measured step time.  Per-kernel durations come from graphs of back-to-back launches of
-that kernel, timed with HIP events on the stream they run on.
+that kernel over the rotated weight copies, timed with HIP events on the stream they run on.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+Usage: python bench.py [--config c2] [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+       python bench.py --kernel-only {gemm,producer,copy} [--config c2] [--m M] [--iters I]
 """
 from __future__ import annotations
 
@@ -27,21 +33,15 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-N_OUT, K_IN = 2560, 9216
-M_SWEEP = (1, 16, 128, 512)
 HBM_PEAK_GBS = 8000.0
-MFMA_PEAK_TFLOPS = 5000.0  # dense MXFP8 (E4M3) scaled MFMA
-WEIGHT_COPIES = 16         # 16 x 24.3 MB = 389 MB > 256 MB Infinity Cache
+MFMA_PEAK_TFLOPS = 5000.0   # dense scaled MFMA, E4M3 x E4M3 and E4M3 x FP6 (both 16x16x128 f8f6f4)
+CACHE_BYTES = 256 << 20     # MI355X Infinity Cache
+METRIC = "GEMM TFLOP/s & HBM GB/s (% roofline) at M=1..512; bit-exact quant codes"
 
 
-def algorithmic(M: int):
-    """flops and bytes of the fused producer + GEMM at one M (SURVEY 8(d) counts):
-    weight codes + E8M0 scales + gate_up bf16 in (4 B per K element) + bf16 out."""
-    flops = 2.0 * M * N_OUT * K_IN
-    w_bytes = N_OUT * K_IN + N_OUT * K_IN // 32
-    bytes_ = w_bytes + M * K_IN * 4 + M * N_OUT * 2
-    gemm_bytes = w_bytes + M * K_IN * (1 + 1 / 32) + M * N_OUT * 2  # GEMM alone reads MXFP8 A
-    return flops, bytes_, gemm_bytes
+def copies_for(nbytes: int) -> int:
+    """Weight copies so that a rotation over them streams at least 1.5 x the Infinity Cache."""
+    return max(2, -(-int(1.5 * CACHE_BYTES) // max(nbytes, 1)))
 
 
 def graph_time_us(fn_list, stream, replays=20, trials=9):
@@ -70,19 +70,290 @@ def graph_time_us(fn_list, stream, replays=20, trials=9):
     return times[len(times) // 2], g
 
 
+def kernel_entry(flops: float, nbytes: float, us: float) -> dict:
+    """Throughput and roofline fraction of one kernel from its algorithmic flops/bytes."""
+    t_mfma = flops / (MFMA_PEAK_TFLOPS * 1e12)
+    t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+    return {"us": round(us, 2), "tflops": round(flops / us / 1e6, 2), "gbs": round(nbytes / us / 1e3, 1),
+            "roofline_frac": round(max(t_mfma, t_hbm) * 1e6 / us, 3), "bound": "mfma" if t_mfma > t_hbm else "hbm",
+            "flops": flops, "bytes": int(nbytes)}
+
+
+def roofline_of(name: str, k: dict) -> dict:
+    if k["bound"] == "hbm":
+        r = {"bound": "hbm", "achieved": k["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+             "frac": round(k["gbs"] / HBM_PEAK_GBS, 4)}
+    else:
+        r = {"bound": "mfma", "achieved": k["tflops"], "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+             "frac": round(k["tflops"] / MFMA_PEAK_TFLOPS, 4)}
+    r.update({"traffic": None, "kernel": name, "algorithmic_bytes_per_launch": k["bytes"],
+              "algorithmic_flops_per_launch": k["flops"], "us_per_launch": k["us"]})
+    return r
+
+
+def mx_weight_bytes(N: int, K: int, fmt: int) -> int:
+    """Weight codes (1 B or 3/4 B per element) + E8M0 scales (1 B per 32)."""
+    return (N * K if fmt == 0 else N * K * 3 // 4) + N * K // 32
+
+
+# ----------------------------------------------------------------- workloads
+
+class Workload:
+    """A benchmark configuration: weights (rotated copies), inputs, the step, and its kernels."""
+    name = ""
+    describe = ""
+    sweep: tuple = ()
+    dtype = ""
+    copies: list = []
+
+    def step_fns(self, ci: int) -> list:
+        raise NotImplementedError
+
+    def kernels(self, x) -> dict:
+        """{kernel: (callables over weight copies, flops per launch, algorithmic bytes per launch)};
+        the GEMM comes first, the producer/quantizer second."""
+        raise NotImplementedError
+
+    def flops(self, x) -> float:
+        raise NotImplementedError
+
+
+class SwigluDown(Workload):
+    """c2: SwiGLU -> MXFP8 producer + MXFP8 down projection."""
+    name, describe = "c2", "c2: SwiGLU->MXFP8 producer + MXFP8 down projection N=2560 K=9216"
+    dtype = "mxfp8(e4m3+e8m0) x mxfp8, fp32 accumulate, bf16 out"
+    N, K = 2560, 9216
+    sweep = (1, 16, 128, 512)
+
+    def __init__(self, ops, dev, gen, sweep=None):
+        self.ops = ops
+        self.sweep = tuple(sweep or self.sweep)
+        w = (torch.randn(self.N, self.K, generator=gen, device=dev) * 0.02).bfloat16()
+        wc, ws = torch.ops.mach_amd.quantize_mxfp8(w, ops.FLOOR_CARRY175)
+        tiled, tiled_s = ops.pack_weight(wc, ws, ops.E4M3)
+        self.copies = [(tiled.clone(), tiled_s.clone()) for _ in range(copies_for(tiled.numel() + tiled_s.numel()))]
+        self.inputs = {M: torch.randn(M, 2 * self.K, generator=gen, device=dev).bfloat16() for M in self.sweep}
+        self.quant = {M: torch.ops.mach_amd.swiglu_mxfp8(self.inputs[M], ops.CEIL_DIV448, False) for M in self.sweep}
+
+    def step_fns(self, ci):
+        wt, st = self.copies[ci % len(self.copies)]
+        ops = self.ops
+        return [lambda M=M: ops.swiglu_mx_down(self.inputs[M], wt, st, self.N, ops.E4M3) for M in self.sweep]
+
+    def flops(self, M):
+        return 2.0 * M * self.N * self.K
+
+    def kernels(self, M):
+        ops, N, K = self.ops, self.N, self.K
+        a, sa = self.quant[M]
+        gemm = [lambda wt=wt, st=st: torch.ops.mach_amd.mx_gemm(a, sa, wt, st, N, K, ops.E4M3, None)
+                for wt, st in self.copies]
+        prod = [lambda: torch.ops.mach_amd.swiglu_mxfp8(self.inputs[M], ops.CEIL_DIV448, False)] * 8
+        return {
+            f"mxfp8 gemm M={M} N={N} K={K}": (gemm, self.flops(M),
+                                              mx_weight_bytes(N, K, 0) + M * K * (1 + 1 / 32) + M * N * 2),
+            f"swiglu_mxfp8 M={M} K={K}": (prod, 0.0, M * K * 4 + M * K * (1 + 1 / 32)),
+        }
+
+
+class MxLinear(Workload):
+    """c1 (MXFP8 weights) and c4 (packed MXFP6 E2M3 weights): on-the-fly MXFP8 activation
+    quantization (1% outlier channels x20) + MX GEMM."""
+
+    def __init__(self, ops, dev, gen, name, N, K, fmt, std, sweep):
+        self.ops, self.name, self.N, self.K, self.fmt = ops, name, N, K, fmt
+        self.sweep = tuple(sweep)
+        wname = "mxfp8(e4m3)" if fmt == ops.E4M3 else "mxfp6(e2m3, 4 values in 3 bytes)"
+        self.describe = f"{name}: MXFP8 activation quant + {wname} linear N={N} K={K}"
+        self.dtype = f"mxfp8 activations x {wname}, fp32 accumulate, bf16 out"
+        w = (torch.randn(N, K, generator=gen, device=dev) * std).bfloat16()
+        if fmt == ops.E4M3:
+            wc, ws = torch.ops.mach_amd.quantize_mxfp8(w, ops.FLOOR_CARRY175)
+        else:
+            wc, ws = torch.ops.mach_amd.quantize_mxfp6(w, fmt)
+        del w
+        tiled, tiled_s = ops.pack_weight(wc, ws, fmt)
+        del wc, ws
+        self.copies = [(tiled.clone(), tiled_s.clone()) for _ in range(copies_for(tiled.numel() + tiled_s.numel()))]
+        self.inputs = {}
+        for M in self.sweep:
+            x = torch.randn(M, K, generator=gen, device=dev)
+            idx = torch.randperm(K, generator=gen, device=dev)[: max(1, K // 100)]
+            x[:, idx] *= 20
+            self.inputs[M] = x.bfloat16()
+        self.quant = {M: torch.ops.mach_amd.quantize_mxfp8(self.inputs[M], ops.FLOOR_CARRY175) for M in self.sweep}
+
+    def step_fns(self, ci):
+        wt, st = self.copies[ci % len(self.copies)]
+        ops = self.ops
+        return [lambda M=M: ops.mx_gemm_from_float(self.inputs[M], wt, st, self.N, self.fmt) for M in self.sweep]
+
+    def flops(self, M):
+        return 2.0 * M * self.N * self.K
+
+    def kernels(self, M):
+        ops, N, K, fmt = self.ops, self.N, self.K, self.fmt
+        a, sa = self.quant[M]
+        gemm = [lambda wt=wt, st=st: torch.ops.mach_amd.mx_gemm(a, sa, wt, st, N, K, fmt, None)
+                for wt, st in self.copies]
+        quant = [lambda: torch.ops.mach_amd.quantize_mxfp8(self.inputs[M], ops.FLOOR_CARRY175)] * 8
+        tag = "mxfp8" if fmt == ops.E4M3 else "mxfp6"
+        return {
+            f"{tag} gemm M={M} N={N} K={K}": (gemm, self.flops(M),
+                                              mx_weight_bytes(N, K, fmt) + M * K * (1 + 1 / 32) + M * N * 2),
+            f"quantize_mxfp8 M={M} K={K}": (quant, 0.0, M * K * 2 + M * K * (1 + 1 / 32)),
+        }
+
+
+class BlockFp8Linear(Workload):
+    """c3: per-token group-128 FP8 activation quant + block-FP8 GEMM (128x128 fp32 weight scales)."""
+    name = "c3"
+    N, K = 18432, 2560
+    describe = f"c3: block-FP8 linear (fused gate_up) N={N} K={K}"
+    dtype = "e4m3 x e4m3 with fp32 block scales (1x128 act, 128x128 weight), fp32 accumulate, bf16 out"
+    sweep = (1, 16, 128, 512)
+
+    def __init__(self, ops, dev, gen, sweep=None):
+        self.ops = ops
+        self.sweep = tuple(sweep or self.sweep)
+        N, K = self.N, self.K
+        w = torch.randn(N, K, generator=gen, device=dev) * 0.02
+        blocks = w.view(N // 128, 128, K // 128, 128)
+        sb = (blocks.abs().amax(dim=(1, 3)) / 448.0).clamp_min(1e-12)
+        codes = (blocks / sb[:, None, :, None]).view(N, K).to(torch.float8_e4m3fn)
+        del w, blocks
+        tiled, _ = ops.pack_weight(codes, None, ops.E4M3)
+        del codes
+        sb = sb.float().contiguous()
+        self.copies = [(tiled.clone(), sb.clone()) for _ in range(copies_for(tiled.numel() + sb.numel() * 4))]
+        self.inputs = {M: torch.randn(M, K, generator=gen, device=dev).bfloat16() for M in self.sweep}
+        self.quant = {M: torch.ops.mach_amd.quantize_block_fp8(self.inputs[M]) for M in self.sweep}
+
+    def _linear(self, x, wt, sb):
+        q, s = torch.ops.mach_amd.quantize_block_fp8(x)
+        return torch.ops.mach_amd.block_fp8_gemm(q, s, wt, sb, self.N, self.K, None)
+
+    def step_fns(self, ci):
+        wt, sb = self.copies[ci % len(self.copies)]
+        return [lambda M=M: self._linear(self.inputs[M], wt, sb) for M in self.sweep]
+
+    def flops(self, M):
+        return 2.0 * M * self.N * self.K
+
+    def kernels(self, M):
+        N, K = self.N, self.K
+        q, s = self.quant[M]
+        gemm = [lambda wt=wt, sb=sb: torch.ops.mach_amd.block_fp8_gemm(q, s, wt, sb, N, K, None)
+                for wt, sb in self.copies]
+        quant = [lambda: torch.ops.mach_amd.quantize_block_fp8(self.inputs[M])] * 8
+        w_bytes = N * K + (N // 128) * (K // 128) * 4
+        return {
+            f"block_fp8 gemm M={M} N={N} K={K}": (gemm, self.flops(M), w_bytes + M * K * (1 + 4 / 128) + M * N * 2),
+            f"quantize_block_fp8 M={M} K={K}": (quant, 0.0, M * K * 2 + M * K * (1 + 4 / 128)),
+        }
+
+
+class MoeLayer(Workload):
+    """c5: MXFP6 (E2M3) routed experts, 256 experts, top-8, hidden 2048, intermediate 512."""
+    name = "c5"
+    E, H, I, TOPK = 256, 2048, 512, 8
+    describe = "c5: MXFP6 MoE (256 experts, top-8, hidden 2048, I 512): quant + sort + grouped GEMMs + combine"
+    dtype = "mxfp8 activations x mxfp6(e2m3) experts, fp32 accumulate, bf16 out"
+    sweep = (128, 2048)
+
+    def __init__(self, pkg, dev, gen, sweep=None):
+        ops = pkg.ops
+        self.ops = ops
+        self.sweep = tuple(sweep or self.sweep)
+        E, H, I = self.E, self.H, self.I
+        w13 = (torch.randn(E * 2 * I, H, generator=gen, device=dev) * 0.015).bfloat16()
+        c13, s13 = torch.ops.mach_amd.quantize_mxfp6(w13, ops.E2M3)
+        del w13
+        w2 = (torch.randn(E * H, I, generator=gen, device=dev) * 0.015).bfloat16()
+        c2, s2 = torch.ops.mach_amd.quantize_mxfp6(w2, ops.E2M3)
+        del w2
+        self.experts = pkg.Mxfp6Experts(fmt=ops.E2M3)
+        self.w1, self.w2 = self.experts.process_weights_after_loading(
+            c13.view(E, 2 * I, H * 3 // 4), s13.view(E, 2 * I, H // 32),
+            c2.view(E, H, I * 3 // 4), s2.view(E, H, I // 32))
+        del c13, s13, c2, s2
+        self.copies = [0]  # 256 experts x 2.4 MB = 604 MB already exceed the Infinity Cache
+        self.inputs, self.route, self.out, self.mid = {}, {}, {}, {}
+        for T in self.sweep:
+            x = torch.randn(T, H, generator=gen, device=dev).bfloat16()
+            logits = torch.randn(T, E, generator=gen, device=dev)
+            wts, ids = pkg.select_experts(logits, self.TOPK)
+            self.inputs[T] = (x, wts, ids)
+            self.out[T] = torch.empty_like(x)
+            # each stage's inputs, for the per-kernel timings
+            a, sa = torch.ops.mach_amd.quantize_mxfp8(x, ops.FLOOR_CARRY175)
+            sr, offs, inv = torch.ops.mach_amd.moe_route(ids, E)
+            gu = torch.ops.mach_amd.grouped_gemm(a, sa, sr, self.TOPK, offs, T * self.TOPK, self.w1,
+                                                 self.experts.w1_scale, 2 * I, H, ops.E2M3)
+            a2, sa2 = torch.ops.mach_amd.swiglu_mxfp8(gu, ops.CEIL_DIV448, False)
+            self.route[T] = (a, sa, sr, offs, inv)
+            self.mid[T] = (a2, sa2)
+
+    def step_fns(self, ci):
+        ex = self.experts
+        return [lambda T=T: ex.apply(self.out[T], self.inputs[T][0], self.w1, self.w2, self.inputs[T][1],
+                                     self.inputs[T][2], "silu", self.E, None, None, None, None, None, None, False)
+                for T in self.sweep]
+
+    def flops(self, T):
+        return 2.0 * T * self.TOPK * (2 * self.I * self.H + self.H * self.I)
+
+    def kernels(self, T):
+        ops, H, I, k = self.ops, self.H, self.I, self.TOPK
+        a, sa, sr, offs, inv = self.route[T]
+        a2, sa2 = self.mid[T]
+        ex = self.experts
+        active = int((offs[1:] > offs[:-1]).sum().item())
+        routes = T * k
+        g1 = [lambda: torch.ops.mach_amd.grouped_gemm(a, sa, sr, k, offs, routes, self.w1, ex.w1_scale,
+                                                      2 * I, H, ops.E2M3)] * 4
+        g2 = [lambda: torch.ops.mach_amd.grouped_gemm(a2, sa2, None, 1, offs, routes, self.w2, ex.w2_scale,
+                                                      H, I, ops.E2M3)] * 4
+        return {
+            f"grouped w13 T={T} ({active} active experts) N={2 * I} K={H}": (
+                g1, 2.0 * routes * 2 * I * H,
+                active * mx_weight_bytes(2 * I, H, 2) + routes * H * (1 + 1 / 32) + routes * 2 * I * 2),
+            f"grouped w2 T={T} ({active} active experts) N={H} K={I}": (
+                g2, 2.0 * routes * H * I,
+                active * mx_weight_bytes(H, I, 2) + routes * I * (1 + 1 / 32) + routes * H * 2),
+        }
+
+
+def make_workload(pkg, name, dev, gen, sweep=None):
+    ops = pkg.ops
+    if name == "c2":
+        return SwigluDown(ops, dev, gen, sweep)
+    if name == "c1":
+        return MxLinear(ops, dev, gen, "c1", 2048, 2048, ops.E4M3, 0.02, sweep or (16,))
+    if name == "c3":
+        return BlockFp8Linear(ops, dev, gen, sweep)
+    if name == "c4":
+        return MxLinear(ops, dev, gen, "c4", 17408, 5120, ops.E2M3, 0.015, sweep or (1, 16, 128, 256))
+    if name == "c5":
+        return MoeLayer(pkg, dev, gen, sweep)
+    raise ValueError(name)
+
+
+# ------------------------------------------------------------------ CPU leg
+
 def cpu_baseline(budget_s: float = 15.0):
     """The oracle's CPU path (C producer + exact dequantize + BLAS matmul) on a bounded
-    sample of the same workload: M = 16 rows of c2, repeated for about `budget_s`."""
-    import numpy as np
+    sample of the c2 workload: M = 16 rows, repeated for about `budget_s`."""
     import oracle
+    N, K = SwigluDown.N, SwigluDown.K
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
-    w = (torch.randn(N_OUT, K_IN, generator=g) * 0.02).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
     wc, ws = oracle.quant_mxfp8(w, 0)
     wdq = torch.from_numpy(oracle.dequant_mx(wc, ws, 0))
     M = 16
-    gu = torch.randn(M, 2 * K_IN, generator=g).bfloat16()
+    gu = torch.randn(M, 2 * K, generator=g).bfloat16()
     n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < budget_s or n < 2:
         c, s = oracle.swiglu_mxfp8(gu, oracle.RULE_CEIL_DIV448)
@@ -90,16 +361,17 @@ def cpu_baseline(budget_s: float = 15.0):
         _ = (a @ wdq.T).bfloat16()
         n += 1
     dt = (time.perf_counter() - t0) / n
-    flops = 2.0 * M * N_OUT * K_IN
+    flops = 2.0 * M * N * K
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"c2 at M={M}: oracle SwiGLU->MXFP8 (C, 1 thread) + exact dequant + torch fp32 matmul "
                       f"({threads} threads) + bf16, weights pre-dequantized, {n} runs x {dt * 1e3:.1f} ms"}
 
 
+# ------------------------------------------------------------- profiling mode
+
 def kernel_only(pkg, args):
     """Launch one kernel `iters` times (weights rotated as in the step) and print its
     event-timed average, for rocprofv3 kernel-trace and counter runs."""
-    ops = pkg.ops
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(1234)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -120,41 +392,34 @@ def kernel_only(pkg, args):
         print(json.dumps({"kernel": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "us": round(us, 2),
                           "GBs": round(2 * nbytes / us / 1e3, 1)}))
         return
-    w = (torch.randn(N_OUT, K_IN, generator=gen, device=dev) * 0.02).bfloat16()
-    wc, ws = torch.ops.mach_amd.quantize_mxfp8(w, 0)
-    tiled, tiled_s = ops.pack_weight(wc, ws, ops.E4M3)
-    copies = [(tiled.clone(), tiled_s.clone()) for _ in range(WEIGHT_COPIES)]
-    gate_up = torch.randn(args.m, 2 * K_IN, generator=gen, device=dev).bfloat16()
-    a, sa = torch.ops.mach_amd.swiglu_mxfp8(gate_up, ops.CEIL_DIV448, False)
-    if args.kernel_only == "producer":
-        fn = lambda i: torch.ops.mach_amd.swiglu_mxfp8(gate_up, ops.CEIL_DIV448, False)
-    else:
-        fn = lambda i: torch.ops.mach_amd.mx_gemm(a, sa, copies[i % WEIGHT_COPIES][0],
-                                                  copies[i % WEIGHT_COPIES][1], N_OUT, K_IN, ops.E4M3, None)
-    for i in range(WEIGHT_COPIES):
-        fn(i)
+    wl = make_workload(pkg, args.config, dev, gen, (args.m,))
+    kernels = list(wl.kernels(args.m).items())
+    name, (fns, flops, nbytes) = kernels[0] if args.kernel_only == "gemm" else kernels[1]
+    for fn in fns:
+        fn()
     torch.cuda.synchronize()
     s.record()
     for i in range(args.iters):
-        fn(i)
+        fns[i % len(fns)]()
     e.record()
     e.synchronize()
     us = s.elapsed_time(e) * 1000 / args.iters
-    flops, bytes_, gemm_bytes = algorithmic(args.m)
-    print(json.dumps({"kernel": args.kernel_only, "M": args.m, "N": N_OUT, "K": K_IN, "us_eager": round(us, 2),
-                      "algorithmic_bytes": int(gemm_bytes if args.kernel_only == "gemm" else args.m * K_IN * 5 + args.m * K_IN // 32),
-                      "flops": flops}))
+    print(json.dumps({"kernel": name, "config": args.config, "us_eager": round(us, 2),
+                      "algorithmic_bytes": int(nbytes), "flops": flops}))
 
+
+# ---------------------------------------------------------------------- main
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5"], default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-only", choices=["gemm", "producer", "copy"],
                     help="profiling mode: launch one kernel back to back (for rocprofv3)")
-    ap.add_argument("--m", type=int, default=512, help="rows for --kernel-only")
+    ap.add_argument("--m", type=int, default=512, help="rows (tokens for c5) for --kernel-only")
     ap.add_argument("--iters", type=int, default=64, help="launches for --kernel-only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -164,97 +429,64 @@ def main():
 
     import __graft_entry__
     pkg = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
     if args.kernel_only:
         kernel_only(pkg, args)
         return
-    ops = pkg.ops
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev).manual_seed(1234)
-
-    # weights: quantize once with the product quantizer, pack, then replicate
-    w = (torch.randn(N_OUT, K_IN, generator=gen, device=dev) * 0.02).bfloat16()
-    wc, ws = torch.ops.mach_amd.quantize_mxfp8(w, 0)
-    tiled, tiled_s = ops.pack_weight(wc, ws, ops.E4M3)
-    copies = [(tiled.clone(), tiled_s.clone()) for _ in range(WEIGHT_COPIES)]
-    del w, wc, ws, tiled, tiled_s
-    inputs = {M: torch.randn(M, 2 * K_IN, generator=gen, device=dev).bfloat16() for M in M_SWEEP}
+    wl = make_workload(pkg, args.config, dev, gen)
     stream = torch.cuda.Stream()
-
-    def step_fns(ci):
-        wt, st = copies[ci]
-        return [lambda M=M: ops.swiglu_mx_down(inputs[M], wt, st, N_OUT, ops.E4M3) for M in M_SWEEP]
+    ncopies = len(wl.copies)
 
     # one graph per weight copy; a step replays the next one
     graphs = []
     with torch.cuda.stream(stream):
-        for ci in range(WEIGHT_COPIES):
-            for fn in step_fns(ci):
+        for ci in range(ncopies):
+            for fn in wl.step_fns(ci):
                 fn()
         stream.synchronize()
-        for ci in range(WEIGHT_COPIES):
+        for ci in range(ncopies):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
-                for fn in step_fns(ci):
+                for fn in wl.step_fns(ci):
                     fn()
             graphs.append(g)
         for i in range(args.warmup):
-            graphs[i % WEIGHT_COPIES].replay()
+            graphs[i % ncopies].replay()
         stream.synchronize()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         for i in range(args.steps):
-            graphs[i % WEIGHT_COPIES].replay()
+            graphs[i % ncopies].replay()
         end.record(stream)
         end.synchronize()
     torch.cuda.synchronize()
     ms_per_step = start.elapsed_time(end) / args.steps
-    total_flops = sum(algorithmic(M)[0] for M in M_SWEEP)
-    value = total_flops / (ms_per_step * 1e-3) / 1e12
+    value = sum(wl.flops(x) for x in wl.sweep) / (ms_per_step * 1e-3) / 1e12
 
-    # per-kernel timing: back-to-back launches of one op over rotated weight copies
-    per_m = {}
-    for M in M_SWEEP:
-        a, sa = torch.ops.mach_amd.swiglu_mxfp8(inputs[M], ops.CEIL_DIV448, False)
-        prod_us, _ = graph_time_us([lambda M=M: torch.ops.mach_amd.swiglu_mxfp8(inputs[M], ops.CEIL_DIV448, False)] * 8,
-                                   stream)
-        gemm_fns = [lambda wt=wt, st=st, a=a, sa=sa: torch.ops.mach_amd.mx_gemm(a, sa, wt, st, N_OUT, K_IN, ops.E4M3, None)
-                    for wt, st in copies]
-        gemm_us, _ = graph_time_us(gemm_fns, stream)
-        gemm_us /= len(gemm_fns)
-        prod_us /= 8
-        flops, bytes_, gemm_bytes = algorithmic(M)
-        t_min = max(flops / (MFMA_PEAK_TFLOPS * 1e12), gemm_bytes / (HBM_PEAK_GBS * 1e9)) * 1e6
-        per_m[M] = {"producer_us": round(prod_us, 2), "gemm_us": round(gemm_us, 2),
-                    "gemm_tflops": round(flops / gemm_us / 1e6, 2),
-                    "gemm_gbs": round(gemm_bytes / gemm_us / 1e3, 1),
-                    "gemm_roofline_frac": round(t_min / gemm_us, 3),
-                    "bound": "mfma" if flops / (MFMA_PEAK_TFLOPS * 1e12) > gemm_bytes / (HBM_PEAK_GBS * 1e9) else "hbm"}
-
-    dom = max(M_SWEEP, key=lambda M: per_m[M]["gemm_us"])
-    d = per_m[dom]
-    flops, _, gemm_bytes = algorithmic(dom)
-    if d["bound"] == "hbm":
-        roof = {"bound": "hbm", "achieved": d["gemm_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["gemm_gbs"] / HBM_PEAK_GBS, 4), "traffic": None}
-    else:
-        roof = {"bound": "mfma", "achieved": d["gemm_tflops"], "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(d["gemm_tflops"] / MFMA_PEAK_TFLOPS, 4), "traffic": None}
-    roof["kernel"] = f"mxfp8 gemm_kernel M={dom} N={N_OUT} K={K_IN}"
-    roof["algorithmic_bytes_per_launch"] = int(gemm_bytes)
+    # per-kernel timing: back-to-back launches of one op over the rotated weight copies
+    per_m, dom = {}, None
+    for x in wl.sweep:
+        per_m[x] = {}
+        for kname, (fns, flops, nbytes) in wl.kernels(x).items():
+            us, _ = graph_time_us(fns, stream)
+            k = kernel_entry(flops, nbytes, us / len(fns))
+            per_m[x][kname] = k
+            if flops and (dom is None or k["us"] > dom[1]["us"]):
+                dom = (kname, k)
 
     out = {
-        "metric": "GEMM TFLOP/s & HBM GB/s (% roofline) at M=1..512; bit-exact quant codes",
+        "metric": METRIC,
         "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "mxfp8(e4m3+e8m0) x mxfp8, fp32 accumulate, bf16 out",
-        "data": "synthetic (seeded randn), weights rotated over 16 copies (cold HBM)",
-        "config": {"workload": "c2: SwiGLU->MXFP8 producer + MXFP8 down projection",
-                   "M": list(M_SWEEP), "N": N_OUT, "K": K_IN, "parallelism": "single GPU"},
-        "per_m": per_m, "roofline": roof,
+        "vs_baseline": None, "dtype": wl.dtype,
+        "data": f"synthetic (seeded randn), weights rotated over {ncopies} copies (cold HBM)",
+        "config": {"workload": wl.describe, "M": list(wl.sweep), "parallelism": "single GPU"},
+        "per_m": per_m, "roofline": roofline_of(dom[0], dom[1]),
     }
-    if not args.no_cpu_baseline:
+    if args.config == "c2" and not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
 

@@ -47,6 +47,14 @@ int mxl_device_supported(int device);
 int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t ldx, int rule,
                        void* codes, void* scales, void* stream);
 
+/* MXFP6 weight quantization (OCP MX v1.0 floor rule): bf16 x [M, K] (row
+ * stride ldx elements) -> packed FP6 [M, 3K/4] (fmt 2 = E2M3, 3 = E3M2) + E8M0
+ * [M, K/32].  Replaces the offline MXFP6 quantizer the reference's checkpoints
+ * and tests come from (mxfp6.quantize_mxfp6, tests/native_mxfp6/test_moe.py:179-184,
+ * tests/native_mxfp6/test_mxfp6_sm120.py:37). */
+int mxl_quantize_mxfp6(const void* x, int64_t M, int64_t K, int64_t ldx, int fmt, void* packed, void* scales,
+                       void* stream);
+
 /* Bytes of the swizzled scale buffer for [M, K] (mxfp8_mlp.py:122). */
 int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K);
 

@@ -94,3 +94,15 @@ def test_silu_mul_block_fp8_bit_exact(pkg, oracle_mod, dev, rows, transposed):
     rq, rs = oracle_mod.silu_mul_block_fp8(x, transposed)
     assert np.array_equal(_u8(out), rq)
     assert np.array_equal(scales.cpu().numpy().view(np.uint32), np.ascontiguousarray(rs).view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", [2, 3])
+@pytest.mark.parametrize("M,K,std", [(1, 32, 1.0), (17, 512, 0.015), (256, 5120, 0.015)])
+def test_quantize_mxfp6_bit_exact(pkg, oracle_mod, dev, fmt, M, K, std):
+    g = torch.Generator().manual_seed(17 + M)
+    w = (torch.randn(M, K, generator=g) * std).bfloat16()
+    w[0, :32] = 0  # an all-zero block
+    packed, scales = torch.ops.mach_amd.quantize_mxfp6(w.to(dev), fmt)
+    rc, rs = oracle_mod.quant_mxfp6(w, fmt)
+    assert np.array_equal(scales.cpu().numpy(), rs)
+    assert np.array_equal(packed.cpu().numpy(), oracle_mod.pack_fp6(rc))

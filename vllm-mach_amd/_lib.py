@@ -27,6 +27,7 @@ SIGNATURES = {
     "mxl_last_error": (ctypes.c_char_p, []),
     "mxl_device_supported": (_I, [_I]),
     "mxl_quantize_mxfp8": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "mxl_quantize_mxfp6": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "mxl_swizzled_scale_bytes": (_I64, [_I64, _I64]),
     "mxl_swiglu_mxfp8": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P]),
     "mxl_quantize_block_fp8": (_I, [_P, _I64, _I64, _P, _P, _P]),

@@ -46,6 +46,25 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
   return sign | ((a - (120u << 23) + 0x7FFFFu + odd) >> 20);
 }
 
+// binary32 -> FP6 code (fmt 2 = E2M3, 3 = E3M2; bit 5 = sign), OCP MX v1.0:
+// round-to-nearest-even, saturating to the largest normal.
+template <int FMT>
+__device__ __forceinline__ uint32_t f32_to_fp6(float f) {
+  constexpr int MB = FMT == kE2M3 ? 3 : 2, BIAS = FMT == kE2M3 ? 1 : 3;
+  const uint32_t u = f2u(f);
+  const uint32_t sign = (u >> 26) & 0x20u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  uint32_t code;
+  if (a < ((uint32_t)(128 - BIAS) << 23)) {
+    code = (uint32_t)__builtin_rintf(__builtin_ldexpf(u2f(a), BIAS - 1 + MB));  // subnormal grid
+  } else {
+    constexpr int SH = 23 - MB;
+    const uint32_t odd = (a >> SH) & 1u;
+    code = (a - ((uint32_t)(127 - BIAS) << 23) + ((1u << (SH - 1)) - 1u) + odd) >> SH;
+  }
+  return sign | (code > 31u ? 31u : code);
+}
+
 // E8M0 code of the floor_carry175 rule from the bf16 bits of the block amax
 __device__ __forceinline__ uint32_t scale_floor_carry175(uint32_t amax_bf16) {
   uint32_t e = (((amax_bf16 + 32u) & 0xFF80u) >> 7) & 0xFFu;

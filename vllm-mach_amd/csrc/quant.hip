@@ -39,6 +39,49 @@ __global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __rest
   if (sub == 0) scales[row * blocks_per_row + blk] = (uint8_t)s;
 }
 
+// ------------------------------------------------------------ MXFP6 weights
+
+// OCP MX v1.0 section 6.3 quantization of bf16 weights to MXFP6: shared exponent
+// e = floor(log2(amax)) - emax (2 for E2M3, 4 for E3M2), clamped to the E8M0
+// range (an all-zero block gets code 0), elements = saturating RNE(x / 2^e),
+// packed four 6-bit codes per three bytes (little-endian bit stream).  Four
+// lanes own a 32-element block; each writes its 8 codes as 6 bytes.
+template <int FMT>
+__global__ __launch_bounds__(256) void quant_mxfp6_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                          uint8_t* __restrict__ packed,
+                                                          uint8_t* __restrict__ scales, int64_t M, int64_t K) {
+  const int64_t blocks_per_row = K / 32;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int sub = (int)(tid & 3);
+  const int64_t total = M * blocks_per_row;
+  const bool live = (tid >> 2) < total;
+  const int64_t id = live ? (tid >> 2) : total - 1;
+  const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
+  float v[8];
+  bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * ldx + blk * 32 + sub * 8), v);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+  amax = __builtin_fmaxf(amax, __shfl_xor(amax, 1, 4));
+  amax = __builtin_fmaxf(amax, __shfl_xor(amax, 2, 4));
+  constexpr int EMAX = FMT == kE2M3 ? 2 : 4;
+  // floor(log2(amax)) from the exponent field; zero and subnormal amax (floor(log2) <= -127) clamp to -127
+  const int ef = (int)((f2u(amax) >> 23) & 0xFFu);
+  int e = ef == 0 ? -127 : ef - 127 - EMAX;
+  e = e < -127 ? -127 : (e > 127 ? 127 : e);
+  uint32_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = f32_to_fp6<FMT>(__builtin_ldexpf(v[i], -e));
+  const uint32_t w0 = c[0] | (c[1] << 6) | (c[2] << 12) | (c[3] << 18);
+  const uint32_t w1 = c[4] | (c[5] << 6) | (c[6] << 12) | (c[7] << 18);
+  if (!live) return;
+  uint16_t* dst = reinterpret_cast<uint16_t*>(packed + row * (K * 3 / 4) + blk * 24 + sub * 6);
+  dst[0] = (uint16_t)w0;
+  dst[1] = (uint16_t)((w0 >> 16) | ((w1 & 0xFFu) << 8));
+  dst[2] = (uint16_t)(w1 >> 8);
+  if (sub == 0) scales[row * blocks_per_row + blk] = (uint8_t)(e + 127);
+}
+
 // ------------------------------------------------------------ SwiGLU -> MXFP8
 
 __device__ __forceinline__ int64_t swizzle_offset(int64_t r, int64_t g, int64_t K) {
@@ -194,6 +237,24 @@ extern "C" int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t l
   else
     quant_mxfp8_kernel<kCeilDiv448><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)codes, (uint8_t*)scales, M, K);
   MXL_CHECK_LAUNCH("mxl_quantize_mxfp8");
+  return MXL_OK;
+}
+
+extern "C" int mxl_quantize_mxfp6(const void* x, int64_t M, int64_t K, int64_t ldx, int fmt, void* packed,
+                                  void* scales, void* stream) {
+  MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_quantize_mxfp6: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
+  MXL_CHECK_ARG(fmt == kE2M3 || fmt == kE3M2, "mxl_quantize_mxfp6: fmt must be 2 (E2M3) or 3 (E3M2), got %d", fmt);
+  MXL_CHECK_ARG(ldx >= K && ldx % 8 == 0, "mxl_quantize_mxfp6: ldx must be >= K and a multiple of 8");
+  MXL_CHECK_ARG(aligned16(x) && ((uintptr_t)packed & 1) == 0, "mxl_quantize_mxfp6: misaligned buffers");
+  if (M == 0) return MXL_OK;
+  const int64_t n = M * (K / 32) * 4;
+  dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (fmt == kE2M3)
+    quant_mxfp6_kernel<kE2M3><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)packed, (uint8_t*)scales, M, K);
+  else
+    quant_mxfp6_kernel<kE3M2><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)packed, (uint8_t*)scales, M, K);
+  MXL_CHECK_LAUNCH("mxl_quantize_mxfp6");
   return MXL_OK;
 }
 

@@ -98,6 +98,33 @@ def _(x, rule=FLOOR_CARRY175):
             x.new_empty((x.shape[0], x.shape[1] // 32), dtype=torch.uint8))
 
 
+@torch.library.custom_op("mach_amd::quantize_mxfp6", mutates_args=())
+def quantize_mxfp6(x: torch.Tensor, fmt: int = E2M3) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 [N, K] -> (packed FP6 u8 [N, 3K/4], E8M0 u8 [N, K/32]), OCP MX v1.0 floor rule.
+
+    Replaces the offline MXFP6 quantizer behind the reference's checkpoints and tests
+    (``mxfp6.quantize_mxfp6``, tests/native_mxfp6/test_moe.py:179-184).
+    """
+    _check_cuda(x)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.shape[1] % 32:
+        raise ValueError("quantize_mxfp6 needs a 2-D bf16 tensor with K % 32 == 0")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M, K = x.shape
+    packed = torch.empty((M, K * 3 // 4), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((M, K // 32), dtype=torch.uint8, device=x.device)
+    if M:
+        call("mxl_quantize_mxfp6", ptr(x), M, K, x.stride(0), fmt, ptr(packed), ptr(scales), stream_handle(x.device))
+    _count("quantize_mxfp6")
+    return packed, scales
+
+
+@quantize_mxfp6.register_fake
+def _(x, fmt=E2M3):
+    return (x.new_empty((x.shape[0], x.shape[1] * 3 // 4), dtype=torch.uint8),
+            x.new_empty((x.shape[0], x.shape[1] // 32), dtype=torch.uint8))
+
+
 @torch.library.custom_op("mach_amd::swiglu_mxfp8", mutates_args=())
 def swiglu_mxfp8(gate_up: torch.Tensor, rule: int = CEIL_DIV448,
                  swizzled: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
