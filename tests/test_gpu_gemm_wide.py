@@ -1,0 +1,96 @@
+"""GPU parity of the wide-tile prefill GEMM (128-row workgroup tiles, K-stage ring,
+optional K splits) against the oracle, on the shapes that exercise its edges:
+ragged M and N, a K that ends in half a 512-wide super-tile, forced split counts,
+every weight format, bias, block-FP8 scales, and grouped experts with skewed,
+empty and multi-block row ranges.  Same bar as the other GEMM tests."""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_gemm import _act, _check, _weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,N,K,fmt,cfg,bias", [
+    (64, 256, 512, 0, None, False),
+    (200, 1000, 768, 0, "2,1", True),     # K = 1.5 super-tiles, ragged M
+    (300, 640, 2304, 2, "2,3", False),    # 3 K splits over 4.5 super-tiles
+    (130, 384, 1280, 3, "1,2", False),
+    (512, 512, 1792, 0, "1,4", True),
+    (257, 136, 1280, 2, None, False),     # N not a multiple of 16
+    (96, 2048, 4096, 0, "2,8", False),
+])
+def test_wide_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias):
+    if cfg:
+        monkeypatch.setenv("MXL_WIDE_CONFIG", cfg)
+    ops = pkg.ops
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 11 + N + K)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    x = _act(M, K, 7 + M)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    b = (torch.randn(N, generator=torch.Generator().manual_seed(3)) * 0.5).bfloat16() if bias else None
+    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, b.to(dev) if bias else None)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)))
+    if bias:
+        ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().numpy()[None, :]))
+    _check(y.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [
+    (64, 256, 512, None),
+    (200, 384, 1280, "2,2"),
+    (300, 1024, 768, "1,1"),
+    (512, 18432, 2560, None),
+])
+def test_wide_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
+    if cfg:
+        monkeypatch.setenv("MXL_WIDE_CONFIG", cfg)
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(91 + M + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    wb = w.reshape(N // 128, 128, K // 128, 128)
+    sb = (wb.abs().amax(dim=(1, 3)) / 448.0).float()
+    wq = (wb / sb[:, None, :, None]).reshape(N, K).to(torch.float8_e4m3fn)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    tiled, _ = ops.pack_weight(wq.to(dev), None, 0)
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x.to(dev))
+    y = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, None)
+    rq, rs = oracle_mod.quant_block_fp8(x)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), rq)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.block_fp8_gemm_ref(rq, rs, wq.view(torch.uint8).numpy(), sb.numpy()))
+    _check(y.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("fmt", [0, 2])
+def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, fmt):
+    """Expert 0 takes 300 routes (three 128-row blocks), expert 1 none, the rest a few
+    dozen each; rows are gathered through the sorted route list (row_div = topk)."""
+    ops = pkg.ops
+    E, N, K, T, topk = 8, 384, 1024, 400, 2
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(2, E, (T, topk), generator=g, dtype=torch.int32)
+    ids[:300, 0] = 0
+    parts = [_weights(oracle_mod, N, K, fmt, 0.02, 40 + e) for e in range(E)]
+    stored = np.stack([p[2] for p in parts])
+    scales = np.stack([p[1] for p in parts])
+    w_t, s_t = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(scales).to(dev), fmt)
+    x = _act(T, K, 77)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    routes, offsets, _ = torch.ops.mach_amd.moe_route(ids.to(dev), E)
+    R = T * topk
+    assert R >= 32 * E  # the wide grouped kernel serves this shape
+    y = torch.ops.mach_amd.grouped_gemm(a, sa, routes, topk, offsets, R, w_t, s_t, N, K, fmt)
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    off = offsets.cpu().numpy()
+    rt = routes.cpu().numpy()
+    got = y.float().cpu().numpy()
+    assert off[1] - off[0] == 300 and off[2] == off[1]
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if lo == hi:
+            continue
+        rows = rt[lo:hi] // topk
+        ref = oracle_mod.mx_gemm_ref(rc[rows], rs[rows], parts[e][0], parts[e][1], fmt)
+        _check(got[lo:hi], oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref)))

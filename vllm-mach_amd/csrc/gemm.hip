@@ -382,11 +382,12 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
   p.row_div = 1;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
-  if (lds_gemm_eligible(M, N, K, fmt, block)) {
-    int S = lds_gemm_splits(M, N, K);
-    if ((int64_t)S * M * N * 4 > workspace_bytes || workspace == nullptr) S = 1;  // no room: skip the K split
-    p.S = S;
-    e = launch_gemm_lds(fmt, p, S, s);
+  if (wide_gemm_eligible(M, K)) {
+    WideConfig wc = wide_config(M, N, K, fmt);
+    if (wc.S > 1 && ((int64_t)wc.S * M * N * 4 > workspace_bytes || workspace == nullptr))
+      wc = WideConfig{wc.NT, 1, (K + kTileK - 1) / kTileK};  // no room: skip the K split
+    p.S = wc.S;
+    e = launch_gemm_wide(fmt, block, wc, p, 0, s);
   } else {
     GemmConfig c = choose_config(M, N, K);
     const int64_t need = c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
@@ -412,9 +413,9 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
 extern "C" int64_t mxl_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0) return 0;
   int S = choose_config(M, N, K).S;
-  if (lds_gemm_eligible(M, N, K, kE4M3, false)) {
-    const int S2 = lds_gemm_splits(M, N, K);
-    if (S2 > S) S = S2;
+  if (wide_gemm_eligible(M, K)) {
+    const int S8 = wide_config(M, N, K, kE4M3).S, S6 = wide_config(M, N, K, kE2M3).S;
+    S = S8 > S6 ? S8 : S6;
   }
   return S > 1 ? (int64_t)S * M * N * 4 : 0;
 }
@@ -443,6 +444,23 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
                 "mxl_grouped_gemm: need N > 0, K %% 128 == 0, experts > 0");
   MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0, "mxl_grouped_gemm: misaligned operands");
   if (routed_rows == 0) return MXL_OK;
+  if (K % 256 == 0 && routed_rows >= 32 * num_experts && a_rows * K < (int64_t(1) << 32)) {
+    // enough rows per expert on average for 128-row blocks: the wide kernel
+    GemmParams p{};
+    p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;
+    p.out = (uint16_t*)out; p.row_index = row_index; p.expert_offsets = expert_offsets;
+    p.lda = K; p.ldc = N; p.M = routed_rows; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = a_rows;
+    p.w_expert_stride = mxl_tiled_weight_bytes(N, K, w_fmt);
+    p.sw_expert_stride = mxl_tiled_scale_bytes(N, K);
+    p.row_div = row_div; p.S = 1;
+    const WideConfig wc{2, 1, (K + kTileK - 1) / kTileK};
+    hipError_t e = launch_gemm_wide(w_fmt, false, wc, p, num_experts, (hipStream_t)stream);
+    if (e != hipSuccess) {
+      set_error("mxl_grouped_gemm: launch failed: %s", hipGetErrorString(e));
+      return MXL_EHIP;
+    }
+    return MXL_OK;
+  }
   GemmConfig c;
   const int64_t KT = (K + kTileK - 1) / kTileK;
   c.MT = 1; c.NT = 1; c.S = 1;

@@ -114,9 +114,18 @@ __device__ __forceinline__ v4f mfma_raw(v8i a, v8i b) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, kE4M3, FMT, 0, 127, 0, 127);
 }
 
-// LDS-staged kernel for prefill-sized M (gemm_lds.hip).
-bool lds_gemm_eligible(int64_t M, int64_t N, int64_t K, int fmt, bool block);
-int lds_gemm_splits(int64_t M, int64_t N, int64_t K);
-hipError_t launch_gemm_lds(int fmt, const GemmParams& p, int S, hipStream_t stream);
+// Wide-tile LDS-pipelined kernel for prefill-sized M (gemm_wide.hip): NT
+// n-tiles per wave (workgroup tile 128 x 64 NT), S K-splits of kt_per_split
+// 512-wide super-tiles each.
+struct WideConfig {
+  int NT, S;
+  int64_t kt_per_split;
+};
+WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt);
+bool wide_gemm_eligible(int64_t M, int64_t K);
+hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const GemmParams& p, int64_t num_experts,
+                            hipStream_t s);
+
+
 
 }  // namespace mxl
