@@ -94,3 +94,26 @@ def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, fmt):
         rows = rt[lo:hi] // topk
         ref = oracle_mod.mx_gemm_ref(rc[rows], rs[rows], parts[e][0], parts[e][1], fmt)
         _check(got[lo:hi], oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref)))
+
+
+@pytest.mark.parametrize("M,N,K,fmt", [
+    (1, 2560, 9216, 0),      # sixteen single-buffered waves
+    (16, 2560, 9216, 0),
+    (7, 17408, 5120, 2),     # persistent workgroups with 4 and 5 n-tiles (double-buffered pairs)
+    (3, 200, 384, 3),        # ragged N, three K128 slices over eight waves
+    (16, 4096, 10240, 0),
+    (16, 1000, 128, 2),      # a single slice
+])
+def test_stream_decode_gemm(pkg, oracle_mod, dev, M, N, K, fmt):
+    """The weight-streaming decode kernel (M <= 16) against the oracle."""
+    ops = pkg.ops
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 13 + N + K)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    x = _act(M, K, 3 + M)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    b = (torch.randn(N, generator=torch.Generator().manual_seed(9)) * 0.5).bfloat16()
+    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, b.to(dev))
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)))
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().numpy()[None, :]))
+    _check(y.float().cpu().numpy(), ref)

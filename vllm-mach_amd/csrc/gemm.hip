@@ -382,7 +382,10 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
   p.row_div = 1;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
-  if (wide_gemm_eligible(M, K)) {
+  if (!block && stream_gemm_eligible(M, K)) {
+    p.S = 1;
+    e = launch_gemm_stream(fmt, p, s);
+  } else if (wide_gemm_eligible(M, K)) {
     WideConfig wc = wide_config(M, N, K, fmt);
     if (wc.S > 1 && ((int64_t)wc.S * M * N * 4 > workspace_bytes || workspace == nullptr))
       wc = WideConfig{wc.NT, 1, (K + kTileK - 1) / kTileK};  // no room: skip the K split

@@ -1,0 +1,260 @@
+// Weight-streaming GEMM for decode-sized M (M <= 16) on gfx950.
+//
+// With at most 16 activation rows the GEMM is a stream over the weights: each
+// weight byte is used once, so the kernel is bound by HBM bandwidth and the
+// design goal is to keep enough weight bytes in flight on every CU.
+//
+//   * A workgroup of W = ceil(KT / RUN) wavefronts owns one n-tile (16 weight
+//     rows) at a time; wave w takes the RUN consecutive 512-wide super-tiles
+//     starting at RUN w, so each of its four K128 slices per super-tile has a
+//     static position (fixed chunk offsets, fixed op_sel of the E8M0 dwords).
+//   * Workgroups are persistent over n-tiles (g, g + G, g + 2G, ... with G at
+//     most one per CU).  Each wave keeps its activation fragments and scales in
+//     registers for every n-tile (the at most 16 activation rows are the same
+//     throughout); the first weights are requested before them.
+//   * Weight fragments are loaded straight from the MFMA-tiled layout into
+//     registers (1 KiB per wave per load).  With RUN = 1 they are double-
+//     buffered by n-tile: the next n-tile's loads are issued before the current
+//     MFMAs, in a loop unrolled by two with unconditional loads (the last
+//     prefetch re-reads a valid tile), so the compiler's own waits stay exact.
+//   * The W per-wave 16 x 16 fp32 partials are summed in LDS in wave order
+//     (double-buffered by n-tile, one barrier per n-tile), rounded to bf16,
+//     bias added in bf16.
+#include "gemm_common.h"
+
+
+namespace mxl {
+
+namespace {
+
+constexpr int kStreamMaxWaves = 16;
+constexpr int64_t kStreamMaxK = 12288;  // two super-tiles per wave, at most twelve waves
+
+template <int FMT>
+struct StreamFmt {
+  static constexpr int CH = FmtTraits<FMT>::CH;
+  static constexpr int DW = FMT == kE4M3 ? 8 : 6;  // operand dwords per lane per K128 slice
+};
+
+template <int FMT, int RUN>
+struct StreamB {
+  uint32_t d[RUN][4][StreamFmt<FMT>::DW];
+  uint32_t s[RUN];  // tiled E8M0 dword of the super-tile (byte j = slice j)
+  uint32_t bias;    // bf16 bias bits of output column (t % 16) of the n-tile, loaded with the
+                    // weights and converted at use, so no wait lands between the prefetches
+};
+
+// Weight operands of super-tile kt of n-tile nt (the lane's 16 bytes of every chunk).
+template <int FMT>
+__device__ __forceinline__ void stream_load_tile(const uint8_t* w, const uint8_t* sw, int64_t KT, int64_t nt,
+                                                 int64_t kt, int lane, uint32_t (&d)[4][StreamFmt<FMT>::DW],
+                                                 uint32_t& sd) {
+  constexpr int CH = StreamFmt<FMT>::CH;
+  const uint8_t* tile = w + (nt * KT + kt) * (CH * 1024) + lane * 16;
+  uint4 c[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) c[i] = *reinterpret_cast<const uint4*>(tile + i * 1024);
+  if (FMT == kE4M3) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 lo = c[2 * j], hi = c[2 * j + 1];
+      d[j][0] = lo.x; d[j][1] = lo.y; d[j][2] = lo.z; d[j][3] = lo.w;
+      d[j][4] = hi.x; d[j][5] = hi.y; d[j][6] = hi.z; d[j][7] = hi.w;
+    }
+  } else {  // the lane's 24 dwords; slice j takes dwords [6 j, 6 j + 6)
+    uint32_t all[24];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      all[4 * i] = c[i].x; all[4 * i + 1] = c[i].y; all[4 * i + 2] = c[i].z; all[4 * i + 3] = c[i].w;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int k = 0; k < 6; ++k) d[j][k] = all[6 * j + k];
+  }
+  sd = *reinterpret_cast<const uint32_t*>(sw + (nt * KT + kt) * 256 + lane * 4);
+}
+
+template <int FMT, int RUN>
+__device__ __forceinline__ void stream_load_b(const GemmParams& p, const uint8_t* w, const uint8_t* sw, int64_t nt,
+                                              const int64_t (&kt)[RUN], int lane, StreamB<FMT, RUN>& b) {
+#pragma unroll
+  for (int u = 0; u < RUN; ++u) stream_load_tile<FMT>(w, sw, p.KT, nt, kt[u], lane, b.d[u], b.s[u]);
+  const int64_t col = nt * 16 + (lane & 15);
+  // unconditional load (without a bias, any valid halfword: the value is unused)
+  const uint16_t* bp = p.bias ? p.bias + (col < p.N ? col : p.N - 1) : reinterpret_cast<const uint16_t*>(sw);
+  b.bias = *bp;
+}
+
+// With two super-tiles per wave, two independent accumulators (even and odd
+// slices) summed at the end: two short MFMA dependency chains instead of one long
+// one.  One super-tile keeps a single chain (its register budget is tighter).
+template <int FMT, int RUN>
+__device__ __forceinline__ v4f stream_mfma(const v8i (&a)[RUN][4], const uint32_t (&sa)[RUN][4],
+                                           const StreamB<FMT, RUN>& b, const bool (&valid)[RUN]) {
+  v4f acc[RUN] = {};
+#pragma unroll
+  for (int u = 0; u < RUN; ++u) {
+    if (!valid[u]) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t* d = b.d[u][j];
+      const v8i bf = FMT == kE4M3 ? v8i{(int)d[0], (int)d[1], (int)d[2], (int)d[3], (int)d[4], (int)d[5], (int)d[6], (int)d[7]}
+                                  : v8i{(int)d[0], (int)d[1], (int)d[2], (int)d[3], (int)d[4], (int)d[5], 0, 0};
+      if (j == 0) acc[0] = mfma_step<FMT, 0>(a[u][j], bf, acc[0], sa[u][j], b.s[u]);
+      if (j == 1) acc[RUN - 1] = mfma_step<FMT, 1>(a[u][j], bf, acc[RUN - 1], sa[u][j], b.s[u]);
+      if (j == 2) acc[0] = mfma_step<FMT, 2>(a[u][j], bf, acc[0], sa[u][j], b.s[u]);
+      if (j == 3) acc[RUN - 1] = mfma_step<FMT, 3>(a[u][j], bf, acc[RUN - 1], sa[u][j], b.s[u]);
+    }
+  }
+  v4f out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = RUN == 2 ? acc[0][i] + acc[RUN - 1][i] : acc[0][i];
+  return out;
+}
+
+}  // namespace
+
+template <int FMT, int RUN, bool DB>
+__global__ __launch_bounds__(RUN == 1 ? 1024 : 768) void gemm_stream_kernel(GemmParams p) {
+  __shared__ float red[2][kStreamMaxWaves][4][64];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int W = (int)(blockDim.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t ntiles = (p.N + 15) / 16;
+  const int64_t G = gridDim.x, g = blockIdx.x;
+  const uint8_t* w = p.w;
+  const uint8_t* sw = static_cast<const uint8_t*>(p.sw);
+
+  // this wave's super-tiles; waves past the end re-read the last tile and add nothing
+  int64_t kt[RUN];
+  bool valid[RUN];
+#pragma unroll
+  for (int u = 0; u < RUN; ++u) {
+    const int64_t k = (int64_t)wv * RUN + u;
+    valid[u] = k < p.KT;
+    kt[u] = valid[u] ? k : p.KT - 1;
+  }
+
+  // Weights first (the HBM stream is the critical path), then this wave's activation
+  // fragments and scales, kept in registers for every n-tile (rows >= M read row
+  // M - 1 and are never stored; loads are clamped inside K so all are unconditional)
+  const int64_t count = g < ntiles ? (ntiles - g + G - 1) / G : 0;  // n-tiles of this workgroup
+  StreamB<FMT, RUN> b0;
+  stream_load_b<FMT, RUN>(p, w, sw, g < ntiles ? g : ntiles - 1, kt, lane, b0);
+  v8i a[RUN][4];
+  uint32_t sraw[RUN][4];
+  {
+    const int64_t row = r < p.M ? r : p.M - 1;
+    const uint8_t* srow = static_cast<const uint8_t*>(p.sa) + row * (p.K / 32);
+    const uint8_t* arow = p.a + row * p.lda;
+#pragma unroll
+    for (int u = 0; u < RUN; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t k0 = kt[u] * kTileK + 128 * j;
+        const int64_t kc = k0 < p.K ? k0 : p.K - 128;
+        const uint4 lo = *reinterpret_cast<const uint4*>(arow + kc + 16 * q);
+        const uint4 hi = *reinterpret_cast<const uint4*>(arow + kc + 64 + 16 * q);
+        a[u][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        sraw[u][j] = *reinterpret_cast<const uint32_t*>(srow + kc / 32);
+      }
+  }
+  // slices past the end of K (the upper half of a K % 512 == 256 tail) contribute zero
+  uint32_t sa[RUN][4];
+#pragma unroll
+  for (int u = 0; u < RUN; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool in = kt[u] * kTileK + 128 * j < p.K;
+      sa[u][j] = in ? (sraw[u][j] >> (8 * q)) & 0xFFu : 0u;
+      if (!in) a[u][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+
+  // reduce the W wave partials of n-tile nt (buffer `buf`) and store bf16
+  auto finish = [&](const v4f& acc, uint32_t bias_bits, int64_t nt, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[buf][wv][i][lane] = acc[i];
+    // LDS handover without a memory fence (a fence would also drain the weight
+    // prefetch in flight): wait for this wave's LDS writes, then the barrier
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    for (int e = t; e < 256; e += 64 * W) {  // fewer than four waves loop
+      const int i = e >> 6, l = e & 63;
+      float sum = red[buf][0][i][l];
+      for (int v = 1; v < W; ++v) sum += red[buf][v][i][l];
+      const int64_t row = 4 * (l >> 4) + i, col = nt * 16 + (l & 15);
+      if (row < p.M && col < p.N) {
+        float y = bf16_round(sum);
+        if (p.bias) y = y + bf16_to_f32((uint16_t)bias_bits);
+        p.out[row * p.ldc + col] = f32_to_bf16(y);
+      }
+    }
+  };
+
+  if (DB) {
+    StreamB<FMT, RUN> b1;
+    for (int64_t j = 0; j < count; j += 2) {
+      const int64_t nt0 = g + j * G;
+      // prefetch the second n-tile of the pair (or re-read the first)
+      const int64_t nt1 = j + 1 < count ? nt0 + G : nt0;
+      stream_load_b<FMT, RUN>(p, w, sw, nt1, kt, lane, b1);
+      finish(stream_mfma<FMT, RUN>(a, sa, b0, valid), b0.bias, nt0, 0);
+      const int64_t nt2 = j + 2 < count ? nt0 + 2 * G : nt1;
+      stream_load_b<FMT, RUN>(p, w, sw, nt2, kt, lane, b0);
+      if (j + 1 < count) finish(stream_mfma<FMT, RUN>(a, sa, b1, valid), b1.bias, nt1, 1);
+    }
+  } else {
+    for (int64_t j = 0; j < count; ++j) {
+      const int64_t nt = g + j * G;
+      if (j > 0) stream_load_b<FMT, RUN>(p, w, sw, nt, kt, lane, b0);
+      finish(stream_mfma<FMT, RUN>(a, sa, b0, valid), b0.bias, nt, (int)(j & 1));
+    }
+  }
+}
+
+// ------------------------------------------------------------ configuration
+
+// One super-tile per wave (double-buffered) up to 16 super-tiles (K <= 8192);
+// two per wave, single-buffered, up to 24 (K <= 12288, twelve waves of at most
+// 168 registers).  A super-tile costs 32 + 4 VGPRs of activations and 32 (24
+// for FP6) + 1 of weights per buffer.
+bool stream_gemm_eligible(int64_t M, int64_t K) {
+  return M >= 1 && M <= 16 && K % 128 == 0 && K >= 128 && K <= kStreamMaxK;
+}
+
+namespace {
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int FMT>
+hipError_t launch_stream_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (p.KT <= kStreamMaxWaves) {
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 2, false>), grid, dim3((unsigned)((p.KT + 1) / 2 * 64)), 0, s, p);
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_gemm_stream(int fmt, const GemmParams& p, hipStream_t s) {
+  const int64_t ntiles = (p.N + 15) / 16;
+  const int64_t G = ntiles < cu_count() ? ntiles : cu_count();
+  const dim3 grid((unsigned)G);
+  if (fmt == kE4M3) return launch_stream_fmt<kE4M3>(p, grid, s);
+  if (fmt == kE2M3) return launch_stream_fmt<kE2M3>(p, grid, s);
+  if (fmt == kE3M2) return launch_stream_fmt<kE3M2>(p, grid, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mxl
