@@ -20,6 +20,9 @@ pytestmark = pytest.mark.gpu
     (512, 512, 1792, 0, "1,4", True),
     (257, 136, 1280, 2, None, False),     # N not a multiple of 16
     (96, 2048, 4096, 0, "2,8", False),
+    (384, 1024, 2560, 0, "4,2", True),    # 3-slot ring, ragged K split
+    (130, 1280, 768, 2, "4,1", False),
+    (256, 700, 1280, 3, "4,3", False),    # N not a multiple of 256
 ])
 def test_wide_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias):
     if cfg:
@@ -42,6 +45,7 @@ def test_wide_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias
     (64, 256, 512, None),
     (200, 384, 1280, "2,2"),
     (300, 1024, 768, "1,1"),
+    (200, 1024, 1280, "4,2"),
     (512, 18432, 2560, None),
 ])
 def test_wide_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):

@@ -1,27 +1,29 @@
 // Wide-tile, LDS-pipelined GEMM for prefill-sized M on gfx950 (MX, block-FP8,
 // dense and MoE-grouped).
 //
-// Workgroup tile: 128 rows x 64*NT columns (NT = 1 or 2), four wavefronts.
+// Workgroup tile: 128 rows x 64*NT columns (NT = 1, 2 or 4), four wavefronts.
 // Every wave owns all 8 m-tiles of the 128 rows and its own NT n-tiles; per
 // K128 slice it reads each A fragment once from LDS and issues NT MFMAs with it.
 //
 // All operands reach LDS by direct global->LDS loads (global_load_lds: lane i
 // of a wave writes 4 or 16 bytes at LDS base + 4i / 16i, no staging
-// registers) into a ring of four K128 stage slots, three stages ahead of the
-// MFMAs.  A slot holds
+// registers) into a ring of K128 stage slots (four, or three for NT = 4 whose
+// 53 KiB stages would not fit four times), issued two or three stages ahead of
+// the MFMAs.  A slot holds
 //   A    8 m-tiles x 2 KiB in MFMA fragment order: chunk (m-tile i, half h) has
 //        at lane l = 16q + r the 16 bytes K [64 h + 16 q, +16) of row 16 i + r,
 //        so a fragment is two lane-contiguous 16-byte LDS reads;
 //   B    per wave, its NT n-tiles' 2 KiB of the MFMA-tiled weight (copied
 //        verbatim: the tiled layout already is fragment order);
 //   SA   the activation scales of the 128 rows (E8M0 dword of blocks 4j..4j+3,
-//        or the block-FP8 fp32 scale);
+//        or the block-FP8 fp32 scale), copied by waves 0 and 1;
 //   SB   per wave, the tiled E8M0 weight-scale dwords of its n-tiles (MX only).
 // The copies are issued from inline assembly, so the compiler neither counts
 // them nor adds waits of its own: each step waits (vmcnt) for exactly its own
-// stage -- the two stages issued after it may stay in flight, vector-memory
-// loads completing in issue order -- then one barrier hands the slot to all
-// waves and frees the slot of the previous step for the next copy.
+// stage -- the stages issued after it may stay in flight, vector-memory loads
+// completing in issue order -- then one barrier hands the slot to all waves and
+// frees the slot of the previous step for the next copy.  The slice index of a
+// stage is a run-time value, so E8M0 bytes are shifted into place for op_sel 0.
 //
 // Grid: one workgroup per (m-block, n-block, K split), remapped so that the
 // m-blocks sharing a weight slice are consecutive on one XCD (workgroup L runs
@@ -45,10 +47,12 @@ template <int NT, bool BLOCK>
 struct WideSlot {
   static constexpr int A = 0;                          // 16 KiB
   static constexpr int B = 16 * 1024;                  // wave w: NT x 2 KiB at B + w NT 2 KiB
-  static constexpr int SA = B + 4 * NT * 2048;         // 512 B (+512 B written by waves 2, 3, unused)
-  static constexpr int SB = SA + 1024;                 // wave w: NT x 256 B (MX)
+  static constexpr int SA = B + 4 * NT * 2048;         // 512 B, copied by waves 0 and 1
+  static constexpr int SB = SA + 512;                  // wave w: NT x 256 B (MX)
   static constexpr int BYTES = SB + (BLOCK ? 0 : 4 * NT * 256);
-  static constexpr int COPIES = 4 + 2 * NT + 1 + (BLOCK ? 0 : NT);  // per wave per stage
+  static constexpr int SLOTS = NT == 4 ? 3 : 4;        // 4 x 53 KiB would not fit the LDS
+  // copies per wave per stage (waves 0 and 1 also copy the activation scales)
+  static constexpr int COPIES = 4 + 2 * NT + (BLOCK ? 0 : NT);
 };
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -84,33 +88,39 @@ struct WideLanes {
   const uint8_t* sw_tile[NT];
 };
 
-// Copy K128 stage `t` (super-tile t / 4, slice J = t % 4) into a slot.
-template <int FMT, int NT, bool BLOCK, int J>
+// Copy K128 stage `t` (super-tile t / 4, slice j = t % 4) into a slot.
+template <int FMT, int NT, bool BLOCK>
 __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, int64_t t, int wv, int lane,
                                           const WideLanes<NT>& L) {
   using S = WideSlot<NT, BLOCK>;
   constexpr int CH = FmtTraits<FMT>::CH;
   const int64_t kt = t >> 2;
+  const int j = (int)(t & 3);
 #pragma unroll
   for (int u = 0; u < 4; ++u) {  // A: m-tile 2 wv + u / 2, half u % 2
     const int i = 2 * wv + (u >> 1), hl = u & 1;
     copy16(p.a + t * 128 + 64 * hl, L.a_off[u >> 1], lds_addr(slot + S::A + (i * 2 + hl) * 1024));
   }
+  // B: the two 1 KiB chunks of the tile that hold slice j (FP6: its 24 bytes per lane
+  // straddle two chunks)
+  const int c0 = FMT == kE4M3 ? 2 * j : (3 * j) >> 1;
 #pragma unroll
-  for (int n = 0; n < NT; ++n) {  // B: the two 1 KiB chunks of the tile that hold slice J
-    constexpr int c0 = FMT == kE4M3 ? 2 * J : (3 * J) / 2;
-    const uint8_t* tile = L.w_tile[n] + kt * (CH * 1024);
+  for (int n = 0; n < NT; ++n) {
+    const uint8_t* tile = L.w_tile[n] + kt * (CH * 1024) + c0 * 1024;
 #pragma unroll
     for (int c2 = 0; c2 < 2; ++c2)
-      copy16(tile + (c0 + c2) * 1024, (uint32_t)(lane * 16), lds_addr(slot + S::B + ((wv * NT + n) * 2 + c2) * 1024));
+      copy16(tile + c2 * 1024, (uint32_t)(lane * 16), lds_addr(slot + S::B + ((wv * NT + n) * 2 + c2) * 1024));
   }
-  if (!BLOCK) {  // E8M0 bytes of blocks 4t .. 4t + 3 of row t % 128
-    copy4(static_cast<const uint8_t*>(p.sa) + t * 4, L.sa_off, lds_addr(slot + S::SA + wv * 256));
+  if (wv < 2) {  // activation scales of the 128 rows (row = t % 128 of waves 0, 1)
+    if (!BLOCK)  // E8M0 bytes of blocks 4t .. 4t + 3
+      copy4(static_cast<const uint8_t*>(p.sa) + t * 4, L.sa_off, lds_addr(slot + S::SA + wv * 256));
+    else  // fp32 scale of K128 group t (column-major [K/128, M])
+      copy4(static_cast<const uint8_t*>(p.sa) + t * 4 * p.M, L.sa_off, lds_addr(slot + S::SA + wv * 256));
+  }
+  if (!BLOCK) {
 #pragma unroll
     for (int n = 0; n < NT; ++n)
       copy4(L.sw_tile[n] + kt * 256, (uint32_t)(lane * 4), lds_addr(slot + S::SB + (wv * NT + n) * 256));
-  } else {  // fp32 scale of row t % 128, K128 group t (column-major [K/128, M])
-    copy4(static_cast<const uint8_t*>(p.sa) + t * 4 * p.M, L.sa_off, lds_addr(slot + S::SA + wv * 256));
   }
 }
 
@@ -133,14 +143,18 @@ __device__ __forceinline__ WideFrag wide_frag(const uint8_t* slot, int i, int la
   return x;
 }
 
-// The 8 x NT MFMAs of one K128 stage (slice J of its super-tile).  Fragment
-// reads run one m-tile ahead of the MFMAs that consume them.
-template <int FMT, int NT, bool BLOCK, int J>
-__device__ __forceinline__ void wide_compute(const uint8_t* slot, float sbv, v4f (&acc)[8][NT], int wv, int lane,
-                                             int q, int r) {
+// The 8 x NT MFMAs of one K128 stage (slice j of its super-tile).  The E8M0
+// bytes are shifted into place (op_sel 0), since j is not a compile-time value
+// under a 3-slot ring.  Fragment reads run one m-tile ahead of the MFMAs.
+template <int FMT, int NT, bool BLOCK>
+__device__ __forceinline__ void wide_compute(const uint8_t* slot, int j, float sbv, v4f (&acc)[8][NT], int wv,
+                                             int lane, int q, int r) {
   using S = WideSlot<NT, BLOCK>;
   v8i bf[NT];
   uint32_t sb[NT];
+  // FP6: the slice's 24 bytes start at byte 0 (even j) or 8 (odd j) of the first chunk
+  const int odd = j & 1;
+  const int o0 = 8 * odd, o1 = odd ? 1024 : 8, o2 = odd ? 1032 : 1024;
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const uint8_t* base = slot + S::B + (wv * NT + n) * 2048 + lane * 16;
@@ -148,16 +162,13 @@ __device__ __forceinline__ void wide_compute(const uint8_t* slot, float sbv, v4f
       const uint4 lo = *reinterpret_cast<const uint4*>(base);
       const uint4 hi = *reinterpret_cast<const uint4*>(base + 1024);
       bf[n] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    } else if ((J & 1) == 0) {  // FP6: the slice's 24 bytes start at byte 0 of the first chunk
-      const uint4 c0 = *reinterpret_cast<const uint4*>(base);
-      const uint2 c1 = *reinterpret_cast<const uint2*>(base + 1024);
-      bf[n] = v8i{(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w, (int)c1.x, (int)c1.y, 0, 0};
-    } else {  // ... or at byte 8
-      const uint2 c0 = *reinterpret_cast<const uint2*>(base + 8);
-      const uint4 c1 = *reinterpret_cast<const uint4*>(base + 1024);
-      bf[n] = v8i{(int)c0.x, (int)c0.y, (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w, 0, 0};
+    } else {
+      const uint2 d0 = *reinterpret_cast<const uint2*>(base + o0);
+      const uint2 d1 = *reinterpret_cast<const uint2*>(base + o1);
+      const uint2 d2 = *reinterpret_cast<const uint2*>(base + o2);
+      bf[n] = v8i{(int)d0.x, (int)d0.y, (int)d1.x, (int)d1.y, (int)d2.x, (int)d2.y, 0, 0};
     }
-    if (!BLOCK) sb[n] = *reinterpret_cast<const uint32_t*>(slot + S::SB + (wv * NT + n) * 256 + lane * 4);
+    if (!BLOCK) sb[n] = (*reinterpret_cast<const uint32_t*>(slot + S::SB + (wv * NT + n) * 256 + lane * 4) >> (8 * j)) & 0xFFu;
   }
   WideFrag cur = wide_frag<NT, BLOCK>(slot, 0, lane, q, r);
 #pragma unroll
@@ -167,7 +178,7 @@ __device__ __forceinline__ void wide_compute(const uint8_t* slot, float sbv, v4f
     if (!BLOCK) {
       const uint32_t sa = (cur.sd >> (8 * q)) & 0xFFu;
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[i][n] = mfma_step<FMT, J>(cur.a, bf[n], acc[i][n], sa, sb[n]);
+      for (int n = 0; n < NT; ++n) acc[i][n] = mfma_step<FMT, 0>(cur.a, bf[n], acc[i][n], sa, sb[n]);
     } else {
       const float fs[4] = {cur.s4.x * sbv, cur.s4.y * sbv, cur.s4.z * sbv, cur.s4.w * sbv};
 #pragma unroll
@@ -181,13 +192,19 @@ __device__ __forceinline__ void wide_compute(const uint8_t* slot, float sbv, v4f
   }
 }
 
-// Wait for this wave's copies of the current stage; `later` stages (0..2) were
-// issued after it and may stay in flight.
+// Wait for this wave's copies of the current stage: the copies of the `later`
+// stages issued after it (C per stage, C + 1 for waves 0 and 1) may stay in flight.
 template <int C>
-__device__ __forceinline__ void wide_wait(int later) {
-  if (later >= 2) wait_vm<2 * C>();
-  else if (later == 1) wait_vm<C>();
-  else wait_vm<0>();
+__device__ __forceinline__ void wide_wait(int later, bool scales) {
+  if (scales) {
+    if (later >= 2) wait_vm<2 * (C + 1)>();
+    else if (later == 1) wait_vm<C + 1>();
+    else wait_vm<0>();
+  } else {
+    if (later >= 2) wait_vm<2 * C>();
+    else if (later == 1) wait_vm<C>();
+    else wait_vm<0>();
+  }
 }
 
 }  // namespace
@@ -202,11 +219,12 @@ struct WideGrid {
 template <int FMT, int NT, bool BLOCK, bool GROUPED>
 __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g) {
   using S = WideSlot<NT, BLOCK>;
-  // separate objects per slot (the LDS budget of one workgroup per CU)
-  __shared__ __attribute__((aligned(1024))) uint8_t slot0[S::BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot1[S::BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot2[S::BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot3[S::BYTES];
+  // separate objects per slot (the LDS budget of one workgroup per CU; with
+  // three slots the fourth object is a 16-byte stub)
+  __shared__ __attribute__((aligned(16))) uint8_t slot0[S::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t slot1[S::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t slot2[S::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t slot3[S::SLOTS == 4 ? S::BYTES : 16];
   __shared__ int64_t sh_scan[256];
   __shared__ int64_t sh_grp[3];
   constexpr int C = S::COPIES;
@@ -276,7 +294,7 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   WideLanes<NT> L;
 #pragma unroll
   for (int i = 0; i < 2; ++i) L.a_off[i] = (uint32_t)(a_row(row_base + (2 * wv + i) * 16 + r) * p.lda + 16 * q);
-  L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & 127)) : a_row(row_base + (t & 127)) * (p.K / 32));
+  L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & 127)) : a_row(row_base + (t & 127)) * (p.K / 32));  // t < 128 copy
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int64_t nt = nt_wave + n < ntiles_total ? nt_wave + n : ntiles_total - 1;
@@ -300,29 +318,39 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
     for (int n = 0; n < NT; ++n) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
 
   if (tb < te) {
-    // prologue: stages tb .. tb + 2 (tb is a multiple of 4: slot and slice indices are static)
-    wide_copy<FMT, NT, BLOCK, 0>(p, slot0, tb, wv, lane, L);
-    if (tb + 1 < te) wide_copy<FMT, NT, BLOCK, 1>(p, slot1, tb + 1, wv, lane, L);
-    if (tb + 2 < te) wide_copy<FMT, NT, BLOCK, 2>(p, slot2, tb + 2, wv, lane, L);
+    constexpr int R = S::SLOTS;
+    // prologue: stages tb .. tb + R - 2
+    wide_copy<FMT, NT, BLOCK>(p, slot0, tb, wv, lane, L);
+    if (tb + 1 < te) wide_copy<FMT, NT, BLOCK>(p, slot1, tb + 1, wv, lane, L);
+    if (R == 4 && tb + 2 < te) wide_copy<FMT, NT, BLOCK>(p, slot2, tb + 2, wv, lane, L);
 
-// Step tt = t0 + J: wait for stage tt, barrier (the slot of tt - 1 is free),
-// copy stage tt + 3 into it, then the stage's MFMAs.
-#define MXL_WIDE_STEP(J_, SLOT_, NEXT_SLOT_)                                                        \
-  {                                                                                                \
-    const int64_t tt = t0 + J_;                                                                    \
-    if (tt < te) {                                                                                 \
-      wide_wait<C>((int)(tt + 1 < te) + (int)(tt + 2 < te));                                       \
-      wide_barrier();                                                                              \
-      if (tt + 3 < te) wide_copy<FMT, NT, BLOCK, (J_ + 3) & 3>(p, NEXT_SLOT_, tt + 3, wv, lane, L); \
-      wide_compute<FMT, NT, BLOCK, J_>(SLOT_, BLOCK ? sbp[tt] : 0.f, acc, wv, lane, q, r);         \
-    }                                                                                              \
+// Step tt = t0 + I: wait for stage tt, barrier (the slot of tt - 1 is free),
+// copy stage tt + R - 1 into it, then the stage's MFMAs.
+#define MXL_WIDE_STEP(I_, SLOT_, NEXT_SLOT_)                                                       \
+  {                                                                                               \
+    const int64_t tt = t0 + I_;                                                                   \
+    if (tt < te) {                                                                                \
+      const int64_t later = te - 1 - tt < R - 2 ? te - 1 - tt : R - 2;                            \
+      wide_wait<C>((int)later, wv < 2);                                                           \
+      wide_barrier();                                                                             \
+      if (tt + R - 1 < te) wide_copy<FMT, NT, BLOCK>(p, NEXT_SLOT_, tt + R - 1, wv, lane, L);     \
+      wide_compute<FMT, NT, BLOCK>(SLOT_, (int)(tt & 3), BLOCK ? sbp[tt] : 0.f, acc, wv, lane, q, r); \
+    }                                                                                             \
   }
 
-    for (int64_t t0 = tb; t0 < te; t0 += 4) {
-      MXL_WIDE_STEP(0, slot0, slot3)
-      MXL_WIDE_STEP(1, slot1, slot0)
-      MXL_WIDE_STEP(2, slot2, slot1)
-      MXL_WIDE_STEP(3, slot3, slot2)
+    if (R == 4) {
+      for (int64_t t0 = tb; t0 < te; t0 += 4) {
+        MXL_WIDE_STEP(0, slot0, slot3)
+        MXL_WIDE_STEP(1, slot1, slot0)
+        MXL_WIDE_STEP(2, slot2, slot1)
+        MXL_WIDE_STEP(3, slot3, slot2)
+      }
+    } else {
+      for (int64_t t0 = tb; t0 < te; t0 += 3) {
+        MXL_WIDE_STEP(0, slot0, slot2)
+        MXL_WIDE_STEP(1, slot1, slot0)
+        MXL_WIDE_STEP(2, slot2, slot1)
+      }
     }
 #undef MXL_WIDE_STEP
   }
@@ -355,11 +383,11 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
 
 namespace {
 
-// Optional override "NT,S" (tuning runs only), e.g. MXL_WIDE_CONFIG=2,4.
+// Optional override "NT,S" (tuning runs only), e.g. MXL_WIDE_CONFIG=4,3.
 bool wide_override(int& nt, int& s) {
   const char* v = std::getenv("MXL_WIDE_CONFIG");
   int o_nt = 0, o_s = 0;
-  if (!v || std::sscanf(v, "%d,%d", &o_nt, &o_s) != 2 || (o_nt != 1 && o_nt != 2) || o_s < 1) return false;
+  if (!v || std::sscanf(v, "%d,%d", &o_nt, &o_s) != 2 || (o_nt != 1 && o_nt != 2 && o_nt != 4) || o_s < 1) return false;
   nt = o_nt;
   s = o_s;
   return true;
@@ -367,11 +395,11 @@ bool wide_override(int& nt, int& s) {
 
 }  // namespace
 
-// Pick the n-tiles per wave and the K split from a simple time model (clock
-// cycles at one workgroup per CU): per 512-wide super-tile a wave spends
-// max(4 x 8 NT MFMAs x 32, ~2500 load-bound) cycles; weights stream at
-// ~5 TB/s; split partials cost a write and a read of M x N x 4 bytes per split
-// at ~4 TB/s.
+// Pick the n-tiles per wave and the K split from a time model fitted to
+// measurements on MI355X (clock cycles at 2.4 GHz, one workgroup per CU): a
+// K128 stage costs about 1200 + 900 NT cycles (the stage copies, not the
+// MFMAs, set the pace); weights stream at ~5 TB/s; split partials cost a write
+// and a read of M x N x 4 bytes per split at ~3 TB/s.
 WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
   const int64_t KT = (K + kTileK - 1) / kTileK, MB = (M + 127) / 128;
   int o_nt, o_s;
@@ -383,7 +411,7 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
   double best_cost = 1e300;
   const double wbytes = (double)N * K * (fmt == kE4M3 ? 1.0 : 0.75) + (double)N * K / 32;
   const double hbm = (wbytes + (double)M * K * 1.04) / (5.0e12 / 2.4e9);
-  const int nts[2] = {2, 1};
+  const int nts[3] = {4, 2, 1};
   for (int nt : nts) {
     const int64_t NBk = (N + 64 * nt - 1) / (64 * nt);
     const int64_t tiles = MB * NBk;
@@ -391,9 +419,9 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
       const int64_t per = (KT + s - 1) / s;
       if ((KT + per - 1) / per != s) continue;
       const double rounds = (double)((tiles * s + 255) / 256);
-      const double t_st = 4.0 * 8 * nt * 32 > 2500.0 ? 4.0 * 8 * nt * 32 : 2500.0;
-      const double compute = rounds * per * t_st + 3000.0;
-      const double partial = s > 1 ? ((double)M * N * 4 * s * 2 + (double)M * N * 2) / (4.0e12 / 2.4e9) : 0.0;
+      const double t_stage = 1200.0 + 900.0 * nt;
+      const double compute = rounds * per * 4 * t_stage + 3000.0;
+      const double partial = s > 1 ? ((double)M * N * 4 * s * 2 + (double)M * N * 2) / (3.0e12 / 2.4e9) : 0.0;
       const double cost = (compute > hbm ? compute : hbm) + partial;
       if (cost < best_cost) {
         best_cost = cost;
@@ -412,7 +440,8 @@ bool wide_gemm_eligible(int64_t M, int64_t K) {
 template <int FMT, bool BLOCK, bool GROUPED>
 static hipError_t launch_wide_fmt(const WideConfig& c, const GemmParams& p, const WideGrid& g, int64_t grid,
                                   hipStream_t s) {
-  if (c.NT == 2) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 2, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
+  if (c.NT == 4) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 4, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
+  else if (c.NT == 2) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 2, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
   else if (c.NT == 1) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 1, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
   else return hipErrorInvalidValue;
   return hipGetLastError();
