@@ -143,11 +143,20 @@ def test_moe_graph_replay_changing_routes(pkg, oracle_mod, dev):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             run()
+        gen = torch.Generator(device=dev).manual_seed(77)
         for shift in range(3):
-            xd.normal_()
+            xd.normal_(generator=gen)
             idd.copy_(torch.tensor([[(j + shift) % E, (j + shift + 1) % E] for j in range(T)], dtype=torch.int32))
             graph.replay()
             stream.synchronize()
-            ref = oracle_mod.moe_ref(xd.cpu(), c13, s13, c2, s2, wd.cpu().numpy(), idd.cpu().numpy(), 2)
-            np.testing.assert_allclose(out.float().cpu().numpy(), oracle_mod.bf16_to_f32(ref), rtol=0.03, atol=0.03)
+            replayed = out.clone()
+            run()  # eager on the same inputs: the replay must match it bit for bit
+            stream.synchronize()
+            assert torch.equal(replayed, out)
+            # against the oracle: the bf16 gate_up intermediate may flip an MXFP8 code of
+            # the SwiGLU output, so the whole-layer bar is the relative one
+            ref = oracle_mod.bf16_to_f32(oracle_mod.moe_ref(xd.cpu(), c13, s13, c2, s2, wd.cpu().numpy(),
+                                                            idd.cpu().numpy(), 2))
+            got = replayed.float().cpu().numpy()
+            assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
     torch.cuda.current_stream().wait_stream(stream)

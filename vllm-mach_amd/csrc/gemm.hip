@@ -193,7 +193,7 @@ __global__ __launch_bounds__(MT == 1 && NT == 1 ? 1024 : 512) void gemm_kernel(G
     int64_t arow[MT], r4[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      int64_t row = rowbase + mt * 16 + r;
+      int64_t row = rowbase + mt * 16 + (lane >> 2);  // the row this lane loads (row-major loads)
       if (row >= hi) row = hi - 1;  // padding rows reuse a valid row; their outputs are not stored
       arow[mt] = (GROUPED && p.row_index) ? (int64_t)(p.row_index[row] / p.row_div) : row;
       r4[mt] = rowbase + mt * 16 + 4 * q;  // first output row held by this lane
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(MT == 1 && NT == 1 ? 1024 : 512) void gemm_kernel(G
       BTile<FMT, NT> B;
       ATile<MT> A;
       load_b<FMT, NT, BLOCK>(p, w, sw, ntile_ld, kt, lane, B);
-      load_a<MT, BLOCK>(p, arow, kt, q, A);
+      load_a<MT, BLOCK>(p, arow, kt, lane, A);
       compute_tile<FMT, MT, NT, BLOCK>(p, A, B, acc, kt, q, r4, hi, ntile_ld,
                                        BLOCK ? static_cast<const float*>(p.sw) : nullptr);
     }

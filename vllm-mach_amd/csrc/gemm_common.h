@@ -42,22 +42,38 @@ struct ATile {
 // Load the activation operands of one super-tile for MT 16-row tiles.  A
 // super-tile wholly inside K takes a branch-free path (a uniform condition),
 // so the loads are not waited on before the MFMAs that consume them.
+// The loads are row-major: `arow[mt]` is the row this lane reads, row lane / 4
+// of m-tile mt, piece lane % 4, so four neighbouring lanes move one row's 64
+// bytes in one access (lanes on sixteen rows, the fragment order, would cost an
+// access each); a lane-permute then hands fragment lane 16 q + r its piece q of
+// row r.
 template <int MT, bool BLOCK>
-__device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow)[MT], int64_t kt, int q,
+__device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow)[MT], int64_t kt, int lane,
                                        ATile<MT>& t) {
   const bool full = (kt + 1) * kTileK <= p.K;
+  const int cp = lane & 3, r = lane & 15, q = lane >> 4;
+  const int from = 4 * (4 * r + q);  // byte address of the source lane 4 r + q
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const uint8_t* base = p.a + arow[mt] * p.lda;
     const uint8_t* sbase = static_cast<const uint8_t*>(p.sa) + arow[mt] * (p.K / 32);
+    uint32_t sd = 0;
+    if (!BLOCK) {  // scale dword of slice cp (clamped inside K; slices past K are zeroed below)
+      const int64_t ks = kt * kTileK + 128 * cp;
+      sd = *reinterpret_cast<const uint32_t*>(sbase + (ks < p.K ? ks : p.K - 128) / 32);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t k0 = kt * kTileK + 128 * j;
       if (full || k0 < p.K) {
-        const uint4 lo = *reinterpret_cast<const uint4*>(base + k0 + 16 * q);
-        const uint4 hi = *reinterpret_cast<const uint4*>(base + k0 + 64 + 16 * q);
-        t.d[mt][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        if (!BLOCK) t.s[mt][j] = *reinterpret_cast<const uint32_t*>(sbase + kt * 16 + 4 * j);
+        const uint4 lo = *reinterpret_cast<const uint4*>(base + k0 + 16 * cp);
+        const uint4 hi = *reinterpret_cast<const uint4*>(base + k0 + 64 + 16 * cp);
+        const uint32_t x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        int y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = __builtin_amdgcn_ds_bpermute(from, (int)x[e]);
+        t.d[mt][j] = v8i{y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]};
+        t.s[mt][j] = BLOCK ? 0u : (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * r + j), (int)sd);
       } else {
         t.d[mt][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
         t.s[mt][j] = 0;

@@ -143,23 +143,41 @@ __global__ __launch_bounds__(RUN == 1 ? 1024 : 768) void gemm_stream_kernel(Gemm
   const int64_t count = g < ntiles ? (ntiles - g + G - 1) / G : 0;  // n-tiles of this workgroup
   StreamB<FMT, RUN> b0;
   stream_load_b<FMT, RUN>(p, w, sw, g < ntiles ? g : ntiles - 1, kt, lane, b0);
+  // The loads are row-major -- lane l reads piece l % 4 of row l / 4, so four
+  // neighbouring lanes move one row's 64 bytes in one access (lanes on sixteen
+  // rows, the fragment order, would cost an access each) -- and a lane-permute
+  // hands fragment lane 16 q + r its piece q of row r.
   v8i a[RUN][4];
   uint32_t sraw[RUN][4];
   {
-    const int64_t row = r < p.M ? r : p.M - 1;
+    const int cr = lane >> 2, cp = lane & 3;
+    const int64_t row = cr < p.M ? cr : p.M - 1;
     const uint8_t* srow = static_cast<const uint8_t*>(p.sa) + row * (p.K / 32);
     const uint8_t* arow = p.a + row * p.lda;
+    const int from = 4 * (4 * r + q);  // byte address of the source lane (4 r + q)
 #pragma unroll
-    for (int u = 0; u < RUN; ++u)
+    for (int u = 0; u < RUN; ++u) {
+      uint4 lo[4], hi[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int64_t k0 = kt[u] * kTileK + 128 * j;
         const int64_t kc = k0 < p.K ? k0 : p.K - 128;
-        const uint4 lo = *reinterpret_cast<const uint4*>(arow + kc + 16 * q);
-        const uint4 hi = *reinterpret_cast<const uint4*>(arow + kc + 64 + 16 * q);
-        a[u][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        sraw[u][j] = *reinterpret_cast<const uint32_t*>(srow + kc / 32);
+        lo[j] = *reinterpret_cast<const uint4*>(arow + kc + 16 * cp);
+        hi[j] = *reinterpret_cast<const uint4*>(arow + kc + 64 + 16 * cp);
       }
+      // scale dword of slice cp (E8M0 of blocks 4 cp .. 4 cp + 3 of the super-tile)
+      const int64_t ks = kt[u] * kTileK + 128 * cp;
+      const uint32_t sd = *reinterpret_cast<const uint32_t*>(srow + (ks < p.K ? ks : p.K - 128) / 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t x[8] = {lo[j].x, lo[j].y, lo[j].z, lo[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
+        int y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = __builtin_amdgcn_ds_bpermute(from, (int)x[e]);
+        a[u][j] = v8i{y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]};
+        sraw[u][j] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * r + j), (int)sd);
+      }
+    }
   }
   // slices past the end of K (the upper half of a K % 512 == 256 tail) contribute zero
   uint32_t sa[RUN][4];

@@ -10,9 +10,15 @@
 // registers) into a ring of K128 stage slots (four, or three for NT = 4 whose
 // 53 KiB stages would not fit four times), issued two or three stages ahead of
 // the MFMAs.  A slot holds
-//   A    8 m-tiles x 2 KiB in MFMA fragment order: chunk (m-tile i, half h) has
-//        at lane l = 16q + r the 16 bytes K [64 h + 16 q, +16) of row 16 i + r,
-//        so a fragment is two lane-contiguous 16-byte LDS reads;
+//   A    8 m-tiles x 2 KiB: chunk (m-tile i, half h) holds the 16 rows x 64 bytes
+//        K [64 h, +64) of rows 16 i .. 16 i + 15 row by row, the four 16-byte
+//        pieces of row r permuted by piece ^ a_swz(r).  The copy is row-major
+//        because the memory pipeline coalesces neighbouring lanes: four lanes
+//        reading one row's 64 bytes move them in one access, while lanes on
+//        sixteen different rows (MFMA fragment order) cost one access each --
+//        measured 10.8 vs 3.0 TB/s for this 16 x 64 B pattern.  The permutation
+//        keeps the fragment reads (lane 16 q + r: row r, piece q) free of LDS
+//        bank conflicts;
 //   B    per wave, its NT n-tiles' 2 KiB of the MFMA-tiled weight (copied
 //        verbatim: the tiled layout already is fragment order);
 //   SA   the activation scales of the 128 rows (E8M0 dword of blocks 4j..4j+3,
@@ -57,6 +63,12 @@ struct WideSlot {
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
+// Piece permutation of row r (0..15) of an A chunk: for every piece q the LDS
+// offsets 64 r + 16 (q ^ a_swz(r)) of rows 0..7 (8..15) are distinct modulo
+// 128 bytes, and those of rows 0..15 distinct modulo 256 bytes, so a 16-byte
+// fragment read meets no bank conflict with either 32 or 64 banks.
+__device__ __forceinline__ int a_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) { return (uint32_t)(uintptr_t)(const lds_u8*)p; }
 
 // Lane i copies 16 (4) bytes from base + voff to LDS [lds + 16 i] ([lds + 4 i]).
@@ -82,7 +94,7 @@ __device__ __forceinline__ void wide_barrier() { asm volatile("s_barrier" ::: "m
 
 template <int NT>
 struct WideLanes {
-  uint32_t a_off[2];  // row * lda + 16 q of the rows of m-tiles 2 wv, 2 wv + 1
+  uint32_t a_off[2];  // copy lane l of m-tiles 2 wv, 2 wv + 1: row (l / 4) * lda + 16 (l % 4 ^ a_swz(l / 4))
   uint32_t sa_off;    // MX: row * K/32; block-FP8: 4 row  (row = t % 128)
   const uint8_t* w_tile[NT];  // wave-uniform: tile (ntile, 0) of each of the wave's n-tiles
   const uint8_t* sw_tile[NT];
@@ -124,34 +136,23 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
   }
 }
 
-struct WideFrag {
-  v8i a;
-  uint32_t sd;  // MX: E8M0 dword of the fragment row (byte q is the lane's block)
-  float4 s4;    // block-FP8: fp32 scales of the lane's four output rows
+// Operands of one K128 stage, read from its ring slot into registers.
+template <int NT, bool BLOCK>
+struct WideRegs {
+  v8i a[8];          // A fragment of m-tile i
+  uint32_t sa[8];    // MX: E8M0 of the lane's block (row r of m-tile i, block q of the slice)
+  float4 s4[8];      // block-FP8: fp32 activation scales of the lane's four output rows of m-tile i
+  v8i b[NT];         // B fragment of the wave's n-tile n
+  uint32_t sb[NT];   // MX: E8M0 of the lane's weight row, block q of the slice
+  float sbv;         // block-FP8: the stage's weight block scale
 };
 
-template <int NT, bool BLOCK>
-__device__ __forceinline__ WideFrag wide_frag(const uint8_t* slot, int i, int lane, int q, int r) {
-  using S = WideSlot<NT, BLOCK>;
-  const uint8_t* fr = slot + S::A + i * 2048 + lane * 16;
-  const uint4 lo = *reinterpret_cast<const uint4*>(fr);
-  const uint4 hi = *reinterpret_cast<const uint4*>(fr + 1024);
-  WideFrag x;
-  x.a = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-  if (!BLOCK) x.sd = *reinterpret_cast<const uint32_t*>(slot + S::SA + (16 * i + r) * 4);
-  else x.s4 = *reinterpret_cast<const float4*>(slot + S::SA + (16 * i + 4 * q) * 4);
-  return x;
-}
-
-// The 8 x NT MFMAs of one K128 stage (slice j of its super-tile).  The E8M0
-// bytes are shifted into place (op_sel 0), since j is not a compile-time value
-// under a 3-slot ring.  Fragment reads run one m-tile ahead of the MFMAs.
+// Read stage operands (slice j of its super-tile) from a slot: B fragments
+// and scales first, then the eight A fragments in MFMA order.
 template <int FMT, int NT, bool BLOCK>
-__device__ __forceinline__ void wide_compute(const uint8_t* slot, int j, float sbv, v4f (&acc)[8][NT], int wv,
-                                             int lane, int q, int r) {
+__device__ __forceinline__ void wide_read(const uint8_t* slot, int j, int wv, int lane, int q, int r,
+                                          WideRegs<NT, BLOCK>& x) {
   using S = WideSlot<NT, BLOCK>;
-  v8i bf[NT];
-  uint32_t sb[NT];
   // FP6: the slice's 24 bytes start at byte 0 (even j) or 8 (odd j) of the first chunk
   const int odd = j & 1;
   const int o0 = 8 * odd, o1 = odd ? 1024 : 8, o2 = odd ? 1032 : 1024;
@@ -161,50 +162,100 @@ __device__ __forceinline__ void wide_compute(const uint8_t* slot, int j, float s
     if (FMT == kE4M3) {
       const uint4 lo = *reinterpret_cast<const uint4*>(base);
       const uint4 hi = *reinterpret_cast<const uint4*>(base + 1024);
-      bf[n] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      x.b[n] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     } else {
       const uint2 d0 = *reinterpret_cast<const uint2*>(base + o0);
       const uint2 d1 = *reinterpret_cast<const uint2*>(base + o1);
       const uint2 d2 = *reinterpret_cast<const uint2*>(base + o2);
-      bf[n] = v8i{(int)d0.x, (int)d0.y, (int)d1.x, (int)d1.y, (int)d2.x, (int)d2.y, 0, 0};
+      x.b[n] = v8i{(int)d0.x, (int)d0.y, (int)d1.x, (int)d1.y, (int)d2.x, (int)d2.y, 0, 0};
     }
-    if (!BLOCK) sb[n] = (*reinterpret_cast<const uint32_t*>(slot + S::SB + (wv * NT + n) * 256 + lane * 4) >> (8 * j)) & 0xFFu;
+    if (!BLOCK) x.sb[n] = slot[S::SB + (wv * NT + n) * 256 + lane * 4 + j];  // byte j: slice j
   }
-  WideFrag cur = wide_frag<NT, BLOCK>(slot, 0, lane, q, r);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    WideFrag nxt;
-    if (i < 7) nxt = wide_frag<NT, BLOCK>(slot, i + 1, lane, q, r);
-    if (!BLOCK) {
-      const uint32_t sa = (cur.sd >> (8 * q)) & 0xFFu;
-#pragma unroll
-      for (int n = 0; n < NT; ++n) acc[i][n] = mfma_step<FMT, 0>(cur.a, bf[n], acc[i][n], sa, sb[n]);
-    } else {
-      const float fs[4] = {cur.s4.x * sbv, cur.s4.y * sbv, cur.s4.z * sbv, cur.s4.w * sbv};
-#pragma unroll
-      for (int n = 0; n < NT; ++n) {
-        const v4f raw = mfma_raw<FMT>(cur.a, bf[n]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[i][n][e] = __builtin_fmaf(raw[e], fs[e], acc[i][n][e]);
-      }
-    }
-    if (i < 7) cur = nxt;
+    const uint8_t* fr = slot + S::A + i * 2048 + 16 * (4 * r + (q ^ a_swz(r)));
+    const uint4 lo = *reinterpret_cast<const uint4*>(fr);
+    const uint4 hi = *reinterpret_cast<const uint4*>(fr + 1024);
+    x.a[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    if (!BLOCK) x.sa[i] = slot[S::SA + (16 * i + r) * 4 + q];
+    else x.s4[i] = *reinterpret_cast<const float4*>(slot + S::SA + (16 * i + 4 * q) * 4);
   }
 }
 
-// Wait for this wave's copies of the current stage: the copies of the `later`
-// stages issued after it (C per stage, C + 1 for waves 0 and 1) may stay in flight.
-template <int C>
-__device__ __forceinline__ void wide_wait(int later, bool scales) {
-  if (scales) {
-    if (later >= 2) wait_vm<2 * (C + 1)>();
-    else if (later == 1) wait_vm<C + 1>();
-    else wait_vm<0>();
+// The 8 x NT MFMAs of one stage, from registers.  The E8M0 scales are single
+// bytes (op_sel 0), since the slice index is not a compile-time value under a
+// 3-slot ring.
+template <int FMT, int NT, bool BLOCK>
+__device__ __forceinline__ void wide_mfma(const WideRegs<NT, BLOCK>& x, v4f (&acc)[8][NT]) {
+  if (!BLOCK) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[i][n] = mfma_step<FMT, 0>(x.a[i], x.b[n], acc[i][n], x.sa[i], x.sb[n]);
   } else {
-    if (later >= 2) wait_vm<2 * C>();
-    else if (later == 1) wait_vm<C>();
-    else wait_vm<0>();
+    // block-FP8: each K128 product is folded with fma(raw, sa * sb, acc); the raw
+    // products of m-tile i + 1 are issued before the folds of m-tile i, so no
+    // fold waits on the MFMA just issued
+    v4f raw[2][NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) raw[0][n] = mfma_raw<FMT>(x.a[0], x.b[n]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i + 1 < 8) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) raw[(i + 1) & 1][n] = mfma_raw<FMT>(x.a[i + 1], x.b[n]);
+      }
+      const float fs[4] = {x.s4[i].x * x.sbv, x.s4[i].y * x.sbv, x.s4[i].z * x.sbv, x.s4[i].w * x.sbv};
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][n][e] = __builtin_fmaf(raw[i & 1][n][e], fs[e], acc[i][n][e]);
+    }
   }
+}
+
+// Scheduling groups for one step (MX): each MFMA followed by its share of the
+// next stage's LDS reads.  (Block-FP8 steps are left to the default schedule,
+// which measured faster than any grouping of their scale folds.)
+template <int FMT, int NT, bool BLOCK>
+__device__ __forceinline__ void wide_interleave() {
+  if (!BLOCK) {
+    constexpr int kMfma = 8 * NT;
+    constexpr int kReads = 16 + 8 + (FMT == kE4M3 ? 2 * NT : 3 * NT) + NT;
+    constexpr int kPer = (kReads + kMfma - 1) / kMfma;
+#pragma unroll
+    for (int k = 0; k < kMfma; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, kPer, 0);  // LDS reads
+    }
+  }
+}
+
+// Wait for this wave's copies of one stage: the copies of the `later` (at most
+// L) stages issued after it (C per stage, C + 1 for waves 0 and 1) may stay in
+// flight.
+template <int C, int L>
+__device__ __forceinline__ void wide_wait(int later, bool scales) {
+  if constexpr (L == 0) {
+    wait_vm<0>();
+  } else {
+    if (later >= L) {
+      if (scales) wait_vm<L * (C + 1)>();
+      else wait_vm<L * C>();
+    } else {
+      wide_wait<C, L - 1>(later, scales);
+    }
+  }
+}
+
+// RNE binary32 pair -> packed bf16 pair (v_cvt_pk_bf16_f32), NaN -> 0x7FC0 as f32_to_bf16.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, bf2));
+  if (lo != lo) u = (u & 0xFFFF0000u) | 0x7FC0u;
+  if (hi != hi) u = (u & 0x0000FFFFu) | 0x7FC00000u;
+  return u;
 }
 
 }  // namespace
@@ -219,12 +270,13 @@ struct WideGrid {
 template <int FMT, int NT, bool BLOCK, bool GROUPED>
 __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g) {
   using S = WideSlot<NT, BLOCK>;
-  // separate objects per slot (the LDS budget of one workgroup per CU; with
-  // three slots the fourth object is a 16-byte stub)
-  __shared__ __attribute__((aligned(16))) uint8_t slot0[S::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t slot1[S::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t slot2[S::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t slot3[S::SLOTS == 4 ? S::BYTES : 16];
+  // the stage ring (the LDS budget of one workgroup per CU); after the last
+  // stage it holds the output tile of the epilogue
+  __shared__ __attribute__((aligned(16))) uint8_t ring[S::SLOTS * S::BYTES];
+  uint8_t* const slot0 = ring;
+  uint8_t* const slot1 = ring + S::BYTES;
+  uint8_t* const slot2 = ring + 2 * S::BYTES;
+  uint8_t* const slot3 = ring + (S::SLOTS == 4 ? 3 : 0) * S::BYTES;  // unused with three slots
   __shared__ int64_t sh_scan[256];
   __shared__ int64_t sh_grp[3];
   constexpr int C = S::COPIES;
@@ -293,7 +345,10 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   constexpr int CH = FmtTraits<FMT>::CH;
   WideLanes<NT> L;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) L.a_off[i] = (uint32_t)(a_row(row_base + (2 * wv + i) * 16 + r) * p.lda + 16 * q);
+  for (int i = 0; i < 2; ++i) {
+    const int cr = lane >> 2;  // the row this lane copies (row-major chunk order)
+    L.a_off[i] = (uint32_t)(a_row(row_base + (2 * wv + i) * 16 + cr) * p.lda + 16 * ((lane & 3) ^ a_swz(cr)));
+  }
   L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & 127)) : a_row(row_base + (t & 127)) * (p.K / 32));  // t < 128 copy
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
@@ -319,63 +374,122 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
 
   if (tb < te) {
     constexpr int R = S::SLOTS;
-    // prologue: stages tb .. tb + R - 2
-    wide_copy<FMT, NT, BLOCK>(p, slot0, tb, wv, lane, L);
-    if (tb + 1 < te) wide_copy<FMT, NT, BLOCK>(p, slot1, tb + 1, wv, lane, L);
-    if (R == 4 && tb + 2 < te) wide_copy<FMT, NT, BLOCK>(p, slot2, tb + 2, wv, lane, L);
+    // prologue: stages tb .. tb + R - 1 fill the ring; stage tb is read into registers
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+      if (tb + k < te) wide_copy<FMT, NT, BLOCK>(p, ring + k * S::BYTES, tb + k, wv, lane, L);
+    wide_wait<C, R - 1>((int)(te - 1 - tb < R - 1 ? te - 1 - tb : R - 1), wv < 2);
+    wide_barrier();
+    WideRegs<NT, BLOCK> x0, x1;
+    wide_read<FMT, NT, BLOCK>(ring, (int)(tb & 3), wv, lane, q, r, x0);
+    if (BLOCK) x0.sbv = sbp[tb];
 
-// Step tt = t0 + I: wait for stage tt, barrier (the slot of tt - 1 is free),
-// copy stage tt + R - 1 into it, then the stage's MFMAs.
-#define MXL_WIDE_STEP(I_, SLOT_, NEXT_SLOT_)                                                       \
-  {                                                                                               \
-    const int64_t tt = t0 + I_;                                                                   \
-    if (tt < te) {                                                                                \
-      const int64_t later = te - 1 - tt < R - 2 ? te - 1 - tt : R - 2;                            \
-      wide_wait<C>((int)later, wv < 2);                                                           \
-      wide_barrier();                                                                             \
-      if (tt + R - 1 < te) wide_copy<FMT, NT, BLOCK>(p, NEXT_SLOT_, tt + R - 1, wv, lane, L);     \
-      wide_compute<FMT, NT, BLOCK>(SLOT_, (int)(tt & 3), BLOCK ? sbp[tt] : 0.f, acc, wv, lane, q, r); \
-    }                                                                                             \
+// Step tt = t0 + I (ring slot I % R): wait for stage tt + 1 and for this wave's
+// reads of stage tt, barrier (every wave holds stage tt in registers, so its slot
+// is free), copy stage tt + R into that slot, then the MFMAs of stage tt with the
+// LDS reads of stage tt + 1 (into the other register set) interleaved between
+// them: issued as one block, the reads would stall the wave's in-order issue on
+// the LDS queue and the MFMAs would only start once the last read is queued.
+// In the last step the reads fetch a stale slot and are never used.
+#define MXL_WIDE_STEP(I_, CUR_, NXT_)                                                                 \
+  {                                                                                                 \
+    const int64_t tt = t0 + I_;                                                                     \
+    if (tt < te) {                                                                                  \
+      if (tt + 1 < te) {                                                                            \
+        const int64_t later = te - 2 - tt < R - 2 ? te - 2 - tt : R - 2;                            \
+        wide_wait<C, R - 2>((int)later, wv < 2);                                                           \
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                          \
+        wide_barrier();                                                                             \
+        if (tt + R < te) wide_copy<FMT, NT, BLOCK>(p, ring + ((I_) % R) * S::BYTES, tt + R, wv, lane, L); \
+      }                                                                                             \
+      wide_read<FMT, NT, BLOCK>(ring + ((I_ + 1) % R) * S::BYTES, (int)((tt + 1) & 3), wv, lane, q, r, NXT_); \
+      if (BLOCK) NXT_.sbv = sbp[tt + 1 < te ? tt + 1 : tt];                                         \
+      wide_mfma<FMT, NT, BLOCK>(CUR_, acc);                                                         \
+      wide_interleave<FMT, NT, BLOCK>();                                                            \
+    }                                                                                               \
   }
 
     if (R == 4) {
       for (int64_t t0 = tb; t0 < te; t0 += 4) {
-        MXL_WIDE_STEP(0, slot0, slot3)
-        MXL_WIDE_STEP(1, slot1, slot0)
-        MXL_WIDE_STEP(2, slot2, slot1)
-        MXL_WIDE_STEP(3, slot3, slot2)
+        MXL_WIDE_STEP(0, x0, x1)
+        MXL_WIDE_STEP(1, x1, x0)
+        MXL_WIDE_STEP(2, x0, x1)
+        MXL_WIDE_STEP(3, x1, x0)
       }
     } else {
-      for (int64_t t0 = tb; t0 < te; t0 += 3) {
-        MXL_WIDE_STEP(0, slot0, slot2)
-        MXL_WIDE_STEP(1, slot1, slot0)
-        MXL_WIDE_STEP(2, slot2, slot1)
+      for (int64_t t0 = tb; t0 < te; t0 += 6) {
+        MXL_WIDE_STEP(0, x0, x1)
+        MXL_WIDE_STEP(1, x1, x0)
+        MXL_WIDE_STEP(2, x0, x1)
+        MXL_WIDE_STEP(3, x1, x0)
+        MXL_WIDE_STEP(4, x0, x1)
+        MXL_WIDE_STEP(5, x1, x0)
       }
     }
 #undef MXL_WIDE_STEP
   }
 
-  // epilogue: lane holds rows 4q + e, column r of each 16 x 16 tile
+  // Epilogue through LDS: the waves write their fp32 accumulators into a
+  // row-major 128 x 64 NT tile (row stride padded by 4 floats, so the 64 lanes
+  // of a write -- rows 4 q + e, column r -- hit 64 distinct banks), then all
+  // threads store whole 16-byte pieces of output rows.  Lane-scattered 2-byte
+  // stores straight from the accumulator layout would cost a store instruction
+  // per 64 values with 64-bit address arithmetic for each.
+  constexpr int TW = 64 * NT, ST = TW + 4;
+  static_assert(128 * ST * 4 <= S::SLOTS * S::BYTES, "epilogue tile exceeds the ring");
+  float* const tile = reinterpret_cast<float*>(ring);
+  wide_barrier();  // every wave is past its last fragment reads
 #pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    const int64_t nt = nt_wave + n;
-    const int64_t col = nt * 16 + r;
-    if (nt >= ntiles_total || col >= p.N) continue;
-    const float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.0f;
+  for (int n = 0; n < NT; ++n)
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t row = row_base + 16 * i + 4 * q + e;
-        if (row >= hi) continue;
-        if (p.S > 1) {
-          p.partial[(split * p.M + row) * p.N + col] = acc[i][n][e];
-        } else {
-          float y = bf16_round(acc[i][n][e]);
-          if (p.bias) y = y + bias;
-          p.out[row * p.ldc + col] = f32_to_bf16(y);
-        }
+      for (int e = 0; e < 4; ++e) tile[(16 * i + 4 * q + e) * ST + 16 * (wv * NT + n) + r] = acc[i][n][e];
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  const int64_t col0 = nb * TW;
+  if (p.S > 1) {  // fp32 partials, 4 columns per piece
+    const bool vec = p.N % 4 == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
+    for (int c = t; c < 128 * (TW / 4); c += 256) {
+      const int rr = c / (TW / 4), cc = (c % (TW / 4)) * 4;
+      const int64_t row = row_base + rr, col = col0 + cc;
+      if (row >= hi || col >= p.N) continue;
+      const float4 v = *reinterpret_cast<const float4*>(tile + rr * ST + cc);
+      float* dst = p.partial + (split * p.M + row) * p.N + col;
+      if (vec) {
+        *reinterpret_cast<float4*>(dst) = v;
+      } else {
+        const float f[4] = {v.x, v.y, v.z, v.w};
+        for (int k = 0; k < 4 && col + k < p.N; ++k) dst[k] = f[k];
       }
+    }
+  } else {  // bf16 out (bias added in bf16), 8 columns per piece
+    const bool vec = p.ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+    for (int c = t; c < 128 * (TW / 8); c += 256) {
+      const int rr = c / (TW / 8), cc = (c % (TW / 8)) * 8;
+      const int64_t row = row_base + rr, col = col0 + cc;
+      if (row >= hi || col >= p.N) continue;
+      const float4 v0 = *reinterpret_cast<const float4*>(tile + rr * ST + cc);
+      const float4 v1 = *reinterpret_cast<const float4*>(tile + rr * ST + cc + 4);
+      float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+      uint32_t h[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) h[k] = pack_bf16x2(f[2 * k], f[2 * k + 1]);
+      if (p.bias) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float y = u2f(k & 1 ? h[k >> 1] & 0xFFFF0000u : h[k >> 1] << 16);
+          f[k] = y + bf16_to_f32(p.bias[col + k < p.N ? col + k : p.N - 1]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) h[k] = pack_bf16x2(f[2 * k], f[2 * k + 1]);
+      }
+      uint16_t* dst = p.out + row * p.ldc + col;
+      if (vec && col + 8 <= p.N) {
+        *reinterpret_cast<uint4*>(dst) = uint4{h[0], h[1], h[2], h[3]};
+      } else {
+        for (int k = 0; k < 8 && col + k < p.N; ++k) dst[k] = (uint16_t)(k & 1 ? h[k >> 1] >> 16 : h[k >> 1]);
+      }
+    }
   }
 }
 
