@@ -65,6 +65,21 @@ int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K);
 int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int rule, int swizzled,
                      void* codes, void* scales, void* stream);
 
+/* Residual add + Gemma RMSNorm -> MXFP8 producer feeding gate_up: per row of N
+ * (32 <= N <= 16384, N % 32 == 0), x' = x + residual (fp32; residual may be
+ * null), summed = bf16(x') (written when residual is given), y = bf16((x' *
+ * rsqrt(mean(x'^2) + eps)) * (weight + 1)), then E4M3 codes [M, N] and E8M0
+ * scales of y per 32 (rule, logical [M, N/32] or swizzled as in
+ * mxl_swiglu_mxfp8).  The rsqrt is 1 / sqrt with IEEE sqrt and divide.
+ * Replaces _norm_quant / quantize (src/vllm_mach/mxfp6/mxfp8_norm_quant.py:15-49). */
+int mxl_rmsnorm_mxfp8(const void* x, const void* residual, const void* weight, int64_t M, int64_t N, float eps,
+                      int rule, int swizzled, void* codes, void* scales, void* summed, void* stream);
+
+/* The same residual add + Gemma RMSNorm with a bf16 output y [M, N] instead of
+ * MXFP8.  Replaces _norm / _impl (src/vllm_mach/mxfp6/gemma_norm.py:13-41). */
+int mxl_gemma_rmsnorm(const void* x, const void* residual, const void* weight, int64_t M, int64_t N, float eps,
+                      void* y, void* summed, void* stream);
+
 /* Per-token group-128 FP8 quantization: bf16 x [M, K] -> E4M3 q [M, K] +
  * fp32 scales column-major s[g * M + m].  Replaces _quantize_kernel.quantize_out
  * (src/vllm_mach/fp8/_quantize_kernel.py:7-25). */

@@ -72,6 +72,7 @@ def lib():
             "mxo_dequant_mx": (None, [P, P, I64, I64, I, P]),
             "mxo_moe_route": (None, [P, I64, I64, I64, P, P, P]),
             "mxo_moe_reduce": (None, [P, P, P, I64, I64, I64, P]),
+            "mxo_rmsnorm_mx": (None, [P, P, P, I64, I64, ctypes.c_float, I, P, P, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -181,6 +182,29 @@ def swiglu_mxfp8(gate_up, rule: int = RULE_CEIL_DIV448):
     scales = np.empty((R, K // 32), np.uint8)
     lib().mxo_swiglu_mxfp8(_p(b), R, K, rule, _p(codes), _p(scales))
     return codes, scales
+
+
+def rmsnorm_mx(x, residual, weight, eps: float, rule: int = RULE_CEIL_DIV448, quant: bool = True):
+    """Residual add + Gemma RMSNorm (+ MXFP8) per row (mxfp6/mxfp8_norm_quant.py:15-39,
+    mxfp6/gemma_norm.py:13-29).  x, residual bf16 [R, N] (residual may be None), weight
+    bf16 [N].  Returns (codes [R, N], logical scales [R, N/32], summed bf16 bits [R, N]) when
+    `quant`, else (y bf16 bits [R, N], summed bf16 bits [R, N])."""
+    xb = bf16_bits(x)
+    R, N = xb.shape
+    rb = bf16_bits(residual) if residual is not None else None
+    wb = bf16_bits(weight).reshape(-1)
+    assert wb.shape[0] == N and N % 32 == 0
+    summed = np.empty((R, N), np.uint16)
+    if quant:
+        codes = np.empty((R, N), np.uint8)
+        scales = np.empty((R, N // 32), np.uint8)
+        lib().mxo_rmsnorm_mx(_p(xb), _p(rb) if rb is not None else None, _p(wb), R, N, eps, rule,
+                             _p(codes), _p(scales), _p(summed), None)
+        return codes, scales, summed
+    y = np.empty((R, N), np.uint16)
+    lib().mxo_rmsnorm_mx(_p(xb), _p(rb) if rb is not None else None, _p(wb), R, N, eps, rule,
+                         None, None, _p(summed), _p(y))
+    return y, summed
 
 
 def swizzle_offset(r: int, g: int, K: int) -> int:

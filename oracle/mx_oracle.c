@@ -226,6 +226,69 @@ void mxo_swizzle_scales(const uint8_t* logical, int64_t rows, int64_t K, uint8_t
     for (int64_t g = 0; g < K / 32; ++g) out[mxo_swizzle_offset(r, g, K)] = logical[r * (K / 32) + g];
 }
 
+/* -------------------------------------------- residual + RMSNorm producer */
+
+/* Residual add + Gemma RMSNorm (+ MXFP8), mxfp6/mxfp8_norm_quant.py:15-39 and
+ * mxfp6/gemma_norm.py:13-29.  Per row of N (N % 32 == 0):
+ *   x      = f32(x) + f32(residual)        (no residual: x alone)
+ *   summed = bf16(x)                        (the residual output)
+ *   var    = (sum of x*x) / N               (sum order below)
+ *   r      = 1 / sqrtf(var + eps)           (IEEE sqrt and divide; the reference's
+ *                                            tl.rsqrt is an approximation that is not
+ *                                            restated, so r is this build's definition)
+ *   y      = bf16((x * r) * (f32(w) + 1))   (both products rounded, no FMA)
+ * then either the bf16 y (gemma_norm) or the MXFP8 codes and E8M0 scales of y per
+ * 32-block under `rule` (ceil_div448 in the reference, :27-33).
+ * Sum order of the variance -- the order of the HIP kernel, which is what makes
+ * the codes bit-exact: 256 workers; worker t owns the 8-element chunks
+ * c = t, t + 256, ... and accumulates x*x over its chunks in chunk and element
+ * order; the 64 workers of each group of 64 are combined as lane 0 of an xor
+ * butterfly with distances 32, 16, 8, 4, 2, 1; the 4 group sums are added in
+ * group order.                                                                  */
+static float rms_sum_order(const float* x, int64_t N) {
+  float part[256];
+  for (int t = 0; t < 256; ++t) {
+    float p = 0.0f;
+    for (int64_t c = t; c < N / 8; c += 256)
+      for (int k = 0; k < 8; ++k) p = p + x[c * 8 + k] * x[c * 8 + k];
+    part[t] = p;
+  }
+  float total = 0.0f;
+  for (int w = 0; w < 4; ++w) {
+    float a[64], b[64];
+    for (int l = 0; l < 64; ++l) a[l] = part[w * 64 + l];
+    for (int off = 32; off >= 1; off >>= 1) {
+      for (int l = 0; l < 64; ++l) b[l] = a[l] + a[l ^ off];
+      memcpy(a, b, sizeof a);
+    }
+    total = w == 0 ? a[0] : total + a[0];
+  }
+  return total;
+}
+
+void mxo_rmsnorm_mx(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, int64_t rows,
+                    int64_t N, float eps, int rule, uint8_t* codes, uint8_t* scales, uint16_t* summed,
+                    uint16_t* y_out) {
+  float* v = (float*)malloc(sizeof(float) * (size_t)N);
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t i = 0; i < N; ++i) {
+      float a = mxo_bf16_to_f32(x[r * N + i]);
+      if (residual) a = a + mxo_bf16_to_f32(residual[r * N + i]);
+      v[i] = a;
+      if (summed) summed[r * N + i] = mxo_f32_to_bf16(a);
+    }
+    const float var = rms_sum_order(v, N) / (float)N;
+    const float rs = 1.0f / sqrtf(var + eps);
+    for (int64_t i = 0; i < N; ++i) v[i] = bf16_round((v[i] * rs) * (mxo_bf16_to_f32(weight[i]) + 1.0f));
+    if (y_out) {
+      for (int64_t i = 0; i < N; ++i) y_out[r * N + i] = mxo_f32_to_bf16(v[i]);
+    } else {
+      for (int64_t b = 0; b < N / 32; ++b) quant_block32(v + b * 32, rule, codes + r * N + b * 32, scales + r * (N / 32) + b);
+    }
+  }
+  free(v);
+}
+
 /* ------------------------------------------------------------ block FP8 */
 
 /* Per-token group-128 activation quantization, fp8/_quantize_kernel.py:8-18:

@@ -20,6 +20,7 @@ LIB_PATH = Path(os.environ.get("MXLINEAR_LIBRARY_PATH", HERE / "libmxlinear.so")
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
+_F = ctypes.c_float
 
 # name -> (restype, argtypes); mirrors include/mxlinear.h
 SIGNATURES = {
@@ -30,6 +31,8 @@ SIGNATURES = {
     "mxl_quantize_mxfp6": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "mxl_swizzled_scale_bytes": (_I64, [_I64, _I64]),
     "mxl_swiglu_mxfp8": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P]),
+    "mxl_rmsnorm_mxfp8": (_I, [_P, _P, _P, _I64, _I64, _F, _I, _I, _P, _P, _P, _P]),
+    "mxl_gemma_rmsnorm": (_I, [_P, _P, _P, _I64, _I64, _F, _P, _P, _P]),
     "mxl_quantize_block_fp8": (_I, [_P, _I64, _I64, _P, _P, _P]),
     "mxl_silu_mul_block_fp8": (_I, [_P, _I64, _I64, _I, _P, _P, _P]),
     "mxl_tiled_weight_bytes": (_I64, [_I64, _I64, _I]),

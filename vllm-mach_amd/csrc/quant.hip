@@ -214,6 +214,89 @@ __global__ __launch_bounds__(256) void silu_mul_block_fp8_kernel(const uint16_t*
   if (sub == 0) scales[TRANSPOSED ? col * rows + row : row * (H / 128) + col] = scale;
 }
 
+// ------------------------------------------ residual + RMSNorm -> MXFP8
+
+// Residual add + Gemma RMSNorm, then MXFP8 (or bf16) of the normalized row
+// (mxfp6/mxfp8_norm_quant.py:15-39, mxfp6/gemma_norm.py:13-29).  One
+// workgroup of 256 threads per row of N (N % 32 == 0, N <= 16384): thread t
+// owns the 8-element chunks c = t, t + 256, ..., kept in registers between
+// the two passes.  The variance is summed in a fixed order -- serially per
+// thread, then lane 0 of an xor butterfly per wavefront, then the four
+// wavefronts in order -- so the codes are a pure function of the input.  A
+// 32-element block is four consecutive chunks held by four consecutive lanes
+// of one iteration (N / 8 is a multiple of 4, so a quad is live or dead as a
+// whole), quantized by quant8x4.
+constexpr int kNormMaxChunks = 8;
+
+template <bool QUANT, int RULE, bool SWIZZLED, bool RES>
+__global__ __launch_bounds__(256) void rmsnorm_mx_kernel(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ res,
+                                                         const uint16_t* __restrict__ weight, int64_t N,
+                                                         float eps, uint8_t* __restrict__ codes,
+                                                         uint8_t* __restrict__ scales,
+                                                         uint16_t* __restrict__ summed,
+                                                         uint16_t* __restrict__ y) {
+  __shared__ float wsum[4];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int64_t row = blockIdx.x;
+  const int64_t chunks = N / 8;
+  float v[kNormMaxChunks][8];
+  float part = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i) {
+    const int64_t c = t + 256 * i;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[i][k] = 0.0f;
+    if (c < chunks) {
+      bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * N + c * 8), v[i]);
+      if (RES) {
+        float r8[8];
+        bf16x8_to_f32(*reinterpret_cast<const uint4*>(res + row * N + c * 8), r8);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[i][k] = v[i][k] + r8[k];
+        uint32_t h[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) h[k] = f32_to_bf16(v[i][2 * k]) | (uint32_t)f32_to_bf16(v[i][2 * k + 1]) << 16;
+        *reinterpret_cast<uint4*>(summed + row * N + c * 8) = uint4{h[0], h[1], h[2], h[3]};
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) part = part + v[i][k] * v[i][k];
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
+  if (lane == 0) wsum[wv] = part;
+  __syncthreads();
+  const float total = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+  const float rs = 1.0f / __builtin_sqrtf(total / (float)N + eps);
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i) {
+    if (256 * i >= chunks) break;  // uniform
+    const int64_t c = t + 256 * i;
+    const bool live = c < chunks;
+    float w8[8], yv[8];
+    bf16x8_to_f32(*reinterpret_cast<const uint4*>(weight + (live ? c : 0) * 8), w8);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) yv[k] = bf16_round((v[i][k] * rs) * (w8[k] + 1.0f));
+    if (QUANT) {
+      uint32_t packed[2];
+      const uint32_t sc = quant8x4<RULE>(yv, packed);
+      if (!live) continue;
+      *reinterpret_cast<uint2*>(codes + row * N + c * 8) = make_uint2(packed[0], packed[1]);
+      if ((t & 3) == 0) {
+        const int64_t blk = c / 4;
+        if (SWIZZLED) scales[swizzle_offset(row, blk, N)] = (uint8_t)sc;
+        else scales[row * (N / 32) + blk] = (uint8_t)sc;
+      }
+    } else if (live) {
+      uint32_t h[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) h[k] = f32_to_bf16(yv[2 * k]) | (uint32_t)f32_to_bf16(yv[2 * k + 1]) << 16;
+      *reinterpret_cast<uint4*>(y + row * N + c * 8) = uint4{h[0], h[1], h[2], h[3]};
+    }
+  }
+}
+
 }  // namespace mxl
 
 // ------------------------------------------------------------------- C ABI
@@ -312,5 +395,67 @@ extern "C" int mxl_silu_mul_block_fp8(const void* input, int64_t rows, int64_t H
   else
     silu_mul_block_fp8_kernel<false><<<grid, 256, 0, s>>>((const uint16_t*)input, (uint8_t*)q, (float*)scales, rows, H);
   MXL_CHECK_LAUNCH("mxl_silu_mul_block_fp8");
+  return MXL_OK;
+}
+
+namespace {
+template <bool QUANT, int RULE, bool SWZ>
+void launch_rmsnorm(const void* x, const void* residual, const void* weight, int64_t M, int64_t N, float eps,
+                    void* codes, void* scales, void* summed, void* y, hipStream_t s) {
+  const dim3 grid((unsigned)M);
+  if (residual)
+    mxl::rmsnorm_mx_kernel<QUANT, RULE, SWZ, true><<<grid, 256, 0, s>>>(
+        (const uint16_t*)x, (const uint16_t*)residual, (const uint16_t*)weight, N, eps, (uint8_t*)codes,
+        (uint8_t*)scales, (uint16_t*)summed, (uint16_t*)y);
+  else
+    mxl::rmsnorm_mx_kernel<QUANT, RULE, SWZ, false><<<grid, 256, 0, s>>>(
+        (const uint16_t*)x, nullptr, (const uint16_t*)weight, N, eps, (uint8_t*)codes, (uint8_t*)scales,
+        nullptr, (uint16_t*)y);
+}
+
+int check_norm_args(const char* what, const void* x, const void* residual, const void* weight, int64_t M, int64_t N,
+                    const void* summed) {
+  MXL_CHECK_ARG(M >= 0 && N >= 32 && N % 32 == 0 && N <= 256 * 8 * mxl::kNormMaxChunks,
+                "%s: need 32 <= N <= %d, N %% 32 == 0 (N=%lld)", what, 256 * 8 * mxl::kNormMaxChunks, (long long)N);
+  MXL_CHECK_ARG(M <= 0x7FFFFFFF, "%s: too many rows (%lld)", what, (long long)M);
+  MXL_CHECK_ARG(aligned16(x) && aligned16(weight) && (!residual || aligned16(residual)),
+                "%s: x, residual and weight must be 16-byte aligned", what);
+  MXL_CHECK_ARG(!residual || (summed && aligned16(summed)), "%s: a residual needs a 16-byte aligned summed output",
+                what);
+  return MXL_OK;
+}
+}  // namespace
+
+extern "C" int mxl_rmsnorm_mxfp8(const void* x, const void* residual, const void* weight, int64_t M, int64_t N,
+                                 float eps, int rule, int swizzled, void* codes, void* scales, void* summed,
+                                 void* stream) {
+  int rc = check_norm_args("mxl_rmsnorm_mxfp8", x, residual, weight, M, N, summed);
+  if (rc != MXL_OK) return rc;
+  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_rmsnorm_mxfp8: unknown rule %d", rule);
+  MXL_CHECK_ARG(((uintptr_t)codes & 7) == 0, "mxl_rmsnorm_mxfp8: codes must be 8-byte aligned");
+  if (M == 0) return MXL_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (swizzled) {
+    const int64_t total = mxl_swizzled_scale_bytes(M, N);
+    mxl::swizzle_pad_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, s>>>((uint8_t*)scales, M, N, total);
+    if (rule == kFloorCarry175) launch_rmsnorm<true, kFloorCarry175, true>(x, residual, weight, M, N, eps, codes, scales, summed, nullptr, s);
+    else launch_rmsnorm<true, kCeilDiv448, true>(x, residual, weight, M, N, eps, codes, scales, summed, nullptr, s);
+  } else {
+    if (rule == kFloorCarry175) launch_rmsnorm<true, kFloorCarry175, false>(x, residual, weight, M, N, eps, codes, scales, summed, nullptr, s);
+    else launch_rmsnorm<true, kCeilDiv448, false>(x, residual, weight, M, N, eps, codes, scales, summed, nullptr, s);
+  }
+  MXL_CHECK_LAUNCH("mxl_rmsnorm_mxfp8");
+  return MXL_OK;
+}
+
+extern "C" int mxl_gemma_rmsnorm(const void* x, const void* residual, const void* weight, int64_t M, int64_t N,
+                                 float eps, void* y, void* summed, void* stream) {
+  int rc = check_norm_args("mxl_gemma_rmsnorm", x, residual, weight, M, N, summed);
+  if (rc != MXL_OK) return rc;
+  MXL_CHECK_ARG(aligned16(y), "mxl_gemma_rmsnorm: y must be 16-byte aligned");
+  if (M == 0) return MXL_OK;
+  launch_rmsnorm<false, kCeilDiv448, false>(x, residual, weight, M, N, eps, nullptr, nullptr, summed, y,
+                                            (hipStream_t)stream);
+  MXL_CHECK_LAUNCH("mxl_gemma_rmsnorm");
   return MXL_OK;
 }

@@ -161,6 +161,75 @@ def _(gate_up, rule=CEIL_DIV448, swizzled=False):
     return codes, gate_up.new_empty((M, K // 32), dtype=torch.uint8)
 
 
+def _norm_args(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor, what: str):
+    _check_cuda(x, weight, *([residual] if residual is not None else []))
+    if (x.dtype != torch.bfloat16 or x.ndim != 2 or weight.dtype != torch.bfloat16
+            or weight.numel() != x.shape[1] or (residual is not None and (residual.shape != x.shape
+                                                                          or residual.dtype != x.dtype))):
+        raise ValueError(f"{what} needs bf16 x [M, N], residual like x (or None) and bf16 weight [N]")
+    if x.shape[1] % 32 or not 32 <= x.shape[1] <= 16384:
+        raise ValueError(f"{what} needs 32 <= N <= 16384 with N % 32 == 0 (N={x.shape[1]})")
+    return x.contiguous(), residual.contiguous() if residual is not None else None, weight.contiguous()
+
+
+@torch.library.custom_op("mach_amd::rmsnorm_mxfp8", mutates_args=())
+def rmsnorm_mxfp8(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
+                  rule: int = CEIL_DIV448, swizzled: bool = True
+                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Residual add + Gemma RMSNorm -> MXFP8 producer (the contract of ``quantize``,
+    src/vllm_mach/mxfp6/mxfp8_norm_quant.py:42-55): returns (E4M3 [M, N], scales, summed
+    bf16 [M, N]).  Scales are the reference's swizzled buffer by default, logical [M, N/32]
+    with ``swizzled=False``.  Without a residual, summed is x itself.
+    """
+    x, residual, weight = _norm_args(x, residual, weight, "rmsnorm_mxfp8")
+    M, N = x.shape
+    codes = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x.device)
+    if swizzled:
+        scales = torch.empty((query("mxl_swizzled_scale_bytes", M, N),), dtype=torch.uint8, device=x.device)
+    else:
+        scales = torch.empty((M, N // 32), dtype=torch.uint8, device=x.device)
+    summed = torch.empty_like(x) if residual is not None else x.clone()
+    if M:
+        call("mxl_rmsnorm_mxfp8", ptr(x), ptr(residual), ptr(weight), M, N, float(eps), rule, int(swizzled),
+             ptr(codes), ptr(scales), ptr(summed) if residual is not None else None, stream_handle(x.device))
+    _count("rmsnorm_mxfp8")
+    return codes, scales, summed
+
+
+@rmsnorm_mxfp8.register_fake
+def _(x, residual, weight, eps, rule=CEIL_DIV448, swizzled=True):
+    M, N = x.shape
+    codes = x.new_empty((M, N), dtype=torch.float8_e4m3fn)
+    if swizzled:
+        rows = (M + 127) // 128 * 128
+        scales = x.new_empty((rows * ((N // 32 + 3) // 4) * 4,), dtype=torch.uint8)
+    else:
+        scales = x.new_empty((M, N // 32), dtype=torch.uint8)
+    return codes, scales, torch.empty_like(x)
+
+
+@torch.library.custom_op("mach_amd::gemma_rmsnorm", mutates_args=())
+def gemma_rmsnorm(x: torch.Tensor, residual: Optional[torch.Tensor], weight: torch.Tensor,
+                  eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Residual add + Gemma RMSNorm with a bf16 output (the contract of ``mach_gemma_norm``,
+    src/vllm_mach/mxfp6/gemma_norm.py:32-46): returns (y, summed); summed is empty [0]
+    without a residual, as in the reference."""
+    x, residual, weight = _norm_args(x, residual, weight, "gemma_rmsnorm")
+    M, N = x.shape
+    y = torch.empty_like(x)
+    summed = torch.empty_like(x) if residual is not None else x.new_empty((0,))
+    if M:
+        call("mxl_gemma_rmsnorm", ptr(x), ptr(residual), ptr(weight), M, N, float(eps), ptr(y),
+             ptr(summed) if residual is not None else None, stream_handle(x.device))
+    _count("gemma_rmsnorm")
+    return y, summed
+
+
+@gemma_rmsnorm.register_fake
+def _(x, residual, weight, eps):
+    return torch.empty_like(x), (torch.empty_like(x) if residual is not None else x.new_empty((0,)))
+
+
 @torch.library.custom_op("mach_amd::quantize_block_fp8", mutates_args=())
 def quantize_block_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-token group-128 FP8 quantization -> (E4M3 [M, K], fp32 [M, K/128] stride (1, M)).
@@ -306,6 +375,19 @@ def swiglu_mx_down(gate_up: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: 
         return gate_up.new_empty((0, n))
     a, sa = torch.ops.mach_amd.swiglu_mxfp8(gate_up, rule, False)
     return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, gate_up.shape[1] // 2, w_fmt, None)
+
+
+def norm_mx_gate_up(x: torch.Tensor, residual: Optional[torch.Tensor], norm_weight: torch.Tensor, eps: float,
+                    w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int = E4M3,
+                    rule: int = CEIL_DIV448) -> tuple[torch.Tensor, torch.Tensor]:
+    """Residual + Gemma RMSNorm -> MXFP8 producer then the gate_up GEMM; returns (gate_up,
+    summed) like ``mach_norm_quant_mxfp8_gate_up`` (src/vllm_mach/mxfp6/mxfp8_norm_quant.py:58-72).
+    The reference switches to an unquantized norm + float GEMM above 32 rows; here the
+    MXFP8 producer serves every M."""
+    a, sa, summed = torch.ops.mach_amd.rmsnorm_mxfp8(x, residual, norm_weight, eps, rule, False)
+    if x.shape[0] == 0:
+        return x.new_empty((0, n)), summed
+    return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, x.shape[1], w_fmt, None), summed
 
 
 @torch.library.custom_op("mach_amd::block_fp8_gemm", mutates_args=())
