@@ -27,9 +27,11 @@
 //   contiguous region.
 //
 // Activations stay row-major (the producers' natural layout and the gather
-// layout the MoE path needs): for MFMA j lane l loads row r's two 16-byte
-// pieces at K 512kt + 128j + 16q and + 64, and the dword of four E8M0 bytes
-// at block 16kt + 4j, keeping byte q.
+// layout the MoE path needs).  MFMA j needs, at lane l, row r's two 16-byte
+// pieces at K 512kt + 128j + 16q and + 64 and byte q of the E8M0 dword of
+// block 16kt + 4j; the loads are issued row by row (four neighbouring lanes
+// read one row's 64 bytes, which the memory pipeline serves as one access)
+// and a lane permute delivers each lane its pieces.
 //
 // Work split: a workgroup of KW wavefronts owns an MT x NT grid of 16x16
 // output tiles; its waves take interleaved 512-wide K super-tiles and their

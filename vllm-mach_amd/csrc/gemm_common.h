@@ -1,4 +1,4 @@
-// Declarations shared by the GEMM kernels (gemm.hip, gemm_lds.hip).
+// Declarations shared by the GEMM kernels (gemm.hip, gemm_wide.hip, gemm_stream.hip).
 #pragma once
 
 #include "mx_common.h"
