@@ -121,3 +121,39 @@ def test_stream_decode_gemm(pkg, oracle_mod, dev, M, N, K, fmt):
     ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)))
     ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().numpy()[None, :]))
     _check(y.float().cpu().numpy(), ref)
+
+
+def test_wide_split_repeat_and_replay(pkg, oracle_mod, dev, monkeypatch):
+    """K splits: repeated calls and graph replays (with eager calls between them) give
+    the same bits, since the partials are summed in split order."""
+    ops = pkg.ops
+    M, N, K = 300, 1024, 2304
+    monkeypatch.setenv("MXL_WIDE_CONFIG", "2,3")
+    wc, ws, stored = _weights(oracle_mod, N, K, 0, 0.02, 17)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), 0)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(_act(M, K, 5).to(dev), 0)
+    b = (torch.randn(N, generator=torch.Generator().manual_seed(2)) * 0.5).bfloat16().to(dev)
+
+    def run():
+        return torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, 0, b)
+
+    first = run()
+    for _ in range(3):
+        assert torch.equal(run(), first)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        run()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = run()
+        for _ in range(3):
+            graph.replay()
+            stream.synchronize()
+            assert torch.equal(out, first)
+            assert torch.equal(run(), first)  # eager between replays
+    torch.cuda.current_stream().wait_stream(stream)
+    rc, rs = oracle_mod.quant_mxfp8(_act(M, K, 5), 0)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, 0)))
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().cpu().numpy()[None, :]))
+    _check(first.float().cpu().numpy(), ref)

@@ -39,11 +39,12 @@ def inspect() -> dict:
                 "workspaces": {f"{d}:{s:#x}": t.numel() for (d, s), t in _workspaces.items()}}
 
 
-def workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
-    """Per-(device, stream) scratch of at least ``nbytes``; never reallocated during capture."""
+def workspace(device: torch.device, nbytes: int, kind: str = "gemm") -> Optional[torch.Tensor]:
+    """Per-(device, stream, kind) scratch of at least ``nbytes``; never reallocated during
+    capture."""
     if nbytes <= 0:
         return None
-    key = (device.index, stream_handle(device))
+    key = (device.index, stream_handle(device), kind)
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
@@ -441,7 +442,7 @@ def moe_route(topk_ids: torch.Tensor, num_experts: int) -> tuple[torch.Tensor, t
     offsets = torch.empty(num_experts + 1, dtype=torch.int64, device=dev)
     inverse = torch.empty(R, dtype=torch.int32, device=dev)
     nbytes = query("mxl_moe_route_workspace_bytes", T, topk, num_experts)
-    buf = workspace(dev, nbytes)
+    buf = workspace(dev, nbytes, "route")
     call("mxl_moe_route", ptr(ids), T, topk, num_experts, ptr(sorted_routes), ptr(offsets), ptr(inverse),
          ptr(buf), nbytes, stream_handle(dev))
     _count("moe_route")
