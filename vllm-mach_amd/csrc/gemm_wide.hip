@@ -51,10 +51,14 @@ namespace {
 
 template <int NT, bool BLOCK>
 struct WideSlot {
+  // MX with NT <= 2: the activation scales live in a separate ring of three
+  // super-tile entries (128 rows x 16 bytes), filled a super-tile ahead, so a
+  // copy moves 16 bytes per row instead of one dword from each of 128 rows.
+  static constexpr bool SA_RING = !BLOCK && NT <= 2;
   static constexpr int A = 0;                          // 16 KiB
   static constexpr int B = 16 * 1024;                  // wave w: NT x 2 KiB at B + w NT 2 KiB
-  static constexpr int SA = B + 4 * NT * 2048;         // 512 B, copied by waves 0 and 1
-  static constexpr int SB = SA + 512;                  // wave w: NT x 256 B (MX)
+  static constexpr int SA = B + 4 * NT * 2048;         // 512 B, copied by waves 0 and 1 (no ring)
+  static constexpr int SB = SA + (SA_RING ? 0 : 512);  // wave w: NT x 256 B (MX)
   static constexpr int BYTES = SB + (BLOCK ? 0 : 4 * NT * 256);
   static constexpr int SLOTS = NT == 4 ? 3 : 4;        // 4 x 53 KiB would not fit the LDS
   // copies per wave per stage (waves 0 and 1 also copy the activation scales)
@@ -96,14 +100,20 @@ template <int NT>
 struct WideLanes {
   uint32_t a_off[2];  // copy lane l of m-tiles 2 wv, 2 wv + 1: row (l / 4) * lda + 16 (l % 4 ^ a_swz(l / 4))
   uint32_t sa_off;    // MX: row * K/32; block-FP8: 4 row  (row = t % 128)
+  uint32_t sa_piece[4];  // scale ring: lane l of wave w (0, 1) reads dword l % 4 of row 32 j + 16 w + l / 4
+  uint32_t sa_last[4];   // the same for the last super-tile when it is half (K % 512 = 256), from p.sa and
+                         // clamped inside the row (its dwords 2, 3 would lie past the row)
   const uint8_t* w_tile[NT];  // wave-uniform: tile (ntile, 0) of each of the wave's n-tiles
   const uint8_t* sw_tile[NT];
 };
 
-// Copy K128 stage `t` (super-tile t / 4, slice j = t % 4) into a slot.
+// Copy K128 stage `t` (super-tile t / 4, slice j = t % 4) into a slot; with
+// the scale ring, waves 0 and 1 also copy piece j (32 rows) of the next
+// super-tile's activation scales (clamped inside K: a piece past the last
+// super-tile is never read).
 template <int FMT, int NT, bool BLOCK>
 __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, int64_t t, int wv, int lane,
-                                          const WideLanes<NT>& L) {
+                                          const WideLanes<NT>& L, uint8_t* sa_ring) {
   using S = WideSlot<NT, BLOCK>;
   constexpr int CH = FmtTraits<FMT>::CH;
   const int64_t kt = t >> 2;
@@ -123,7 +133,14 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
     for (int c2 = 0; c2 < 2; ++c2)
       copy16(tile + c2 * 1024, (uint32_t)(lane * 16), lds_addr(slot + S::B + ((wv * NT + n) * 2 + c2) * 1024));
   }
-  if (wv < 2) {  // activation scales of the 128 rows (row = t % 128 of waves 0, 1)
+  if (S::SA_RING) {
+    if (wv < 2) {
+      const int64_t ks = kt + 1 < p.KT ? kt + 1 : p.KT - 1;
+      const uint32_t dst = lds_addr(sa_ring + ((kt + 1) % 3) * 2048 + (32 * j + 16 * wv) * 16);
+      if (ks == p.KT - 1 && p.K % kTileK != 0) copy4(static_cast<const uint8_t*>(p.sa), L.sa_last[j], dst);
+      else copy4(static_cast<const uint8_t*>(p.sa) + ks * 16, L.sa_piece[j], dst);
+    }
+  } else if (wv < 2) {  // activation scales of the 128 rows (row = t % 128 of waves 0, 1)
     if (!BLOCK)  // E8M0 bytes of blocks 4t .. 4t + 3
       copy4(static_cast<const uint8_t*>(p.sa) + t * 4, L.sa_off, lds_addr(slot + S::SA + wv * 256));
     else  // fp32 scale of K128 group t (column-major [K/128, M])
@@ -150,8 +167,8 @@ struct WideRegs {
 // Read stage operands (slice j of its super-tile) from a slot: B fragments
 // and scales first, then the eight A fragments in MFMA order.
 template <int FMT, int NT, bool BLOCK>
-__device__ __forceinline__ void wide_read(const uint8_t* slot, int j, int wv, int lane, int q, int r,
-                                          WideRegs<NT, BLOCK>& x) {
+__device__ __forceinline__ void wide_read(const uint8_t* slot, const uint8_t* sa_entry, int j, int wv, int lane,
+                                          int q, int r, WideRegs<NT, BLOCK>& x) {
   using S = WideSlot<NT, BLOCK>;
   // FP6: the slice's 24 bytes start at byte 0 (even j) or 8 (odd j) of the first chunk
   const int odd = j & 1;
@@ -177,7 +194,8 @@ __device__ __forceinline__ void wide_read(const uint8_t* slot, int j, int wv, in
     const uint4 lo = *reinterpret_cast<const uint4*>(fr);
     const uint4 hi = *reinterpret_cast<const uint4*>(fr + 1024);
     x.a[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    if (!BLOCK) x.sa[i] = slot[S::SA + (16 * i + r) * 4 + q];
+    if (S::SA_RING) x.sa[i] = sa_entry[(16 * i + r) * 16 + 4 * j + q];
+    else if (!BLOCK) x.sa[i] = slot[S::SA + (16 * i + r) * 4 + q];
     else x.s4[i] = *reinterpret_cast<const float4*>(slot + S::SA + (16 * i + 4 * q) * 4);
   }
 }
@@ -277,6 +295,7 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   uint8_t* const slot1 = ring + S::BYTES;
   uint8_t* const slot2 = ring + 2 * S::BYTES;
   uint8_t* const slot3 = ring + (S::SLOTS == 4 ? 3 : 0) * S::BYTES;  // unused with three slots
+  __shared__ __attribute__((aligned(16))) uint8_t sa_ring[S::SA_RING ? 3 * 2048 : 16];
   __shared__ int64_t sh_scan[256];
   __shared__ int64_t sh_grp[3];
   constexpr int C = S::COPIES;
@@ -351,6 +370,13 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   }
   L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & 127)) : a_row(row_base + (t & 127)) * (p.K / 32));  // t < 128 copy
 #pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t srow = a_row(row_base + 32 * j + 16 * (wv & 1) + (lane >> 2)) * (p.K / 32);
+    L.sa_piece[j] = (uint32_t)(srow + 4 * (lane & 3));
+    const int64_t last = 16 * (p.KT - 1) + 4 * (lane & 3);
+    L.sa_last[j] = (uint32_t)(srow + (last < p.K / 32 - 4 ? last : p.K / 32 - 4));
+  }
+#pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int64_t nt = nt_wave + n < ntiles_total ? nt_wave + n : ntiles_total - 1;
     L.w_tile[n] = w + nt * p.KT * (CH * 1024);
@@ -374,14 +400,24 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
 
   if (tb < te) {
     constexpr int R = S::SLOTS;
-    // prologue: stages tb .. tb + R - 1 fill the ring; stage tb is read into registers
+    // prologue: the scale ring entry of the first super-tile; stages tb .. tb + R - 1
+    // fill the ring; stage tb is read into registers
+    if (S::SA_RING && wv < 2) {
+      const bool half = (tb >> 2) == p.KT - 1 && p.K % kTileK != 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t dst = lds_addr(sa_ring + ((tb >> 2) % 3) * 2048 + (32 * j + 16 * wv) * 16);
+        if (half) copy4(static_cast<const uint8_t*>(p.sa), L.sa_last[j], dst);
+        else copy4(static_cast<const uint8_t*>(p.sa) + (tb >> 2) * 16, L.sa_piece[j], dst);
+      }
+    }
 #pragma unroll
     for (int k = 0; k < R; ++k)
-      if (tb + k < te) wide_copy<FMT, NT, BLOCK>(p, ring + k * S::BYTES, tb + k, wv, lane, L);
+      if (tb + k < te) wide_copy<FMT, NT, BLOCK>(p, ring + k * S::BYTES, tb + k, wv, lane, L, sa_ring);
     wide_wait<C, R - 1>((int)(te - 1 - tb < R - 1 ? te - 1 - tb : R - 1), wv < 2);
     wide_barrier();
     WideRegs<NT, BLOCK> x0, x1;
-    wide_read<FMT, NT, BLOCK>(ring, (int)(tb & 3), wv, lane, q, r, x0);
+    wide_read<FMT, NT, BLOCK>(ring, sa_ring + ((tb >> 2) % 3) * 2048, (int)(tb & 3), wv, lane, q, r, x0);
     if (BLOCK) x0.sbv = sbp[tb];
 
 // Step tt = t0 + I (ring slot I % R): wait for stage tt + 1 and for this wave's
@@ -400,9 +436,10 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
         wide_wait<C, R - 2>((int)later, wv < 2);                                                           \
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                          \
         wide_barrier();                                                                             \
-        if (tt + R < te) wide_copy<FMT, NT, BLOCK>(p, ring + ((I_) % R) * S::BYTES, tt + R, wv, lane, L); \
+        if (tt + R < te) wide_copy<FMT, NT, BLOCK>(p, ring + ((I_) % R) * S::BYTES, tt + R, wv, lane, L, sa_ring); \
       }                                                                                             \
-      wide_read<FMT, NT, BLOCK>(ring + ((I_ + 1) % R) * S::BYTES, (int)((tt + 1) & 3), wv, lane, q, r, NXT_); \
+      wide_read<FMT, NT, BLOCK>(ring + ((I_ + 1) % R) * S::BYTES, sa_ring + (((tt + 1) >> 2) % 3) * 2048,  \
+                                (int)((tt + 1) & 3), wv, lane, q, r, NXT_);                         \
       if (BLOCK) NXT_.sbv = sbp[tt + 1 < te ? tt + 1 : tt];                                         \
       wide_mfma<FMT, NT, BLOCK>(CUR_, acc);                                                         \
       wide_interleave<FMT, NT, BLOCK>();                                                            \
