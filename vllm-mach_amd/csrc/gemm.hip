@@ -449,7 +449,8 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
                 "mxl_grouped_gemm: need N > 0, K %% 128 == 0, experts > 0");
   MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0, "mxl_grouped_gemm: misaligned operands");
   if (routed_rows == 0) return MXL_OK;
-  if (K % 256 == 0 && routed_rows >= 32 * num_experts && a_rows * K < (int64_t(1) << 32)) {
+  if (K % 256 == 0 && routed_rows >= 32 * num_experts && a_rows * K < (int64_t(1) << 32) &&
+      num_experts <= kWideGroupedMaxExperts) {
     // enough rows per expert on average for 128-row blocks: the wide kernel
     GemmParams p{};
     p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;

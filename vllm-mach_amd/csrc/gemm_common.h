@@ -139,6 +139,9 @@ struct WideConfig {
 };
 WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt);
 bool wide_gemm_eligible(int64_t M, int64_t K);
+// Grouped wide kernel: at most this many experts (their prefix lives in LDS).
+constexpr int64_t kWideGroupedMaxExperts = 1024;
+int cu_count();
 hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const GemmParams& p, int64_t num_experts,
                             hipStream_t s);
 

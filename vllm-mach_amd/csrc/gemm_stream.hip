@@ -241,7 +241,7 @@ bool stream_gemm_eligible(int64_t M, int64_t K) {
   return M >= 1 && M <= 16 && K % 128 == 0 && K >= 128 && K <= kStreamMaxK;
 }
 
-namespace {
+// Compute units of the current device (cached per device).
 int cu_count() {
   static int cached[64] = {0};
   int dev = 0;
@@ -254,6 +254,7 @@ int cu_count() {
   return cached[dev];
 }
 
+namespace {
 template <int FMT>
 hipError_t launch_stream_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
   if (p.KT <= kStreamMaxWaves) {

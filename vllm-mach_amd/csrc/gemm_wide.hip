@@ -285,76 +285,15 @@ struct WideGrid {
   int64_t num_experts;   // grouped only
 };
 
+// One output tile: rows [row_base, hi) of m-block rows (hi bounds the valid rows
+// of a grouped expert), n-block nb, K split `split`; w / sw are the expert's
+// weights.  The ring and the scale ring are the workgroup's LDS.
 template <int FMT, int NT, bool BLOCK, bool GROUPED>
-__global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g) {
+__device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g, int64_t mb, int64_t row_base,
+                                          int64_t hi, const uint8_t* w, const uint8_t* sw, int64_t nb, int64_t split,
+                                          uint8_t* ring, uint8_t* sa_ring, int t, int lane, int wv, int r, int q) {
   using S = WideSlot<NT, BLOCK>;
-  // the stage ring (the LDS budget of one workgroup per CU); after the last
-  // stage it holds the output tile of the epilogue
-  __shared__ __attribute__((aligned(16))) uint8_t ring[S::SLOTS * S::BYTES];
-  uint8_t* const slot0 = ring;
-  uint8_t* const slot1 = ring + S::BYTES;
-  uint8_t* const slot2 = ring + 2 * S::BYTES;
-  uint8_t* const slot3 = ring + (S::SLOTS == 4 ? 3 : 0) * S::BYTES;  // unused with three slots
-  __shared__ __attribute__((aligned(16))) uint8_t sa_ring[S::SA_RING ? 3 * 2048 : 16];
-  __shared__ int64_t sh_scan[256];
-  __shared__ int64_t sh_grp[3];
   constexpr int C = S::COPIES;
-
-  const int t = threadIdx.x, lane = t & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int r = lane & 15, q = lane >> 4;
-
-  // XCD-aware remap of the linear workgroup id
-  const int64_t G = gridDim.x, Lid = blockIdx.x;
-  const int64_t xcd = Lid & 7, per = G >> 3, extra = G & 7;
-  const int64_t logical = xcd * per + (xcd < extra ? xcd : extra) + (Lid >> 3);
-  const int64_t mb = logical % g.mblocks;
-  const int64_t rest = logical / g.mblocks;
-  const int64_t nb = rest % g.nblocks;
-  const int64_t split = rest / g.nblocks;
-
-  int64_t row_base = mb * 128, hi = p.M;
-  const uint8_t* w = p.w;
-  const uint8_t* sw = static_cast<const uint8_t*>(p.sw);
-  if (GROUPED) {
-    // find the expert whose m-blocks contain global m-block `mb`
-    const int64_t E = g.num_experts;
-    const int64_t chunk = (E + 255) / 256;
-    const int64_t e0 = t * chunk < E ? t * chunk : E, e1 = e0 + chunk < E ? e0 + chunk : E;
-    int64_t cnt = 0;
-    for (int64_t e = e0; e < e1; ++e) cnt += (p.expert_offsets[e + 1] - p.expert_offsets[e] + 127) / 128;
-    sh_scan[t] = cnt;
-    if (t == 0) sh_grp[0] = -1;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-      const int64_t v = t >= off ? sh_scan[t - off] : 0;
-      __syncthreads();
-      sh_scan[t] += v;
-      __syncthreads();
-    }
-    int64_t base = sh_scan[t] - cnt;  // exclusive prefix
-    if (mb >= base && mb < base + cnt) {
-      for (int64_t e = e0; e < e1; ++e) {
-        const int64_t lo_e = p.expert_offsets[e], hi_e = p.expert_offsets[e + 1];
-        const int64_t nbk = (hi_e - lo_e + 127) / 128;
-        if (mb < base + nbk) {
-          sh_grp[0] = e;
-          sh_grp[1] = lo_e + (mb - base) * 128;
-          sh_grp[2] = hi_e;
-          break;
-        }
-        base += nbk;
-      }
-    }
-    __syncthreads();
-    if (sh_grp[0] < 0) return;  // beyond the routed m-blocks (uniform)
-    const int64_t e = __builtin_amdgcn_readfirstlane((int)sh_grp[0]);
-    w += e * p.w_expert_stride;
-    sw += e * p.sw_expert_stride;
-    row_base = sh_grp[1];
-    hi = sh_grp[2];
-  }
-
   auto a_row = [&](int64_t row) -> int64_t {
     if (row >= hi) row = hi - 1;  // padding rows copy a valid row; their outputs are not stored
     return (GROUPED && p.row_index) ? (int64_t)(p.row_index[row] / p.row_div) : row;
@@ -530,6 +469,88 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   }
 }
 
+// Largest number of experts the grouped variant keeps in LDS.
+constexpr int kWideMaxExperts = (int)kWideGroupedMaxExperts;
+
+template <int FMT, int NT, bool BLOCK, bool GROUPED>
+__global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g) {
+  using S = WideSlot<NT, BLOCK>;
+  // the stage ring (the LDS budget of one workgroup per CU); after the last
+  // stage it holds the output tile of the epilogue
+  __shared__ __attribute__((aligned(16))) uint8_t ring[S::SLOTS * S::BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t sa_ring[S::SA_RING ? 3 * 2048 : 16];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int r = lane & 15, q = lane >> 4;
+
+  if (!GROUPED) {
+    // XCD-aware remap of the linear workgroup id: the m-blocks sharing a weight
+    // slice run consecutively on one XCD (workgroup L runs on XCD L % 8)
+    const int64_t G = gridDim.x, Lid = blockIdx.x;
+    const int64_t xcd = Lid & 7, per = G >> 3, extra = G & 7;
+    const int64_t logical = xcd * per + (xcd < extra ? xcd : extra) + (Lid >> 3);
+    const int64_t mb = logical % g.mblocks;
+    const int64_t rest = logical / g.mblocks;
+    wide_tile<FMT, NT, BLOCK, GROUPED>(p, g, mb, mb * 128, p.M, p.w, static_cast<const uint8_t*>(p.sw),
+                                       rest % g.nblocks, rest / g.nblocks, ring, sa_ring, t, lane, wv, r, q);
+    return;
+  }
+
+  // Grouped: persistent workgroups.  The experts' 128-row block counts are
+  // prefix-summed once per workgroup into LDS; each workgroup then walks the
+  // tiles L = blockIdx, blockIdx + grid, ... of the (m-block bound x n-block)
+  // grid (the same XCD remap, so a workgroup stays on its XCD's tiles) and
+  // finds its expert by a parallel search of the prefix.
+  __shared__ int32_t sh_pre[kWideMaxExperts + 1];   // m-blocks before expert e
+  __shared__ int32_t sh_row[kWideMaxExperts + 1];   // expert_offsets
+  __shared__ int32_t sh_hit;
+  const int E = (int)g.num_experts;
+  for (int e = t; e <= E; e += 256) sh_row[e] = (int32_t)p.expert_offsets[e];
+  __syncthreads();
+  // block counts per thread chunk, then a block-wide inclusive scan of the chunk sums
+  const int chunk = (E + 255) / 256;
+  const int e0 = t * chunk < E ? t * chunk : E, e1 = e0 + chunk < E ? e0 + chunk : E;
+  int cnt = 0;
+  for (int e = e0; e < e1; ++e) cnt += (sh_row[e + 1] - sh_row[e] + 127) / 128;
+  __shared__ int32_t sh_scan[256];
+  sh_scan[t] = cnt;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int v = t >= off ? sh_scan[t - off] : 0;
+    __syncthreads();
+    sh_scan[t] += v;
+    __syncthreads();
+  }
+  int base = sh_scan[t] - cnt;  // exclusive prefix of this thread's chunk
+  for (int e = e0; e < e1; ++e) {
+    sh_pre[e] = base;
+    base += (sh_row[e + 1] - sh_row[e] + 127) / 128;
+  }
+  if (t == 255) sh_pre[E] = sh_scan[255];
+  __syncthreads();
+  const int64_t total_mb = sh_pre[E];
+  const int64_t Gt = g.mblocks * g.nblocks;  // the launch bound on tiles
+  const int64_t per = Gt >> 3, extra = Gt & 7;
+  for (int64_t Lid = blockIdx.x; Lid < Gt; Lid += gridDim.x) {
+    const int64_t xcd = Lid & 7;
+    const int64_t logical = xcd * per + (xcd < extra ? xcd : extra) + (Lid >> 3);
+    const int64_t mb = logical % g.mblocks;
+    const int64_t nb = logical / g.mblocks;
+    if (mb >= total_mb) continue;  // beyond the routed m-blocks (uniform)
+    if (t == 0) sh_hit = 0;
+    __syncthreads();
+    for (int e = t; e < E; e += 256)
+      if (sh_pre[e] <= mb && mb < sh_pre[e + 1]) sh_hit = e;
+    __syncthreads();
+    const int e = __builtin_amdgcn_readfirstlane(sh_hit);
+    wide_tile<FMT, NT, BLOCK, GROUPED>(p, g, mb, sh_row[e] + (mb - sh_pre[e]) * 128, sh_row[e + 1],
+                                       p.w + e * p.w_expert_stride,
+                                       static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride, nb, 0, ring,
+                                       sa_ring, t, lane, wv, r, q);
+    __syncthreads();  // the epilogue's LDS reads are done before the next tile's copies
+  }
+}
+
 // ------------------------------------------------------------ configuration
 
 namespace {
@@ -591,7 +612,10 @@ bool wide_gemm_eligible(int64_t M, int64_t K) {
 template <int FMT, bool BLOCK, bool GROUPED>
 static hipError_t launch_wide_fmt(const WideConfig& c, const GemmParams& p, const WideGrid& g, int64_t grid,
                                   hipStream_t s) {
-  if (c.NT == 4) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 4, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
+  if (c.NT == 4) {
+    if constexpr (GROUPED) return hipErrorInvalidValue;  // the grouped variant runs NT <= 2 (LDS)
+    else hipLaunchKernelGGL((gemm_wide_kernel<FMT, 4, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
+  }
   else if (c.NT == 2) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 2, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
   else if (c.NT == 1) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 1, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
   else return hipErrorInvalidValue;
@@ -606,8 +630,9 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
   g.num_experts = num_experts;
   int64_t grid;
   if (num_experts > 0) {
-    g.mblocks = (p.M + 127) / 128 + num_experts;
+    g.mblocks = (p.M + 127) / 128 + num_experts;  // bound on the routed m-blocks
     grid = g.mblocks * g.nblocks;
+    if (grid > cu_count()) grid = cu_count();     // persistent workgroups walk the tiles
     if (fmt == kE4M3) return launch_wide_fmt<kE4M3, false, true>(c, p, g, grid, s);
     if (fmt == kE2M3) return launch_wide_fmt<kE2M3, false, true>(c, p, g, grid, s);
     if (fmt == kE3M2) return launch_wide_fmt<kE3M2, false, true>(c, p, g, grid, s);
