@@ -80,6 +80,14 @@ int mxl_rmsnorm_mxfp8(const void* x, const void* residual, const void* weight, i
 int mxl_gemma_rmsnorm(const void* x, const void* residual, const void* weight, int64_t M, int64_t N, float eps,
                       void* y, void* summed, void* stream);
 
+/* Two-limb MXFP8 activations: per 32-block, hi = MXFP8(x) under `rule`, the
+ * residual r = bf16(x - dequant(hi)), res = MXFP8(r) under the same rule; codes
+ * [M, K] and logical scales [M, K/32] for each limb.  The contract of the
+ * reference's dual quantizer (src/vllm_mach/mxfp8/dual.py:45-47, from the
+ * absent mxfp6 wheel: this rule is this library's definition). */
+int mxl_quantize_mxfp8_dual(const void* x, int64_t M, int64_t K, int64_t ldx, int rule, void* hi, void* s_hi,
+                            void* res, void* s_res, void* stream);
+
 /* Per-token group-128 FP8 quantization: bf16 x [M, K] -> E4M3 q [M, K] +
  * fp32 scales column-major s[g * M + m].  Replaces _quantize_kernel.quantize_out
  * (src/vllm_mach/fp8/_quantize_kernel.py:7-25). */
@@ -107,6 +115,15 @@ int mxl_pack_weight(const void* codes, const void* scales, int64_t N, int64_t K,
 /* Scratch bytes the GEMMs may use for split-K partials at (M, N, K); with a
  * smaller workspace they run unsplit. */
 int64_t mxl_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* Two-limb MX GEMM for M <= 64: y = bf16(hi . W^T + res . W^T) with the limbs
+ * accumulated separately in fp32 (each limb's partial goes to the workspace,
+ * >= 2 M N 4 bytes) and summed before the one bf16 rounding; bias as in
+ * mxl_mx_gemm.  Replaces gemm_out(hi, w, s_hi, ws, residual, s_res, out)
+ * (src/vllm_mach/mxfp8/dual.py:45-50, docs/mxfp8-champion.md:12). */
+int mxl_mx_gemm_dual(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
+                     const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, const void* bias,
+                     void* out, int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* MX block-scaled GEMM: y[M, N] (bf16, row stride ldc) = A . W^T, A = E4M3
  * codes [M, K] + E8M0 [M, K/32]; W tiled (fmt 0/2/3); bias bf16 [N] or NULL

@@ -73,6 +73,7 @@ def lib():
             "mxo_moe_route": (None, [P, I64, I64, I64, P, P, P]),
             "mxo_moe_reduce": (None, [P, P, P, I64, I64, I64, P]),
             "mxo_rmsnorm_mx": (None, [P, P, P, I64, I64, ctypes.c_float, I, P, P, P, P]),
+            "mxo_quant_mxfp8_dual": (None, [P, I64, I64, I, P, P, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -171,6 +172,17 @@ def quant_mxfp8(x, rule: int = RULE_FLOOR_CARRY175):
     scales = np.empty((R, K // 32), np.uint8)
     lib().mxo_quant_mxfp8(_p(b), R, K, rule, _p(codes), _p(scales))
     return codes, scales
+
+
+def quant_mxfp8_dual(x, rule: int = RULE_FLOOR_CARRY175):
+    """Two-limb MXFP8 (src/vllm_mach/mxfp8/dual.py:45-50): bf16 [R, K] -> (hi codes, hi
+    scales, residual codes, residual scales), each [R, K] / [R, K/32]."""
+    b = bf16_bits(x)
+    R, K = b.shape
+    hi = np.empty((R, K), np.uint8); s_hi = np.empty((R, K // 32), np.uint8)
+    res = np.empty((R, K), np.uint8); s_res = np.empty((R, K // 32), np.uint8)
+    lib().mxo_quant_mxfp8_dual(_p(b), R, K, rule, _p(hi), _p(s_hi), _p(res), _p(s_res))
+    return hi, s_hi, res, s_res
 
 
 def swiglu_mxfp8(gate_up, rule: int = RULE_CEIL_DIV448):

@@ -175,6 +175,27 @@ void mxo_quant_mxfp8(const uint16_t* x, int64_t rows, int64_t K, int rule,
  * (S. L. Moshier, Cephes Math Library), evaluated with explicit fmaf.
  * Inputs below -87 return 0 and above 88 return +inf; SiLU only uses
  * 1 + exp(-g), which rounds identically for any value under 2^-25.          */
+/* Two-limb ("dual") MXFP8 activations, the contract of the reference's dual
+ * path (src/vllm_mach/mxfp8/dual.py:45-50; docs/mxfp8-champion.md:12 "high plus
+ * BF16-rounded residual, separate FP32 accumulators and final BF16 rounding").
+ * The quantizer itself is in the absent mxfp6 wheel; this build defines it per
+ * 32-block as: hi = MXFP8(x) under `rule`; residual r = bf16(x - deq(hi)) with
+ * deq(hi) = E4M3(code) * 2^(s - 127) exact in binary32 and one f32 subtraction;
+ * res = MXFP8(r) under the same rule.                                          */
+void mxo_quant_mxfp8_dual(const uint16_t* x, int64_t rows, int64_t K, int rule, uint8_t* hi, uint8_t* s_hi,
+                          uint8_t* res, uint8_t* s_res) {
+  float v[32], rv[32];
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t b = 0; b < K / 32; ++b) {
+      for (int i = 0; i < 32; ++i) v[i] = mxo_bf16_to_f32(x[r * K + b * 32 + i]);
+      uint8_t* hc = hi + r * K + b * 32;
+      uint8_t* hs = s_hi + r * (K / 32) + b;
+      quant_block32(v, rule, hc, hs);
+      for (int i = 0; i < 32; ++i) rv[i] = bf16_round(v[i] - ldexpf(mxo_e4m3_to_f32(hc[i]), (int)*hs - 127));
+      quant_block32(rv, rule, res + r * K + b * 32, s_res + r * (K / 32) + b);
+    }
+}
+
 float mxo_exp(float x) {
   if (x < -87.0f) return 0.0f;
   if (x > 88.0f) return INFINITY;

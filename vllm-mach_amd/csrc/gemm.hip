@@ -166,7 +166,10 @@ __global__ __launch_bounds__(MT == 1 && NT == 1 ? 1024 : 512) void gemm_kernel(G
   extern __shared__ float red[];  // [KW][MT][NT][4][64] when KW > 1
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, KW = blockDim.x >> 6;
   const int r = lane & 15, q = lane >> 4;
+  // blockIdx.z is the K split, or with two-limb activations (a2 set) the limb:
+  // both limbs cover all of K and write fp32 partials that the reduce sums
   const int64_t split = blockIdx.z;
+  const bool dual = p.a2 != nullptr;
 
   const int64_t ntiles_total = (p.N + 15) / 16;
   int64_t ntile[NT], ntile_ld[NT];  // ntile_ld stays inside the packed buffer for a ragged last group
@@ -208,12 +211,17 @@ __global__ __launch_bounds__(MT == 1 && NT == 1 ? 1024 : 512) void gemm_kernel(G
 
     // waves take interleaved super-tiles; each super-tile's loads are all issued
     // before its MFMAs wait on them (enough waves per CU keep HBM busy)
-    const int64_t kstride = (int64_t)p.S * KW;
-    for (int64_t kt = split * KW + wv; kt < p.KT; kt += kstride) {
+    const int64_t kstride = dual ? KW : (int64_t)p.S * KW;
+    GemmParams pa = p;
+    if (dual && split == 1) {
+      pa.a = p.a2;
+      pa.sa = p.sa2;
+    }
+    for (int64_t kt = (dual ? 0 : split * KW) + wv; kt < p.KT; kt += kstride) {
       BTile<FMT, NT> B;
       ATile<MT> A;
       load_b<FMT, NT, BLOCK>(p, w, sw, ntile_ld, kt, lane, B);
-      load_a<MT, BLOCK>(p, arow, kt, lane, A);
+      load_a<MT, BLOCK>(pa, arow, kt, lane, A);
       compute_tile<FMT, MT, NT, BLOCK>(p, A, B, acc, kt, q, r4, hi, ntile_ld,
                                        BLOCK ? static_cast<const float*>(p.sw) : nullptr);
     }
@@ -431,6 +439,44 @@ extern "C" int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void*
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm: unknown weight format %d", w_fmt);
   return gemm_common(a, sa, M, w_tiled, sw_tiled, N, K, w_fmt, false, bias, out, ldc, workspace, workspace_bytes,
                      stream, "mxl_mx_gemm");
+}
+
+extern "C" int mxl_mx_gemm_dual(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
+                                const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
+                                const void* bias, void* out, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm_dual: unknown weight format %d", w_fmt);
+  MXL_CHECK_ARG(M >= 0 && M <= 64 && N > 0 && K > 0 && K % 128 == 0,
+                "mxl_mx_gemm_dual: need M <= 64, N > 0, K %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
+                (long long)N, (long long)K);
+  MXL_CHECK_ARG(ldc >= N, "mxl_mx_gemm_dual: ldc < N");
+  MXL_CHECK_ARG(((uintptr_t)hi & 15) == 0 && ((uintptr_t)res & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
+                "mxl_mx_gemm_dual: hi, res and w must be 16-byte aligned");
+  MXL_CHECK_ARG(workspace && workspace_bytes >= 2 * M * N * 4,
+                "mxl_mx_gemm_dual: workspace too small (%lld < %lld)", (long long)workspace_bytes,
+                (long long)(2 * M * N * 4));
+  if (M == 0) return MXL_OK;
+  GemmParams p{};
+  p.a = (const uint8_t*)hi; p.sa = s_hi; p.a2 = (const uint8_t*)res; p.sa2 = s_res;
+  p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled; p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out;
+  p.partial = (float*)workspace;
+  p.lda = K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
+  p.row_div = 1;
+  p.S = 2;  // the two limbs' fp32 partials
+  GemmConfig c = choose_config(M, N, K);
+  c.S = 1;
+  const int64_t n_groups = ((N + 15) / 16 + c.NT - 1) / c.NT;
+  const int64_t m_groups = (M + 16 * c.MT - 1) / (16 * c.MT);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dispatch_fmt<false, false>(w_fmt, c, dim3((unsigned)n_groups, (unsigned)m_groups, 2), p, s);
+  if (e != hipSuccess) {
+    set_error("mxl_mx_gemm_dual: launch failed: %s", hipGetErrorString(e));
+    return MXL_EHIP;
+  }
+  splitk_reduce_kernel<<<dim3((unsigned)((M * N + 255) / 256)), 256, 0, s>>>(
+      (const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, 2);
+  MXL_CHECK_LAUNCH("mxl_mx_gemm_dual");
+  return MXL_OK;
 }
 
 extern "C" int mxl_block_fp8_gemm(const void* a, const void* sa_colmajor, int64_t M, const void* w_tiled,

@@ -26,6 +26,8 @@ struct GemmParams {
   const uint16_t* bias;  // bf16 [N] or null
   uint16_t* out;         // bf16, row stride ldc
   float* partial;        // [S, rows, N] when split
+  const uint8_t* a2;     // two-limb activations: residual codes (gemm_kernel only), or null
+  const void* sa2;       // and their E8M0 scales
   const int32_t* row_index;     // grouped: sorted_routes (A row = row_index[r] / row_div)
   const int64_t* expert_offsets;
   int64_t lda, ldc, M, N, K, KT, a_rows;

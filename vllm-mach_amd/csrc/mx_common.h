@@ -46,6 +46,15 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
   return sign | ((a - (120u << 23) + 0x7FFFFu + odd) >> 20);
 }
 
+// E4M3 ("fn") code -> binary32 (exact; 0x7F / 0xFF decode as NaN).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  const uint32_t e = (c >> 3) & 0xFu, m = c & 7u;
+  const float sgn = (c & 0x80u) ? -1.0f : 1.0f;
+  if (e == 0xFu && m == 7u) return __builtin_nanf("");
+  if (e == 0u) return sgn * __builtin_ldexpf((float)m, -9);
+  return sgn * __builtin_ldexpf((float)(8u + m), (int)e - 10);
+}
+
 // binary32 -> FP6 code (fmt 2 = E2M3, 3 = E3M2; bit 5 = sign), OCP MX v1.0:
 // round-to-nearest-even, saturating to the largest normal.
 template <int FMT>

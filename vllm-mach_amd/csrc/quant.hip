@@ -82,6 +82,41 @@ __global__ __launch_bounds__(256) void quant_mxfp6_kernel(const uint16_t* __rest
   if (sub == 0) scales[row * blocks_per_row + blk] = (uint8_t)(e + 127);
 }
 
+// Two-limb MXFP8: hi = MXFP8(x), residual = bf16(x - deq(hi)), res = MXFP8(residual),
+// both under RULE (the contract of mxfp8/dual.py:45-50; the quantizer itself is
+// this build's definition).  Same lane mapping as quant_mxfp8_kernel.
+template <int RULE>
+__global__ __launch_bounds__(256) void quant_mxfp8_dual_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                               uint8_t* __restrict__ hi, uint8_t* __restrict__ s_hi,
+                                                               uint8_t* __restrict__ res,
+                                                               uint8_t* __restrict__ s_res, int64_t M, int64_t K) {
+  const int64_t blocks_per_row = K / 32;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int sub = (int)(tid & 3);
+  const int64_t total = M * blocks_per_row;
+  const bool live = (tid >> 2) < total;
+  const int64_t id = live ? (tid >> 2) : total - 1;
+  const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
+  float v[8], rv[8];
+  bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * ldx + blk * 32 + sub * 8), v);
+  uint32_t ph[2], pr[2];
+  const uint32_t sh = quant8x4<RULE>(v, ph);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float deq = __builtin_ldexpf(e4m3_to_f32((ph[i >> 2] >> (8 * (i & 3))) & 0xFFu), (int)sh - 127);
+    rv[i] = bf16_round(v[i] - deq);
+  }
+  const uint32_t sr = quant8x4<RULE>(rv, pr);
+  if (!live) return;
+  const int64_t off = row * K + blk * 32 + sub * 8;
+  *reinterpret_cast<uint2*>(hi + off) = make_uint2(ph[0], ph[1]);
+  *reinterpret_cast<uint2*>(res + off) = make_uint2(pr[0], pr[1]);
+  if (sub == 0) {
+    s_hi[row * blocks_per_row + blk] = (uint8_t)sh;
+    s_res[row * blocks_per_row + blk] = (uint8_t)sr;
+  }
+}
+
 // ------------------------------------------------------------ SwiGLU -> MXFP8
 
 __device__ __forceinline__ int64_t swizzle_offset(int64_t r, int64_t g, int64_t K) {
@@ -338,6 +373,27 @@ extern "C" int mxl_quantize_mxfp6(const void* x, int64_t M, int64_t K, int64_t l
   else
     quant_mxfp6_kernel<kE3M2><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)packed, (uint8_t*)scales, M, K);
   MXL_CHECK_LAUNCH("mxl_quantize_mxfp6");
+  return MXL_OK;
+}
+
+extern "C" int mxl_quantize_mxfp8_dual(const void* x, int64_t M, int64_t K, int64_t ldx, int rule, void* hi,
+                                       void* s_hi, void* res, void* s_res, void* stream) {
+  MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0 && ldx >= K && ldx % 8 == 0,
+                "mxl_quantize_mxfp8_dual: need K %% 32 == 0, ldx >= K, ldx %% 8 == 0");
+  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_quantize_mxfp8_dual: unknown rule %d", rule);
+  MXL_CHECK_ARG(aligned16(x) && ((uintptr_t)hi & 7) == 0 && ((uintptr_t)res & 7) == 0,
+                "mxl_quantize_mxfp8_dual: misaligned buffers");
+  if (M == 0) return MXL_OK;
+  const int64_t n = M * (K / 32) * 4;
+  dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  if (rule == kFloorCarry175)
+    quant_mxfp8_dual_kernel<kFloorCarry175><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)hi,
+                                                                (uint8_t*)s_hi, (uint8_t*)res, (uint8_t*)s_res, M, K);
+  else
+    quant_mxfp8_dual_kernel<kCeilDiv448><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)hi,
+                                                             (uint8_t*)s_hi, (uint8_t*)res, (uint8_t*)s_res, M, K);
+  MXL_CHECK_LAUNCH("mxl_quantize_mxfp8_dual");
   return MXL_OK;
 }
 

@@ -82,6 +82,14 @@ class Mxfp8LinearKernel(_Kernel):
 
     act_rule = ops.FLOOR_CARRY175
 
+    def __init__(self, config: Optional[MxLinearLayerConfig] = None, dual_m: tuple[int, ...] = ()):
+        """``dual_m``: row counts served by two-limb activations (the reference's M32/M64
+        dual dispatch, src/vllm_mach/mxfp8/dual.py:53-75); every other M uses one limb."""
+        super().__init__(config)
+        if any(m <= 0 or m > 64 for m in dual_m):
+            raise ValueError("two-limb activations serve 1 <= M <= 64")
+        self.dual_m = frozenset(dual_m)
+
     @classmethod
     def can_implement(cls, config: MxLinearLayerConfig) -> tuple[bool, Optional[str]]:
         return True, None
@@ -111,8 +119,9 @@ class Mxfp8LinearKernel(_Kernel):
             raise ValueError("MXFP8 requires BF16 activations with matching K")
         if x.numel() == 0:
             return x.new_empty((*x.shape[:-1], n))
-        y = ops.mx_gemm_from_float(_flatten(x, k).contiguous(), layer.weight, layer.weight_scale, n,
-                                   layer.mxl_format, self.act_rule)
+        x2 = _flatten(x, k).contiguous()
+        gemm = ops.mx_gemm_from_float_dual if x2.shape[0] in self.dual_m else ops.mx_gemm_from_float
+        y = gemm(x2, layer.weight, layer.weight_scale, n, layer.mxl_format, self.act_rule)
         y = y.reshape(*x.shape[:-1], n)
         return y if bias is None else y + bias
 

@@ -357,6 +357,72 @@ def _(a, sa, w, sw, n, k, w_fmt, bias=None):
     return a.new_empty((a.shape[0], n), dtype=torch.bfloat16)
 
 
+@torch.library.custom_op("mach_amd::quantize_mxfp8_dual", mutates_args=())
+def quantize_mxfp8_dual(x: torch.Tensor, rule: int = FLOOR_CARRY175
+                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Two-limb MXFP8 activations (the contract of the reference's dual ``quantize``,
+    src/vllm_mach/mxfp8/dual.py:45-47): bf16 [M, K] -> (hi E4M3 [M, K], hi scales [M, K/32],
+    residual E4M3 [M, K], residual scales [M, K/32]); residual = bf16(x - dequant(hi))."""
+    _check_cuda(x)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.shape[1] % 32:
+        raise ValueError("quantize_mxfp8_dual needs bf16 [M, K] with K % 32 == 0")
+    x = x.contiguous()
+    M, K = x.shape
+    hi = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
+    res = torch.empty_like(hi)
+    s_hi = torch.empty((M, K // 32), dtype=torch.uint8, device=x.device)
+    s_res = torch.empty_like(s_hi)
+    if M:
+        call("mxl_quantize_mxfp8_dual", ptr(x), M, K, K, rule, ptr(hi), ptr(s_hi), ptr(res), ptr(s_res),
+             stream_handle(x.device))
+    _count("quantize_mxfp8_dual")
+    return hi, s_hi, res, s_res
+
+
+@quantize_mxfp8_dual.register_fake
+def _(x, rule=FLOOR_CARRY175):
+    M, K = x.shape
+    codes = x.new_empty((M, K), dtype=torch.float8_e4m3fn)
+    scales = x.new_empty((M, K // 32), dtype=torch.uint8)
+    return codes, scales, torch.empty_like(codes), torch.empty_like(scales)
+
+
+@torch.library.custom_op("mach_amd::mx_gemm_dual", mutates_args=())
+def mx_gemm_dual(hi: torch.Tensor, s_hi: torch.Tensor, res: torch.Tensor, s_res: torch.Tensor, w: torch.Tensor,
+                 sw: torch.Tensor, n: int, k: int, w_fmt: int, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Two-limb MX GEMM, M <= 64: y = bf16(hi . W^T + res . W^T), limbs accumulated in separate
+    fp32 partials (the contract of the reference's dual ``gemm_out``,
+    src/vllm_mach/mxfp8/dual.py:45-50; docs/mxfp8-champion.md:12)."""
+    _check_cuda(hi, s_hi, res, s_res, w, sw, bias)
+    h8, r8 = _u8(hi).contiguous(), _u8(res).contiguous()
+    M = h8.shape[0]
+    if h8.shape != r8.shape or h8.ndim != 2 or h8.shape[1] != k or M > 64:
+        raise ValueError("mx_gemm_dual needs two [M, K] limbs with M <= 64 matching the weight's K")
+    sh8, sr8 = _u8(s_hi).contiguous(), _u8(s_res).contiguous()
+    if tuple(sh8.shape) != (M, k // 32) or tuple(sr8.shape) != (M, k // 32):
+        raise ValueError(f"limb scales must be [M, K/32] = [{M}, {k // 32}]")
+    out = torch.empty((M, n), dtype=torch.bfloat16, device=hi.device)
+    if M:
+        nbytes = 2 * M * n * 4
+        buf = workspace(hi.device, nbytes)
+        call("mxl_mx_gemm_dual", ptr(h8), ptr(sh8), ptr(r8), ptr(sr8), M, ptr(w), ptr(sw), n, k, w_fmt,
+             ptr(bias), ptr(out), n, ptr(buf), nbytes, stream_handle(hi.device))
+    _count("mx_gemm_dual")
+    return out
+
+
+@mx_gemm_dual.register_fake
+def _(hi, s_hi, res, s_res, w, sw, n, k, w_fmt, bias=None):
+    return hi.new_empty((hi.shape[0], n), dtype=torch.bfloat16)
+
+
+def mx_gemm_from_float_dual(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
+                            rule: int = FLOOR_CARRY175, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Two-limb quantization then the two-limb GEMM (``_dual``, src/vllm_mach/mxfp8/dual.py:45-50)."""
+    hi, s_hi, res, s_res = torch.ops.mach_amd.quantize_mxfp8_dual(x, rule)
+    return torch.ops.mach_amd.mx_gemm_dual(hi, s_hi, res, s_res, w, sw, n, x.shape[1], w_fmt, bias)
+
+
 def mx_gemm_from_float(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
                        rule: int = FLOOR_CARRY175, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Quantize bf16 activations to MXFP8 and run the MX GEMM.
