@@ -3,7 +3,8 @@
 Dynamic MXFP8 activation quantization, the SwiGLU -> MXFP8 producer, and the
 block-scaled GEMMs for MXFP8, packed MXFP6 (W6A8) and block-FP8, dense and
 MoE-grouped, as hand-written HIP kernels behind a C ABI (``include/mxlinear.h``,
-``libmxlinear.so``) and vLLM's quantization-method surface (``linear``, ``moe``).
+``libmxlinear.so``) and vLLM's quantization-method surface (``linear``, ``moe``),
+with loaders for the checkpoint formats that feed it (``checkpoint``).
 
 Importing the package registers the ``torch.ops.mach_amd`` operators; it does
 not touch the GPU or load the HIP library (that happens on first use).
@@ -19,6 +20,14 @@ from .linear import (  # noqa: F401
     register_kernels,
     swiglu_mxfp8_down,
 )
-from .moe import Mxfp6Experts, select_experts  # noqa: F401
+from .moe import Mxfp6Experts, Mxfp6MoEMethod, select_experts  # noqa: F401
+from .checkpoint import (  # noqa: F401
+    SafetensorsCheckpoint,
+    linear_quant_key,
+    load_linear,
+    load_moe,
+    moe_quant_key,
+    quant_config_of,
+)
 
 __version__ = "0.1.0"

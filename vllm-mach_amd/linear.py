@@ -52,6 +52,34 @@ def _replace(layer: torch.nn.Module, name: str, value: torch.Tensor) -> None:
     setattr(layer, name, torch.nn.Parameter(value, requires_grad=False))
 
 
+_QKV_SHARDS = {"q": 0, "k": 1, "v": 2}
+
+
+def load_partition(param: torch.nn.Parameter, loaded_weight: torch.Tensor, loaded_shard_id=None) -> None:
+    """Copy one checkpoint tensor into a parameter made by ``MxLinearMethod.create_weights``.
+
+    ``loaded_shard_id`` None loads the whole parameter; an index (or ``"q"``/``"k"``/``"v"``)
+    loads partition ``i`` of a merged layer (gate/up, q/k/v) into rows
+    ``sum(widths[:i]) / r`` .. of the parameter, r being the output rows one entry covers
+    (1 for codes and E8M0 scales, 128 for block-FP8 scales), as vLLM's merged-column
+    loaders do.  Shape and dtype must match exactly: a checkpoint in another format is an
+    error, never a silent conversion.
+    """
+    widths = param.mxl_logical_widths
+    rows = param.mxl_rows_per_entry
+    target = param.data
+    if loaded_shard_id is not None:
+        idx = _QKV_SHARDS.get(loaded_shard_id, loaded_shard_id)
+        if not isinstance(idx, int) or not 0 <= idx < len(widths):
+            raise ValueError(f"shard {loaded_shard_id!r} is not one of {len(widths)} partitions")
+        start = sum(widths[:idx])
+        target = target.narrow(0, start // rows, (widths[idx] + rows - 1) // rows)
+    if loaded_weight.dtype != target.dtype or tuple(loaded_weight.shape) != tuple(target.shape):
+        raise ValueError(f"checkpoint tensor {loaded_weight.dtype}{tuple(loaded_weight.shape)} does not match "
+                         f"parameter slice {target.dtype}{tuple(target.shape)}")
+    target.copy_(loaded_weight)
+
+
 def _flatten(x: torch.Tensor, k: int) -> torch.Tensor:
     return x.reshape(-1, k)
 
@@ -255,11 +283,21 @@ class MxLinearMethod:
     def create_weights(self, layer: torch.nn.Module, input_size_per_partition: int,
                        output_partition_sizes: list[int], input_size: int, output_size: int,
                        params_dtype: torch.dtype, **extra_weight_attrs) -> None:
+        """Registers the checkpoint parameters.  Each carries ``output_dim``/``input_dim``
+        and a ``weight_loader(param, loaded_weight, loaded_shard_id=None)``: the caller's
+        (vLLM passes the layer's own in ``extra_weight_attrs``) or ``load_partition``,
+        which places shard ``i`` of a merged layer at rows ``sum(widths[:i])``.  Other
+        ``extra_weight_attrs`` are set on the parameters as vLLM's ``set_weight_attrs`` does;
+        ``device`` picks where the empty parameters live."""
         n, k = sum(output_partition_sizes), input_size_per_partition
         if k % 128:
             raise ValueError("input size per partition must be a multiple of 128")
+        if n <= 0 or any(w <= 0 for w in output_partition_sizes):
+            raise ValueError("output partition sizes must be positive")
         key = self.config.weight_quant_key
-        device = extra_weight_attrs.get("device", None)
+        attrs = dict(extra_weight_attrs)
+        device = attrs.pop("device", None)
+        rows_per_scale = 1
         if key == MXFP8_STATIC:
             w = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=device)
             s = torch.empty((n, k // 32), dtype=torch.uint8, device=device)
@@ -269,11 +307,22 @@ class MxLinearMethod:
             s = torch.empty((n, k // 32), dtype=torch.uint8, device=device)
             names = ("weight", "weight_scale")
         else:
+            # vLLM's block-shape validation: merged partitions start on a 128-row block
+            if len(output_partition_sizes) > 1 and any(w % 128 for w in output_partition_sizes):
+                raise ValueError("merged block-FP8 partitions must be multiples of 128 rows")
             w = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=device)
             s = torch.empty(((n + 127) // 128, k // 128), dtype=torch.float32, device=device)
             names = ("weight", "weight_scale_inv")
-        layer.register_parameter(names[0], torch.nn.Parameter(w, requires_grad=False))
-        layer.register_parameter(names[1], torch.nn.Parameter(s, requires_grad=False))
+            rows_per_scale = 128
+        for name, data, rows in ((names[0], w, 1), (names[1], s, rows_per_scale)):
+            param = torch.nn.Parameter(data, requires_grad=False)
+            param.output_dim, param.input_dim = 0, 1
+            param.mxl_rows_per_entry = rows
+            param.mxl_logical_widths = list(output_partition_sizes)
+            param.weight_loader = load_partition
+            for attr, value in attrs.items():
+                setattr(param, attr, value)
+            layer.register_parameter(name, param)
         layer.params_dtype = params_dtype
         layer.logical_widths = list(output_partition_sizes)
         layer.input_size_per_partition = k

@@ -102,3 +102,86 @@ class Mxfp6Experts:
         self.apply(out, hidden_states, w1, w2, topk_weights, topk_ids, SILU, self.shapes[0], None,
                    None, None, None, None, None, False)
         return out
+
+
+_MOE_PARAMS = ("w13_weight", "w13_weight_scale", "w2_weight", "w2_weight_scale")
+
+
+def load_expert_shard(param: torch.nn.Parameter, loaded_weight: torch.Tensor, weight_name: str,
+                      shard_id: str, expert_id: int) -> None:
+    """vLLM's ``FusedMoE.weight_loader`` contract for one expert's tensor: shard ``w1`` (gate)
+    fills rows [0, I) of expert ``expert_id``'s w13 entry, ``w3`` (up) rows [I, 2I), ``w2``
+    (down) the whole w2 entry.  Shapes and dtypes must match exactly."""
+    if not 0 <= expert_id < param.shape[0]:
+        raise ValueError(f"expert {expert_id} is outside [0, {param.shape[0]})")
+    target = param.data[expert_id]
+    is_w13 = param.mxl_moe_name.startswith("w13")
+    if shard_id in ("w1", "w3"):
+        if not is_w13:
+            raise ValueError(f"shard {shard_id} loads w13 parameters, not {param.mxl_moe_name}")
+        half = target.shape[0] // 2
+        target = target.narrow(0, 0 if shard_id == "w1" else half, half)
+    elif shard_id == "w2":
+        if is_w13:
+            raise ValueError(f"shard w2 loads w2 parameters, not {param.mxl_moe_name}")
+    else:
+        raise ValueError(f"unknown expert shard {shard_id!r} (w1, w2 or w3)")
+    if loaded_weight.dtype != target.dtype or tuple(loaded_weight.shape) != tuple(target.shape):
+        raise ValueError(f"{weight_name}: checkpoint tensor {loaded_weight.dtype}{tuple(loaded_weight.shape)} "
+                         f"does not match {target.dtype}{tuple(target.shape)}")
+    target.copy_(loaded_weight)
+
+
+class Mxfp6MoEMethod:
+    """``FusedMoEMethodBase``-shaped owner of routed-expert MXFP6 parameters.
+
+    ``create_weights`` registers the Quark OCP-MX checkpoint layout that the reference's
+    patched ``QuarkOCP_MX_MoEMethod`` loads (src/vllm_mach/mxfp6/profile/runtime.patch:207-250):
+    ``w13_weight`` u8 [E, 2I, 3H/4], ``w13_weight_scale`` u8 [E, 2I, H/32], ``w2_weight``
+    u8 [E, H, 3I/4], ``w2_weight_scale`` u8 [E, H, I/32], each with vLLM's
+    ``weight_loader(param, loaded_weight, weight_name, shard_id, expert_id)``.
+    ``process_weights_after_loading`` replaces them with the MFMA-tiled layout (where the
+    reference repacks scales, runtime.patch:227-239), and ``apply`` routes and runs them.
+    H and I must be multiples of 128 (the tiled layout's K granule).
+    """
+
+    def __init__(self, fmt: int = ops.E3M2, act_rule: int = ops.FLOOR_CARRY175,
+                 mid_rule: int = ops.CEIL_DIV448):
+        if fmt not in (ops.E2M3, ops.E3M2):
+            raise ValueError("MXFP6 MoE weights are E2M3 or E3M2")
+        self.experts = Mxfp6Experts(fmt, act_rule, mid_rule)
+
+    def create_weights(self, layer: torch.nn.Module, num_experts: int, hidden_size: int,
+                       intermediate_size_per_partition: int, params_dtype: torch.dtype,
+                       **extra_weight_attrs) -> None:
+        E, H, I = num_experts, hidden_size, intermediate_size_per_partition
+        if E <= 0 or H <= 0 or I <= 0 or H % 128 or I % 128:
+            raise ValueError("MXFP6 MoE needs experts > 0 and hidden and intermediate sizes divisible by 128")
+        attrs = dict(extra_weight_attrs)
+        device = attrs.pop("device", None)
+        shapes = ((E, 2 * I, H * 3 // 4), (E, 2 * I, H // 32), (E, H, I * 3 // 4), (E, H, I // 32))
+        for name, shape in zip(_MOE_PARAMS, shapes):
+            param = torch.nn.Parameter(torch.empty(shape, dtype=torch.uint8, device=device), requires_grad=False)
+            param.mxl_moe_name = name
+            param.weight_loader = load_expert_shard
+            for attr, value in attrs.items():
+                setattr(param, attr, value)
+            layer.register_parameter(name, param)
+        layer.params_dtype = params_dtype
+        layer.local_num_experts = E
+
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        w1, w2 = self.experts.process_weights_after_loading(
+            layer.w13_weight.data, layer.w13_weight_scale.data, layer.w2_weight.data, layer.w2_weight_scale.data)
+        for name, value in zip(_MOE_PARAMS, (w1, self.experts.w1_scale, w2, self.experts.w2_scale)):
+            setattr(layer, name, torch.nn.Parameter(value, requires_grad=False))
+
+    def apply(self, layer: torch.nn.Module, x: torch.Tensor, topk_weights: torch.Tensor,
+              topk_ids: torch.Tensor, expert_map: Optional[torch.Tensor] = None,
+              global_num_experts: Optional[int] = None) -> torch.Tensor:
+        out = torch.empty_like(x)
+        E = self.experts.shapes[0] if self.experts.shapes is not None else layer.local_num_experts
+        self.experts.apply(out, x, layer.w13_weight, layer.w2_weight, topk_weights, topk_ids, SILU,
+                           E if global_num_experts is None else global_num_experts, expert_map,
+                           None, None, None, None, None, False)
+        return out
