@@ -1,6 +1,7 @@
 """GPU parity of the wide-tile prefill GEMM (128-row workgroup tiles, K-stage ring,
 optional K splits) against the oracle, on the shapes that exercise its edges:
 ragged M and N, a K that ends in half a 512-wide super-tile, forced split counts,
+more tiles than CUs (whole-K rounds plus a K-split remainder),
 every weight format, bias, block-FP8 scales, and grouped experts with skewed,
 empty and multi-block row ranges.  Same bar as the other GEMM tests."""
 import numpy as np
@@ -63,6 +64,48 @@ def test_wide_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
     y = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, None)
     rq, rs = oracle_mod.quant_block_fp8(x)
     assert np.array_equal(q.view(torch.uint8).cpu().numpy(), rq)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.block_fp8_gemm_ref(rq, rs, wq.view(torch.uint8).numpy(), sb.numpy()))
+    _check(y.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,fmt,cfg,bias", [
+    (512, 8320, 1024, 0, "2,1,h", True),     # 260 tiles: 256 whole-K, 4 split two ways
+    (300, 11000, 1536, 2, "2,1,h", False),   # ragged M and N: 258 tiles, remainder split three ways
+    (512, 4160, 1280, 3, "1,1,h", True),     # 64-wide tiles, K = 2.5 super-tiles
+    (512, 16640, 1024, 0, "4,1,h", False),   # 3-slot ring: 260 tiles of 128 x 256
+])
+def test_wide_hybrid_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias):
+    """More tiles than CUs: full rounds of whole-K tiles write bf16, the remainder is split
+    in K into compact partials and summed by the tile reduce; repeated calls agree."""
+    monkeypatch.setenv("MXL_WIDE_CONFIG", cfg)
+    ops = pkg.ops
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 5 + N + K)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    x = _act(M, K, 9 + M)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    b = (torch.randn(N, generator=torch.Generator().manual_seed(4)) * 0.5).bfloat16() if bias else None
+    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, b.to(dev) if bias else None)
+    assert torch.equal(torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, b.to(dev) if bias else None), y)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)))
+    if bias:
+        ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().numpy()[None, :]))
+    _check(y.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [(512, 8320, 1280, "2,1,h"), (512, 16640, 1024, "4,1,h")])
+def test_wide_hybrid_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
+    monkeypatch.setenv("MXL_WIDE_CONFIG", cfg)
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(33 + K)
+    wb = (torch.randn(N, K, generator=g) * 0.02).reshape(N // 128, 128, K // 128, 128)
+    sb = (wb.abs().amax(dim=(1, 3)) / 448.0).float()
+    wq = (wb / sb[:, None, :, None]).reshape(N, K).to(torch.float8_e4m3fn)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    tiled, _ = ops.pack_weight(wq.to(dev), None, 0)
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x.to(dev))
+    y = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, None)
+    rq, rs = oracle_mod.quant_block_fp8(x)
     ref = oracle_mod.bf16_to_f32(oracle_mod.block_fp8_gemm_ref(rq, rs, wq.view(torch.uint8).numpy(), sb.numpy()))
     _check(y.float().cpu().numpy(), ref)
 

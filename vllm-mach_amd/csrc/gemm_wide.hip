@@ -283,6 +283,8 @@ struct WideGrid {
   int64_t nblocks;       // ceil(N / (64 NT))
   int64_t kt_per_split;  // 512-wide super-tiles per split
   int64_t num_experts;   // grouped only
+  int64_t tile0, tiles;  // dense: this launch covers output tiles [tile0, tile0 + tiles) (tile = nb * mblocks + mb)
+  int compact;           // dense, split: partials as [split][tile - tile0][128][64 NT] instead of [split][M][N]
 };
 
 // One output tile: rows [row_base, hi) of m-block rows (hi bounds the valid rows
@@ -291,7 +293,8 @@ struct WideGrid {
 template <int FMT, int NT, bool BLOCK, bool GROUPED>
 __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g, int64_t mb, int64_t row_base,
                                           int64_t hi, const uint8_t* w, const uint8_t* sw, int64_t nb, int64_t split,
-                                          uint8_t* ring, uint8_t* sa_ring, int t, int lane, int wv, int r, int q) {
+                                          float* pdst, int64_t pld, uint8_t* ring, uint8_t* sa_ring, int t, int lane,
+                                          int wv, int r, int q) {
   using S = WideSlot<NT, BLOCK>;
   constexpr int C = S::COPIES;
   auto a_row = [&](int64_t row) -> int64_t {
@@ -423,14 +426,14 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
       for (int e = 0; e < 4; ++e) tile[(16 * i + 4 * q + e) * ST + 16 * (wv * NT + n) + r] = acc[i][n][e];
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const int64_t col0 = nb * TW;
-  if (p.S > 1) {  // fp32 partials, 4 columns per piece
-    const bool vec = p.N % 4 == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
+  if (p.S > 1) {  // fp32 partials, 4 columns per piece, row rr of the tile at pdst + rr * pld
+    const bool vec = pld % 4 == 0 && (reinterpret_cast<uintptr_t>(pdst) & 15) == 0;
     for (int c = t; c < 128 * (TW / 4); c += 256) {
       const int rr = c / (TW / 4), cc = (c % (TW / 4)) * 4;
       const int64_t row = row_base + rr, col = col0 + cc;
       if (row >= hi || col >= p.N) continue;
       const float4 v = *reinterpret_cast<const float4*>(tile + rr * ST + cc);
-      float* dst = p.partial + (split * p.M + row) * p.N + col;
+      float* dst = pdst + rr * pld + cc;
       if (vec) {
         *reinterpret_cast<float4*>(dst) = v;
       } else {
@@ -489,10 +492,16 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
     const int64_t G = gridDim.x, Lid = blockIdx.x;
     const int64_t xcd = Lid & 7, per = G >> 3, extra = G & 7;
     const int64_t logical = xcd * per + (xcd < extra ? xcd : extra) + (Lid >> 3);
-    const int64_t mb = logical % g.mblocks;
-    const int64_t rest = logical / g.mblocks;
-    wide_tile<FMT, NT, BLOCK, GROUPED>(p, g, mb, mb * 128, p.M, p.w, static_cast<const uint8_t*>(p.sw),
-                                       rest % g.nblocks, rest / g.nblocks, ring, sa_ring, t, lane, wv, r, q);
+    const int64_t local = logical % g.tiles, split = logical / g.tiles;
+    const int64_t tile = g.tile0 + local;
+    const int64_t mb = tile % g.mblocks, nb = tile / g.mblocks;
+    constexpr int TW = 64 * NT;
+    float* const pdst = p.S == 1 ? nullptr
+                        : g.compact ? p.partial + (split * g.tiles + local) * 128 * TW
+                                    : p.partial + (split * p.M + mb * 128) * p.N + nb * TW;
+    const int64_t pld = g.compact ? TW : p.N;
+    wide_tile<FMT, NT, BLOCK, GROUPED>(p, g, mb, mb * 128, p.M, p.w, static_cast<const uint8_t*>(p.sw), nb, split,
+                                       pdst, pld, ring, sa_ring, t, lane, wv, r, q);
     return;
   }
 
@@ -545,9 +554,51 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
     const int e = __builtin_amdgcn_readfirstlane(sh_hit);
     wide_tile<FMT, NT, BLOCK, GROUPED>(p, g, mb, sh_row[e] + (mb - sh_pre[e]) * 128, sh_row[e + 1],
                                        p.w + e * p.w_expert_stride,
-                                       static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride, nb, 0, ring,
-                                       sa_ring, t, lane, wv, r, q);
+                                       static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride, nb, 0, nullptr,
+                                       0, ring, sa_ring, t, lane, wv, r, q);
     __syncthreads();  // the epilogue's LDS reads are done before the next tile's copies
+  }
+}
+
+// Sum the compact split partials of output tiles [tile0, tile0 + tiles) in split
+// order, round to bf16, add the bias in bf16 (the split-K reduce's arithmetic).
+// One thread per 8 columns of one tile row.
+__global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __restrict__ partial,
+                                                               const uint16_t* __restrict__ bias,
+                                                               uint16_t* __restrict__ out, int64_t M, int64_t N,
+                                                               int64_t ldc, int64_t mblocks, int64_t tile0,
+                                                               int64_t tiles, int S, int TW) {
+  const int64_t per_tile = 128 * (TW / 8);
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= tiles * per_tile) return;
+  const int64_t local = id / per_tile, rem = id - local * per_tile;
+  const int rr = (int)(rem / (TW / 8)), cc = (int)(rem % (TW / 8)) * 8;
+  const int64_t tile = tile0 + local, mb = tile % mblocks, nb = tile / mblocks;
+  const int64_t row = mb * 128 + rr, col = nb * TW + cc;
+  if (row >= M || col >= N) return;
+  const float* src = partial + (local * 128 + rr) * TW + cc;
+  const int64_t split_stride = tiles * 128 * TW;
+  float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
+  for (int k = 1; k < S; ++k) {
+    const float4 a = *reinterpret_cast<const float4*>(src + k * split_stride);
+    const float4 b = *reinterpret_cast<const float4*>(src + k * split_stride + 4);
+    lo.x += a.x; lo.y += a.y; lo.z += a.z; lo.w += a.w;
+    hi.x += b.x; hi.y += b.y; hi.z += b.z; hi.w += b.w;
+  }
+  const float f[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  uint16_t h[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float y = bf16_round(f[k]);
+    if (bias) y = y + bf16_to_f32(bias[col + k < N ? col + k : N - 1]);
+    h[k] = f32_to_bf16(y);
+  }
+  uint16_t* dst = out + row * ldc + col;
+  if (col + 8 <= N && ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    *reinterpret_cast<uint4*>(dst) = uint4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                                           h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
+  } else {
+    for (int k = 0; k < 8 && col + k < N; ++k) dst[k] = h[k];
   }
 }
 
@@ -555,14 +606,33 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
 
 namespace {
 
-// Optional override "NT,S" (tuning runs only), e.g. MXL_WIDE_CONFIG=4,3.
-bool wide_override(int& nt, int& s) {
+// Optional override "NT,S" or "NT,1,h" (hybrid) for tuning runs and tests, e.g.
+// MXL_WIDE_CONFIG=4,3.
+bool wide_override(int& nt, int& s, bool& hybrid) {
   const char* v = std::getenv("MXL_WIDE_CONFIG");
   int o_nt = 0, o_s = 0;
-  if (!v || std::sscanf(v, "%d,%d", &o_nt, &o_s) != 2 || (o_nt != 1 && o_nt != 2 && o_nt != 4) || o_s < 1) return false;
+  char h = 0;
+  const int got = v ? std::sscanf(v, "%d,%d,%c", &o_nt, &o_s, &h) : 0;
+  if (got < 2 || (o_nt != 1 && o_nt != 2 && o_nt != 4) || o_s < 1) return false;
   nt = o_nt;
   s = o_s;
+  hybrid = got == 3 && h == 'h' && o_s == 1;
   return true;
+}
+
+// The hybrid split of `tiles` whole-K tiles over `cus` workgroup slots: full
+// rounds first, the remainder split in K as evenly as the CUs allow.  Returns
+// false when there is no partial last round to balance.
+bool wide_hybrid(int64_t tiles, int64_t KT, int64_t cus, WideConfig& c) {
+  if (tiles <= cus || tiles % cus == 0 || KT < 2) return false;
+  const int64_t rem = tiles % cus;
+  int64_t s2 = cus / rem < KT ? cus / rem : KT;
+  if (s2 < 2) return false;
+  const int64_t per = (KT + s2 - 1) / s2;
+  c.dp_tiles = tiles - rem;
+  c.kt2 = per;
+  c.S2 = (int)((KT + per - 1) / per);
+  return c.S2 >= 2;
 }
 
 }  // namespace
@@ -575,10 +645,14 @@ bool wide_override(int& nt, int& s) {
 WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
   const int64_t KT = (K + kTileK - 1) / kTileK, MB = (M + 127) / 128;
   int o_nt, o_s;
-  if (wide_override(o_nt, o_s)) {
+  bool o_h = false;
+  if (wide_override(o_nt, o_s, o_h)) {
     const int64_t per = (KT + o_s - 1) / o_s;
-    return WideConfig{o_nt, (int)((KT + per - 1) / per), per};
+    WideConfig c{o_nt, (int)((KT + per - 1) / per), per};
+    if (o_h) wide_hybrid(MB * ((N + 64 * o_nt - 1) / (64 * o_nt)), KT, cu_count(), c);
+    return c;
   }
+  const int64_t cus = cu_count();
   WideConfig best{2, 1, KT};
   double best_cost = 1e300;
   const double wbytes = (double)N * K * (fmt == kE4M3 ? 1.0 : 0.75) + (double)N * K / 32;
@@ -590,7 +664,7 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
     for (int64_t s = 1; s <= KT; ++s) {
       const int64_t per = (KT + s - 1) / s;
       if ((KT + per - 1) / per != s) continue;
-      const double rounds = (double)((tiles * s + 255) / 256);
+      const double rounds = (double)((tiles * s + cus - 1) / cus);
       const double t_stage = 1200.0 + 900.0 * nt;
       const double compute = rounds * per * 4 * t_stage + 3000.0;
       const double partial = s > 1 ? ((double)M * N * 4 * s * 2 + (double)M * N * 2) / (3.0e12 / 2.4e9) : 0.0;
@@ -599,9 +673,30 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
         best_cost = cost;
         best = WideConfig{nt, (int)s, per};
       }
+      WideConfig h{nt, 1, KT};
+      // (64-wide tiles re-read the activations too often for extra rounds to pay off)
+      if (s == 1 && nt >= 2 && wide_hybrid(tiles, KT, cus, h)) {
+        // full rounds, then the split remainder, its partials' round trip and two more launches
+        const double rem = (double)(tiles - h.dp_tiles);
+        const double compute_h = (double)(h.dp_tiles / cus) * KT * 4 * t_stage + (double)h.kt2 * 4 * t_stage + 9000.0;
+        const double partial_h = rem * 128 * 64 * nt * 4 * h.S2 * 2 / (3.0e12 / 2.4e9);
+        const double cost_h = (compute_h > hbm ? compute_h : hbm) + partial_h;
+        if (cost_h < best_cost) {
+          best_cost = cost_h;
+          best = h;
+        }
+      }
     }
   }
   return best;
+}
+
+int64_t wide_workspace_bytes(const WideConfig& c, int64_t M, int64_t N) {
+  if (c.dp_tiles > 0) {
+    const int64_t tiles = ((M + 127) / 128) * ((N + 64 * c.NT - 1) / (64 * c.NT));
+    return (int64_t)c.S2 * (tiles - c.dp_tiles) * 128 * 64 * c.NT * 4;
+  }
+  return c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
 }
 
 bool wide_gemm_eligible(int64_t M, int64_t K) {
@@ -624,7 +719,7 @@ static hipError_t launch_wide_fmt(const WideConfig& c, const GemmParams& p, cons
 
 hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const GemmParams& p, int64_t num_experts,
                             hipStream_t s) {
-  WideGrid g;
+  WideGrid g{};
   g.nblocks = (p.N + 64 * c.NT - 1) / (64 * c.NT);
   g.kt_per_split = c.kt_per_split;
   g.num_experts = num_experts;
@@ -639,12 +734,37 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
     return hipErrorInvalidValue;
   }
   g.mblocks = (p.M + 127) / 128;
-  grid = g.mblocks * g.nblocks * c.S;
-  if (block) return fmt == kE4M3 ? launch_wide_fmt<kE4M3, true, false>(c, p, g, grid, s) : hipErrorInvalidValue;
-  if (fmt == kE4M3) return launch_wide_fmt<kE4M3, false, false>(c, p, g, grid, s);
-  if (fmt == kE2M3) return launch_wide_fmt<kE2M3, false, false>(c, p, g, grid, s);
-  if (fmt == kE3M2) return launch_wide_fmt<kE3M2, false, false>(c, p, g, grid, s);
-  return hipErrorInvalidValue;
+  g.tile0 = 0;
+  g.tiles = g.mblocks * g.nblocks;
+  g.compact = 0;
+  auto dense = [&](const GemmParams& q, const WideGrid& gg, int64_t n) -> hipError_t {
+    if (block) return fmt == kE4M3 ? launch_wide_fmt<kE4M3, true, false>(c, q, gg, n, s) : hipErrorInvalidValue;
+    if (fmt == kE4M3) return launch_wide_fmt<kE4M3, false, false>(c, q, gg, n, s);
+    if (fmt == kE2M3) return launch_wide_fmt<kE2M3, false, false>(c, q, gg, n, s);
+    if (fmt == kE3M2) return launch_wide_fmt<kE3M2, false, false>(c, q, gg, n, s);
+    return hipErrorInvalidValue;
+  };
+  if (c.dp_tiles <= 0 || c.dp_tiles >= g.tiles) return dense(p, g, g.tiles * c.S);
+  // hybrid: whole-K tiles in full rounds (bf16 out), then the remainder split in K
+  // into compact partials (p.partial), then their reduce
+  GemmParams q = p;
+  q.S = 1;
+  WideGrid gd = g;
+  gd.tiles = c.dp_tiles;
+  hipError_t e = dense(q, gd, gd.tiles);
+  if (e != hipSuccess) return e;
+  q.S = c.S2;
+  WideGrid gs = g;
+  gs.tile0 = c.dp_tiles;
+  gs.tiles = g.tiles - c.dp_tiles;
+  gs.kt_per_split = c.kt2;
+  gs.compact = 1;
+  e = dense(q, gs, gs.tiles * c.S2);
+  if (e != hipSuccess) return e;
+  const int64_t items = gs.tiles * 128 * (64 * c.NT / 8);
+  wide_tile_reduce_kernel<<<dim3((unsigned)((items + 255) / 256)), 256, 0, s>>>(
+      p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, gs.tile0, gs.tiles, c.S2, 64 * c.NT);
+  return hipGetLastError();
 }
 
 }  // namespace mxl
