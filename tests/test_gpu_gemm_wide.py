@@ -110,10 +110,37 @@ def test_wide_hybrid_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, 
     _check(y.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("M,N,K,fmt,cfg,bias", [
+    (64, 256, 512, 0, None, False),
+    (200, 1000, 768, 0, "2,1", True),      # K = 1.5 super-tiles, ragged M
+    (100, 640, 2304, 2, "2,3", False),     # 3 K splits over 4.5 super-tiles
+    (257, 136, 1280, 3, "2,1", True),      # N not a multiple of 16
+    (130, 1024, 2560, 0, "4,2", True),     # 3-slot ring, ragged K split
+    (190, 700, 1280, 2, "4,1", False),     # N not a multiple of 256
+    (300, 8320, 1024, 0, "2,1,h", True),   # 5 x 65 = 325 tiles: hybrid with 69 split tiles
+    (130, 16640, 1024, 3, "4,1,h", False),  # 3 x 65 = 195 < 256 tiles: the plain launch
+])
+def test_wide_mx_gemm_64_row_tiles(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias):
+    """The 64-row workgroup tile (four m-tiles, one activation-scale wave) on the edge
+    shapes of the 128-row tests."""
+    monkeypatch.setenv("MXL_WIDE_MT", "4")
+    test_wide_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias)
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [(100, 384, 1280, "2,2"), (200, 1024, 1280, "4,1"), (300, 8320, 1280, "2,1,h")])
+def test_wide_block_fp8_64_row_tiles(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
+    monkeypatch.setenv("MXL_WIDE_MT", "4")
+    test_wide_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg)
+
+
+@pytest.mark.parametrize("mt", [None, "4", "8"])
 @pytest.mark.parametrize("fmt", [0, 2])
-def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, fmt):
-    """Expert 0 takes 300 routes (three 128-row blocks), expert 1 none, the rest a few
-    dozen each; rows are gathered through the sorted route list (row_div = topk)."""
+def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, monkeypatch, fmt, mt):
+    """Expert 0 takes 300 routes (three 128-row blocks or five 64-row blocks), expert 1
+    none, the rest a few dozen each; rows are gathered through the sorted route list
+    (row_div = topk)."""
+    if mt:
+        monkeypatch.setenv("MXL_WIDE_MT", mt)
     ops = pkg.ops
     E, N, K, T, topk = 8, 384, 1024, 400, 2
     g = torch.Generator().manual_seed(5)

@@ -39,6 +39,8 @@
 // cannot fill 256 CUs, S workgroups split K further and write fp32 partials
 // that a second kernel sums in split order: both orders are fixed, so every
 // result is deterministic.
+#include <cstdlib>
+
 #include "gemm_common.h"
 
 namespace mxl {
@@ -445,8 +447,11 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
   } else if (wide_gemm_eligible(M, K)) {
     WideConfig wc = wide_config(M, N, K, fmt);
     const int64_t need = wide_workspace_bytes(wc, M, N);
-    if (need > 0 && (need > workspace_bytes || workspace == nullptr))
+    if (need > 0 && (need > workspace_bytes || workspace == nullptr)) {
+      const int mt = wc.MT;
       wc = WideConfig{wc.NT, 1, (K + kTileK - 1) / kTileK};  // no room: skip the K split
+      wc.MT = mt;
+    }
     p.S = wc.S;
     e = launch_gemm_wide(fmt, block, wc, p, 0, s);
   } else {
@@ -561,7 +566,12 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
     p.w_expert_stride = mxl_tiled_weight_bytes(N, K, w_fmt);
     p.sw_expert_stride = mxl_tiled_scale_bytes(N, K);
     p.row_div = row_div; p.S = 1;
-    const WideConfig wc{2, 1, (K + kTileK - 1) / kTileK};
+    WideConfig wc{2, 1, (K + kTileK - 1) / kTileK};
+    // 128-row blocks: with 64 rows per expert on average (c5, T = 2048) 64-row blocks
+    // measured 8-10 % slower, since experts past 64 rows then copy their weights twice
+    wc.MT = 8;
+    const char* mt_env = std::getenv("MXL_WIDE_MT");  // tuning runs and tests
+    if (mt_env && (std::atoi(mt_env) == 4 || std::atoi(mt_env) == 8)) wc.MT = std::atoi(mt_env);
     hipError_t e = launch_gemm_wide(w_fmt, false, wc, p, num_experts, (hipStream_t)stream);
     if (e != hipSuccess) {
       set_error("mxl_grouped_gemm: launch failed: %s", hipGetErrorString(e));

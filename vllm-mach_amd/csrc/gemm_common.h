@@ -133,7 +133,7 @@ __device__ __forceinline__ v4f mfma_raw(v8i a, v8i b) {
 }
 
 // Wide-tile LDS-pipelined kernel for prefill-sized M (gemm_wide.hip): NT
-// n-tiles per wave (workgroup tile 128 x 64 NT), S K-splits of kt_per_split
+// n-tiles per wave (workgroup tile 16 MT x 64 NT), S K-splits of kt_per_split
 // 512-wide super-tiles each.  Hybrid (dp_tiles > 0, S = 1): the first dp_tiles
 // output tiles run whole-K in full rounds of the CUs, the remaining ones split
 // K S2 ways (kt2 super-tiles each) into compact partials summed by a tile reduce.
@@ -143,6 +143,7 @@ struct WideConfig {
   int64_t dp_tiles = 0;
   int S2 = 1;
   int64_t kt2 = 0;
+  int MT = 8;  // 16-row m-tiles per workgroup tile: 8 (128 rows) or 4 (64 rows)
 };
 WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt);
 // Workspace bytes a configuration needs (split partials), 0 when none.

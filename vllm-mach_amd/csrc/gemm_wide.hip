@@ -49,20 +49,23 @@ namespace mxl {
 
 namespace {
 
-template <int NT, bool BLOCK>
+template <int MT, int NT, bool BLOCK>
 struct WideSlot {
+  static_assert(MT == 4 || MT == 8, "64- or 128-row workgroup tiles");
   // MX with NT <= 2: the activation scales live in a separate ring of three
-  // super-tile entries (128 rows x 16 bytes), filled a super-tile ahead, so a
-  // copy moves 16 bytes per row instead of one dword from each of 128 rows.
+  // super-tile entries (16 MT rows x 16 bytes), filled a super-tile ahead, so a
+  // copy moves 16 bytes per row instead of one dword from each row.
   static constexpr bool SA_RING = !BLOCK && NT <= 2;
-  static constexpr int A = 0;                          // 16 KiB
-  static constexpr int B = 16 * 1024;                  // wave w: NT x 2 KiB at B + w NT 2 KiB
-  static constexpr int SA = B + 4 * NT * 2048;         // 512 B, copied by waves 0 and 1 (no ring)
-  static constexpr int SB = SA + (SA_RING ? 0 : 512);  // wave w: NT x 256 B (MX)
+  static constexpr int A = 0;                               // MT x 2 KiB
+  static constexpr int B = MT * 2048;                       // wave w: NT x 2 KiB at B + w NT 2 KiB
+  static constexpr int SA = B + 4 * NT * 2048;              // 64 MT bytes, copied by the scale waves (no ring)
+  static constexpr int SB = SA + (SA_RING ? 0 : 64 * MT);  // wave w: NT x 256 B (MX)
   static constexpr int BYTES = SB + (BLOCK ? 0 : 4 * NT * 256);
-  static constexpr int SLOTS = NT == 4 ? 3 : 4;        // 4 x 53 KiB would not fit the LDS
-  // copies per wave per stage (waves 0 and 1 also copy the activation scales)
-  static constexpr int COPIES = 4 + 2 * NT + (BLOCK ? 0 : NT);
+  static constexpr int SLOTS = NT == 4 ? 3 : 4;             // 4 x 53 KiB would not fit the LDS
+  static constexpr int SW = MT / 4;                         // scale waves: 0 .. SW - 1, 64 rows each
+  static constexpr int RING_ENTRY = 256 * MT;               // scale ring entry: 16 MT rows x 16 bytes
+  // copies per wave per stage (the scale waves also copy the activation scales)
+  static constexpr int COPIES = MT / 2 + 2 * NT + (BLOCK ? 0 : NT);
 };
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -96,11 +99,11 @@ __device__ __forceinline__ void wait_vm() {
 // outstanding load): LDS data is handed over by the explicit waits.
 __device__ __forceinline__ void wide_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <int NT>
+template <int MT, int NT>
 struct WideLanes {
-  uint32_t a_off[2];  // copy lane l of m-tiles 2 wv, 2 wv + 1: row (l / 4) * lda + 16 (l % 4 ^ a_swz(l / 4))
-  uint32_t sa_off;    // MX: row * K/32; block-FP8: 4 row  (row = t % 128)
-  uint32_t sa_piece[4];  // scale ring: lane l of wave w (0, 1) reads dword l % 4 of row 32 j + 16 w + l / 4
+  uint32_t a_off[MT / 4];  // copy lane l of m-tile (MT / 4) wv + i: row (l / 4) * lda + 16 (l % 4 ^ a_swz(l / 4))
+  uint32_t sa_off;    // MX: row * K/32; block-FP8: 4 row  (row = t % 16 MT)
+  uint32_t sa_piece[4];  // scale ring: lane l of scale wave w reads dword l % 4 of row 4 MT j + 16 w + l / 4
   uint32_t sa_last[4];   // the same for the last super-tile when it is half (K % 512 = 256), from p.sa and
                          // clamped inside the row (its dwords 2, 3 would lie past the row)
   const uint8_t* w_tile[NT];  // wave-uniform: tile (ntile, 0) of each of the wave's n-tiles
@@ -111,16 +114,17 @@ struct WideLanes {
 // the scale ring, waves 0 and 1 also copy piece j (32 rows) of the next
 // super-tile's activation scales (clamped inside K: a piece past the last
 // super-tile is never read).
-template <int FMT, int NT, bool BLOCK>
+template <int FMT, int MT, int NT, bool BLOCK>
 __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, int64_t t, int wv, int lane,
-                                          const WideLanes<NT>& L, uint8_t* sa_ring) {
-  using S = WideSlot<NT, BLOCK>;
+                                          const WideLanes<MT, NT>& L, uint8_t* sa_ring) {
+  using S = WideSlot<MT, NT, BLOCK>;
   constexpr int CH = FmtTraits<FMT>::CH;
+  constexpr int AW = MT / 4;  // m-tiles copied per wave
   const int64_t kt = t >> 2;
   const int j = (int)(t & 3);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {  // A: m-tile 2 wv + u / 2, half u % 2
-    const int i = 2 * wv + (u >> 1), hl = u & 1;
+  for (int u = 0; u < 2 * AW; ++u) {  // A: m-tile AW wv + u / 2, half u % 2
+    const int i = AW * wv + (u >> 1), hl = u & 1;
     copy16(p.a + t * 128 + 64 * hl, L.a_off[u >> 1], lds_addr(slot + S::A + (i * 2 + hl) * 1024));
   }
   // B: the two 1 KiB chunks of the tile that hold slice j (FP6: its 24 bytes per lane
@@ -134,13 +138,13 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
       copy16(tile + c2 * 1024, (uint32_t)(lane * 16), lds_addr(slot + S::B + ((wv * NT + n) * 2 + c2) * 1024));
   }
   if (S::SA_RING) {
-    if (wv < 2) {
+    if (wv < S::SW) {
       const int64_t ks = kt + 1 < p.KT ? kt + 1 : p.KT - 1;
-      const uint32_t dst = lds_addr(sa_ring + ((kt + 1) % 3) * 2048 + (32 * j + 16 * wv) * 16);
+      const uint32_t dst = lds_addr(sa_ring + ((kt + 1) % 3) * S::RING_ENTRY + (4 * MT * j + 16 * wv) * 16);
       if (ks == p.KT - 1 && p.K % kTileK != 0) copy4(static_cast<const uint8_t*>(p.sa), L.sa_last[j], dst);
       else copy4(static_cast<const uint8_t*>(p.sa) + ks * 16, L.sa_piece[j], dst);
     }
-  } else if (wv < 2) {  // activation scales of the 128 rows (row = t % 128 of waves 0, 1)
+  } else if (wv < S::SW) {  // activation scales of the 16 MT rows (row = t of the scale waves)
     if (!BLOCK)  // E8M0 bytes of blocks 4t .. 4t + 3
       copy4(static_cast<const uint8_t*>(p.sa) + t * 4, L.sa_off, lds_addr(slot + S::SA + wv * 256));
     else  // fp32 scale of K128 group t (column-major [K/128, M])
@@ -154,22 +158,22 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
 }
 
 // Operands of one K128 stage, read from its ring slot into registers.
-template <int NT, bool BLOCK>
+template <int MT, int NT, bool BLOCK>
 struct WideRegs {
-  v8i a[8];          // A fragment of m-tile i
-  uint32_t sa[8];    // MX: E8M0 of the lane's block (row r of m-tile i, block q of the slice)
-  float4 s4[8];      // block-FP8: fp32 activation scales of the lane's four output rows of m-tile i
+  v8i a[MT];         // A fragment of m-tile i
+  uint32_t sa[MT];   // MX: E8M0 of the lane's block (row r of m-tile i, block q of the slice)
+  float4 s4[MT];     // block-FP8: fp32 activation scales of the lane's four output rows of m-tile i
   v8i b[NT];         // B fragment of the wave's n-tile n
   uint32_t sb[NT];   // MX: E8M0 of the lane's weight row, block q of the slice
   float sbv;         // block-FP8: the stage's weight block scale
 };
 
 // Read stage operands (slice j of its super-tile) from a slot: B fragments
-// and scales first, then the eight A fragments in MFMA order.
-template <int FMT, int NT, bool BLOCK>
+// and scales first, then the MT A fragments in MFMA order.
+template <int FMT, int MT, int NT, bool BLOCK>
 __device__ __forceinline__ void wide_read(const uint8_t* slot, const uint8_t* sa_entry, int j, int wv, int lane,
-                                          int q, int r, WideRegs<NT, BLOCK>& x) {
-  using S = WideSlot<NT, BLOCK>;
+                                          int q, int r, WideRegs<MT, NT, BLOCK>& x) {
+  using S = WideSlot<MT, NT, BLOCK>;
   // FP6: the slice's 24 bytes start at byte 0 (even j) or 8 (odd j) of the first chunk
   const int odd = j & 1;
   const int o0 = 8 * odd, o1 = odd ? 1024 : 8, o2 = odd ? 1032 : 1024;
@@ -189,7 +193,7 @@ __device__ __forceinline__ void wide_read(const uint8_t* slot, const uint8_t* sa
     if (!BLOCK) x.sb[n] = slot[S::SB + (wv * NT + n) * 256 + lane * 4 + j];  // byte j: slice j
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < MT; ++i) {
     const uint8_t* fr = slot + S::A + i * 2048 + 16 * (4 * r + (q ^ a_swz(r)));
     const uint4 lo = *reinterpret_cast<const uint4*>(fr);
     const uint4 hi = *reinterpret_cast<const uint4*>(fr + 1024);
@@ -200,14 +204,14 @@ __device__ __forceinline__ void wide_read(const uint8_t* slot, const uint8_t* sa
   }
 }
 
-// The 8 x NT MFMAs of one stage, from registers.  The E8M0 scales are single
+// The MT x NT MFMAs of one stage, from registers.  The E8M0 scales are single
 // bytes (op_sel 0), since the slice index is not a compile-time value under a
 // 3-slot ring.
-template <int FMT, int NT, bool BLOCK>
-__device__ __forceinline__ void wide_mfma(const WideRegs<NT, BLOCK>& x, v4f (&acc)[8][NT]) {
+template <int FMT, int MT, int NT, bool BLOCK>
+__device__ __forceinline__ void wide_mfma(const WideRegs<MT, NT, BLOCK>& x, v4f (&acc)[MT][NT]) {
   if (!BLOCK) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int n = 0; n < NT; ++n) acc[i][n] = mfma_step<FMT, 0>(x.a[i], x.b[n], acc[i][n], x.sa[i], x.sb[n]);
   } else {
@@ -218,8 +222,8 @@ __device__ __forceinline__ void wide_mfma(const WideRegs<NT, BLOCK>& x, v4f (&ac
 #pragma unroll
     for (int n = 0; n < NT; ++n) raw[0][n] = mfma_raw<FMT>(x.a[0], x.b[n]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i + 1 < 8) {
+    for (int i = 0; i < MT; ++i) {
+      if (i + 1 < MT) {
 #pragma unroll
         for (int n = 0; n < NT; ++n) raw[(i + 1) & 1][n] = mfma_raw<FMT>(x.a[i + 1], x.b[n]);
       }
@@ -235,11 +239,11 @@ __device__ __forceinline__ void wide_mfma(const WideRegs<NT, BLOCK>& x, v4f (&ac
 // Scheduling groups for one step (MX): each MFMA followed by its share of the
 // next stage's LDS reads.  (Block-FP8 steps are left to the default schedule,
 // which measured faster than any grouping of their scale folds.)
-template <int FMT, int NT, bool BLOCK>
+template <int FMT, int MT, int NT, bool BLOCK>
 __device__ __forceinline__ void wide_interleave() {
   if (!BLOCK) {
-    constexpr int kMfma = 8 * NT;
-    constexpr int kReads = 16 + 8 + (FMT == kE4M3 ? 2 * NT : 3 * NT) + NT;
+    constexpr int kMfma = MT * NT;
+    constexpr int kReads = 2 * MT + MT + (FMT == kE4M3 ? 2 * NT : 3 * NT) + NT;
     constexpr int kPer = (kReads + kMfma - 1) / kMfma;
 #pragma unroll
     for (int k = 0; k < kMfma; ++k) {
@@ -279,24 +283,25 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }  // namespace
 
 struct WideGrid {
-  int64_t mblocks;       // dense: ceil(M / 128); grouped: bound on sum_e ceil(rows_e / 128)
+  int64_t mblocks;       // dense: ceil(M / 16 MT); grouped: bound on sum_e ceil(rows_e / 16 MT)
   int64_t nblocks;       // ceil(N / (64 NT))
   int64_t kt_per_split;  // 512-wide super-tiles per split
   int64_t num_experts;   // grouped only
   int64_t tile0, tiles;  // dense: this launch covers output tiles [tile0, tile0 + tiles) (tile = nb * mblocks + mb)
-  int compact;           // dense, split: partials as [split][tile - tile0][128][64 NT] instead of [split][M][N]
+  int compact;           // dense, split: partials as [split][tile - tile0][16 MT][64 NT] instead of [split][M][N]
 };
 
 // One output tile: rows [row_base, hi) of m-block rows (hi bounds the valid rows
 // of a grouped expert), n-block nb, K split `split`; w / sw are the expert's
 // weights.  The ring and the scale ring are the workgroup's LDS.
-template <int FMT, int NT, bool BLOCK, bool GROUPED>
+template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED>
 __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g, int64_t mb, int64_t row_base,
                                           int64_t hi, const uint8_t* w, const uint8_t* sw, int64_t nb, int64_t split,
                                           float* pdst, int64_t pld, uint8_t* ring, uint8_t* sa_ring, int t, int lane,
                                           int wv, int r, int q) {
-  using S = WideSlot<NT, BLOCK>;
+  using S = WideSlot<MT, NT, BLOCK>;
   constexpr int C = S::COPIES;
+  constexpr int AW = MT / 4, BM = 16 * MT;
   auto a_row = [&](int64_t row) -> int64_t {
     if (row >= hi) row = hi - 1;  // padding rows copy a valid row; their outputs are not stored
     return (GROUPED && p.row_index) ? (int64_t)(p.row_index[row] / p.row_div) : row;
@@ -304,16 +309,17 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
   const int64_t ntiles_total = (p.N + 15) / 16;
   const int64_t nt_wave = (nb * 4 + wv) * NT;
   constexpr int CH = FmtTraits<FMT>::CH;
-  WideLanes<NT> L;
+  WideLanes<MT, NT> L;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < AW; ++i) {
     const int cr = lane >> 2;  // the row this lane copies (row-major chunk order)
-    L.a_off[i] = (uint32_t)(a_row(row_base + (2 * wv + i) * 16 + cr) * p.lda + 16 * ((lane & 3) ^ a_swz(cr)));
+    L.a_off[i] = (uint32_t)(a_row(row_base + (AW * wv + i) * 16 + cr) * p.lda + 16 * ((lane & 3) ^ a_swz(cr)));
   }
-  L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & 127)) : a_row(row_base + (t & 127)) * (p.K / 32));  // t < 128 copy
+  // the scale waves' threads t < BM copy row t
+  L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & (BM - 1))) : a_row(row_base + (t & (BM - 1))) * (p.K / 32));
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t srow = a_row(row_base + 32 * j + 16 * (wv & 1) + (lane >> 2)) * (p.K / 32);
+    const int64_t srow = a_row(row_base + 4 * MT * j + 16 * (wv % S::SW) + (lane >> 2)) * (p.K / 32);
     L.sa_piece[j] = (uint32_t)(srow + 4 * (lane & 3));
     const int64_t last = 16 * (p.KT - 1) + 4 * (lane & 3);
     L.sa_last[j] = (uint32_t)(srow + (last < p.K / 32 - 4 ? last : p.K / 32 - 4));
@@ -334,9 +340,9 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
   const int64_t tb = split * g.kt_per_split * 4;
   const int64_t te = tb + g.kt_per_split * 4 < T ? tb + g.kt_per_split * 4 : T;
 
-  v4f acc[8][NT];
+  v4f acc[MT][NT];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
 
@@ -344,22 +350,23 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     constexpr int R = S::SLOTS;
     // prologue: the scale ring entry of the first super-tile; stages tb .. tb + R - 1
     // fill the ring; stage tb is read into registers
-    if (S::SA_RING && wv < 2) {
+    if (S::SA_RING && wv < S::SW) {
       const bool half = (tb >> 2) == p.KT - 1 && p.K % kTileK != 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t dst = lds_addr(sa_ring + ((tb >> 2) % 3) * 2048 + (32 * j + 16 * wv) * 16);
+        const uint32_t dst = lds_addr(sa_ring + ((tb >> 2) % 3) * S::RING_ENTRY + (4 * MT * j + 16 * wv) * 16);
         if (half) copy4(static_cast<const uint8_t*>(p.sa), L.sa_last[j], dst);
         else copy4(static_cast<const uint8_t*>(p.sa) + (tb >> 2) * 16, L.sa_piece[j], dst);
       }
     }
 #pragma unroll
     for (int k = 0; k < R; ++k)
-      if (tb + k < te) wide_copy<FMT, NT, BLOCK>(p, ring + k * S::BYTES, tb + k, wv, lane, L, sa_ring);
-    wide_wait<C, R - 1>((int)(te - 1 - tb < R - 1 ? te - 1 - tb : R - 1), wv < 2);
+      if (tb + k < te) wide_copy<FMT, MT, NT, BLOCK>(p, ring + k * S::BYTES, tb + k, wv, lane, L, sa_ring);
+    wide_wait<C, R - 1>((int)(te - 1 - tb < R - 1 ? te - 1 - tb : R - 1), wv < S::SW);
     wide_barrier();
-    WideRegs<NT, BLOCK> x0, x1;
-    wide_read<FMT, NT, BLOCK>(ring, sa_ring + ((tb >> 2) % 3) * 2048, (int)(tb & 3), wv, lane, q, r, x0);
+    WideRegs<MT, NT, BLOCK> x0, x1;
+    wide_read<FMT, MT, NT, BLOCK>(ring, sa_ring + ((tb >> 2) % 3) * S::RING_ENTRY, (int)(tb & 3), wv, lane, q, r,
+                                  x0);
     if (BLOCK) x0.sbv = sbp[tb];
 
 // Step tt = t0 + I (ring slot I % R): wait for stage tt + 1 and for this wave's
@@ -375,16 +382,17 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     if (tt < te) {                                                                                  \
       if (tt + 1 < te) {                                                                            \
         const int64_t later = te - 2 - tt < R - 2 ? te - 2 - tt : R - 2;                            \
-        wide_wait<C, R - 2>((int)later, wv < 2);                                                           \
+        wide_wait<C, R - 2>((int)later, wv < S::SW);                                                  \
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                          \
         wide_barrier();                                                                             \
-        if (tt + R < te) wide_copy<FMT, NT, BLOCK>(p, ring + ((I_) % R) * S::BYTES, tt + R, wv, lane, L, sa_ring); \
+        if (tt + R < te) wide_copy<FMT, MT, NT, BLOCK>(p, ring + ((I_) % R) * S::BYTES, tt + R, wv, lane, L, sa_ring); \
       }                                                                                             \
-      wide_read<FMT, NT, BLOCK>(ring + ((I_ + 1) % R) * S::BYTES, sa_ring + (((tt + 1) >> 2) % 3) * 2048,  \
+      wide_read<FMT, MT, NT, BLOCK>(ring + ((I_ + 1) % R) * S::BYTES,                               \
+                                    sa_ring + (((tt + 1) >> 2) % 3) * S::RING_ENTRY,            \
                                 (int)((tt + 1) & 3), wv, lane, q, r, NXT_);                         \
       if (BLOCK) NXT_.sbv = sbp[tt + 1 < te ? tt + 1 : tt];                                         \
-      wide_mfma<FMT, NT, BLOCK>(CUR_, acc);                                                         \
-      wide_interleave<FMT, NT, BLOCK>();                                                            \
+      wide_mfma<FMT, MT, NT, BLOCK>(CUR_, acc);                                                     \
+      wide_interleave<FMT, MT, NT, BLOCK>();                                                        \
     }                                                                                               \
   }
 
@@ -409,26 +417,26 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
   }
 
   // Epilogue through LDS: the waves write their fp32 accumulators into a
-  // row-major 128 x 64 NT tile (row stride padded by 4 floats, so the 64 lanes
+  // row-major 16 MT x 64 NT tile (row stride padded by 4 floats, so the 64 lanes
   // of a write -- rows 4 q + e, column r -- hit 64 distinct banks), then all
   // threads store whole 16-byte pieces of output rows.  Lane-scattered 2-byte
   // stores straight from the accumulator layout would cost a store instruction
   // per 64 values with 64-bit address arithmetic for each.
   constexpr int TW = 64 * NT, ST = TW + 4;
-  static_assert(128 * ST * 4 <= S::SLOTS * S::BYTES, "epilogue tile exceeds the ring");
+  static_assert(BM * ST * 4 <= S::SLOTS * S::BYTES, "epilogue tile exceeds the ring");
   float* const tile = reinterpret_cast<float*>(ring);
   wide_barrier();  // every wave is past its last fragment reads
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) tile[(16 * i + 4 * q + e) * ST + 16 * (wv * NT + n) + r] = acc[i][n][e];
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const int64_t col0 = nb * TW;
   if (p.S > 1) {  // fp32 partials, 4 columns per piece, row rr of the tile at pdst + rr * pld
     const bool vec = pld % 4 == 0 && (reinterpret_cast<uintptr_t>(pdst) & 15) == 0;
-    for (int c = t; c < 128 * (TW / 4); c += 256) {
+    for (int c = t; c < BM * (TW / 4); c += 256) {
       const int rr = c / (TW / 4), cc = (c % (TW / 4)) * 4;
       const int64_t row = row_base + rr, col = col0 + cc;
       if (row >= hi || col >= p.N) continue;
@@ -443,7 +451,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     }
   } else {  // bf16 out (bias added in bf16), 8 columns per piece
     const bool vec = p.ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
-    for (int c = t; c < 128 * (TW / 8); c += 256) {
+    for (int c = t; c < BM * (TW / 8); c += 256) {
       const int rr = c / (TW / 8), cc = (c % (TW / 8)) * 8;
       const int64_t row = row_base + rr, col = col0 + cc;
       if (row >= hi || col >= p.N) continue;
@@ -475,13 +483,14 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
 // Largest number of experts the grouped variant keeps in LDS.
 constexpr int kWideMaxExperts = (int)kWideGroupedMaxExperts;
 
-template <int FMT, int NT, bool BLOCK, bool GROUPED>
+template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED>
 __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g) {
-  using S = WideSlot<NT, BLOCK>;
+  using S = WideSlot<MT, NT, BLOCK>;
+  constexpr int BM = 16 * MT;
   // the stage ring (the LDS budget of one workgroup per CU); after the last
   // stage it holds the output tile of the epilogue
   __shared__ __attribute__((aligned(16))) uint8_t ring[S::SLOTS * S::BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t sa_ring[S::SA_RING ? 3 * 2048 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sa_ring[S::SA_RING ? 3 * S::RING_ENTRY : 16];
   const int t = threadIdx.x, lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
   const int r = lane & 15, q = lane >> 4;
@@ -497,15 +506,15 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
     const int64_t mb = tile % g.mblocks, nb = tile / g.mblocks;
     constexpr int TW = 64 * NT;
     float* const pdst = p.S == 1 ? nullptr
-                        : g.compact ? p.partial + (split * g.tiles + local) * 128 * TW
-                                    : p.partial + (split * p.M + mb * 128) * p.N + nb * TW;
+                        : g.compact ? p.partial + (split * g.tiles + local) * BM * TW
+                                    : p.partial + (split * p.M + mb * BM) * p.N + nb * TW;
     const int64_t pld = g.compact ? TW : p.N;
-    wide_tile<FMT, NT, BLOCK, GROUPED>(p, g, mb, mb * 128, p.M, p.w, static_cast<const uint8_t*>(p.sw), nb, split,
-                                       pdst, pld, ring, sa_ring, t, lane, wv, r, q);
+    wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, mb * BM, p.M, p.w, static_cast<const uint8_t*>(p.sw), nb,
+                                           split, pdst, pld, ring, sa_ring, t, lane, wv, r, q);
     return;
   }
 
-  // Grouped: persistent workgroups.  The experts' 128-row block counts are
+  // Grouped: persistent workgroups.  The experts' BM-row block counts are
   // prefix-summed once per workgroup into LDS; each workgroup then walks the
   // tiles L = blockIdx, blockIdx + grid, ... of the (m-block bound x n-block)
   // grid (the same XCD remap, so a workgroup stays on its XCD's tiles) and
@@ -520,7 +529,7 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   const int chunk = (E + 255) / 256;
   const int e0 = t * chunk < E ? t * chunk : E, e1 = e0 + chunk < E ? e0 + chunk : E;
   int cnt = 0;
-  for (int e = e0; e < e1; ++e) cnt += (sh_row[e + 1] - sh_row[e] + 127) / 128;
+  for (int e = e0; e < e1; ++e) cnt += (sh_row[e + 1] - sh_row[e] + BM - 1) / BM;
   __shared__ int32_t sh_scan[256];
   sh_scan[t] = cnt;
   __syncthreads();
@@ -533,7 +542,7 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   int base = sh_scan[t] - cnt;  // exclusive prefix of this thread's chunk
   for (int e = e0; e < e1; ++e) {
     sh_pre[e] = base;
-    base += (sh_row[e + 1] - sh_row[e] + 127) / 128;
+    base += (sh_row[e + 1] - sh_row[e] + BM - 1) / BM;
   }
   if (t == 255) sh_pre[E] = sh_scan[255];
   __syncthreads();
@@ -552,7 +561,7 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
       if (sh_pre[e] <= mb && mb < sh_pre[e + 1]) sh_hit = e;
     __syncthreads();
     const int e = __builtin_amdgcn_readfirstlane(sh_hit);
-    wide_tile<FMT, NT, BLOCK, GROUPED>(p, g, mb, sh_row[e] + (mb - sh_pre[e]) * 128, sh_row[e + 1],
+    wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, sh_row[e] + (mb - sh_pre[e]) * BM, sh_row[e + 1],
                                        p.w + e * p.w_expert_stride,
                                        static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride, nb, 0, nullptr,
                                        0, ring, sa_ring, t, lane, wv, r, q);
@@ -567,17 +576,17 @@ __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __re
                                                                const uint16_t* __restrict__ bias,
                                                                uint16_t* __restrict__ out, int64_t M, int64_t N,
                                                                int64_t ldc, int64_t mblocks, int64_t tile0,
-                                                               int64_t tiles, int S, int TW) {
-  const int64_t per_tile = 128 * (TW / 8);
+                                                               int64_t tiles, int S, int BM, int TW) {
+  const int64_t per_tile = (int64_t)BM * (TW / 8);
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= tiles * per_tile) return;
   const int64_t local = id / per_tile, rem = id - local * per_tile;
   const int rr = (int)(rem / (TW / 8)), cc = (int)(rem % (TW / 8)) * 8;
   const int64_t tile = tile0 + local, mb = tile % mblocks, nb = tile / mblocks;
-  const int64_t row = mb * 128 + rr, col = nb * TW + cc;
+  const int64_t row = mb * BM + rr, col = nb * TW + cc;
   if (row >= M || col >= N) return;
-  const float* src = partial + (local * 128 + rr) * TW + cc;
-  const int64_t split_stride = tiles * 128 * TW;
+  const float* src = partial + (local * BM + rr) * TW + cc;
+  const int64_t split_stride = tiles * BM * TW;
   float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
   for (int k = 1; k < S; ++k) {
     const float4 a = *reinterpret_cast<const float4*>(src + k * split_stride);
@@ -605,6 +614,13 @@ __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __re
 // ------------------------------------------------------------ configuration
 
 namespace {
+
+// Optional m-tile count override (tuning runs and tests): MXL_WIDE_MT=4 or 8.
+int wide_mt_override() {
+  const char* v = std::getenv("MXL_WIDE_MT");
+  const int mt = v ? std::atoi(v) : 0;
+  return mt == 4 || mt == 8 ? mt : 0;
+}
 
 // Optional override "NT,S" or "NT,1,h" (hybrid) for tuning runs and tests, e.g.
 // MXL_WIDE_CONFIG=4,3.
@@ -637,19 +653,26 @@ bool wide_hybrid(int64_t tiles, int64_t KT, int64_t cus, WideConfig& c) {
 
 }  // namespace
 
-// Pick the n-tiles per wave and the K split from a time model fitted to
-// measurements on MI355X (clock cycles at 2.4 GHz, one workgroup per CU): a
-// K128 stage costs about 1200 + 900 NT cycles (the stage copies, not the
-// MFMAs, set the pace); weights stream at ~5 TB/s; split partials cost a write
-// and a read of M x N x 4 bytes per split at ~3 TB/s.
+// Stage cost model (clock cycles at 2.4 GHz, one workgroup per CU) fitted to
+// measurements on MI355X: a K128 stage of a 128-row tile costs about
+// 1200 + 900 NT cycles (the stage copies, not the MFMAs, set the pace); a
+// 64-row tile copies half the activations and issues half the MFMAs.
+static double wide_stage_cycles(int mt, int nt) { return mt == 8 ? 1200.0 + 900.0 * nt : 800.0 + 800.0 * nt; }
+
+// Pick the workgroup tile (MT, NT), the K split and the hybrid split from the
+// stage model; weights stream at ~5 TB/s; split partials cost a write and a
+// read of their bytes at ~3 TB/s.
 WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
-  const int64_t KT = (K + kTileK - 1) / kTileK, MB = (M + 127) / 128;
+  const int64_t KT = (K + kTileK - 1) / kTileK;
+  const int mt_force = wide_mt_override();
   int o_nt, o_s;
   bool o_h = false;
   if (wide_override(o_nt, o_s, o_h)) {
+    const int mt = mt_force ? mt_force : 8;
     const int64_t per = (KT + o_s - 1) / o_s;
     WideConfig c{o_nt, (int)((KT + per - 1) / per), per};
-    if (o_h) wide_hybrid(MB * ((N + 64 * o_nt - 1) / (64 * o_nt)), KT, cu_count(), c);
+    c.MT = mt;
+    if (o_h) wide_hybrid(((M + 16 * mt - 1) / (16 * mt)) * ((N + 64 * o_nt - 1) / (64 * o_nt)), KT, cu_count(), c);
     return c;
   }
   const int64_t cus = cu_count();
@@ -657,33 +680,44 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
   double best_cost = 1e300;
   const double wbytes = (double)N * K * (fmt == kE4M3 ? 1.0 : 0.75) + (double)N * K / 32;
   const double hbm = (wbytes + (double)M * K * 1.04) / (5.0e12 / 2.4e9);
+  // dense problems keep 128-row tiles unless forced: measured on the c2/c3/c4 shapes,
+  // 64-row tiles were 2-30 % slower (half the MFMAs per stage for the same weight copies)
+  const int mts[2] = {8, 4};
   const int nts[3] = {4, 2, 1};
-  for (int nt : nts) {
-    const int64_t NBk = (N + 64 * nt - 1) / (64 * nt);
-    const int64_t tiles = MB * NBk;
-    for (int64_t s = 1; s <= KT; ++s) {
-      const int64_t per = (KT + s - 1) / s;
-      if ((KT + per - 1) / per != s) continue;
-      const double rounds = (double)((tiles * s + cus - 1) / cus);
-      const double t_stage = 1200.0 + 900.0 * nt;
-      const double compute = rounds * per * 4 * t_stage + 3000.0;
-      const double partial = s > 1 ? ((double)M * N * 4 * s * 2 + (double)M * N * 2) / (3.0e12 / 2.4e9) : 0.0;
-      const double cost = (compute > hbm ? compute : hbm) + partial;
-      if (cost < best_cost) {
-        best_cost = cost;
-        best = WideConfig{nt, (int)s, per};
-      }
-      WideConfig h{nt, 1, KT};
-      // (64-wide tiles re-read the activations too often for extra rounds to pay off)
-      if (s == 1 && nt >= 2 && wide_hybrid(tiles, KT, cus, h)) {
-        // full rounds, then the split remainder, its partials' round trip and two more launches
-        const double rem = (double)(tiles - h.dp_tiles);
-        const double compute_h = (double)(h.dp_tiles / cus) * KT * 4 * t_stage + (double)h.kt2 * 4 * t_stage + 9000.0;
-        const double partial_h = rem * 128 * 64 * nt * 4 * h.S2 * 2 / (3.0e12 / 2.4e9);
-        const double cost_h = (compute_h > hbm ? compute_h : hbm) + partial_h;
-        if (cost_h < best_cost) {
-          best_cost = cost_h;
-          best = h;
+  for (int mt : mts) {
+    if (mt_force ? mt != mt_force : mt != 8) continue;
+    const int64_t MB = (M + 16 * mt - 1) / (16 * mt);
+    for (int nt : nts) {
+      if (mt == 4 && nt == 1) continue;  // not instantiated
+      const int64_t NBk = (N + 64 * nt - 1) / (64 * nt);
+      const int64_t tiles = MB * NBk;
+      const double t_stage = wide_stage_cycles(mt, nt);
+      for (int64_t s = 1; s <= KT; ++s) {
+        const int64_t per = (KT + s - 1) / s;
+        if ((KT + per - 1) / per != s) continue;
+        const double rounds = (double)((tiles * s + cus - 1) / cus);
+        const double compute = rounds * per * 4 * t_stage + 3000.0;
+        const double partial = s > 1 ? ((double)M * N * 4 * s * 2 + (double)M * N * 2) / (3.0e12 / 2.4e9) : 0.0;
+        const double cost = (compute > hbm ? compute : hbm) + partial;
+        if (cost < best_cost) {
+          best_cost = cost;
+          best = WideConfig{nt, (int)s, per};
+          best.MT = mt;
+        }
+        WideConfig h{nt, 1, KT};
+        h.MT = mt;
+        // (64-wide tiles re-read the activations too often for extra rounds to pay off)
+        if (s == 1 && nt >= 2 && wide_hybrid(tiles, KT, cus, h)) {
+          // full rounds, then the split remainder, its partials' round trip and two more launches
+          const double rem = (double)(tiles - h.dp_tiles);
+          const double compute_h =
+              (double)(h.dp_tiles / cus) * KT * 4 * t_stage + (double)h.kt2 * 4 * t_stage + 9000.0;
+          const double partial_h = rem * 16 * mt * 64 * nt * 4 * h.S2 * 2 / (3.0e12 / 2.4e9);
+          const double cost_h = (compute_h > hbm ? compute_h : hbm) + partial_h;
+          if (cost_h < best_cost) {
+            best_cost = cost_h;
+            best = h;
+          }
         }
       }
     }
@@ -693,8 +727,9 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
 
 int64_t wide_workspace_bytes(const WideConfig& c, int64_t M, int64_t N) {
   if (c.dp_tiles > 0) {
-    const int64_t tiles = ((M + 127) / 128) * ((N + 64 * c.NT - 1) / (64 * c.NT));
-    return (int64_t)c.S2 * (tiles - c.dp_tiles) * 128 * 64 * c.NT * 4;
+    const int64_t bm = 16 * c.MT;
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + 64 * c.NT - 1) / (64 * c.NT));
+    return (int64_t)c.S2 * (tiles - c.dp_tiles) * bm * 64 * c.NT * 4;
   }
   return c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
 }
@@ -704,28 +739,42 @@ bool wide_gemm_eligible(int64_t M, int64_t K) {
   return !(v && v[0] == '1') && M >= 64 && K % 256 == 0 && M * K < (int64_t(1) << 32);
 }
 
+template <int FMT, int MT, bool BLOCK, bool GROUPED>
+static hipError_t launch_wide_mt(const WideConfig& c, const GemmParams& p, const WideGrid& g, int64_t grid,
+                                 hipStream_t s) {
+  const dim3 gr((unsigned)grid), blk(256);
+  if (c.NT == 4) {
+    if constexpr (GROUPED) return hipErrorInvalidValue;  // the grouped variant runs NT <= 2 (LDS)
+    else hipLaunchKernelGGL((gemm_wide_kernel<FMT, MT, 4, BLOCK, GROUPED>), gr, blk, 0, s, p, g);
+  } else if (c.NT == 2) {
+    hipLaunchKernelGGL((gemm_wide_kernel<FMT, MT, 2, BLOCK, GROUPED>), gr, blk, 0, s, p, g);
+  } else if (c.NT == 1) {
+    if constexpr (MT == 4) return hipErrorInvalidValue;  // 64 x 64 tiles are not instantiated
+    else hipLaunchKernelGGL((gemm_wide_kernel<FMT, MT, 1, BLOCK, GROUPED>), gr, blk, 0, s, p, g);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int FMT, bool BLOCK, bool GROUPED>
 static hipError_t launch_wide_fmt(const WideConfig& c, const GemmParams& p, const WideGrid& g, int64_t grid,
                                   hipStream_t s) {
-  if (c.NT == 4) {
-    if constexpr (GROUPED) return hipErrorInvalidValue;  // the grouped variant runs NT <= 2 (LDS)
-    else hipLaunchKernelGGL((gemm_wide_kernel<FMT, 4, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
-  }
-  else if (c.NT == 2) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 2, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
-  else if (c.NT == 1) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 1, BLOCK, GROUPED>), dim3((unsigned)grid), dim3(256), 0, s, p, g);
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  if (c.MT == 8) return launch_wide_mt<FMT, 8, BLOCK, GROUPED>(c, p, g, grid, s);
+  if (c.MT == 4) return launch_wide_mt<FMT, 4, BLOCK, GROUPED>(c, p, g, grid, s);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const GemmParams& p, int64_t num_experts,
                             hipStream_t s) {
+  const int64_t bm = 16 * c.MT;
   WideGrid g{};
   g.nblocks = (p.N + 64 * c.NT - 1) / (64 * c.NT);
   g.kt_per_split = c.kt_per_split;
   g.num_experts = num_experts;
   int64_t grid;
   if (num_experts > 0) {
-    g.mblocks = (p.M + 127) / 128 + num_experts;  // bound on the routed m-blocks
+    g.mblocks = (p.M + bm - 1) / bm + num_experts;  // bound on the routed m-blocks
     grid = g.mblocks * g.nblocks;
     if (grid > cu_count()) grid = cu_count();     // persistent workgroups walk the tiles
     if (fmt == kE4M3) return launch_wide_fmt<kE4M3, false, true>(c, p, g, grid, s);
@@ -733,7 +782,7 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
     if (fmt == kE3M2) return launch_wide_fmt<kE3M2, false, true>(c, p, g, grid, s);
     return hipErrorInvalidValue;
   }
-  g.mblocks = (p.M + 127) / 128;
+  g.mblocks = (p.M + bm - 1) / bm;
   g.tile0 = 0;
   g.tiles = g.mblocks * g.nblocks;
   g.compact = 0;
@@ -761,9 +810,9 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
   gs.compact = 1;
   e = dense(q, gs, gs.tiles * c.S2);
   if (e != hipSuccess) return e;
-  const int64_t items = gs.tiles * 128 * (64 * c.NT / 8);
+  const int64_t items = gs.tiles * bm * (64 * c.NT / 8);
   wide_tile_reduce_kernel<<<dim3((unsigned)((items + 255) / 256)), 256, 0, s>>>(
-      p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, gs.tile0, gs.tiles, c.S2, 64 * c.NT);
+      p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, gs.tile0, gs.tiles, c.S2, (int)bm, 64 * c.NT);
   return hipGetLastError();
 }
 
