@@ -227,3 +227,31 @@ def test_wide_split_repeat_and_replay(pkg, oracle_mod, dev, monkeypatch):
     ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, 0)))
     ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().cpu().numpy()[None, :]))
     _check(first.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,bias", [
+    (1, 18432, 2560, False),   # c3's shape: five waves, double-buffered n-tiles
+    (5, 200, 384, True),       # ragged N, three slices in one super-tile
+    (16, 1024, 5120, False),   # ten super-tiles: two per wave
+    (3, 512, 8192, True),      # the largest K of the streamed block-FP8 path
+    (16, 2560, 9216, False),   # past it: the generic kernel
+])
+def test_stream_block_fp8_gemm(pkg, oracle_mod, dev, M, N, K, bias):
+    """Block-FP8 at decode sizes on the weight-streaming kernel (raw MFMA per K128
+    slice folded with the fp32 activation and weight block scales)."""
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(7 * M + K)
+    Np = (N + 127) // 128 * 128
+    wb = (torch.randn(Np, K, generator=g) * 0.02).reshape(Np // 128, 128, K // 128, 128)
+    sb = (wb.abs().amax(dim=(1, 3)) / 448.0).float()
+    wq = (wb / sb[:, None, :, None]).reshape(Np, K).to(torch.float8_e4m3fn)[:N].contiguous()
+    x = torch.randn(M, K, generator=g).bfloat16()
+    b = (torch.randn(N, generator=g) * 0.5).bfloat16() if bias else None
+    tiled, _ = ops.pack_weight(wq.to(dev), None, 0)
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x.to(dev))
+    y = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, b.to(dev) if bias else None)
+    rq, rs = oracle_mod.quant_block_fp8(x)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.block_fp8_gemm_ref(rq, rs, wq.view(torch.uint8).numpy(), sb.numpy()))
+    if bias:
+        ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().numpy()[None, :]))
+    _check(y.float().cpu().numpy(), ref)

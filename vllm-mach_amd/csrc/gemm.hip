@@ -441,9 +441,9 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
   p.row_div = 1;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
-  if (!block && stream_gemm_eligible(M, K)) {
+  if (stream_gemm_eligible(M, K, block)) {
     p.S = 1;
-    e = launch_gemm_stream(fmt, p, s);
+    e = launch_gemm_stream(fmt, block, p, s);
   } else if (wide_gemm_eligible(M, K)) {
     WideConfig wc = wide_config(M, N, K, fmt);
     const int64_t need = wide_workspace_bytes(wc, M, N);

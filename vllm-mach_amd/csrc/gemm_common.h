@@ -157,8 +157,8 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
 
 
 
-// Weight-streaming kernel for decode-sized M (gemm_stream.hip).
-bool stream_gemm_eligible(int64_t M, int64_t K);
-hipError_t launch_gemm_stream(int fmt, const GemmParams& p, hipStream_t s);
+// Weight-streaming kernel for decode-sized M (gemm_stream.hip), MX or block-FP8.
+bool stream_gemm_eligible(int64_t M, int64_t K, bool block);
+hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s);
 
 }  // namespace mxl

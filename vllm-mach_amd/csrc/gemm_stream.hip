@@ -20,6 +20,11 @@
 //   * The W per-wave 16 x 16 fp32 partials are summed in LDS in wave order
 //     (double-buffered by n-tile, one barrier per n-tile), rounded to bf16,
 //     bias added in bf16.
+//   * Block-FP8 (E4M3 weights with an fp32 scale per 128 x 128 block, activations
+//     with an fp32 scale per row per 128): each K128 slice is one unscaled MFMA
+//     folded with fma(raw, sa * sb, acc); the activation scales of a lane's four
+//     output rows stay in registers beside its fragments, the weight block scales
+//     ride with each n-tile's weights.  At most eight waves (K <= 8192).
 #include "gemm_common.h"
 
 
@@ -29,6 +34,10 @@ namespace {
 
 constexpr int kStreamMaxWaves = 16;
 constexpr int64_t kStreamMaxK = 12288;  // two super-tiles per wave, at most twelve waves
+// block-FP8 keeps four fp32 activation scales per slice in registers: at most eight
+// waves (two per SIMD, 256 registers each), one super-tile each up to K = 4096, two up to 8192
+constexpr int kStreamBlockMaxWaves = 8;
+constexpr int64_t kStreamBlockMaxK = 8192;
 
 template <int FMT>
 struct StreamFmt {
@@ -36,16 +45,18 @@ struct StreamFmt {
   static constexpr int DW = FMT == kE4M3 ? 8 : 6;  // operand dwords per lane per K128 slice
 };
 
-template <int FMT, int RUN>
+template <int FMT, int RUN, bool BLOCK = false>
 struct StreamB {
   uint32_t d[RUN][4][StreamFmt<FMT>::DW];
   uint32_t s[RUN];  // tiled E8M0 dword of the super-tile (byte j = slice j)
+  float sbv[BLOCK ? RUN : 1][4];  // block-FP8: the weight block scale of slice j (fp32 [N/128, K/128])
   uint32_t bias;    // bf16 bias bits of output column (t % 16) of the n-tile, loaded with the
                     // weights and converted at use, so no wait lands between the prefetches
 };
 
-// Weight operands of super-tile kt of n-tile nt (the lane's 16 bytes of every chunk).
-template <int FMT>
+// Weight operands of super-tile kt of n-tile nt (the lane's 16 bytes of every chunk);
+// with MX scales also the lane's tiled E8M0 dword.
+template <int FMT, bool BLOCK = false>
 __device__ __forceinline__ void stream_load_tile(const uint8_t* w, const uint8_t* sw, int64_t KT, int64_t nt,
                                                  int64_t kt, int lane, uint32_t (&d)[4][StreamFmt<FMT>::DW],
                                                  uint32_t& sd) {
@@ -72,18 +83,57 @@ __device__ __forceinline__ void stream_load_tile(const uint8_t* w, const uint8_t
 #pragma unroll
       for (int k = 0; k < 6; ++k) d[j][k] = all[6 * j + k];
   }
-  sd = *reinterpret_cast<const uint32_t*>(sw + (nt * KT + kt) * 256 + lane * 4);
+  if (BLOCK) sd = 0;
+  else sd = *reinterpret_cast<const uint32_t*>(sw + (nt * KT + kt) * 256 + lane * 4);
 }
 
-template <int FMT, int RUN>
+template <int FMT, int RUN, bool BLOCK>
 __device__ __forceinline__ void stream_load_b(const GemmParams& p, const uint8_t* w, const uint8_t* sw, int64_t nt,
-                                              const int64_t (&kt)[RUN], int lane, StreamB<FMT, RUN>& b) {
+                                              const int64_t (&kt)[RUN], int lane, StreamB<FMT, RUN, BLOCK>& b) {
 #pragma unroll
-  for (int u = 0; u < RUN; ++u) stream_load_tile<FMT>(w, sw, p.KT, nt, kt[u], lane, b.d[u], b.s[u]);
+  for (int u = 0; u < RUN; ++u) stream_load_tile<FMT, BLOCK>(w, sw, p.KT, nt, kt[u], lane, b.d[u], b.s[u]);
+  if constexpr (BLOCK) {  // block scales of the n-tile's 128-row block, clamped inside K
+    const int64_t G = p.K / 128;
+    const float* sbp = reinterpret_cast<const float*>(sw) + (nt / 8) * G;
+#pragma unroll
+    for (int u = 0; u < RUN; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t gi = kt[u] * 4 + j;
+        b.sbv[u][j] = sbp[gi < G ? gi : G - 1];
+      }
+  }
   const int64_t col = nt * 16 + (lane & 15);
   // unconditional load (without a bias, any valid halfword: the value is unused)
   const uint16_t* bp = p.bias ? p.bias + (col < p.N ? col : p.N - 1) : reinterpret_cast<const uint16_t*>(sw);
   b.bias = *bp;
+}
+
+// Block-FP8: each K128 slice is one unscaled MFMA folded in slice order with
+// fma(raw, sa * sb, acc) (sa: the fp32 activation scales of the lane's four rows);
+// even and odd slices feed two accumulators, summed at the end.
+template <int RUN>
+__device__ __forceinline__ v4f stream_mfma_block(const v8i (&a)[RUN][4], const float4 (&s4)[RUN][4],
+                                                 const StreamB<kE4M3, RUN, true>& b, const bool (&valid)[RUN]) {
+  v4f acc[2] = {};
+#pragma unroll
+  for (int u = 0; u < RUN; ++u) {
+    if (!valid[u]) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t* d = b.d[u][j];
+      const v8i bf = v8i{(int)d[0], (int)d[1], (int)d[2], (int)d[3], (int)d[4], (int)d[5], (int)d[6], (int)d[7]};
+      const v4f raw = mfma_raw<kE4M3>(a[u][j], bf);
+      const float sbv = b.sbv[u][j];
+      const float f[4] = {s4[u][j].x * sbv, s4[u][j].y * sbv, s4[u][j].z * sbv, s4[u][j].w * sbv};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j & 1][i] = __builtin_fmaf(raw[i], f[i], acc[j & 1][i]);
+    }
+  }
+  v4f out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = acc[0][i] + acc[1][i];
+  return out;
 }
 
 // With two super-tiles per wave, two independent accumulators (even and odd
@@ -115,8 +165,9 @@ __device__ __forceinline__ v4f stream_mfma(const v8i (&a)[RUN][4], const uint32_
 
 }  // namespace
 
-template <int FMT, int RUN, bool DB>
-__global__ __launch_bounds__(RUN == 1 ? 1024 : 768) void gemm_stream_kernel(GemmParams p) {
+template <int FMT, int RUN, bool DB, bool BLOCK>
+__global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_stream_kernel(GemmParams p) {
+  static_assert(!BLOCK || FMT == kE4M3, "block-FP8 weights are E4M3");
   __shared__ float red[2][kStreamMaxWaves][4][64];
   const int t = threadIdx.x, lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -141,18 +192,35 @@ __global__ __launch_bounds__(RUN == 1 ? 1024 : 768) void gemm_stream_kernel(Gemm
   // fragments and scales, kept in registers for every n-tile (rows >= M read row
   // M - 1 and are never stored; loads are clamped inside K so all are unconditional)
   const int64_t count = g < ntiles ? (ntiles - g + G - 1) / G : 0;  // n-tiles of this workgroup
-  StreamB<FMT, RUN> b0;
-  stream_load_b<FMT, RUN>(p, w, sw, g < ntiles ? g : ntiles - 1, kt, lane, b0);
+  StreamB<FMT, RUN, BLOCK> b0;
+  stream_load_b<FMT, RUN, BLOCK>(p, w, sw, g < ntiles ? g : ntiles - 1, kt, lane, b0);
   // The loads are row-major -- lane l reads piece l % 4 of row l / 4, so four
   // neighbouring lanes move one row's 64 bytes in one access (lanes on sixteen
   // rows, the fragment order, would cost an access each) -- and a lane-permute
   // hands fragment lane 16 q + r its piece q of row r.
   v8i a[RUN][4];
   uint32_t sraw[RUN][4];
+  float4 s4[BLOCK ? RUN : 1][4];  // block-FP8: fp32 scales of the lane's output rows 4 q .. 4 q + 3, slice j
+  if constexpr (BLOCK) {
+    const float* sa = static_cast<const float*>(p.sa);  // column-major [K/128, M]
+    const int64_t G = p.K / 128;
+    int64_t rows[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rows[i] = 4 * q + i < p.M ? 4 * q + i : p.M - 1;
+#pragma unroll
+    for (int u = 0; u < RUN; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t gi = kt[u] * 4 + j < G ? kt[u] * 4 + j : G - 1;
+        s4[u][j] = float4{sa[gi * p.M + rows[0]], sa[gi * p.M + rows[1]], sa[gi * p.M + rows[2]],
+                          sa[gi * p.M + rows[3]]};
+      }
+  }
   {
     const int cr = lane >> 2, cp = lane & 3;
     const int64_t row = cr < p.M ? cr : p.M - 1;
-    const uint8_t* srow = static_cast<const uint8_t*>(p.sa) + row * (p.K / 32);
+    // (block-FP8 has no E8M0 scales: any valid address, the dword is unused)
+    const uint8_t* srow = BLOCK ? p.a : static_cast<const uint8_t*>(p.sa) + row * (p.K / 32);
     const uint8_t* arow = p.a + row * p.lda;
     const int from = 4 * (4 * r + q);  // byte address of the source lane (4 r + q)
 #pragma unroll
@@ -167,7 +235,7 @@ __global__ __launch_bounds__(RUN == 1 ? 1024 : 768) void gemm_stream_kernel(Gemm
       }
       // scale dword of slice cp (E8M0 of blocks 4 cp .. 4 cp + 3 of the super-tile)
       const int64_t ks = kt[u] * kTileK + 128 * cp;
-      const uint32_t sd = *reinterpret_cast<const uint32_t*>(srow + (ks < p.K ? ks : p.K - 128) / 32);
+      const uint32_t sd = BLOCK ? 0u : *reinterpret_cast<const uint32_t*>(srow + (ks < p.K ? ks : p.K - 128) / 32);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t x[8] = {lo[j].x, lo[j].y, lo[j].z, lo[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
@@ -210,35 +278,39 @@ __global__ __launch_bounds__(RUN == 1 ? 1024 : 768) void gemm_stream_kernel(Gemm
     }
   };
 
+  auto mma = [&](const StreamB<FMT, RUN, BLOCK>& b) -> v4f {
+    if constexpr (BLOCK) return stream_mfma_block<RUN>(a, s4, b, valid);
+    else return stream_mfma<FMT, RUN>(a, sa, b, valid);
+  };
   if (DB) {
-    StreamB<FMT, RUN> b1;
+    StreamB<FMT, RUN, BLOCK> b1;
     for (int64_t j = 0; j < count; j += 2) {
       const int64_t nt0 = g + j * G;
       // prefetch the second n-tile of the pair (or re-read the first)
       const int64_t nt1 = j + 1 < count ? nt0 + G : nt0;
-      stream_load_b<FMT, RUN>(p, w, sw, nt1, kt, lane, b1);
-      finish(stream_mfma<FMT, RUN>(a, sa, b0, valid), b0.bias, nt0, 0);
+      stream_load_b<FMT, RUN, BLOCK>(p, w, sw, nt1, kt, lane, b1);
+      finish(mma(b0), b0.bias, nt0, 0);
       const int64_t nt2 = j + 2 < count ? nt0 + 2 * G : nt1;
-      stream_load_b<FMT, RUN>(p, w, sw, nt2, kt, lane, b0);
-      if (j + 1 < count) finish(stream_mfma<FMT, RUN>(a, sa, b1, valid), b1.bias, nt1, 1);
+      stream_load_b<FMT, RUN, BLOCK>(p, w, sw, nt2, kt, lane, b0);
+      if (j + 1 < count) finish(mma(b1), b1.bias, nt1, 1);
     }
   } else {
     for (int64_t j = 0; j < count; ++j) {
       const int64_t nt = g + j * G;
-      if (j > 0) stream_load_b<FMT, RUN>(p, w, sw, nt, kt, lane, b0);
-      finish(stream_mfma<FMT, RUN>(a, sa, b0, valid), b0.bias, nt, (int)(j & 1));
+      if (j > 0) stream_load_b<FMT, RUN, BLOCK>(p, w, sw, nt, kt, lane, b0);
+      finish(mma(b0), b0.bias, nt, (int)(j & 1));
     }
   }
 }
 
 // ------------------------------------------------------------ configuration
 
-// One super-tile per wave (double-buffered) up to 16 super-tiles (K <= 8192);
+// MX: one super-tile per wave (double-buffered) up to 16 super-tiles (K <= 8192);
 // two per wave, single-buffered, up to 24 (K <= 12288, twelve waves of at most
 // 168 registers).  A super-tile costs 32 + 4 VGPRs of activations and 32 (24
 // for FP6) + 1 of weights per buffer.
-bool stream_gemm_eligible(int64_t M, int64_t K) {
-  return M >= 1 && M <= 16 && K % 128 == 0 && K >= 128 && K <= kStreamMaxK;
+bool stream_gemm_eligible(int64_t M, int64_t K, bool block) {
+  return M >= 1 && M <= 16 && K % 128 == 0 && K >= 128 && K <= (block ? kStreamBlockMaxK : kStreamMaxK);
 }
 
 // Compute units of the current device (cached per device).
@@ -255,24 +327,26 @@ int cu_count() {
 }
 
 namespace {
-template <int FMT>
+template <int FMT, bool BLOCK>
 hipError_t launch_stream_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
-  if (p.KT <= kStreamMaxWaves) {
-    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
+  if (p.KT <= (BLOCK ? kStreamBlockMaxWaves : kStreamMaxWaves)) {
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, BLOCK>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
   } else {
-    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 2, false>), grid, dim3((unsigned)((p.KT + 1) / 2 * 64)), 0, s, p);
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 2, false, BLOCK>), grid, dim3((unsigned)((p.KT + 1) / 2 * 64)), 0,
+                       s, p);
   }
   return hipGetLastError();
 }
 }  // namespace
 
-hipError_t launch_gemm_stream(int fmt, const GemmParams& p, hipStream_t s) {
+hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s) {
   const int64_t ntiles = (p.N + 15) / 16;
   const int64_t G = ntiles < cu_count() ? ntiles : cu_count();
   const dim3 grid((unsigned)G);
-  if (fmt == kE4M3) return launch_stream_fmt<kE4M3>(p, grid, s);
-  if (fmt == kE2M3) return launch_stream_fmt<kE2M3>(p, grid, s);
-  if (fmt == kE3M2) return launch_stream_fmt<kE3M2>(p, grid, s);
+  if (block) return fmt == kE4M3 ? launch_stream_fmt<kE4M3, true>(p, grid, s) : hipErrorInvalidValue;
+  if (fmt == kE4M3) return launch_stream_fmt<kE4M3, false>(p, grid, s);
+  if (fmt == kE2M3) return launch_stream_fmt<kE2M3, false>(p, grid, s);
+  if (fmt == kE3M2) return launch_stream_fmt<kE3M2, false>(p, grid, s);
   return hipErrorInvalidValue;
 }
 
