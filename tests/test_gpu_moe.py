@@ -160,3 +160,46 @@ def test_moe_graph_replay_changing_routes(pkg, oracle_mod, dev):
             got = replayed.float().cpu().numpy()
             assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
     torch.cuda.current_stream().wait_stream(stream)
+
+
+@pytest.mark.parametrize("E,N,K,T,topk,gathered,fmt,skew", [
+    (256, 1024, 2048, 128, 8, True, 2, False),   # the MoE gate_up at T = 128 (c5)
+    (256, 2048, 512, 128, 8, False, 2, False),   # the MoE down projection at T = 128 (c5)
+    (8, 384, 1024, 20, 2, True, 0, True),        # E4M3: an expert with 30 rows (two units), empty experts
+    (16, 200, 1280, 40, 2, True, 3, True),       # ragged N, K % 512 != 0 (three K waves, five n-lanes)
+    (4, 256, 4096, 9, 2, True, 0, False),        # eight K waves (E4M3's largest K)
+])
+def test_grouped_stream_small_batch(pkg, oracle_mod, dev, monkeypatch, E, N, K, T, topk, gathered, fmt, skew):
+    """Few routed rows per expert: persistent workgroups stream each expert's weights past its
+    16-row tiles.  Checked against the oracle, and bit for bit against the per-expert kernel
+    when both sum one super-tile per wave in K order (K <= 2048)."""
+    from test_gpu_gemm import _act, _check, _weights
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(E + N + K)
+    ids = torch.randint(0, E, (T, topk), generator=g, dtype=torch.int32)
+    if skew:
+        ids[:15, 0] = 0
+        ids[ids == 1] = 2
+    parts = [_weights(oracle_mod, N, K, fmt, 0.02, 200 + e) for e in range(E)]
+    w_t, s_t = ops.pack_weight(torch.from_numpy(np.stack([p_[2] for p_ in parts])).to(dev),
+                               torch.from_numpy(np.stack([p_[1] for p_ in parts])).to(dev), fmt)
+    routes, offsets, _ = torch.ops.mach_amd.moe_route(ids.to(dev), E)
+    R = T * topk
+    assert R < 32 * E  # the small-batch path
+    x = _act(T if gathered else R, K, 5)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    args = (a, sa, routes, topk) if gathered else (a, sa, None, 1)
+    y = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
+    monkeypatch.setenv("MXL_GROUPED_STREAM", "0")
+    y_ref_kernel = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
+    if K <= 2048:
+        assert torch.equal(y, y_ref_kernel)
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    off, rt, got = offsets.cpu().numpy(), routes.cpu().numpy(), y.float().cpu().numpy()
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if lo == hi or (E > 16 and e % 8):
+            continue
+        rows = rt[lo:hi] // topk if gathered else np.arange(lo, hi)
+        ref = oracle_mod.mx_gemm_ref(rc[rows], rs[rows], parts[e][0], parts[e][1], fmt)
+        _check(got[lo:hi], oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref)))

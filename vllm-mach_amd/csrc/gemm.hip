@@ -579,6 +579,23 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
     }
     return MXL_OK;
   }
+  const char* sg_env = std::getenv("MXL_GROUPED_STREAM");  // tuning runs and tests: 0 = per-expert kernel
+  if (stream_grouped_eligible(K, num_experts, w_fmt) && !(sg_env && sg_env[0] == '0')) {
+    // few rows per expert: persistent workgroups stream each expert's weights past its rows
+    GemmParams p{};
+    p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;
+    p.out = (uint16_t*)out; p.row_index = row_index; p.expert_offsets = expert_offsets;
+    p.lda = K; p.ldc = N; p.M = routed_rows; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = a_rows;
+    p.w_expert_stride = mxl_tiled_weight_bytes(N, K, w_fmt);
+    p.sw_expert_stride = mxl_tiled_scale_bytes(N, K);
+    p.row_div = row_div; p.S = 1;
+    hipError_t e = launch_gemm_stream_grouped(w_fmt, p, num_experts, (hipStream_t)stream);
+    if (e != hipSuccess) {
+      set_error("mxl_grouped_gemm: launch failed: %s", hipGetErrorString(e));
+      return MXL_EHIP;
+    }
+    return MXL_OK;
+  }
   GemmConfig c;
   const int64_t KT = (K + kTileK - 1) / kTileK;
   c.MT = 1; c.NT = 1; c.S = 1;

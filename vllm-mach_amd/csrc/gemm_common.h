@@ -160,5 +160,9 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
 // Weight-streaming kernel for decode-sized M (gemm_stream.hip), MX or block-FP8.
 bool stream_gemm_eligible(int64_t M, int64_t K, bool block);
 hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s);
+// Grouped (MoE) variant for few rows per expert: persistent workgroups over
+// (expert, 16-row tile) units, each streaming the expert's weights.
+bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt);
+hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, hipStream_t s);
 
 }  // namespace mxl

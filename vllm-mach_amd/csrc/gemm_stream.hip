@@ -38,6 +38,7 @@ constexpr int64_t kStreamMaxK = 12288;  // two super-tiles per wave, at most twe
 // waves (two per SIMD, 256 registers each), one super-tile each up to K = 4096, two up to 8192
 constexpr int kStreamBlockMaxWaves = 8;
 constexpr int64_t kStreamBlockMaxK = 8192;
+constexpr int kStreamGroupedMaxExperts = 1024;
 
 template <int FMT>
 struct StreamFmt {
@@ -303,6 +304,142 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
   }
 }
 
+// Grouped (MoE) decode-sized GEMM: few routed rows per expert.  A persistent
+// workgroup owns one unit -- 16 routed rows (one m-tile) of one expert -- at a time
+// and streams all of that expert's weight n-tiles past the unit's activation
+// fragments, which each wave gathers once into registers.  Its WK x NW waves split
+// K (wave w takes super-tile w % WK) and N (n-lane w / WK takes n-tiles w / WK,
+// + NW, ...), so a CU keeps many weight fragments in flight even when K is one
+// super-tile; per round of NW n-tiles the WK partials of each are summed in LDS in
+// K order.  Units are numbered expert by expert (a block scan of the experts' m-tile
+// counts in LDS), so the launch needs no host-side counts.
+// Waves per workgroup: sixteen for FP6 weights; eight for E4M3, whose double-buffered
+// fragments need more than the 128 registers a sixteen-wave workgroup leaves a wave.
+template <int FMT>
+constexpr int stream_grouped_waves() { return FMT == kE4M3 ? 8 : 16; }
+
+template <int FMT>
+__global__ __launch_bounds__(64 * stream_grouped_waves<FMT>()) void gemm_stream_grouped_kernel(GemmParams p, int E,
+                                                                                            int WK, int NW) {
+  __shared__ float red[2][kStreamMaxWaves][4][64];
+  __shared__ int32_t sh_pre[kStreamGroupedMaxExperts + 1];  // m-tiles before expert e
+  __shared__ int32_t sh_off[kStreamGroupedMaxExperts + 1];  // expert_offsets
+  __shared__ int32_t sh_scan[1024];
+  const int t = threadIdx.x, lane = t & 63, nthreads = (int)blockDim.x;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int kw = wv % WK, nl = wv / WK;
+  const int64_t ntiles = (p.N + 15) / 16;
+
+  for (int e = t; e <= E; e += nthreads) sh_off[e] = (int32_t)p.expert_offsets[e];
+  __syncthreads();
+  // m-tile counts per thread chunk of experts, then a block-wide inclusive scan
+  const int chunk = (E + nthreads - 1) / nthreads;
+  const int e0 = t * chunk < E ? t * chunk : E, e1 = e0 + chunk < E ? e0 + chunk : E;
+  int cnt = 0;
+  for (int e = e0; e < e1; ++e) cnt += (sh_off[e + 1] - sh_off[e] + 15) / 16;
+  sh_scan[t] = cnt;
+  __syncthreads();
+  for (int off = 1; off < nthreads; off <<= 1) {
+    const int v = t >= off ? sh_scan[t - off] : 0;
+    __syncthreads();
+    sh_scan[t] += v;
+    __syncthreads();
+  }
+  int base = sh_scan[t] - cnt;
+  for (int e = e0; e < e1; ++e) {
+    sh_pre[e] = base;
+    base += (sh_off[e + 1] - sh_off[e] + 15) / 16;
+  }
+  if (t == nthreads - 1) sh_pre[E] = sh_scan[t];
+  __syncthreads();
+  const int units = __builtin_amdgcn_readfirstlane(sh_pre[E]);
+
+  int buf = 0;
+  for (int u = (int)blockIdx.x; u < units; u += (int)gridDim.x) {
+    // the expert owning unit u: the largest e with sh_pre[e] <= u
+    int lo_e = 0, hi_e = E - 1;
+    while (lo_e < hi_e) {
+      const int mid = (lo_e + hi_e + 1) >> 1;
+      if (__builtin_amdgcn_readfirstlane(sh_pre[mid]) <= u) lo_e = mid;
+      else hi_e = mid - 1;
+    }
+    const int e = lo_e;
+    const int64_t lo = __builtin_amdgcn_readfirstlane(sh_off[e] + (u - sh_pre[e]) * 16);
+    const int64_t end = __builtin_amdgcn_readfirstlane(sh_off[e + 1]);
+    const int64_t hi = lo + 16 < end ? lo + 16 : end;
+    const uint8_t* w = p.w + e * p.w_expert_stride;
+    const uint8_t* sw = static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride;
+    const int64_t kt1[1] = {kw < p.KT ? kw : p.KT - 1};
+    const bool valid[1] = {kw < p.KT};
+
+    // the first round's weights first, then the unit's gathered activation fragments
+    StreamB<FMT, 1> b0, b1;
+    auto nt_of = [&](int64_t round) -> int64_t {
+      const int64_t nt = nl + round * NW;
+      return nt < ntiles ? nt : ntiles - 1;
+    };
+    stream_load_b<FMT, 1, false>(p, w, sw, nt_of(0), kt1, lane, b0);
+    v8i a[1][4];
+    uint32_t sa[1][4];
+    {
+      const int cr = lane >> 2, cp = lane & 3;
+      int64_t row = lo + cr;
+      if (row >= hi) row = hi - 1;  // padding rows read a valid row and are not stored
+      const int64_t arow = p.row_index ? (int64_t)(p.row_index[row] / p.row_div) : row;
+      const uint8_t* srow = static_cast<const uint8_t*>(p.sa) + arow * (p.K / 32);
+      const uint8_t* ap = p.a + arow * p.lda;
+      const int from = 4 * (4 * r + q);
+      uint4 lo4[4], hi4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t k0 = kt1[0] * kTileK + 128 * j;
+        const int64_t kc = k0 < p.K ? k0 : p.K - 128;
+        lo4[j] = *reinterpret_cast<const uint4*>(ap + kc + 16 * cp);
+        hi4[j] = *reinterpret_cast<const uint4*>(ap + kc + 64 + 16 * cp);
+      }
+      const int64_t ks = kt1[0] * kTileK + 128 * cp;
+      const uint32_t sd = *reinterpret_cast<const uint32_t*>(srow + (ks < p.K ? ks : p.K - 128) / 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t x[8] = {lo4[j].x, lo4[j].y, lo4[j].z, lo4[j].w, hi4[j].x, hi4[j].y, hi4[j].z, hi4[j].w};
+        int y[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) y[k] = __builtin_amdgcn_ds_bpermute(from, (int)x[k]);
+        a[0][j] = v8i{y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]};
+        const uint32_t sraw = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * r + j), (int)sd);
+        const bool in = kt1[0] * kTileK + 128 * j < p.K;
+        sa[0][j] = in ? (sraw >> (8 * q)) & 0xFFu : 0u;
+        if (!in) a[0][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+
+    // the WK partials of each of the round's NW n-tiles, summed in K order, stored as bf16
+    auto finish = [&](const v4f& acc, int64_t round) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[buf][wv][i][lane] = acc[i];
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      for (int o = t; o < 256 * NW; o += nthreads) {
+        const int n = o >> 8, i = (o >> 6) & 3, l = o & 63;
+        float sum = red[buf][n * WK][i][l];
+        for (int v = 1; v < WK; ++v) sum += red[buf][n * WK + v][i][l];
+        const int64_t nt = n + round * NW;
+        const int64_t row = lo + 4 * (l >> 4) + i, col = nt * 16 + (l & 15);
+        if (nt < ntiles && row < hi && col < p.N) p.out[row * p.ldc + col] = f32_to_bf16(sum);
+      }
+      buf ^= 1;
+    };
+
+    const int64_t rounds = (ntiles + NW - 1) / NW;
+    for (int64_t rd = 0; rd < rounds; rd += 2) {
+      stream_load_b<FMT, 1, false>(p, w, sw, nt_of(rd + 1 < rounds ? rd + 1 : rd), kt1, lane, b1);
+      finish(stream_mfma<FMT, 1>(a, sa, b0, valid), rd);
+      stream_load_b<FMT, 1, false>(p, w, sw, nt_of(rd + 2 < rounds ? rd + 2 : rd), kt1, lane, b0);
+      if (rd + 1 < rounds) finish(stream_mfma<FMT, 1>(a, sa, b1, valid), rd + 1);
+    }
+  }
+}
+
 // ------------------------------------------------------------ configuration
 
 // MX: one super-tile per wave (double-buffered) up to 16 super-tiles (K <= 8192);
@@ -338,6 +475,29 @@ hipError_t launch_stream_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
   return hipGetLastError();
 }
 }  // namespace
+
+bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt) {
+  const int waves = fmt == kE4M3 ? stream_grouped_waves<kE4M3>() : stream_grouped_waves<kE2M3>();
+  return K % 128 == 0 && K >= 128 && (K + kTileK - 1) / kTileK <= waves && num_experts >= 1 &&
+         num_experts <= kStreamGroupedMaxExperts;
+}
+
+hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, hipStream_t s) {
+  const int waves = fmt == kE4M3 ? stream_grouped_waves<kE4M3>() : stream_grouped_waves<kE2M3>();
+  const int WK = (int)p.KT;
+  if (WK < 1 || WK > waves) return hipErrorInvalidValue;
+  const int NW = waves / WK;
+  // a bound on the units (m-tiles of routed rows): every expert adds at most one partial tile
+  const int64_t bound = (p.M + 15) / 16 + num_experts;
+  const int64_t G = bound < cu_count() ? bound : cu_count();
+  const dim3 grid((unsigned)G), blk((unsigned)(64 * WK * NW));
+  const int E = (int)num_experts;
+  if (fmt == kE4M3) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE4M3>), grid, blk, 0, s, p, E, WK, NW);
+  else if (fmt == kE2M3) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE2M3>), grid, blk, 0, s, p, E, WK, NW);
+  else if (fmt == kE3M2) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE3M2>), grid, blk, 0, s, p, E, WK, NW);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s) {
   const int64_t ntiles = (p.N + 15) / 16;
