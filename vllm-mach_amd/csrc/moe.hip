@@ -8,7 +8,8 @@
 // Three passes over 1024-route chunks: per-chunk histograms (LDS atomics,
 // order free), one workgroup scanning chunks and experts, then a pass that
 // ranks each route inside its chunk (shuffle count inside the wavefront plus
-// an LDS prefix over the chunk's 16 wavefronts) and scatters.
+// an LDS prefix over the chunk's 16 wavefronts) and scatters.  A single chunk
+// (decode-sized steps) runs all three in one workgroup.
 //
 // Combine: out[t, h] = bf16(sum_k y[inverse[t*topk + k], h] * w[t, k]),
 // each product rounded to binary32 and added in ascending k from zero.
@@ -102,6 +103,63 @@ __global__ __launch_bounds__(kChunk) void route_scatter_kernel(const int32_t* __
   inverse[r] = (int32_t)pos;
 }
 
+// All routes in one chunk (R <= 1024, E <= 1024): the three passes in one
+// workgroup -- per-wavefront expert counts in LDS, per-expert totals scanned into
+// the offsets, then the same rank and scatter -- so a decode-sized step pays one
+// launch.  The result is the multi-chunk path's (chunk base 0).
+constexpr int kSingleMaxExperts = 1024;
+
+__global__ __launch_bounds__(kChunk) void route_single_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
+                                                             int64_t* __restrict__ expert_offsets,
+                                                             int32_t* __restrict__ sorted_routes,
+                                                             int32_t* __restrict__ inverse) {
+  constexpr int W = kChunk / 64;
+  __shared__ int32_t whist[W * kSingleMaxExperts];
+  __shared__ int32_t tot[2][kSingleMaxExperts];
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  for (int i = t; i < W * E; i += kChunk) whist[i] = 0;
+  const int32_t e = t < R ? ids[t] : -1;
+  const bool valid = e >= 0 && e < E;
+  int rank = 0;  // routes of the same expert in earlier lanes of this wavefront
+  for (int l = 0; l < 64; ++l) {
+    const int32_t el = __shfl(e, l);
+    rank += (l < lane && el == e) ? 1 : 0;
+  }
+  __syncthreads();
+  if (valid) atomicAdd(&whist[w * E + e], 1);
+  __syncthreads();
+  for (int x = t; x < E; x += kChunk) {  // per-wavefront bases and the expert's total
+    int32_t run = 0;
+    for (int v = 0; v < W; ++v) {
+      const int32_t n = whist[v * E + x];
+      whist[v * E + x] = run;
+      run += n;
+    }
+    tot[0][x] = run;
+  }
+  __syncthreads();
+  int src = 0;  // inclusive scan of the totals (ping-pong)
+  for (int d = 1; d < E; d <<= 1) {
+    for (int x = t; x < E; x += kChunk) {
+      int32_t v = tot[src][x];
+      if (x >= d) v += tot[src][x - d];
+      tot[1 - src][x] = v;
+    }
+    __syncthreads();
+    src = 1 - src;
+  }
+  for (int x = t; x < E; x += kChunk) expert_offsets[x + 1] = tot[src][x];
+  if (t == 0) expert_offsets[0] = 0;
+  if (t >= R) return;
+  if (!valid) {
+    inverse[t] = -1;
+    return;
+  }
+  const int32_t pos = (e > 0 ? tot[src][e - 1] : 0) + whist[w * E + e] + rank;
+  sorted_routes[pos] = t;
+  inverse[t] = pos;
+}
+
 // One thread: 8 consecutive hidden columns of one token.
 __global__ __launch_bounds__(256) void moe_reduce_kernel(const uint16_t* __restrict__ y,
                                                          const float* __restrict__ topk_weights,
@@ -153,6 +211,11 @@ extern "C" int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, i
                 "mxl_moe_route: workspace too small (%lld < %lld bytes)", (long long)workspace_bytes,
                 (long long)mxl_moe_route_workspace_bytes(T, topk, E));
   hipStream_t s = (hipStream_t)stream;
+  if (R <= kChunk && E <= kSingleMaxExperts) {  // one chunk: one launch
+    route_single_kernel<<<1, kChunk, 0, s>>>(topk_ids, R, (int)E, expert_offsets, sorted_routes, inverse);
+    MXL_CHECK_LAUNCH("mxl_moe_route(single)");
+    return MXL_OK;
+  }
   int32_t* counts = (int32_t*)workspace;
   if (C > 0) {
     route_hist_kernel<<<dim3((unsigned)C), kChunk, E * sizeof(int32_t), s>>>(topk_ids, R, (int)E, counts);
