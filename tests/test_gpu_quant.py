@@ -106,3 +106,73 @@ def test_quantize_mxfp6_bit_exact(pkg, oracle_mod, dev, fmt, M, K, std):
     rc, rs = oracle_mod.quant_mxfp6(w, fmt)
     assert np.array_equal(scales.cpu().numpy(), rs)
     assert np.array_equal(packed.cpu().numpy(), oracle_mod.pack_fp6(rc))
+
+
+# ---------------------------------------------------------- every bf16 input
+
+def _every_bf16(rows, K, seed=None):
+    """All 65536 bf16 bit patterns once -- signed zeros, subnormals, infinities and
+    NaNs of both signs and many payloads -- row-major, in order (so blocks mix
+    infinities with NaNs) or in a seeded random order."""
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    if seed is not None:
+        pats = pats[np.random.default_rng(seed).permutation(65536)]
+    assert rows * K == 65536
+    return torch.from_numpy(pats.view(np.int16).copy()).view(torch.bfloat16).reshape(rows, K)
+
+
+@pytest.mark.parametrize("rule", [0, 1])
+@pytest.mark.parametrize("seed", [None, 11])
+def test_quantize_mxfp8_every_bf16(pkg, oracle_mod, dev, rule, seed):
+    x = _every_bf16(8, 8192, seed)
+    codes, scales = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), rule)
+    rc, rs = oracle_mod.quant_mxfp8(x, rule)
+    assert np.array_equal(_u8(scales), rs)
+    assert np.array_equal(_u8(codes), rc)
+    hi, shi, res, sres = torch.ops.mach_amd.quantize_mxfp8_dual(x.to(dev), rule)
+    oh, osh, ores, osres = oracle_mod.quant_mxfp8_dual(x, rule)
+    for got, want in ((hi, oh), (shi, osh), (res, ores), (sres, osres)):
+        assert np.array_equal(_u8(got), want)
+
+
+@pytest.mark.parametrize("rule", [0, 1])
+@pytest.mark.parametrize("seed", [None, 12])
+def test_swiglu_mxfp8_every_bf16(pkg, oracle_mod, dev, rule, seed):
+    """Every bf16 pattern as gate (up ~ N(0,1)) and as up (gate ~ N(0,1))."""
+    pats = _every_bf16(8, 8192, seed)
+    other = _inputs(8, 8192, 1.0, 99, outliers=False)
+    for gu in (torch.cat([pats, other], dim=1), torch.cat([other, pats], dim=1)):
+        codes, scales = torch.ops.mach_amd.swiglu_mxfp8(gu.to(dev), rule, False)
+        rc, rs = oracle_mod.swiglu_mxfp8(gu, rule)
+        assert np.array_equal(_u8(scales), rs)
+        assert np.array_equal(_u8(codes), rc)
+
+
+@pytest.mark.parametrize("seed", [None, 13])
+def test_block_fp8_producers_every_bf16(pkg, oracle_mod, dev, seed):
+    x = _every_bf16(8, 8192, seed)
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x.to(dev))
+    rq, rsc = oracle_mod.quant_block_fp8(x)
+    assert np.array_equal(_u8(q), rq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), np.ascontiguousarray(rsc).view(np.uint32))
+    other = _inputs(8, 8192, 1.0, 98, outliers=False)
+    for gu in (torch.cat([x, other], dim=1), torch.cat([other, x], dim=1)):
+        out = torch.empty(8, 8192, dtype=torch.float8_e4m3fn, device=dev)
+        scales = torch.empty(8, 64, dtype=torch.float32, device=dev)
+        torch.ops.mach_amd.silu_and_mul_per_block_quant(out, gu.to(dev), scales, False)
+        rq, rs = oracle_mod.silu_mul_block_fp8(gu, False)
+        assert np.array_equal(_u8(out), rq)
+        assert np.array_equal(scales.cpu().numpy().view(np.uint32), np.ascontiguousarray(rs).view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", [2, 3])
+@pytest.mark.parametrize("seed", [None, 14])
+def test_quantize_mxfp6_every_bf16(pkg, oracle_mod, dev, fmt, seed):
+    """Weights are finite: the two infinity patterns are zeroed (the scale of a block
+    with an infinite amax is left unspecified); NaNs, subnormals and signed zeros stay."""
+    w = _every_bf16(8, 8192, seed)
+    w[torch.isinf(w)] = 0
+    packed, scales = torch.ops.mach_amd.quantize_mxfp6(w.to(dev), fmt)
+    rc, rs = oracle_mod.quant_mxfp6(w, fmt)
+    assert np.array_equal(scales.cpu().numpy(), rs)
+    assert np.array_equal(packed.cpu().numpy(), oracle_mod.pack_fp6(rc))

@@ -2,8 +2,9 @@
 //
 // Every conversion here is a binary32 / integer operation sequence with
 // round-to-nearest-even and no contraction (the library is compiled with
-// -ffp-contract=off; fused steps call __builtin_fmaf explicitly), so codes
-// and scales are bit-identical to a CPU evaluation of the same sequence.
+// -ffp-contract=off; fused steps call __builtin_fmaf explicitly), or a hardware
+// conversion shown equal to such a sequence on every input, so codes and scales
+// are bit-identical to a CPU evaluation of the same sequence.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -25,14 +26,51 @@ __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(flo
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 
+// Hardware pair conversions of gfx950.  Each was compared on the device with the
+// integer sequence it replaces for all 2^32 binary32 inputs:
+//  * v_cvt_pk_bf16_f32 (RNE) equals (u + 0x7FFF + bit16(u)) >> 16 on every non-NaN
+//    input, overflow to infinity and subnormals included; a NaN keeps its sign and
+//    the top of its payload.
+//  * v_cvt_pk_fp8_f32 (OCP E4M3, RNE, no clamp) equals f32_to_e4m3 on every non-NaN
+//    input (values from 464 up and infinities give sign | 0x7F); every NaN gives 0xFF.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// bf16 bits of (lo, hi) in the low / high half; NaN payloads pass through
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
 // round-to-nearest-even binary32 -> bf16, NaN -> 0x7FC0
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = f2u(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
-  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+  return f != f ? (uint16_t)0x7FC0 : (uint16_t)cvt_pk_bf16(f, 0.0f);
 }
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// bf16_round of a pair in one conversion, without NaN canonicalization: a NaN stays
+// a NaN of unspecified sign and payload (for values whose NaNs are all coded alike)
+__device__ __forceinline__ void bf16_round2_nan_any(float& lo, float& hi) {
+  const uint32_t w = cvt_pk_bf16(lo, hi);
+  lo = u2f(w << 16);
+  hi = u2f(w & 0xFFFF0000u);
+}
+
+// Four binary32 values -> four E4M3 codes (byte i = value i), equal to f32_to_e4m3 on
+// every input: a positive NaN, which the instruction would code 0xFF, is first replaced
+// by 480 (code 0x7F).
+__device__ __forceinline__ float e4m3_pos_nan_to_480(float y) {
+  return (int32_t)f2u(y) > (int32_t)0x7F800000 ? 480.0f : y;
+}
+// (exact unless an input is a positive NaN)
+__device__ __forceinline__ uint32_t e4m3x4_raw(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  return e4m3x4_raw(e4m3_pos_nan_to_480(a), e4m3_pos_nan_to_480(b), e4m3_pos_nan_to_480(c),
+                    e4m3_pos_nan_to_480(d));
+}
 
 // binary32 -> E4M3 ("fn") with torch's cast semantics: RNE onto the E4M3
 // grid; magnitudes that round past 448, or are >= 480, give the NaN code.
@@ -56,13 +94,15 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
 }
 
 // binary32 -> FP6 code (fmt 2 = E2M3, 3 = E3M2; bit 5 = sign), OCP MX v1.0:
-// round-to-nearest-even, saturating to the largest normal.
+// round-to-nearest-even, saturating to the largest normal; FP6 has no NaN, and a
+// NaN gives the signed zero code.
 template <int FMT>
 __device__ __forceinline__ uint32_t f32_to_fp6(float f) {
   constexpr int MB = FMT == kE2M3 ? 3 : 2, BIAS = FMT == kE2M3 ? 1 : 3;
   const uint32_t u = f2u(f);
   const uint32_t sign = (u >> 26) & 0x20u;
   const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign;
   uint32_t code;
   if (a < ((uint32_t)(128 - BIAS) << 23)) {
     code = (uint32_t)__builtin_rintf(__builtin_ldexpf(u2f(a), BIAS - 1 + MB));  // subnormal grid
@@ -90,9 +130,9 @@ __device__ __forceinline__ uint32_t pow2_ceil_div448(float amax) {
 // exp() with a fixed binary32 operation sequence: Cody-Waite reduction by ln2
 // and the Cephes expf minimax polynomial (S. L. Moshier), explicit FMAs.
 __device__ __forceinline__ float mx_exp(float x) {
-  if (x < -87.0f) return 0.0f;
-  if (x > 88.0f) return __builtin_inff();
-  float n = __builtin_rintf(x * 1.44269504088896341f);
+  // branch-free: the range limits select the result; the exponent is clamped before
+  // the integer conversion so that it is defined for every x (NaN included)
+  const float n = __builtin_rintf(x * 1.44269504088896341f);
   float r = __builtin_fmaf(n, -0.693359375f, x);
   r = __builtin_fmaf(n, 2.12194440e-4f, r);
   float p = 1.9875691500e-4f;
@@ -101,17 +141,23 @@ __device__ __forceinline__ float mx_exp(float x) {
   p = __builtin_fmaf(p, r, 4.1665795894e-2f);
   p = __builtin_fmaf(p, r, 1.6666665459e-1f);
   p = __builtin_fmaf(p, r, 5.0000001201e-1f);
-  float r2 = r * r;
-  float y = __builtin_fmaf(p, r2, r) + 1.0f;
-  return __builtin_ldexpf(y, (int)n);
+  const float r2 = r * r;
+  const float y = __builtin_fmaf(p, r2, r) + 1.0f;
+  const float nc = __builtin_fminf(__builtin_fmaxf(n, -300.0f), 300.0f);
+  float e = __builtin_ldexpf(y, (int)nc);
+  e = x < -87.0f ? 0.0f : e;
+  return x > 88.0f ? __builtin_inff() : e;
 }
 
 // Quantize one 32-element block held by 4 consecutive lanes (8 values each,
 // lane (tid & 3) owns elements [8 (tid & 3), +8)).  The block amax is an
 // xor-shuffle max over the 4 lanes (order-free, so identical to a serial max).
 // Returns the E8M0 code (valid in every lane) and the lane's 8 codes packed
-// into two dwords.
-template <int RULE>
+// into two dwords.  The codes equal f32_to_e4m3 of the scaled values.
+// NAN_ANY: the caller's NaNs stand for the canonical positive NaN whatever their
+// sign and payload (values that bf16_round2_nan_any produced), so every NaN is
+// coded 0x7F, as f32_to_e4m3 codes the canonical one.
+template <int RULE, bool NAN_ANY = false>
 __device__ __forceinline__ uint32_t quant8x4(const float* v, uint32_t* packed) {
   float amax = 0.0f;
 #pragma unroll
@@ -119,26 +165,37 @@ __device__ __forceinline__ uint32_t quant8x4(const float* v, uint32_t* packed) {
   amax = __builtin_fmaxf(amax, __shfl_xor(amax, 1, 4));
   amax = __builtin_fmaxf(amax, __shfl_xor(amax, 2, 4));
   uint32_t s;
-  float mul = 1.0f;
-  int e2 = 0;
+  float y[8];
   if (RULE == kFloorCarry175) {
     s = scale_floor_carry175(f2u(amax) >> 16);
-    e2 = 127 - (int)s;
+    const int e2 = 127 - (int)s;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = __builtin_ldexpf(v[i], e2);
   } else {
-    uint32_t bits = pow2_ceil_div448(amax);
+    const uint32_t bits = pow2_ceil_div448(amax);
     s = bits >> 23;
-    mul = 1.0f / u2f(bits);
-  }
+    const float mul = 1.0f / u2f(bits);
+    if (NAN_ANY && bits == 0x7F800000u) {
+      // an infinite amax: mul = 0 and inf * 0 makes a NaN of the multiply's own sign,
+      // coded by f32_to_e4m3 from the product of the canonical values
 #pragma unroll
-  for (int d = 0; d < 2; ++d) {
-    uint32_t w = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      float x = v[d * 4 + b];
-      float y = RULE == kFloorCarry175 ? __builtin_ldexpf(x, e2) : x * mul;
-      w |= f32_to_e4m3(y) << (8 * b);
+      for (int i = 0; i < 8; ++i) y[i] = (v[i] != v[i] ? u2f(0x7FC00000u) : v[i]) * mul;
+      packed[0] = f32_to_e4m3(y[0]) | f32_to_e4m3(y[1]) << 8 | f32_to_e4m3(y[2]) << 16 | f32_to_e4m3(y[3]) << 24;
+      packed[1] = f32_to_e4m3(y[4]) | f32_to_e4m3(y[5]) << 8 | f32_to_e4m3(y[6]) << 16 | f32_to_e4m3(y[7]) << 24;
+      return s;
     }
-    packed[d] = w;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = v[i] * mul;
+  }
+  if (NAN_ANY) {
+    // every NaN (and every value from 480 up) -> 480 -> 0x7F
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = __builtin_fminf(y[i], 480.0f);
+    packed[0] = e4m3x4_raw(y[0], y[1], y[2], y[3]);
+    packed[1] = e4m3x4_raw(y[4], y[5], y[6], y[7]);
+  } else {
+    packed[0] = e4m3x4(y[0], y[1], y[2], y[3]);
+    packed[1] = e4m3x4(y[4], y[5], y[6], y[7]);
   }
   return s;
 }
@@ -151,6 +208,14 @@ __device__ __forceinline__ void bf16x8_to_f32(uint4 q, float* f) {
     f[2 * i] = u2f(w[i] << 16);
     f[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
   }
+}
+
+// Quiet signaling NaNs (sign, payload top bits and subnormals are kept).  An amax
+// over raw inputs needs it: in IEEE mode v_max_f32 / v_max3_f32 return a NaN when an
+// operand is a signaling NaN, where the block amax skips every NaN.
+__device__ __forceinline__ void quiet8(float* f) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = __builtin_canonicalizef(f[i]);
 }
 
 }  // namespace mxl

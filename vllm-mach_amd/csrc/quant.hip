@@ -14,6 +14,25 @@
 
 namespace mxl {
 
+// Lane -> (row, block) of a G-lanes-per-block mapping (G = 4 for 32-element MX
+// blocks, 16 for 128-element groups) in 32-bit arithmetic: the host keeps the lane
+// count below 2^31 (lanes_fit).  Lanes past the end shadow the last block with
+// live = false, so every lane takes part in the block's shuffles.
+template <int G>
+struct BlockLane {
+  uint32_t row, blk;
+  int sub;
+  bool live;
+  __device__ __forceinline__ BlockLane(uint32_t blocks_per_row, uint32_t blocks) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    sub = (int)(t % G);
+    live = t / G < blocks;
+    const uint32_t id = live ? t / G : blocks - 1;
+    row = id / blocks_per_row;
+    blk = id - row * blocks_per_row;
+  }
+};
+
 // --------------------------------------------------------------- MXFP8 quant
 
 // Four lanes own one 32-element block (8 values, one 16-byte load each), so a
@@ -24,14 +43,13 @@ __global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __rest
                                                           uint8_t* __restrict__ scales, int64_t M,
                                                           int64_t K) {
   const int64_t blocks_per_row = K / 32;
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int sub = (int)(tid & 3);
-  const int64_t total = M * blocks_per_row;
-  const bool live = (tid >> 2) < total;
-  const int64_t id = live ? (tid >> 2) : total - 1;  // dead lanes shadow a live block for the shuffle
-  const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
+  const BlockLane<4> bl((uint32_t)blocks_per_row, (uint32_t)(M * blocks_per_row));
+  const int sub = bl.sub;
+  const bool live = bl.live;
+  const int64_t row = bl.row, blk = bl.blk;
   float v[8];
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * ldx + blk * 32 + sub * 8), v);
+  quiet8(v);
   uint32_t packed[2];
   const uint32_t s = quant8x4<RULE>(v, packed);
   if (!live) return;
@@ -51,14 +69,13 @@ __global__ __launch_bounds__(256) void quant_mxfp6_kernel(const uint16_t* __rest
                                                           uint8_t* __restrict__ packed,
                                                           uint8_t* __restrict__ scales, int64_t M, int64_t K) {
   const int64_t blocks_per_row = K / 32;
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int sub = (int)(tid & 3);
-  const int64_t total = M * blocks_per_row;
-  const bool live = (tid >> 2) < total;
-  const int64_t id = live ? (tid >> 2) : total - 1;
-  const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
+  const BlockLane<4> bl((uint32_t)blocks_per_row, (uint32_t)(M * blocks_per_row));
+  const int sub = bl.sub;
+  const bool live = bl.live;
+  const int64_t row = bl.row, blk = bl.blk;
   float v[8];
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * ldx + blk * 32 + sub * 8), v);
+  quiet8(v);
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
@@ -91,14 +108,13 @@ __global__ __launch_bounds__(256) void quant_mxfp8_dual_kernel(const uint16_t* _
                                                                uint8_t* __restrict__ res,
                                                                uint8_t* __restrict__ s_res, int64_t M, int64_t K) {
   const int64_t blocks_per_row = K / 32;
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int sub = (int)(tid & 3);
-  const int64_t total = M * blocks_per_row;
-  const bool live = (tid >> 2) < total;
-  const int64_t id = live ? (tid >> 2) : total - 1;
-  const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
+  const BlockLane<4> bl((uint32_t)blocks_per_row, (uint32_t)(M * blocks_per_row));
+  const int sub = bl.sub;
+  const bool live = bl.live;
+  const int64_t row = bl.row, blk = bl.blk;
   float v[8], rv[8];
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * ldx + blk * 32 + sub * 8), v);
+  quiet8(v);
   uint32_t ph[2], pr[2];
   const uint32_t sh = quant8x4<RULE>(v, ph);
 #pragma unroll
@@ -130,23 +146,27 @@ __global__ __launch_bounds__(256) void swiglu_mxfp8_kernel(const uint16_t* __res
                                                            uint8_t* __restrict__ scales, int64_t M,
                                                            int64_t K) {
   const int64_t blocks_per_row = K / 32;
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int sub = (int)(tid & 3);
-  const int64_t total = M * blocks_per_row;
-  const bool live = (tid >> 2) < total;
-  const int64_t id = live ? (tid >> 2) : total - 1;
-  const int64_t row = id / blocks_per_row, blk = id - row * blocks_per_row;
+  const BlockLane<4> bl((uint32_t)blocks_per_row, (uint32_t)(M * blocks_per_row));
+  const int sub = bl.sub;
+  const bool live = bl.live;
+  const int64_t row = bl.row, blk = bl.blk;
   const int64_t off = row * 2 * K + blk * 32 + sub * 8;
   float g[8], u[8], v[8];
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(gate_up + off), g);
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(gate_up + off + K), u);
+  // act = bf16(g / (1 + exp(-g))), v = bf16(act * u): a NaN act makes a NaN v, and
+  // quant8x4<RULE, true> codes every NaN v as the canonical one, so the pair roundings
+  // leave NaN sign and payload as they come
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float act = bf16_round(g[i] / (1.0f + mx_exp(-g[i])));
-    v[i] = bf16_round(act * u[i]);
+  for (int i = 0; i < 8; i += 2) {
+    float a0 = g[i] / (1.0f + mx_exp(-g[i])), a1 = g[i + 1] / (1.0f + mx_exp(-g[i + 1]));
+    bf16_round2_nan_any(a0, a1);
+    v[i] = a0 * u[i];
+    v[i + 1] = a1 * u[i + 1];
+    bf16_round2_nan_any(v[i], v[i + 1]);
   }
   uint32_t packed[2];
-  const uint32_t s = quant8x4<RULE>(v, packed);
+  const uint32_t s = quant8x4<RULE, true>(v, packed);
   if (!live) return;
   *reinterpret_cast<uint2*>(codes + row * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
   if (sub == 0) {
@@ -187,28 +207,24 @@ __global__ __launch_bounds__(256) void quant_block_fp8_kernel(const uint16_t* __
                                                               uint8_t* __restrict__ q,
                                                               float* __restrict__ s_colmajor,
                                                               int64_t M, int64_t K) {
-  const int64_t groups = M * (K / 128);
-  const int64_t gid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 16;
-  const int sub = threadIdx.x & 15;
-  const bool live = gid < groups;
-  const int64_t g = live ? gid : groups - 1;  // keep every lane in the shuffle
-  const int64_t row = g / (K / 128), col = g - row * (K / 128);
+  const BlockLane<16> bl((uint32_t)(K / 128), (uint32_t)(M * (K / 128)));
+  const int sub = bl.sub;
+  const bool live = bl.live;
+  const int64_t row = bl.row, col = bl.blk;
   float v[8];
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * K + col * 128 + sub * 8), v);
+  quiet8(v);
   float m = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
   m = group16_amax(m);
   m = __builtin_fmaxf(m, 1e-10f);
   const float scale = m / 448.0f;
-  uint32_t w0 = 0, w1 = 0;
+  float y[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float y = v[i] / scale;
-    y = __builtin_fminf(__builtin_fmaxf(y, -448.0f), 448.0f);
-    uint32_t c = f32_to_e4m3(y);
-    if (i < 4) w0 |= c << (8 * i); else w1 |= c << (8 * (i - 4));
-  }
+  for (int i = 0; i < 8; ++i) y[i] = __builtin_fminf(__builtin_fmaxf(v[i] / scale, -448.0f), 448.0f);
+  // the clamp leaves no NaN: the hardware conversion equals f32_to_e4m3 here
+  const uint32_t w0 = e4m3x4_raw(y[0], y[1], y[2], y[3]), w1 = e4m3x4_raw(y[4], y[5], y[6], y[7]);
   if (!live) return;
   *reinterpret_cast<uint2*>(q + row * K + col * 128 + sub * 8) = make_uint2(w0, w1);
   if (sub == 0) s_colmajor[col * M + row] = scale;
@@ -219,12 +235,10 @@ __global__ __launch_bounds__(256) void silu_mul_block_fp8_kernel(const uint16_t*
                                                                  uint8_t* __restrict__ q,
                                                                  float* __restrict__ scales,
                                                                  int64_t rows, int64_t H) {
-  const int64_t groups = rows * (H / 128);
-  const int64_t gid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 16;
-  const int sub = threadIdx.x & 15;
-  const bool live = gid < groups;
-  const int64_t g = live ? gid : groups - 1;
-  const int64_t row = g / (H / 128), col = g - row * (H / 128);
+  const BlockLane<16> bl((uint32_t)(H / 128), (uint32_t)(rows * (H / 128)));
+  const int sub = bl.sub;
+  const bool live = bl.live;
+  const int64_t row = bl.row, col = bl.blk;
   float gt[8], up[8], v[8];
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(in + row * 2 * H + col * 128 + sub * 8), gt);
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(in + row * 2 * H + H + col * 128 + sub * 8), up);
@@ -237,13 +251,11 @@ __global__ __launch_bounds__(256) void silu_mul_block_fp8_kernel(const uint16_t*
   }
   m = group16_amax(m);
   const float scale = __builtin_fmaxf(m / 448.0f, 1.0f / (448.0f * 512.0f));
-  uint32_t w0 = 0, w1 = 0;
+  float y[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float y = __builtin_fmaxf(-448.0f, __builtin_fminf(v[i] / scale, 448.0f));
-    uint32_t c = f32_to_e4m3(y);
-    if (i < 4) w0 |= c << (8 * i); else w1 |= c << (8 * (i - 4));
-  }
+  for (int i = 0; i < 8; ++i) y[i] = __builtin_fmaxf(-448.0f, __builtin_fminf(v[i] / scale, 448.0f));
+  // the clamp leaves no NaN: the hardware conversion equals f32_to_e4m3 here
+  const uint32_t w0 = e4m3x4_raw(y[0], y[1], y[2], y[3]), w1 = e4m3x4_raw(y[4], y[5], y[6], y[7]);
   if (!live) return;
   *reinterpret_cast<uint2*>(q + row * H + col * 128 + sub * 8) = make_uint2(w0, w1);
   if (sub == 0) scales[TRANSPOSED ? col * rows + row : row * (H / 128) + col] = scale;
@@ -340,12 +352,16 @@ using namespace mxl;
 
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// the kernels index lanes in 32 bits (BlockLane)
+static inline bool lanes_fit(int64_t lanes) { return lanes <= (int64_t)0x7FFFFF00; }
+
 extern "C" int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t ldx, int rule,
                                   void* codes, void* scales, void* stream) {
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_quantize_mxfp8: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
   MXL_CHECK_ARG(ldx >= K && ldx % 8 == 0, "mxl_quantize_mxfp8: ldx must be >= K and a multiple of 8");
   MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_quantize_mxfp8: unknown rule %d", rule);
   MXL_CHECK_ARG(aligned16(x) && aligned16(codes), "mxl_quantize_mxfp8: x and codes must be 16-byte aligned");
+  MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_quantize_mxfp8: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
   if (M == 0) return MXL_OK;
   const int64_t n = M * (K / 32) * 4;
   dim3 grid((unsigned)((n + 255) / 256));
@@ -364,6 +380,7 @@ extern "C" int mxl_quantize_mxfp6(const void* x, int64_t M, int64_t K, int64_t l
   MXL_CHECK_ARG(fmt == kE2M3 || fmt == kE3M2, "mxl_quantize_mxfp6: fmt must be 2 (E2M3) or 3 (E3M2), got %d", fmt);
   MXL_CHECK_ARG(ldx >= K && ldx % 8 == 0, "mxl_quantize_mxfp6: ldx must be >= K and a multiple of 8");
   MXL_CHECK_ARG(aligned16(x) && ((uintptr_t)packed & 1) == 0, "mxl_quantize_mxfp6: misaligned buffers");
+  MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_quantize_mxfp6: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
   if (M == 0) return MXL_OK;
   const int64_t n = M * (K / 32) * 4;
   dim3 grid((unsigned)((n + 255) / 256));
@@ -383,6 +400,7 @@ extern "C" int mxl_quantize_mxfp8_dual(const void* x, int64_t M, int64_t K, int6
   MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_quantize_mxfp8_dual: unknown rule %d", rule);
   MXL_CHECK_ARG(aligned16(x) && ((uintptr_t)hi & 7) == 0 && ((uintptr_t)res & 7) == 0,
                 "mxl_quantize_mxfp8_dual: misaligned buffers");
+  MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_quantize_mxfp8_dual: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
   if (M == 0) return MXL_OK;
   const int64_t n = M * (K / 32) * 4;
   dim3 grid((unsigned)((n + 255) / 256));
@@ -406,6 +424,7 @@ extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int r
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_swiglu_mxfp8: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
   MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_swiglu_mxfp8: unknown rule %d", rule);
   MXL_CHECK_ARG(aligned16(gate_up) && aligned16(codes), "mxl_swiglu_mxfp8: gate_up and codes must be 16-byte aligned");
+  MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_swiglu_mxfp8: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
   if (M == 0) return MXL_OK;
   const int64_t n = M * (K / 32) * 4;
   dim3 grid((unsigned)((n + 255) / 256));
@@ -430,6 +449,7 @@ extern "C" int mxl_quantize_block_fp8(const void* x, int64_t M, int64_t K, void*
                                       void* stream) {
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 128 == 0, "mxl_quantize_block_fp8: need K %% 128 == 0 (K=%lld)", (long long)K);
   MXL_CHECK_ARG(aligned16(x) && ((uintptr_t)q & 7) == 0, "mxl_quantize_block_fp8: misaligned buffers");
+  MXL_CHECK_ARG(lanes_fit(M * (K / 128) * 16), "mxl_quantize_block_fp8: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
   if (M == 0) return MXL_OK;
   const int64_t threads = M * (K / 128) * 16;
   quant_block_fp8_kernel<<<dim3((unsigned)((threads + 255) / 256)), 256, 0, (hipStream_t)stream>>>(
@@ -442,6 +462,7 @@ extern "C" int mxl_silu_mul_block_fp8(const void* input, int64_t rows, int64_t H
                                       void* scales, void* stream) {
   MXL_CHECK_ARG(rows >= 0 && H > 0 && H % 128 == 0, "mxl_silu_mul_block_fp8: need H %% 128 == 0 (H=%lld)", (long long)H);
   MXL_CHECK_ARG(aligned16(input) && ((uintptr_t)q & 7) == 0, "mxl_silu_mul_block_fp8: misaligned buffers");
+  MXL_CHECK_ARG(lanes_fit(rows * (H / 128) * 16), "mxl_silu_mul_block_fp8: too large (rows=%lld, H=%lld)", (long long)rows, (long long)H);
   if (rows == 0) return MXL_OK;
   const int64_t threads = rows * (H / 128) * 16;
   dim3 grid((unsigned)((threads + 255) / 256));
