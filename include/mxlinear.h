@@ -12,7 +12,10 @@
  * bits [6i, 6i+6)).  Scales are E8M0 bytes (2^(s-127)), one per 32 along K.
  * rule 0 = floor_carry175 (the reference quantizer quantize_block,
  * src/vllm_mach/mxfp8/reconstruct_model.py:34-50), rule 1 = ceil_div448
- * (src/vllm_mach/mxfp6/mxfp8_mlp.py:100-105).
+ * (src/vllm_mach/mxfp6/mxfp8_mlp.py:100-105), rule 2 = rp_ue8m0 (FlashInfer's
+ * mxfp8_quantize convention as src/vllm_mach/mxfp8/swiglu_quant.py:58-66 writes
+ * it: amax * (1/448) rounded up onto E8M0, saturating; codes of the clamped
+ * +-448 products; quantizers, dual and SwiGLU only).
  *
  * Each declaration cites the reference interface (troycheng/vllm-mach
  * v0.4.0) it replaces.
@@ -60,8 +63,11 @@ int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K);
 
 /* SwiGLU -> MXFP8 producer: gate_up bf16 [M, 2K] (gate = cols [0, K), up =
  * [K, 2K)) -> codes [M, K] + scales, logical [M, K/32] (swizzled = 0) or the
- * reference's swizzled layout (swizzled = 1, padding zeroed).  Replaces
- * _silu_quant / _triton_quantize (src/vllm_mach/mxfp6/mxfp8_mlp.py:87-127). */
+ * reference's swizzled layout (swizzled = 1, padding zeroed).  Rules 0 and 1
+ * round the SiLU to bf16 before the product; replaces _silu_quant /
+ * _triton_quantize (src/vllm_mach/mxfp6/mxfp8_mlp.py:87-127).  Rule 2 rounds
+ * once, bf16((g / (1 + exp(-g))) * up); replaces the champion producer
+ * swiglu_quant._kernel (src/vllm_mach/mxfp8/swiglu_quant.py:46-70). */
 int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int rule, int swizzled,
                      void* codes, void* scales, void* stream);
 

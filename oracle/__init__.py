@@ -27,7 +27,7 @@ LIB_PATH = HERE / "libmxoracle.so"
 SOURCE = HERE / "mx_oracle.c"
 
 FMT_E4M3, FMT_E2M3, FMT_E3M2 = 0, 2, 3
-RULE_FLOOR_CARRY175, RULE_CEIL_DIV448 = 0, 1
+RULE_FLOOR_CARRY175, RULE_CEIL_DIV448, RULE_RP_UE8M0 = 0, 1, 2
 
 _lib = None
 
@@ -163,7 +163,9 @@ def quant_mxfp8(x, rule: int = RULE_FLOOR_CARRY175):
     """bf16 [R, K] -> (E4M3 codes [R, K] u8, E8M0 scales [R, K/32] u8).
 
     rule 0 restates ``quantize_block`` (src/vllm_mach/mxfp8/reconstruct_model.py:34-50);
-    rule 1 is the ``ceil_div448`` E8M0 rule of mxfp6/mxfp8_mlp.py:100-105.
+    rule 1 is the ``ceil_div448`` E8M0 rule of mxfp6/mxfp8_mlp.py:100-105;
+    rule 2 (``rp_ue8m0``) is FlashInfer's ``mxfp8_quantize`` convention as
+    src/vllm_mach/mxfp8/swiglu_quant.py:58-66 writes it (1/448 correctly rounded).
     """
     b = bf16_bits(x)
     R, K = b.shape
@@ -186,7 +188,8 @@ def quant_mxfp8_dual(x, rule: int = RULE_FLOOR_CARRY175):
 
 
 def swiglu_mxfp8(gate_up, rule: int = RULE_CEIL_DIV448):
-    """bf16 [R, 2K] -> codes [R, K], logical scales [R, K/32] (mxfp6/mxfp8_mlp.py:87-110)."""
+    """bf16 [R, 2K] -> codes [R, K], logical scales [R, K/32] (mxfp6/mxfp8_mlp.py:87-110;
+    rule 2: the single-rounding champion variant, mxfp8/swiglu_quant.py:54-66)."""
     b = bf16_bits(gate_up)
     R, K2 = b.shape
     K = K2 // 2

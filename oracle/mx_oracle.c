@@ -136,11 +136,41 @@ static uint32_t pow2_ceil_div448(float amax) {
   return (f2u(raw) + 0x007FFFFFu) & 0x7F800000u;
 }
 
+/* Rule "rp_ue8m0": the FlashInfer mxfp8_quantize convention that the reference's
+ * champion producer writes out (mxfp8/swiglu_quant.py:58-66).  raw = amax * r448
+ * with r448 the reciprocal of 448; s = raw rounded toward +inf onto E8M0
+ * (2^(s-127), s in 0..254, saturating at 254; raw <= 2^-127 gives 0);
+ * inverse = 2^(127-s), 0 for s = 0 (the reference's where(scale > 0)) and for
+ * s = 254 (2^-127 is subnormal and the reference's reciprocal flushes it);
+ * codes = E4M3(min(max(v * inverse, -448), 448)), the clamp taken in that order
+ * (a NaN product gives -448).  The reference takes rcp.approx.ftz of 448 on
+ * NVIDIA hardware; this build uses the correctly rounded 1/448 (0x3B124925):
+ * parity unpinned for that constant, whose exact value decides the scale only
+ * where amax * r448 lands within an ulp of a power of two.                    */
+static const float kRcp448 = 1.0f / 448.0f;
+
+static uint8_t e8m0_rp(float raw) {
+  uint32_t u = f2u(raw);
+  if (u >= 0x7F800000u) return 254;          /* +inf (raw is never negative or NaN) */
+  uint32_t e = u >> 23, m = u & 0x7FFFFFu;
+  if (e == 0) return u <= 0x00400000u ? 0 : 1;  /* 2^-127 is the subnormal 0x00400000 */
+  uint32_t s = e + (m != 0);
+  return (uint8_t)(s > 254 ? 254 : s);
+}
+
 /* Quantize one 32-element block of binary32 values that are exactly bf16
- * (all values are bf16-representable).  rule 0 = floor_carry175, 1 = ceil_div448. */
+ * (all values are bf16-representable).  rule 0 = floor_carry175, 1 = ceil_div448,
+ * 2 = rp_ue8m0. */
 static void quant_block32(const float* v, int rule, uint8_t* codes, uint8_t* scale) {
   float amax = 0.0f;
   for (int i = 0; i < 32; ++i) { float a = fabsf(v[i]); if (a > amax) amax = a; }
+  if (rule == 2) {
+    uint8_t s = e8m0_rp(amax * kRcp448);
+    float inverse = (s == 0 || s == 254) ? 0.0f : ldexpf(1.0f, 127 - (int)s);
+    for (int i = 0; i < 32; ++i) codes[i] = mxo_f32_to_e4m3(fminf(fmaxf(v[i] * inverse, -448.0f), 448.0f));
+    *scale = s;
+    return;
+  }
   if (rule == 0) {
     uint8_t s = scale_floor_carry175(mxo_f32_to_bf16(amax));
     /* x / 2^(s-127) (reconstruct_model.py:47-48); an exact power-of-two divide */
@@ -215,7 +245,9 @@ float mxo_exp(float x) {
 
 /* SwiGLU -> MXFP8, mxfp6/mxfp8_mlp.py:87-110 (_silu_quant): gate = cols [0,K),
  * up = cols [K,2K); act = bf16(g / (1 + exp(-g))); v = bf16(act * up); rule
- * ceil_div448.  Outputs codes [rows, K] and logical scales [rows, K/32].     */
+ * ceil_div448.  Rule 2 is the champion variant, mxfp8/swiglu_quant.py:54-66:
+ * one bf16 rounding, v = bf16((g / (1 + exp(-g))) * up), then rp_ue8m0.
+ * Outputs codes [rows, K] and logical scales [rows, K/32].                   */
 void mxo_swiglu_mxfp8(const uint16_t* gate_up, int64_t rows, int64_t K, int rule,
                       uint8_t* codes, uint8_t* scales) {
   float v[32];
@@ -224,8 +256,12 @@ void mxo_swiglu_mxfp8(const uint16_t* gate_up, int64_t rows, int64_t K, int rule
       for (int i = 0; i < 32; ++i) {
         float g = mxo_bf16_to_f32(gate_up[r * 2 * K + b * 32 + i]);
         float u = mxo_bf16_to_f32(gate_up[r * 2 * K + K + b * 32 + i]);
-        float act = bf16_round(g / (1.0f + mxo_exp(-g)));
-        v[i] = bf16_round(act * u);
+        if (rule == 2) {
+          v[i] = bf16_round((g / (1.0f + mxo_exp(-g))) * u);
+        } else {
+          float act = bf16_round(g / (1.0f + mxo_exp(-g)));
+          v[i] = bf16_round(act * u);
+        }
       }
       quant_block32(v, rule, codes + r * K + b * 32, scales + r * (K / 32) + b);
     }

@@ -177,3 +177,22 @@ def test_graph_replay_with_changing_inputs(pkg, oracle_mod, dev):
             else:
                 _check(got, ref)
     torch.cuda.current_stream().wait_stream(stream)
+
+
+@pytest.mark.parametrize("rule", [1, 2])
+@pytest.mark.parametrize("M", [1, 16, 200])
+def test_swiglu_mx_down_matches_oracle(pkg, oracle_mod, dev, rule, M):
+    """SwiGLU -> MXFP8 -> down projection (mach_swiglu_mxfp8_down, mxfp6/mxfp8_mlp.py:15-22;
+    rule 2: the champion producer of mxfp8/swiglu_quant.py feeding the same GEMM)."""
+    ops = pkg.ops
+    N, K = 512, 2048
+    wc, ws, stored = _weights(oracle_mod, N, K, 0, 0.02, 91)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), 0)
+    gu = (torch.randn(M, 2 * K, generator=torch.Generator().manual_seed(92 + M)) * 2).bfloat16()
+    y = ops.swiglu_mx_down(gu.to(dev), tiled, tiled_s, N, 0, rule)
+    rc, rs = oracle_mod.swiglu_mxfp8(gu, rule)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, 0)))
+    _check(y.float().cpu().numpy(), ref)
+    # the producer's own codes are the oracle's
+    a, sa = torch.ops.mach_amd.swiglu_mxfp8(gu.to(dev), rule, False)
+    assert np.array_equal(a.view(torch.uint8).cpu().numpy(), rc) and np.array_equal(sa.cpu().numpy(), rs)

@@ -121,7 +121,7 @@ def _every_bf16(rows, K, seed=None):
     return torch.from_numpy(pats.view(np.int16).copy()).view(torch.bfloat16).reshape(rows, K)
 
 
-@pytest.mark.parametrize("rule", [0, 1])
+@pytest.mark.parametrize("rule", [0, 1, 2])
 @pytest.mark.parametrize("seed", [None, 11])
 def test_quantize_mxfp8_every_bf16(pkg, oracle_mod, dev, rule, seed):
     x = _every_bf16(8, 8192, seed)
@@ -135,7 +135,7 @@ def test_quantize_mxfp8_every_bf16(pkg, oracle_mod, dev, rule, seed):
         assert np.array_equal(_u8(got), want)
 
 
-@pytest.mark.parametrize("rule", [0, 1])
+@pytest.mark.parametrize("rule", [0, 1, 2])
 @pytest.mark.parametrize("seed", [None, 12])
 def test_swiglu_mxfp8_every_bf16(pkg, oracle_mod, dev, rule, seed):
     """Every bf16 pattern as gate (up ~ N(0,1)) and as up (gate ~ N(0,1))."""
@@ -176,3 +176,59 @@ def test_quantize_mxfp6_every_bf16(pkg, oracle_mod, dev, fmt, seed):
     rc, rs = oracle_mod.quant_mxfp6(w, fmt)
     assert np.array_equal(scales.cpu().numpy(), rs)
     assert np.array_equal(packed.cpu().numpy(), oracle_mod.pack_fp6(rc))
+
+
+# ------------------------------------- champion producer (rp_ue8m0, one rounding)
+
+def _champion_expected(oracle_mod, x):
+    codes, scales = oracle_mod.swiglu_mxfp8(x.cpu(), oracle_mod.RULE_RP_UE8M0)
+    return codes, oracle_mod.swizzle_scales(scales, x.shape[1] // 2)
+
+
+@pytest.mark.parametrize("k", [6144, 9216])
+@pytest.mark.parametrize("m", [1, 4, 16, 24, 32, 64, 128])
+def test_champion_swiglu_bit_exact(pkg, oracle_mod, dev, m, k):
+    """Shapes and magnitudes of tests/test_mxfp8_swiglu_quant.py:86-109."""
+    g = torch.Generator().manual_seed(1000 + m + k)
+    for magnitude in [1.0, 0.0, 1e-15, 50.0]:
+        x = (torch.randn(m, 2 * k, generator=g) * magnitude).bfloat16()
+        codes, scales = pkg.swiglu_quant.quantize(x.to(dev))
+        rc, rs = _champion_expected(oracle_mod, x)
+        assert np.array_equal(_u8(codes), rc), magnitude
+        assert np.array_equal(_u8(scales), rs), magnitude
+
+
+def test_champion_graph_replay_with_changing_inputs(pkg, oracle_mod, dev):
+    """tests/test_mxfp8_swiglu_quant.py:86-109: capture once, refill the input eagerly,
+    replay, compare every replay."""
+    m, k = 24, 6144
+    x = torch.randn(m, 2 * k, device=dev, dtype=torch.bfloat16)
+    pkg.swiglu_quant.quantize(x)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        codes, scales = pkg.swiglu_quant.quantize(x)
+    for magnitude in [1.0, 0.0, 1e-15, 50.0, 1.0]:
+        x.normal_().mul_(magnitude)
+        graph.replay()
+        torch.cuda.synchronize()
+        rc, rs = _champion_expected(oracle_mod, x)
+        assert np.array_equal(_u8(codes), rc), magnitude
+        assert np.array_equal(_u8(scales), rs), magnitude
+
+
+def test_champion_contract(pkg, dev):
+    """swiglu_quant.py:23-32: unsupported tensors raise; m == 0 and m > 128 return None."""
+    q = pkg.swiglu_quant.quantize
+    assert q(torch.zeros(0, 12288, device=dev, dtype=torch.bfloat16)) is None
+    assert q(torch.zeros(129, 18432, device=dev, dtype=torch.bfloat16)) is None
+    for bad in (torch.zeros(4, 4096, device=dev, dtype=torch.bfloat16),
+                torch.zeros(4, 12288, device=dev, dtype=torch.float16),
+                torch.zeros(12288, 8, device=dev, dtype=torch.bfloat16).t(),
+                torch.zeros(4, 12288, dtype=torch.bfloat16)):
+        with pytest.raises(RuntimeError):
+            q(bad)
+    codes, scales = q(torch.ones(3, 12288, device=dev, dtype=torch.bfloat16))
+    assert codes.shape == (3, 6144) and codes.dtype == torch.float8_e4m3fn
+    assert scales.shape == (128 * 48 * 4,) and scales.dtype == torch.uint8
+    assert pkg.swiglu_quant.inspect()["counts"]

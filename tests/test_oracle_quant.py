@@ -178,3 +178,83 @@ def test_mxfp6_quant_ocp_rule(oracle_mod, fmt):
         for k in range(256):
             x = Fraction(float(wf[r, k])) / Fraction(2) ** (int(scales[r, k // 32]) - 127)
             assert codes[r, k] == _nearest_fp6(float(x), table) | (32 if np.signbit(wf[r, k]) else 0) & 63
+
+
+# ------------------------------------------------ rp_ue8m0 (champion producer)
+
+def _rp_scale_bruteforce(amax: np.float32) -> int:
+    """Smallest E8M0 code s (0..254) with 2^(s-127) >= fl32(amax * fl32(1/448)),
+    254 when none is (mxfp8/swiglu_quant.py:58-61, satfinite), by exhaustive search."""
+    raw = float(np.float32(np.float32(amax) * (np.float32(1.0) / np.float32(448.0))))
+    for s in range(255):
+        if Fraction(2) ** (s - 127) >= Fraction(raw):
+            return s
+    return 254
+
+
+def test_rp_ue8m0_constant_is_correctly_rounded():
+    r = np.float32(1.0) / np.float32(448.0)
+    assert r.view(np.uint32) == 0x3B124925
+    assert abs(Fraction(float(r)) - Fraction(1, 448)) <= Fraction(1, 2) * Fraction(2) ** -32  # half an ulp
+
+
+def test_rp_ue8m0_scales_bruteforce(oracle_mod):
+    rng = np.random.default_rng(3)
+    amax = np.concatenate([
+        rng.standard_normal(300) * np.exp2(rng.integers(-130, 120, 300)),
+        # exact powers of two times 448 (raw lands on a power of two), the E4M3
+        # maximum's neighbours, subnormal raw on both sides of 2^-127, zero, huge
+        np.float32([448, 896, 448 * 2.0 ** -20, 447, 449, 1.75, 0.0, 2.0 ** -126,
+                    2.0 ** -117, 2.0 ** -118, 3.0e38, 1.0e-38]),
+    ])
+    rows = np.zeros((amax.size, 32), np.float32)
+    rows[:, 7] = amax
+    x = torch.from_numpy(rows).bfloat16()
+    _, scales = oracle_mod.quant_mxfp8(x, oracle_mod.RULE_RP_UE8M0)
+    amax_bf = x.float().abs().amax(-1).numpy()
+    assert scales.ravel().tolist() == [_rp_scale_bruteforce(a) for a in amax_bf]
+    # raw = 2^k exactly for amax = 448 * 2^k: no round-up (the constant is correctly rounded)
+    assert scales[300, 0] == 127 and scales[301, 0] == 128
+    assert scales[306, 0] == 0  # zero block
+
+
+def test_rp_ue8m0_codes_match_torch(oracle_mod):
+    g = torch.Generator().manual_seed(6)
+    x = (torch.randn(64, 512, generator=g) * torch.exp2(torch.randint(-30, 30, (64, 1), generator=g))).bfloat16()
+    x[0] = 0
+    codes, scales = oracle_mod.quant_mxfp8(x, oracle_mod.RULE_RP_UE8M0)
+    s = torch.from_numpy(scales).float()
+    inv = torch.where((s == 0) | (s == 254), torch.zeros_like(s), torch.exp2(127 - s)).repeat_interleave(32, -1)
+    ref = (x.float() * inv).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(codes, ref)
+    assert (codes[0] == 0).all() and scales[0].tolist() == [0] * 16
+
+
+def test_rp_ue8m0_special_values(oracle_mod):
+    """inf amax saturates the scale at 254, whose inverse is 0 (2^-127 flushed); a NaN
+    element is skipped by the amax and, as the clamp max(., -448) comes first, coded -448."""
+    row = np.zeros((2, 32), np.float32)
+    row[0, 3], row[0, 4] = np.inf, 2.0
+    row[1, 3], row[1, 4] = np.nan, 448.0
+    codes, scales = oracle_mod.quant_mxfp8(torch.from_numpy(row).bfloat16(), oracle_mod.RULE_RP_UE8M0)
+    assert scales[0, 0] == 254 and codes[0, 3] == 0xFE and codes[0, 4] == 0  # inf * 0 = NaN -> -448
+    assert scales[1, 0] == 127 and codes[1, 3] == 0xFE and codes[1, 4] == 0x7E
+
+
+def test_champion_swiglu_is_quantize_of_single_rounded_silu(oracle_mod):
+    """The reference test's identity (tests/test_mxfp8_swiglu_quant.py:86-109): the fused
+    producer equals the rp_ue8m0 quantizer applied to bf16((g / (1 + exp(-g))) * up)."""
+    g = torch.Generator().manual_seed(71)
+    M, K = 6, 512
+    for magnitude in [1.0, 0.0, 1e-15, 50.0]:
+        gu = (torch.randn(M, 2 * K, generator=g) * magnitude).bfloat16()
+        codes, scales = oracle_mod.swiglu_mxfp8(gu, oracle_mod.RULE_RP_UE8M0)
+        gate, up = gu[:, :K].float(), gu[:, K:].float()
+        e = torch.from_numpy(oracle_mod.exp_f32((-gate).numpy()))
+        v = ((gate / (1.0 + e)) * up).bfloat16()  # one rounding: no bf16 SiLU
+        c2, s2 = oracle_mod.quant_mxfp8(v, oracle_mod.RULE_RP_UE8M0)
+        assert np.array_equal(codes, c2) and np.array_equal(scales, s2), magnitude
+    # torch's own SiLU composition differs only by exp ulps
+    v_t = (torch.nn.functional.silu(gate) * up).bfloat16()
+    c3, _ = oracle_mod.quant_mxfp8(v_t, oracle_mod.RULE_RP_UE8M0)
+    assert (codes == c3).mean() > 0.99

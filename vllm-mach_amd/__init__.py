@@ -10,6 +10,7 @@ Importing the package registers the ``torch.ops.mach_amd`` operators; it does
 not touch the GPU or load the HIP library (that happens on first use).
 """
 from . import ops  # noqa: F401  (registers torch.ops.mach_amd.*)
+from . import swiglu_quant  # noqa: F401
 from .linear import (  # noqa: F401
     BlockFp8LinearKernel,
     Mxfp6LinearKernel,

@@ -19,7 +19,7 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 enum Fmt : int { kE4M3 = 0, kE5M2 = 1, kE2M3 = 2, kE3M2 = 3 };
 
 // E8M0 scale rules
-enum Rule : int { kFloorCarry175 = 0, kCeilDiv448 = 1 };
+enum Rule : int { kFloorCarry175 = 0, kCeilDiv448 = 1, kRpUe8m0 = 2 };
 
 __device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -127,6 +127,22 @@ __device__ __forceinline__ uint32_t pow2_ceil_div448(float amax) {
   return (f2u(raw) + 0x007FFFFFu) & 0x7F800000u;
 }
 
+// rp_ue8m0 (FlashInfer's mxfp8_quantize convention, mxfp8/swiglu_quant.py:58-66):
+// E8M0 code of raw = amax * (1/448) rounded toward +inf, saturating at 254 (raw is
+// never negative or NaN: the amax skips NaNs); 2^-127 is the subnormal 0x00400000.
+__device__ __forceinline__ uint32_t e8m0_rp(float amax) {
+  const uint32_t u = f2u(amax * (1.0f / 448.0f));
+  const uint32_t e = u >> 23, up = e + ((u & 0x7FFFFFu) != 0u);
+  const uint32_t sub = u <= 0x00400000u ? 0u : 1u;
+  const uint32_t s = e == 0u ? sub : (up > 254u ? 254u : up);
+  return u >= 0x7F800000u ? 254u : s;
+}
+// its element multiplier: 2^(127 - s); 0 for s = 0 and for s = 254 (2^-127 is subnormal,
+// flushed by the reference's reciprocal)
+__device__ __forceinline__ float e8m0_rp_inverse(uint32_t s) {
+  return (s == 0u || s == 254u) ? 0.0f : u2f((254u - s) << 23);
+}
+
 // exp() with a fixed binary32 operation sequence: Cody-Waite reduction by ln2
 // and the Cephes expf minimax polynomial (S. L. Moshier), explicit FMAs.
 __device__ __forceinline__ float mx_exp(float x) {
@@ -166,6 +182,16 @@ __device__ __forceinline__ uint32_t quant8x4(const float* v, uint32_t* packed) {
   amax = __builtin_fmaxf(amax, __shfl_xor(amax, 2, 4));
   uint32_t s;
   float y[8];
+  if (RULE == kRpUe8m0) {
+    // min(max(v * inverse, -448), 448): no NaN is left for the conversion
+    s = e8m0_rp(amax);
+    const float inv = e8m0_rp_inverse(s);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = __builtin_fminf(__builtin_fmaxf(v[i] * inv, -448.0f), 448.0f);
+    packed[0] = e4m3x4_raw(y[0], y[1], y[2], y[3]);
+    packed[1] = e4m3x4_raw(y[4], y[5], y[6], y[7]);
+    return s;
+  }
   if (RULE == kFloorCarry175) {
     s = scale_floor_carry175(f2u(amax) >> 16);
     const int e2 = 127 - (int)s;

@@ -157,10 +157,11 @@ __global__ __launch_bounds__(256) void swiglu_mxfp8_kernel(const uint16_t* __res
   // act = bf16(g / (1 + exp(-g))), v = bf16(act * u): a NaN act makes a NaN v, and
   // quant8x4<RULE, true> codes every NaN v as the canonical one, so the pair roundings
   // leave NaN sign and payload as they come
+  // (rule rp_ue8m0, the champion variant: no rounding of act, one bf16 rounding of v)
 #pragma unroll
   for (int i = 0; i < 8; i += 2) {
     float a0 = g[i] / (1.0f + mx_exp(-g[i])), a1 = g[i + 1] / (1.0f + mx_exp(-g[i + 1]));
-    bf16_round2_nan_any(a0, a1);
+    if (RULE != kRpUe8m0) bf16_round2_nan_any(a0, a1);
     v[i] = a0 * u[i];
     v[i + 1] = a1 * u[i + 1];
     bf16_round2_nan_any(v[i], v[i + 1]);
@@ -359,7 +360,7 @@ extern "C" int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t l
                                   void* codes, void* scales, void* stream) {
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_quantize_mxfp8: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
   MXL_CHECK_ARG(ldx >= K && ldx % 8 == 0, "mxl_quantize_mxfp8: ldx must be >= K and a multiple of 8");
-  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_quantize_mxfp8: unknown rule %d", rule);
+  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448 || rule == kRpUe8m0, "mxl_quantize_mxfp8: unknown rule %d", rule);
   MXL_CHECK_ARG(aligned16(x) && aligned16(codes), "mxl_quantize_mxfp8: x and codes must be 16-byte aligned");
   MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_quantize_mxfp8: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
   if (M == 0) return MXL_OK;
@@ -368,8 +369,10 @@ extern "C" int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t l
   hipStream_t s = (hipStream_t)stream;
   if (rule == kFloorCarry175)
     quant_mxfp8_kernel<kFloorCarry175><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)codes, (uint8_t*)scales, M, K);
-  else
+  else if (rule == kCeilDiv448)
     quant_mxfp8_kernel<kCeilDiv448><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)codes, (uint8_t*)scales, M, K);
+  else
+    quant_mxfp8_kernel<kRpUe8m0><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)codes, (uint8_t*)scales, M, K);
   MXL_CHECK_LAUNCH("mxl_quantize_mxfp8");
   return MXL_OK;
 }
@@ -397,7 +400,7 @@ extern "C" int mxl_quantize_mxfp8_dual(const void* x, int64_t M, int64_t K, int6
                                        void* s_hi, void* res, void* s_res, void* stream) {
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0 && ldx >= K && ldx % 8 == 0,
                 "mxl_quantize_mxfp8_dual: need K %% 32 == 0, ldx >= K, ldx %% 8 == 0");
-  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_quantize_mxfp8_dual: unknown rule %d", rule);
+  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448 || rule == kRpUe8m0, "mxl_quantize_mxfp8_dual: unknown rule %d", rule);
   MXL_CHECK_ARG(aligned16(x) && ((uintptr_t)hi & 7) == 0 && ((uintptr_t)res & 7) == 0,
                 "mxl_quantize_mxfp8_dual: misaligned buffers");
   MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_quantize_mxfp8_dual: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
@@ -408,9 +411,12 @@ extern "C" int mxl_quantize_mxfp8_dual(const void* x, int64_t M, int64_t K, int6
   if (rule == kFloorCarry175)
     quant_mxfp8_dual_kernel<kFloorCarry175><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)hi,
                                                                 (uint8_t*)s_hi, (uint8_t*)res, (uint8_t*)s_res, M, K);
-  else
+  else if (rule == kCeilDiv448)
     quant_mxfp8_dual_kernel<kCeilDiv448><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)hi,
                                                              (uint8_t*)s_hi, (uint8_t*)res, (uint8_t*)s_res, M, K);
+  else
+    quant_mxfp8_dual_kernel<kRpUe8m0><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint8_t*)hi,
+                                                          (uint8_t*)s_hi, (uint8_t*)res, (uint8_t*)s_res, M, K);
   MXL_CHECK_LAUNCH("mxl_quantize_mxfp8_dual");
   return MXL_OK;
 }
@@ -422,7 +428,7 @@ extern "C" int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K) {
 extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int rule, int swizzled,
                                 void* codes, void* scales, void* stream) {
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_swiglu_mxfp8: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
-  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448, "mxl_swiglu_mxfp8: unknown rule %d", rule);
+  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448 || rule == kRpUe8m0, "mxl_swiglu_mxfp8: unknown rule %d", rule);
   MXL_CHECK_ARG(aligned16(gate_up) && aligned16(codes), "mxl_swiglu_mxfp8: gate_up and codes must be 16-byte aligned");
   MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_swiglu_mxfp8: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
   if (M == 0) return MXL_OK;
@@ -436,10 +442,12 @@ extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int r
     const int64_t total = mxl_swizzled_scale_bytes(M, K);
     swizzle_pad_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, s>>>(sc, M, K, total);
     if (rule == kFloorCarry175) swiglu_mxfp8_kernel<kFloorCarry175, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
-    else swiglu_mxfp8_kernel<kCeilDiv448, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+    else if (rule == kCeilDiv448) swiglu_mxfp8_kernel<kCeilDiv448, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+    else swiglu_mxfp8_kernel<kRpUe8m0, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
   } else {
     if (rule == kFloorCarry175) swiglu_mxfp8_kernel<kFloorCarry175, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
-    else swiglu_mxfp8_kernel<kCeilDiv448, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+    else if (rule == kCeilDiv448) swiglu_mxfp8_kernel<kCeilDiv448, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+    else swiglu_mxfp8_kernel<kRpUe8m0, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
   }
   MXL_CHECK_LAUNCH("mxl_swiglu_mxfp8");
   return MXL_OK;

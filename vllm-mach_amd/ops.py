@@ -20,7 +20,7 @@ from . import _lib
 from ._lib import call, ptr, query, stream_handle
 
 E4M3, E2M3, E3M2 = 0, 2, 3
-FLOOR_CARRY175, CEIL_DIV448 = 0, 1
+FLOOR_CARRY175, CEIL_DIV448, RP_UE8M0 = 0, 1, 2
 FORMATS = {"e4m3": E4M3, "e2m3": E2M3, "e3m2": E3M2}
 
 _ws_lock = threading.RLock()
