@@ -166,11 +166,19 @@ class SwigluDown(Workload):
         gemm = [lambda wt=wt, st=st: torch.ops.mach_amd.mx_gemm(a, sa, wt, st, N, K, ops.E4M3, None)
                 for wt, st in self.copies]
         prod = [lambda: torch.ops.mach_amd.swiglu_mxfp8(self.inputs[M], ops.CEIL_DIV448, False)] * 8
-        return {
+        out = {
             f"mxfp8 gemm M={M} N={N} K={K}": (gemm, self.flops(M),
                                               mx_weight_bytes(N, K, 0) + M * K * (1 + 1 / 32) + M * N * 2),
             f"swiglu_mxfp8 M={M} K={K}": (prod, 0.0, M * K * 4 + M * K * (1 + 1 / 32)),
         }
+        if ops.swiglu_row_fusable(M, K, ops.CEIL_DIV448):
+            # the step's path at one row: producer and GEMM in one launch
+            fused = [lambda wt=wt, st=st: torch.ops.mach_amd.swiglu_mx_gemm(self.inputs[M], wt, st, N, ops.E4M3,
+                                                                              ops.CEIL_DIV448)
+                     for wt, st in self.copies]
+            out[f"swiglu->mxfp8 gemm, one launch, M={M} N={N} K={K}"] = (
+                fused, self.flops(M), mx_weight_bytes(N, K, 0) + M * K * 4 + M * N * 2)
+        return out
 
 
 class MxLinear(Workload):

@@ -141,6 +141,16 @@ int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void* w_tiled, c
                 int64_t N, int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
+/* SwiGLU -> MXFP8 -> MX GEMM for one activation row, in one launch: the weight-
+ * streaming GEMM computes the row's codes and scales from gate_up bf16 [1, 2K]
+ * itself, with the producer's arithmetic (mxl_swiglu_mxfp8, rule 1 or 2), so y is
+ * bit-identical to mxl_swiglu_mxfp8 followed by mxl_mx_gemm.  K % 128 == 0,
+ * K <= 12288; other shapes return MXL_EUNSUPPORTED (use the two calls).  Replaces
+ * mach_swiglu_mxfp8_down at M = 1 (src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22,71-76). */
+int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
+                       const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
+                       void* stream);
+
 /* Block-FP8 GEMM: y[m, n] = sum_g sa[g*M + m] * sb[(n/128) * (K/128) + g] *
  * (A_g . W_g) with fp32 FMA per K128 block, bf16 out.  A E4M3 [M, K]; W tiled
  * E4M3 (fmt 0, no scales); sb fp32 [ceil(N/128), K/128].  Replaces

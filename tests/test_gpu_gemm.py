@@ -196,3 +196,39 @@ def test_swiglu_mx_down_matches_oracle(pkg, oracle_mod, dev, rule, M):
     # the producer's own codes are the oracle's
     a, sa = torch.ops.mach_amd.swiglu_mxfp8(gu.to(dev), rule, False)
     assert np.array_equal(a.view(torch.uint8).cpu().numpy(), rc) and np.array_equal(sa.cpu().numpy(), rs)
+
+
+@pytest.mark.parametrize("fmt", [0, 2, 3])
+@pytest.mark.parametrize("rule", [1, 2])
+@pytest.mark.parametrize("N,K", [(160, 128), (200, 640), (2560, 9216), (96, 12288), (512, 2048)])
+def test_swiglu_row_fused_is_bit_identical(pkg, oracle_mod, dev, fmt, rule, N, K):
+    """One launch (SwiGLU codes computed inside the weight-streaming GEMM) equals the
+    producer followed by the GEMM bit for bit, and the oracle within the GEMM bar."""
+    ops = pkg.ops
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 300 + N + K)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    g = torch.Generator().manual_seed(301 + K)
+    gu = (torch.randn(1, 2 * K, generator=g) * 2).bfloat16()
+    gu[0, 5] = float("inf")  # an infinite amax block and a NaN lane exercise the special-value path
+    gu[0, K + 40] = float("nan")
+    bias = torch.randn(N, generator=g).bfloat16().to(dev) if N == 200 else None
+    gud = gu.to(dev)
+    a, sa = torch.ops.mach_amd.swiglu_mxfp8(gud, rule, False)
+    y_ref = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, bias)
+    y = torch.ops.mach_amd.swiglu_mx_gemm(gud, tiled, tiled_s, N, fmt, rule, bias)
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    finite = (torch.randn(1, 2 * K, generator=g) * 2).bfloat16()
+    y = ops.swiglu_mx_down(finite.to(dev), tiled, tiled_s, N, fmt, rule)
+    rc, rs = oracle_mod.swiglu_mxfp8(finite, rule)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)))
+    _check(y.float().cpu().numpy(), ref)
+
+
+def test_swiglu_row_fused_rejects_other_shapes(pkg, dev):
+    ops = pkg.ops
+    w = torch.zeros(16 * 512, dtype=torch.uint8, device=dev)
+    with pytest.raises(ValueError):
+        torch.ops.mach_amd.swiglu_mx_gemm(torch.zeros(2, 1024, dtype=torch.bfloat16, device=dev), w, w, 16, 0, 1)
+    with pytest.raises(ValueError):
+        torch.ops.mach_amd.swiglu_mx_gemm(torch.zeros(1, 1024, dtype=torch.bfloat16, device=dev), w, w, 16, 0, 0)
+    assert not ops.swiglu_row_fusable(1, 12800, 1) and ops.swiglu_row_fusable(1, 9216, 2)

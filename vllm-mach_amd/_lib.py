@@ -42,6 +42,7 @@ SIGNATURES = {
     "mxl_pack_weight": (_I, [_P, _P, _I64, _I64, _I, _P, _P, _P]),
     "mxl_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "mxl_mx_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P]),
+    "mxl_swiglu_mx_gemm": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P]),
     "mxl_block_fp8_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "mxl_grouped_gemm": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P]),
     "mxl_moe_route_workspace_bytes": (_I64, [_I64, _I64, _I64]),

@@ -160,6 +160,10 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
 // Weight-streaming kernel for decode-sized M (gemm_stream.hip), MX or block-FP8.
 bool stream_gemm_eligible(int64_t M, int64_t K, bool block);
 hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s);
+// One activation row computed from its bf16 gate/up row inside the weight-streaming
+// GEMM (p.a = gate_up, M = 1, SwiGLU rule 1 or 2)
+bool stream_swiglu_eligible(int64_t M, int64_t K, int rule);
+hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hipStream_t s);
 // Grouped (MoE) variant for few rows per expert: persistent workgroups over
 // (expert, 16-row tile) units, each streaming the expert's weights.
 bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt);

@@ -166,9 +166,13 @@ __device__ __forceinline__ v4f stream_mfma(const v8i (&a)[RUN][4], const uint32_
 
 }  // namespace
 
-template <int FMT, int RUN, bool DB, bool BLOCK>
+// SWIGLU >= 0 (one activation row): p.a is the bf16 gate/up row [2K] and each wave
+// computes its own super-tiles' MXFP8 codes and scales from it with the producer's
+// arithmetic (swiglu8 + quant8x4 under rule SWIGLU) while its weights are in flight.
+template <int FMT, int RUN, bool DB, bool BLOCK, int SWIGLU = -1>
 __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_stream_kernel(GemmParams p) {
   static_assert(!BLOCK || FMT == kE4M3, "block-FP8 weights are E4M3");
+  static_assert(SWIGLU < 0 || !BLOCK, "the fused SwiGLU row feeds MX GEMMs");
   __shared__ float red[2][kStreamMaxWaves][4][64];
   const int t = threadIdx.x, lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -193,6 +197,21 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
   // fragments and scales, kept in registers for every n-tile (rows >= M read row
   // M - 1 and are never stored; loads are clamped inside K so all are unconditional)
   const int64_t count = g < ntiles ? (ntiles - g + G - 1) / G : 0;  // n-tiles of this workgroup
+  // The fused SwiGLU row's bf16 gate/up pieces are requested before the weights: vector
+  // loads complete in issue order, so the SiLU arithmetic then waits for these loads only
+  // and runs while the weights stream in.
+  uint4 gu_raw[SWIGLU >= 0 ? RUN : 1][2];
+  if constexpr (SWIGLU >= 0) {
+    const uint16_t* gu = reinterpret_cast<const uint16_t*>(p.a);
+#pragma unroll
+    for (int u = 0; u < RUN; ++u) {
+      const int64_t k0 = kt[u] * kTileK + (lane >> 2) * 32 + (lane & 3) * 8;
+      const int64_t kc = k0 < p.K ? k0 : p.K - 8;  // blocks past K: any valid data, zeroed below
+      gu_raw[u][0] = *reinterpret_cast<const uint4*>(gu + kc);
+      gu_raw[u][1] = *reinterpret_cast<const uint4*>(gu + p.K + kc);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
+  }
   StreamB<FMT, RUN, BLOCK> b0;
   stream_load_b<FMT, RUN, BLOCK>(p, w, sw, g < ntiles ? g : ntiles - 1, kt, lane, b0);
   // The loads are row-major -- lane l reads piece l % 4 of row l / 4, so four
@@ -217,7 +236,34 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
                           sa[gi * p.M + rows[3]]};
       }
   }
-  {
+  if constexpr (SWIGLU >= 0) {
+    // lanes 4 b .. 4 b + 3 own 32-block b of the super-tile (8 values each, the producer's
+    // lane mapping).  Fragment lane 16 q + r of slice j holds K values 16 q .. 16 q + 15
+    // (dwords 0-3) and 64 + 16 q .. 64 + 16 q + 15 (dwords 4-7) of the slice, the layout the
+    // unfused path loads: dword 4 h + d is word d % 2 of lane 4 b + 2 (q % 2) + d / 2 with
+    // b = 4 j + 2 h + q / 2.  Its scale is block 4 j + q's code, placed in byte q where the
+    // scale dword of the unfused path has it.
+#pragma unroll
+    for (int u = 0; u < RUN; ++u) {
+      float g[8], up[8], v[8];
+      bf16x8_to_f32(gu_raw[u][0], g);
+      bf16x8_to_f32(gu_raw[u][1], up);
+      swiglu8<SWIGLU>(g, up, v);
+      uint32_t pk[2];
+      const uint32_t sc = quant8x4<SWIGLU, true>(v, pk);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int b = 4 * j + 2 * (e >> 2) + (q >> 1);
+          y[e] = __builtin_amdgcn_ds_bpermute(4 * (4 * b + 2 * (q & 1) + ((e & 3) >> 1)), (int)pk[e & 1]);
+        }
+        a[u][j] = v8i{y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]};
+        sraw[u][j] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * 4 * (4 * j + q), (int)sc) << (8 * q);
+      }
+    }
+  } else {
     const int cr = lane >> 2, cp = lane & 3;
     const int64_t row = cr < p.M ? cr : p.M - 1;
     // (block-FP8 has no E8M0 scales: any valid address, the dword is unused)
@@ -475,6 +521,37 @@ hipError_t launch_stream_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
   return hipGetLastError();
 }
 }  // namespace
+
+namespace {
+template <int FMT, int RULE>
+hipError_t launch_swiglu_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (p.KT <= kStreamMaxWaves)
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, false, RULE>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 2, false, false, RULE>), grid,
+                       dim3((unsigned)((p.KT + 1) / 2 * 64)), 0, s, p);
+  return hipGetLastError();
+}
+template <int RULE>
+hipError_t launch_swiglu_rule(int fmt, const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (fmt == kE4M3) return launch_swiglu_fmt<kE4M3, RULE>(p, grid, s);
+  if (fmt == kE2M3) return launch_swiglu_fmt<kE2M3, RULE>(p, grid, s);
+  if (fmt == kE3M2) return launch_swiglu_fmt<kE3M2, RULE>(p, grid, s);
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+bool stream_swiglu_eligible(int64_t M, int64_t K, int rule) {
+  return M == 1 && stream_gemm_eligible(1, K, false) && (rule == kCeilDiv448 || rule == kRpUe8m0);
+}
+
+hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hipStream_t s) {
+  const int64_t ntiles = (p.N + 15) / 16;
+  const dim3 grid((unsigned)(ntiles < cu_count() ? ntiles : cu_count()));
+  if (rule == kCeilDiv448) return launch_swiglu_rule<kCeilDiv448>(fmt, p, grid, s);
+  if (rule == kRpUe8m0) return launch_swiglu_rule<kRpUe8m0>(fmt, p, grid, s);
+  return hipErrorInvalidValue;
+}
 
 bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt) {
   const int waves = fmt == kE4M3 ? stream_grouped_waves<kE4M3>() : stream_grouped_waves<kE2M3>();

@@ -165,6 +165,22 @@ __device__ __forceinline__ float mx_exp(float x) {
   return x > 88.0f ? __builtin_inff() : e;
 }
 
+// SwiGLU of eight (gate, up) pairs: act = bf16(g / (1 + exp(-g))) and v = bf16(act * u)
+// (mxfp8_mlp.py:96-97), or for the rp_ue8m0 rule v = bf16((g / (1 + exp(-g))) * u)
+// (swiglu_quant.py:56-57).  A NaN act makes a NaN v, and quant8x4<RULE, true> codes every
+// NaN v as the canonical one, so the pair roundings leave NaN sign and payload as they come.
+template <int RULE>
+__device__ __forceinline__ void swiglu8(const float* g, const float* u, float* v) {
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    float a0 = g[i] / (1.0f + mx_exp(-g[i])), a1 = g[i + 1] / (1.0f + mx_exp(-g[i + 1]));
+    if (RULE != kRpUe8m0) bf16_round2_nan_any(a0, a1);
+    v[i] = a0 * u[i];
+    v[i + 1] = a1 * u[i + 1];
+    bf16_round2_nan_any(v[i], v[i + 1]);
+  }
+}
+
 // Quantize one 32-element block held by 4 consecutive lanes (8 values each,
 // lane (tid & 3) owns elements [8 (tid & 3), +8)).  The block amax is an
 // xor-shuffle max over the 4 lanes (order-free, so identical to a serial max).

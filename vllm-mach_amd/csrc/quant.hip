@@ -154,18 +154,7 @@ __global__ __launch_bounds__(256) void swiglu_mxfp8_kernel(const uint16_t* __res
   float g[8], u[8], v[8];
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(gate_up + off), g);
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(gate_up + off + K), u);
-  // act = bf16(g / (1 + exp(-g))), v = bf16(act * u): a NaN act makes a NaN v, and
-  // quant8x4<RULE, true> codes every NaN v as the canonical one, so the pair roundings
-  // leave NaN sign and payload as they come
-  // (rule rp_ue8m0, the champion variant: no rounding of act, one bf16 rounding of v)
-#pragma unroll
-  for (int i = 0; i < 8; i += 2) {
-    float a0 = g[i] / (1.0f + mx_exp(-g[i])), a1 = g[i + 1] / (1.0f + mx_exp(-g[i + 1]));
-    if (RULE != kRpUe8m0) bf16_round2_nan_any(a0, a1);
-    v[i] = a0 * u[i];
-    v[i + 1] = a1 * u[i + 1];
-    bf16_round2_nan_any(v[i], v[i + 1]);
-  }
+  swiglu8<RULE>(g, u, v);
   uint32_t packed[2];
   const uint32_t s = quant8x4<RULE, true>(v, packed);
   if (!live) return;

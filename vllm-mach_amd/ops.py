@@ -357,6 +357,38 @@ def _(a, sa, w, sw, n, k, w_fmt, bias=None):
     return a.new_empty((a.shape[0], n), dtype=torch.bfloat16)
 
 
+def swiglu_row_fusable(m: int, k: int, rule: int) -> bool:
+    """Shapes ``mxl_swiglu_mx_gemm`` runs in one launch (one row, the weight-streaming
+    GEMM's K range, rules ceil_div448 and rp_ue8m0)."""
+    return m == 1 and k % 128 == 0 and 128 <= k <= 12288 and rule in (CEIL_DIV448, RP_UE8M0)
+
+
+@torch.library.custom_op("mach_amd::swiglu_mx_gemm", mutates_args=())
+def swiglu_mx_gemm(gate_up: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
+                   rule: int = CEIL_DIV448, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """SwiGLU -> MXFP8 -> MX GEMM of one row in one launch, bit-identical to
+    ``swiglu_mxfp8`` then ``mx_gemm`` (``mach_swiglu_mxfp8_down`` at M = 1,
+    src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22)."""
+    _check_cuda(gate_up, w, sw, bias)
+    if gate_up.dtype != torch.bfloat16 or gate_up.ndim != 2 or gate_up.shape[1] % 64:
+        raise ValueError("swiglu_mx_gemm needs bf16 [1, 2K]")
+    gate_up = gate_up.contiguous()
+    M, K = gate_up.shape[0], gate_up.shape[1] // 2
+    if not swiglu_row_fusable(M, K, rule):
+        raise ValueError(f"swiglu_mx_gemm runs one row with K % 128 == 0, K <= 12288, rule 1 or 2 "
+                         f"(M={M}, K={K}, rule={rule})")
+    out = torch.empty((1, n), dtype=torch.bfloat16, device=gate_up.device)
+    call("mxl_swiglu_mx_gemm", ptr(gate_up), 1, K, rule, ptr(w), ptr(sw), n, w_fmt, ptr(bias), ptr(out), n,
+         stream_handle(gate_up.device))
+    _count("swiglu_mx_gemm")
+    return out
+
+
+@swiglu_mx_gemm.register_fake
+def _(gate_up, w, sw, n, w_fmt, rule=CEIL_DIV448, bias=None):
+    return gate_up.new_empty((gate_up.shape[0], n), dtype=torch.bfloat16)
+
+
 @torch.library.custom_op("mach_amd::quantize_mxfp8_dual", mutates_args=())
 def quantize_mxfp8_dual(x: torch.Tensor, rule: int = FLOOR_CARRY175
                         ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -440,6 +472,8 @@ def swiglu_mx_down(gate_up: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: 
     src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22)."""
     if gate_up.shape[0] == 0:
         return gate_up.new_empty((0, n))
+    if swiglu_row_fusable(gate_up.shape[0], gate_up.shape[1] // 2, rule):
+        return torch.ops.mach_amd.swiglu_mx_gemm(gate_up, w, sw, n, w_fmt, rule)
     a, sa = torch.ops.mach_amd.swiglu_mxfp8(gate_up, rule, False)
     return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, gate_up.shape[1] // 2, w_fmt, None)
 
