@@ -17,7 +17,7 @@ warm, capture, replay, event-timed).  `value` = total algorithmic TFLOP over the
 that kernel over the rotated weight copies, timed with HIP events on the stream they run on.
 
 Usage: python bench.py [--config c2] [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
-       python bench.py --kernel-only {gemm,producer,copy} [--config c2] [--m M] [--iters I]
+       python bench.py --kernel-only {gemm,producer,fused,copy} [--config c2] [--m M] [--iters I]
 """
 from __future__ import annotations
 
@@ -439,7 +439,10 @@ def kernel_only(pkg, args):
         return
     wl = make_workload(pkg, args.config, dev, gen, (args.m,))
     kernels = list(wl.kernels(args.m).items())
-    name, (fns, flops, nbytes) = kernels[0] if args.kernel_only == "gemm" else kernels[1]
+    pick = {"gemm": 0, "producer": 1, "fused": 2}[args.kernel_only]
+    if pick >= len(kernels):
+        raise SystemExit(f"--kernel-only {args.kernel_only}: no such kernel for {args.config} at M={args.m}")
+    name, (fns, flops, nbytes) = kernels[pick]
     for fn in fns:
         fn()
     torch.cuda.synchronize()
@@ -462,7 +465,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5"], default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-only", choices=["gemm", "producer", "copy"],
+    ap.add_argument("--kernel-only", choices=["gemm", "producer", "fused", "copy"],
                     help="profiling mode: launch one kernel back to back (for rocprofv3)")
     ap.add_argument("--m", type=int, default=512, help="rows (tokens for c5) for --kernel-only")
     ap.add_argument("--iters", type=int, default=64, help="launches for --kernel-only")
