@@ -191,7 +191,7 @@ def test_grouped_stream_small_batch(pkg, oracle_mod, dev, monkeypatch, E, N, K, 
     a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
     args = (a, sa, routes, topk) if gathered else (a, sa, None, 1)
     y = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
-    monkeypatch.setenv("MXL_GROUPED_STREAM", "0")
+    monkeypatch.setenv("MXL_GROUPED_MT", "0")
     y_ref_kernel = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
     if K <= 2048:
         assert torch.equal(y, y_ref_kernel)
@@ -200,6 +200,55 @@ def test_grouped_stream_small_batch(pkg, oracle_mod, dev, monkeypatch, E, N, K, 
     for e in range(E):
         lo, hi = int(off[e]), int(off[e + 1])
         if lo == hi or (E > 16 and e % 8):
+            continue
+        rows = rt[lo:hi] // topk if gathered else np.arange(lo, hi)
+        ref = oracle_mod.mx_gemm_ref(rc[rows], rs[rows], parts[e][0], parts[e][1], fmt)
+        _check(got[lo:hi], oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref)))
+
+
+@pytest.mark.parametrize("E,N,K,T,topk,gathered,fmt,skew", [
+    (256, 2048, 512, 2048, 8, False, 2, False),  # the MoE down projection at T = 2048 (c5): the default
+    (256, 1024, 2048, 2048, 8, True, 2, False),  # the MoE gate_up at T = 2048 (c5): forced, four K waves
+    (8, 384, 512, 200, 2, True, 0, True),        # E4M3: an expert with > 80 rows (two units), empty experts
+    (16, 200, 1280, 400, 2, True, 3, True),      # forced: ragged N, K % 512 != 0 (three K waves)
+])
+def test_grouped_stream_80_row_units(pkg, oracle_mod, dev, monkeypatch, E, N, K, T, topk, gathered, fmt, skew):
+    """Tens of routed rows per expert: the streaming kernel over 80-row units (five m-tiles,
+    each expert's weights read about once; the default where K is one super-tile) is
+    bit-identical to the 16-row-unit variant -- every m-tile runs the same MFMA chain --
+    and within the GEMM bar of the default schedule, the wide kernel and the oracle."""
+    from test_gpu_gemm import _act, _check, _weights
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(E + N + K + 1)
+    ids = torch.randint(0, E, (T, topk), generator=g, dtype=torch.int32)
+    if skew:
+        ids[: T // 2, 0] = 0
+        ids[ids == 1] = 2
+    parts = [_weights(oracle_mod, N, K, fmt, 0.02, 400 + e) for e in range(E)]
+    w_t, s_t = ops.pack_weight(torch.from_numpy(np.stack([p_[2] for p_ in parts])).to(dev),
+                               torch.from_numpy(np.stack([p_[1] for p_ in parts])).to(dev), fmt)
+    routes, offsets, _ = torch.ops.mach_amd.moe_route(ids.to(dev), E)
+    R = T * topk
+    assert 32 * E <= R <= 96 * E  # the 80-row-unit path by default
+    x = _act(T if gathered else R, K, 6)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    args = (a, sa, routes, topk) if gathered else (a, sa, None, 1)
+    y_default = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
+    monkeypatch.setenv("MXL_GROUPED_MT", "5")
+    y = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
+    monkeypatch.setenv("MXL_GROUPED_MT", "1")
+    assert torch.equal(y, torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt))
+    if K <= 512:
+        assert torch.equal(y, y_default)
+    monkeypatch.setenv("MXL_GROUPED_MT", "w")
+    y_wide = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
+    _check(y.float().cpu().numpy(), y_wide.float().cpu().numpy())
+    _check(y_default.float().cpu().numpy(), y.float().cpu().numpy())
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    off, rt, got = offsets.cpu().numpy(), routes.cpu().numpy(), y.float().cpu().numpy()
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if lo == hi or (E > 16 and e % 16):
             continue
         rows = rt[lo:hi] // topk if gathered else np.arange(lo, hi)
         ref = oracle_mod.mx_gemm_ref(rc[rows], rs[rows], parts[e][0], parts[e][1], fmt)

@@ -581,8 +581,25 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
                 "mxl_grouped_gemm: need N > 0, K %% 128 == 0, experts > 0");
   MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0, "mxl_grouped_gemm: misaligned operands");
   if (routed_rows == 0) return MXL_OK;
-  if (K % 256 == 0 && routed_rows >= 32 * num_experts && a_rows * K < (int64_t(1) << 32) &&
-      num_experts <= kWideGroupedMaxExperts) {
+  // Schedule by rows per expert: few -> weight streaming over 16-row units; up to 96 on
+  // average with K one super-tile (the MoE down projection) -> weight streaming over 80-row
+  // units, one per expert mostly (each expert's weights read about once); otherwise the wide
+  // kernel's 128-row tiles.  (With K split over waves the 80-row units run one 16-column
+  // n-tile per round and measured 274 against the wide kernel's 143 us at c5's gate_up.)
+  // MXL_GROUPED_MT (tuning runs and tests): 1 or 5 forces that streaming variant where it
+  // applies, 0 the per-expert kernel, w the wide kernel.
+  const char* mt_force = std::getenv("MXL_GROUPED_MT");
+  const char force = mt_force ? mt_force[0] : '\0';
+  int stream_mt = 0;
+  if (force == '1' || force == '5') {
+    stream_mt = force - '0';
+  } else if (force == '\0') {
+    if (routed_rows < 32 * num_experts) stream_mt = 1;
+    else if (routed_rows <= 96 * num_experts && K <= kTileK) stream_mt = kGroupedStreamWideMT;
+  }
+  if (stream_mt && !stream_grouped_eligible(K, num_experts, w_fmt, stream_mt)) stream_mt = 0;
+  const bool wide_ok = K % 256 == 0 && a_rows * K < (int64_t(1) << 32) && num_experts <= kWideGroupedMaxExperts;
+  if (!stream_mt && force != '0' && wide_ok && (force == 'w' || routed_rows >= 32 * num_experts)) {
     // enough rows per expert on average for 128-row blocks: the wide kernel
     GemmParams p{};
     p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;
@@ -604,9 +621,8 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
     }
     return MXL_OK;
   }
-  const char* sg_env = std::getenv("MXL_GROUPED_STREAM");  // tuning runs and tests: 0 = per-expert kernel
-  if (stream_grouped_eligible(K, num_experts, w_fmt) && !(sg_env && sg_env[0] == '0')) {
-    // few rows per expert: persistent workgroups stream each expert's weights past its rows
+  if (stream_mt) {
+    // persistent workgroups stream each expert's weights past its rows
     GemmParams p{};
     p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;
     p.out = (uint16_t*)out; p.row_index = row_index; p.expert_offsets = expert_offsets;
@@ -614,7 +630,7 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
     p.w_expert_stride = mxl_tiled_weight_bytes(N, K, w_fmt);
     p.sw_expert_stride = mxl_tiled_scale_bytes(N, K);
     p.row_div = row_div; p.S = 1;
-    hipError_t e = launch_gemm_stream_grouped(w_fmt, p, num_experts, (hipStream_t)stream);
+    hipError_t e = launch_gemm_stream_grouped(w_fmt, p, num_experts, stream_mt, (hipStream_t)stream);
     if (e != hipSuccess) {
       set_error("mxl_grouped_gemm: launch failed: %s", hipGetErrorString(e));
       return MXL_EHIP;

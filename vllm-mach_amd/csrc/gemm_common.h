@@ -126,6 +126,12 @@ __device__ __forceinline__ v4f mfma_step(v8i a, v8i b, v4f c, uint32_t sa, uint3
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, kE4M3, FMT, 0, (int)sa, J, (int)sb);
 }
 
+// Both scale operands packed by slice: byte J of sa and of sb
+template <int FMT, int J>
+__device__ __forceinline__ v4f mfma_step_packed(v8i a, v8i b, v4f c, uint32_t sa, uint32_t sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, kE4M3, FMT, J, (int)sa, J, (int)sb);
+}
+
 template <int FMT>
 __device__ __forceinline__ v4f mfma_raw(v8i a, v8i b) {
   const v4f z = {0.f, 0.f, 0.f, 0.f};
@@ -151,6 +157,9 @@ int64_t wide_workspace_bytes(const WideConfig& c, int64_t M, int64_t N);
 bool wide_gemm_eligible(int64_t M, int64_t K);
 // Grouped wide kernel: at most this many experts (their prefix lives in LDS).
 constexpr int64_t kWideGroupedMaxExperts = 1024;
+// m-tiles per unit of the grouped weight-streaming variant for tens of rows per expert
+// (80 rows: one unit covers nearly every expert at 64 rows per expert on average)
+constexpr int kGroupedStreamWideMT = 5;
 int cu_count();
 hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const GemmParams& p, int64_t num_experts,
                             hipStream_t s);
@@ -164,9 +173,9 @@ hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStrea
 // GEMM (p.a = gate_up, M = 1, SwiGLU rule 1 or 2)
 bool stream_swiglu_eligible(int64_t M, int64_t K, int rule);
 hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hipStream_t s);
-// Grouped (MoE) variant for few rows per expert: persistent workgroups over
-// (expert, 16-row tile) units, each streaming the expert's weights.
-bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt);
-hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, hipStream_t s);
+// Grouped (MoE) variant: persistent workgroups over (expert, up to 16 mt rows) units,
+// each streaming the expert's weights; mt = 1 (few rows per expert) or 8.
+bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt, int mt);
+hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, int mt, hipStream_t s);
 
 }  // namespace mxl

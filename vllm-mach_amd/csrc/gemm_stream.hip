@@ -164,6 +164,24 @@ __device__ __forceinline__ v4f stream_mfma(const v8i (&a)[RUN][4], const uint32_
   return out;
 }
 
+// stream_mfma<FMT, 1> with the lane's four activation scale bytes packed in one dword
+// (byte j: slice j): the same MFMA chain, in a quarter of the scale registers.
+template <int FMT>
+__device__ __forceinline__ v4f stream_mfma_packed(const v8i (&a)[4], uint32_t sa, const StreamB<FMT, 1>& b) {
+  v4f acc = {};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t* d = b.d[0][j];
+    const v8i bf = FMT == kE4M3 ? v8i{(int)d[0], (int)d[1], (int)d[2], (int)d[3], (int)d[4], (int)d[5], (int)d[6], (int)d[7]}
+                                : v8i{(int)d[0], (int)d[1], (int)d[2], (int)d[3], (int)d[4], (int)d[5], 0, 0};
+    if (j == 0) acc = mfma_step_packed<FMT, 0>(a[j], bf, acc, sa, b.s[0]);
+    if (j == 1) acc = mfma_step_packed<FMT, 1>(a[j], bf, acc, sa, b.s[0]);
+    if (j == 2) acc = mfma_step_packed<FMT, 2>(a[j], bf, acc, sa, b.s[0]);
+    if (j == 3) acc = mfma_step_packed<FMT, 3>(a[j], bf, acc, sa, b.s[0]);
+  }
+  return acc;
+}
+
 }  // namespace
 
 // SWIGLU >= 0 (one activation row): p.a is the bf16 gate/up row [2K] and each wave
@@ -350,27 +368,35 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
   }
 }
 
-// Grouped (MoE) decode-sized GEMM: few routed rows per expert.  A persistent
-// workgroup owns one unit -- 16 routed rows (one m-tile) of one expert -- at a time
-// and streams all of that expert's weight n-tiles past the unit's activation
-// fragments, which each wave gathers once into registers.  Its WK x NW waves split
-// K (wave w takes super-tile w % WK) and N (n-lane w / WK takes n-tiles w / WK,
-// + NW, ...), so a CU keeps many weight fragments in flight even when K is one
-// super-tile; per round of NW n-tiles the WK partials of each are summed in LDS in
-// K order.  Units are numbered expert by expert (a block scan of the experts' m-tile
-// counts in LDS), so the launch needs no host-side counts.
-// Waves per workgroup: sixteen for FP6 weights; eight for E4M3, whose double-buffered
-// fragments need more than the 128 registers a sixteen-wave workgroup leaves a wave.
-template <int FMT>
-constexpr int stream_grouped_waves() { return FMT == kE4M3 ? 8 : 16; }
+// rounds of weight fragments in flight per wave in the grouped variant with MT > 1
+constexpr int kStreamGroupedDepth = 4;
 
-template <int FMT>
-__global__ __launch_bounds__(64 * stream_grouped_waves<FMT>()) void gemm_stream_grouped_kernel(GemmParams p, int E,
-                                                                                            int WK, int NW) {
-  __shared__ float red[2][kStreamMaxWaves][4][64];
-  __shared__ int32_t sh_pre[kStreamGroupedMaxExperts + 1];  // m-tiles before expert e
+// Grouped (MoE) weight-streaming GEMM.  A persistent workgroup owns one unit -- up to
+// 16 MT routed rows (MT m-tiles) of one expert -- at a time and streams all of that
+// expert's weight n-tiles past the unit's activation fragments, which each wave
+// gathers once into registers.  Its WK x NW waves split K (wave w takes super-tile
+// w % WK) and N (n-lane w / WK takes n-tiles w / WK, + NW, ...), so a CU keeps many
+// weight fragments in flight even when K is one super-tile; per round of NW n-tiles
+// the WK partials of each are summed in LDS in K order (one super-tile: stored
+// directly).  Units are numbered expert by expert (a block scan of the experts' unit
+// counts in LDS), so the launch needs no host-side counts.  Every m-tile's product is
+// the same MFMA chain whatever MT is, so the MT variants give identical bits.
+// Waves per workgroup: MT = 1 (a few rows per expert): sixteen for FP6 weights, eight
+// for E4M3, whose double-buffered fragments need more than the 128 registers a
+// sixteen-wave workgroup leaves a wave.  MT > 1: four, whose activation fragments
+// (32 MT registers per super-tile) need the registers of a whole SIMD.
+template <int FMT, int MT>
+constexpr int stream_grouped_waves() { return MT > 1 ? 4 : (FMT == kE4M3 ? 8 : 16); }
+
+template <int FMT, int MT>
+__global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_stream_grouped_kernel(GemmParams p, int E,
+                                                                                                int WK, int NW) {
+  constexpr int WAVES = stream_grouped_waves<FMT, MT>();
+  constexpr int ROWS = 16 * MT;
+  __shared__ float red[2][WAVES][MT][4][64];
+  __shared__ int32_t sh_pre[kStreamGroupedMaxExperts + 1];  // units before expert e
   __shared__ int32_t sh_off[kStreamGroupedMaxExperts + 1];  // expert_offsets
-  __shared__ int32_t sh_scan[1024];
+  __shared__ int32_t sh_scan[64 * WAVES];
   const int t = threadIdx.x, lane = t & 63, nthreads = (int)blockDim.x;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
   const int r = lane & 15, q = lane >> 4;
@@ -379,11 +405,11 @@ __global__ __launch_bounds__(64 * stream_grouped_waves<FMT>()) void gemm_stream_
 
   for (int e = t; e <= E; e += nthreads) sh_off[e] = (int32_t)p.expert_offsets[e];
   __syncthreads();
-  // m-tile counts per thread chunk of experts, then a block-wide inclusive scan
+  // unit counts per thread chunk of experts, then a block-wide inclusive scan
   const int chunk = (E + nthreads - 1) / nthreads;
   const int e0 = t * chunk < E ? t * chunk : E, e1 = e0 + chunk < E ? e0 + chunk : E;
   int cnt = 0;
-  for (int e = e0; e < e1; ++e) cnt += (sh_off[e + 1] - sh_off[e] + 15) / 16;
+  for (int e = e0; e < e1; ++e) cnt += (sh_off[e + 1] - sh_off[e] + ROWS - 1) / ROWS;
   sh_scan[t] = cnt;
   __syncthreads();
   for (int off = 1; off < nthreads; off <<= 1) {
@@ -395,7 +421,7 @@ __global__ __launch_bounds__(64 * stream_grouped_waves<FMT>()) void gemm_stream_
   int base = sh_scan[t] - cnt;
   for (int e = e0; e < e1; ++e) {
     sh_pre[e] = base;
-    base += (sh_off[e + 1] - sh_off[e] + 15) / 16;
+    base += (sh_off[e + 1] - sh_off[e] + ROWS - 1) / ROWS;
   }
   if (t == nthreads - 1) sh_pre[E] = sh_scan[t];
   __syncthreads();
@@ -411,26 +437,28 @@ __global__ __launch_bounds__(64 * stream_grouped_waves<FMT>()) void gemm_stream_
       else hi_e = mid - 1;
     }
     const int e = lo_e;
-    const int64_t lo = __builtin_amdgcn_readfirstlane(sh_off[e] + (u - sh_pre[e]) * 16);
+    const int64_t lo = __builtin_amdgcn_readfirstlane(sh_off[e] + (u - sh_pre[e]) * ROWS);
     const int64_t end = __builtin_amdgcn_readfirstlane(sh_off[e + 1]);
-    const int64_t hi = lo + 16 < end ? lo + 16 : end;
+    const int64_t hi = lo + ROWS < end ? lo + ROWS : end;
     const uint8_t* w = p.w + e * p.w_expert_stride;
     const uint8_t* sw = static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride;
     const int64_t kt1[1] = {kw < p.KT ? kw : p.KT - 1};
     const bool valid[1] = {kw < p.KT};
 
     // the first round's weights first, then the unit's gathered activation fragments
-    StreamB<FMT, 1> b0, b1;
+    StreamB<FMT, 1> b0, b1;  // (b1: MT = 1 only)
     auto nt_of = [&](int64_t round) -> int64_t {
       const int64_t nt = nl + round * NW;
       return nt < ntiles ? nt : ntiles - 1;
     };
     stream_load_b<FMT, 1, false>(p, w, sw, nt_of(0), kt1, lane, b0);
-    v8i a[1][4];
-    uint32_t sa[1][4];
-    {
+    v8i a[MT][1][4];
+    uint32_t sa[MT > 1 ? 1 : MT][1][4];  // MT = 1: one byte per slice
+    uint32_t spk[MT];                    // MT > 1: the four bytes packed (byte j: slice j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
       const int cr = lane >> 2, cp = lane & 3;
-      int64_t row = lo + cr;
+      int64_t row = lo + 16 * i + cr;
       if (row >= hi) row = hi - 1;  // padding rows read a valid row and are not stored
       const int64_t arow = p.row_index ? (int64_t)(p.row_index[row] / p.row_div) : row;
       const uint8_t* srow = static_cast<const uint8_t*>(p.sa) + arow * (p.K / 32);
@@ -452,36 +480,106 @@ __global__ __launch_bounds__(64 * stream_grouped_waves<FMT>()) void gemm_stream_
         int y[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) y[k] = __builtin_amdgcn_ds_bpermute(from, (int)x[k]);
-        a[0][j] = v8i{y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]};
+        a[i][0][j] = v8i{y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]};
         const uint32_t sraw = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * r + j), (int)sd);
         const bool in = kt1[0] * kTileK + 128 * j < p.K;
-        sa[0][j] = in ? (sraw >> (8 * q)) & 0xFFu : 0u;
-        if (!in) a[0][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+        const uint32_t sbyte = in ? (sraw >> (8 * q)) & 0xFFu : 0u;
+        if constexpr (MT > 1) spk[i] = (j == 0 ? 0u : spk[i]) | (sbyte << (8 * j));
+        else sa[0][0][j] = sbyte;
+        if (!in) a[i][0][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
 
-    // the WK partials of each of the round's NW n-tiles, summed in K order, stored as bf16
-    auto finish = [&](const v4f& acc, int64_t round) {
+    // the m-tiles' products of one n-tile (m-tiles without rows are skipped)
+    auto mma = [&](const StreamB<FMT, 1>& b, v4f (&acc)[MT]) {
+      if constexpr (MT == 1) {
+        acc[0] = stream_mfma<FMT, 1>(a[0], sa[0], b, valid);
+      } else {
+        // every m-tile unconditionally (padding rows are never stored), so the MT
+        // independent MFMA chains interleave; a wave past K adds zero
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[buf][wv][i][lane] = acc[i];
+        for (int i = 0; i < MT; ++i) {
+          acc[i] = stream_mfma_packed<FMT>(a[i][0], spk[i], b);
+          if (!valid[0]) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    };
+    // store the round's NW n-tiles: one super-tile per wave stores its own product; else
+    // the WK partials of each n-tile are summed in LDS in K order
+    auto finish = [&](const v4f (&acc)[MT], int64_t round) {
+      if (MT > 1 && WK == 1) {
+        const int64_t nt = nl + round * NW, col = nt * 16 + r;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            const int64_t row = lo + 16 * i + 4 * q + x;
+            if (nt < ntiles && row < hi && col < p.N) p.out[row * p.ldc + col] = f32_to_bf16(acc[i][x]);
+          }
+        return;
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) red[buf][wv][i][x][lane] = acc[i][x];
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      for (int o = t; o < 256 * NW; o += nthreads) {
-        const int n = o >> 8, i = (o >> 6) & 3, l = o & 63;
-        float sum = red[buf][n * WK][i][l];
-        for (int v = 1; v < WK; ++v) sum += red[buf][n * WK + v][i][l];
+      for (int o = t; o < 256 * MT * NW; o += nthreads) {
+        const int n = o / (256 * MT), i = (o >> 8) % MT, x = (o >> 6) & 3, l = o & 63;
+        float sum;
+        if constexpr (MT > 1) {  // at most four K waves: independent reads, summed in K order
+          float part[WAVES];
+#pragma unroll
+          for (int v = 0; v < WAVES; ++v) part[v] = v < WK ? red[buf][n * WK + v][i][x][l] : 0.0f;
+          sum = part[0];
+#pragma unroll
+          for (int v = 1; v < WAVES; ++v)
+            if (v < WK) sum += part[v];
+        } else {
+          sum = red[buf][n * WK][i][x][l];
+          for (int v = 1; v < WK; ++v) sum += red[buf][n * WK + v][i][x][l];
+        }
         const int64_t nt = n + round * NW;
-        const int64_t row = lo + 4 * (l >> 4) + i, col = nt * 16 + (l & 15);
+        const int64_t row = lo + 16 * i + 4 * (l >> 4) + x, col = nt * 16 + (l & 15);
         if (nt < ntiles && row < hi && col < p.N) p.out[row * p.ldc + col] = f32_to_bf16(sum);
       }
       buf ^= 1;
     };
 
     const int64_t rounds = (ntiles + NW - 1) / NW;
-    for (int64_t rd = 0; rd < rounds; rd += 2) {
-      stream_load_b<FMT, 1, false>(p, w, sw, nt_of(rd + 1 < rounds ? rd + 1 : rd), kt1, lane, b1);
-      finish(stream_mfma<FMT, 1>(a, sa, b0, valid), rd);
-      stream_load_b<FMT, 1, false>(p, w, sw, nt_of(rd + 2 < rounds ? rd + 2 : rd), kt1, lane, b0);
-      if (rd + 1 < rounds) finish(stream_mfma<FMT, 1>(a, sa, b1, valid), rd + 1);
+    v4f acc[MT];
+    if constexpr (MT == 1) {
+      for (int64_t rd = 0; rd < rounds; rd += 2) {
+        stream_load_b<FMT, 1, false>(p, w, sw, nt_of(rd + 1 < rounds ? rd + 1 : rd), kt1, lane, b1);
+        mma(b0, acc);
+        finish(acc, rd);
+        stream_load_b<FMT, 1, false>(p, w, sw, nt_of(rd + 2 < rounds ? rd + 2 : rd), kt1, lane, b0);
+        if (rd + 1 < rounds) {
+          mma(b1, acc);
+          finish(acc, rd + 1);
+        }
+      }
+    } else {
+      // four waves keep kStreamGroupedDepth rounds of weights in flight: a register ring,
+      // round rd + D - 1 requested before round rd is used (past the end: the last round
+      // is re-read, and nothing is stored for it)
+      constexpr int D = kStreamGroupedDepth;
+      StreamB<FMT, 1> ring[D];
+      ring[0] = b0;
+#pragma unroll
+      for (int k = 1; k < D - 1; ++k)
+        stream_load_b<FMT, 1, false>(p, w, sw, nt_of(k < rounds ? k : rounds - 1), kt1, lane, ring[k]);
+      for (int64_t rd = 0; rd < rounds; rd += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+          const int64_t ahead = rd + k + D - 1;
+          stream_load_b<FMT, 1, false>(p, w, sw, nt_of(ahead < rounds ? ahead : rounds - 1), kt1, lane,
+                                       ring[(k + D - 1) % D]);
+          if (rd + k < rounds) {
+            mma(ring[k], acc);
+            finish(acc, rd + k);
+          }
+        }
+      }
     }
   }
 }
@@ -553,27 +651,40 @@ hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hip
   return hipErrorInvalidValue;
 }
 
-bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt) {
-  const int waves = fmt == kE4M3 ? stream_grouped_waves<kE4M3>() : stream_grouped_waves<kE2M3>();
-  return K % 128 == 0 && K >= 128 && (K + kTileK - 1) / kTileK <= waves && num_experts >= 1 &&
-         num_experts <= kStreamGroupedMaxExperts;
+namespace {
+template <int MT>
+int grouped_waves(int fmt) {
+  return fmt == kE4M3 ? stream_grouped_waves<kE4M3, MT>() : stream_grouped_waves<kE2M3, MT>();
 }
-
-hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, hipStream_t s) {
-  const int waves = fmt == kE4M3 ? stream_grouped_waves<kE4M3>() : stream_grouped_waves<kE2M3>();
+template <int MT>
+hipError_t launch_grouped_mt(int fmt, const GemmParams& p, int64_t num_experts, hipStream_t s) {
+  const int waves = grouped_waves<MT>(fmt);
   const int WK = (int)p.KT;
   if (WK < 1 || WK > waves) return hipErrorInvalidValue;
   const int NW = waves / WK;
-  // a bound on the units (m-tiles of routed rows): every expert adds at most one partial tile
-  const int64_t bound = (p.M + 15) / 16 + num_experts;
+  // a bound on the units (16 MT routed rows each): every expert adds at most one partial unit
+  const int64_t bound = (p.M + 16 * MT - 1) / (16 * MT) + num_experts;
   const int64_t G = bound < cu_count() ? bound : cu_count();
   const dim3 grid((unsigned)G), blk((unsigned)(64 * WK * NW));
   const int E = (int)num_experts;
-  if (fmt == kE4M3) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE4M3>), grid, blk, 0, s, p, E, WK, NW);
-  else if (fmt == kE2M3) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE2M3>), grid, blk, 0, s, p, E, WK, NW);
-  else if (fmt == kE3M2) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE3M2>), grid, blk, 0, s, p, E, WK, NW);
+  if (fmt == kE4M3) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE4M3, MT>), grid, blk, 0, s, p, E, WK, NW);
+  else if (fmt == kE2M3) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE2M3, MT>), grid, blk, 0, s, p, E, WK, NW);
+  else if (fmt == kE3M2) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE3M2, MT>), grid, blk, 0, s, p, E, WK, NW);
   else return hipErrorInvalidValue;
   return hipGetLastError();
+}
+}  // namespace
+
+bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt, int mt) {
+  const int waves = mt == 1 ? grouped_waves<1>(fmt) : grouped_waves<kGroupedStreamWideMT>(fmt);
+  return (mt == 1 || mt == kGroupedStreamWideMT) && K % 128 == 0 && K >= 128 &&
+         (K + kTileK - 1) / kTileK <= waves && num_experts >= 1 && num_experts <= kStreamGroupedMaxExperts;
+}
+
+hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, int mt, hipStream_t s) {
+  if (mt == 1) return launch_grouped_mt<1>(fmt, p, num_experts, s);
+  if (mt == kGroupedStreamWideMT) return launch_grouped_mt<kGroupedStreamWideMT>(fmt, p, num_experts, s);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s) {
