@@ -582,17 +582,17 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
   MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0, "mxl_grouped_gemm: misaligned operands");
   if (routed_rows == 0) return MXL_OK;
   // Schedule by rows per expert: few -> weight streaming over 16-row units; up to 96 on
-  // average with K one super-tile (the MoE down projection) -> weight streaming over 80-row
-  // units, one per expert mostly (each expert's weights read about once); otherwise the wide
-  // kernel's 128-row tiles.  (With K split over waves the 80-row units run one 16-column
-  // n-tile per round and measured 274 against the wide kernel's 143 us at c5's gate_up.)
-  // MXL_GROUPED_MT (tuning runs and tests): 1 or 5 forces that streaming variant where it
-  // applies, 0 the per-expert kernel, w the wide kernel.
+  // average with K one super-tile (the MoE down projection) -> weight streaming over 96-row
+  // units, one per expert (each expert's weights read once); otherwise the wide kernel's
+  // 128-row tiles.  (With K split over waves the many-row units run one 16-column n-tile
+  // per round and measured 274 against the wide kernel's 143 us at c5's gate_up.)
+  // MXL_GROUPED_MT (tuning runs and tests): 1 forces the 16-row units, m the many-row units
+  // (where they apply), 0 the per-expert kernel, w the wide kernel.
   const char* mt_force = std::getenv("MXL_GROUPED_MT");
   const char force = mt_force ? mt_force[0] : '\0';
   int stream_mt = 0;
-  if (force == '1' || force == '5') {
-    stream_mt = force - '0';
+  if (force == '1' || force == 'm') {
+    stream_mt = force == '1' ? 1 : kGroupedStreamWideMT;
   } else if (force == '\0') {
     if (routed_rows < 32 * num_experts) stream_mt = 1;
     else if (routed_rows <= 96 * num_experts && K <= kTileK) stream_mt = kGroupedStreamWideMT;

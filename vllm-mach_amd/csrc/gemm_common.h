@@ -158,8 +158,9 @@ bool wide_gemm_eligible(int64_t M, int64_t K);
 // Grouped wide kernel: at most this many experts (their prefix lives in LDS).
 constexpr int64_t kWideGroupedMaxExperts = 1024;
 // m-tiles per unit of the grouped weight-streaming variant for tens of rows per expert
-// (80 rows: one unit covers nearly every expert at 64 rows per expert on average)
-constexpr int kGroupedStreamWideMT = 5;
+// (96 rows: one unit per expert at 64 rows per expert on average; with 80-row units the
+// few experts past 80 rows made some CUs run two units, 107 against 74 us at c5)
+constexpr int kGroupedStreamWideMT = 6;
 int cu_count();
 hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const GemmParams& p, int64_t num_experts,
                             hipStream_t s);

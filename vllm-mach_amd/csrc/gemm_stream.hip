@@ -394,6 +394,9 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
   constexpr int WAVES = stream_grouped_waves<FMT, MT>();
   constexpr int ROWS = 16 * MT;
   __shared__ float red[2][WAVES][MT][4][64];
+  // MT > 1, one super-tile: each wave's 16 MT x 16 bf16 output block, staged so that the
+  // stores move 16-byte row pieces (row stride 24 halfwords: 48 bytes keeps pieces aligned)
+  __shared__ __attribute__((aligned(16))) uint16_t stage[MT > 1 ? WAVES : 1][MT > 1 ? ROWS : 1][24];
   __shared__ int32_t sh_pre[kStreamGroupedMaxExperts + 1];  // units before expert e
   __shared__ int32_t sh_off[kStreamGroupedMaxExperts + 1];  // expert_offsets
   __shared__ int32_t sh_scan[64 * WAVES];
@@ -508,13 +511,35 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
     // the WK partials of each n-tile are summed in LDS in K order
     auto finish = [&](const v4f (&acc)[MT], int64_t round) {
       if (MT > 1 && WK == 1) {
-        const int64_t nt = nl + round * NW, col = nt * 16 + r;
+        const int64_t nt = nl + round * NW;
+        if (nt >= ntiles) return;
+        if (p.N % 8 == 0 && p.ldc % 8 == 0 && ((uintptr_t)p.out & 15) == 0) {
+          // lane (q, r) holds column r of rows 16 i + 4 q + x: through the wave's LDS block,
+          // then each lane stores 16-byte pieces (row, half) of it
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) stage[wv][16 * i + 4 * q + x][r] = f32_to_bf16(acc[i][x]);
+          __builtin_amdgcn_wave_barrier();
+#pragma unroll
+          for (int k = 0; k < (2 * ROWS + 63) / 64; ++k) {
+            const int piece = lane + 64 * k, row = piece >> 1, half = piece & 1;
+            const int64_t col = nt * 16 + 8 * half;
+            if (row < ROWS && lo + row < hi && col < p.N) {
+              const uint4 v = *reinterpret_cast<const uint4*>(&stage[wv][row][8 * half]);
+              *reinterpret_cast<uint4*>(p.out + (lo + row) * p.ldc + col) = v;
+            }
+          }
+          __builtin_amdgcn_wave_barrier();
+          return;
+        }
+        const int64_t col = nt * 16 + r;
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
           for (int x = 0; x < 4; ++x) {
             const int64_t row = lo + 16 * i + 4 * q + x;
-            if (nt < ntiles && row < hi && col < p.N) p.out[row * p.ldc + col] = f32_to_bf16(acc[i][x]);
+            if (row < hi && col < p.N) p.out[row * p.ldc + col] = f32_to_bf16(acc[i][x]);
           }
         return;
       }
