@@ -11,9 +11,11 @@ c1 (MXFP8 linear M=16, 2048x2048), c3 (block-FP8 linear, N=18432 K=2560), c4 (MX
 E2M3 dense N=17408 K=5120), c5 (MXFP6 MoE, 256 experts, top-8, hidden 2048, T in
 {128, 2048}).
 
-Timing: each step is one hipGraph (the reference's protocol, tools/benchmark_nvfp4_lm_head.py:17-40:
-warm, capture, replay, event-timed).  `value` = total algorithmic TFLOP over the step
-/ measured step time.  Per-kernel durations come from graphs of back-to-back launches of
+Timing: steps are captured in hipGraphs and replayed (the reference's protocol,
+tools/benchmark_nvfp4_lm_head.py:17-40: warm, capture, replay, event-timed); a graph holds
+G consecutive steps (`steps_per_graph`: the largest divisor of K up to 10), as a serving
+graph holds a whole forward pass, so the host's per-graph launch cost is not what is
+timed.  `value` = total algorithmic TFLOP over the step / measured step time.  Per-kernel durations come from graphs of back-to-back launches of
 that kernel over the rotated weight copies, timed with HIP events on the stream they run on.
 
 Usage: python bench.py [--config c2] [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
@@ -487,7 +489,12 @@ def main():
     stream = torch.cuda.Stream()
     ncopies = len(wl.copies)
 
-    # one graph per weight copy; a step replays the next one
+    # Graph j holds G consecutive steps (weight copies j, j+1, ..., j+G-1): a serving
+    # step replays one graph for a whole forward pass, so the host's per-graph launch
+    # cost is spread over many kernels; one graph per two-kernel step (c1) would time the
+    # host instead (29 us per step against 7 us of kernels).  G divides K, so exactly K
+    # steps are timed.
+    G = max(g for g in range(1, 11) if args.steps % g == 0)
     graphs = []
     with torch.cuda.stream(stream):
         for ci in range(ncopies):
@@ -497,17 +504,18 @@ def main():
         for ci in range(ncopies):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
-                for fn in wl.step_fns(ci):
-                    fn()
+                for s in range(G):
+                    for fn in wl.step_fns((ci + s) % ncopies):
+                        fn()
             graphs.append(g)
-        for i in range(args.warmup):
-            graphs[i % ncopies].replay()
+        for i in range(-(-args.warmup // G)):
+            graphs[(i * G) % ncopies].replay()
         stream.synchronize()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        for i in range(args.steps):
-            graphs[i % ncopies].replay()
+        for i in range(args.steps // G):
+            graphs[(i * G) % ncopies].replay()
         end.record(stream)
         end.synchronize()
     torch.cuda.synchronize()
@@ -532,7 +540,7 @@ def main():
     out = {
         "metric": METRIC,
         "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "ms_per_step": round(ms_per_step, 5), "steps_per_graph": G, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": wl.dtype,
         "data": f"synthetic (seeded randn), weights rotated over {ncopies} copies (cold HBM); "
                 "per-kernel us_warm relaunches one copy",
