@@ -30,7 +30,7 @@ def test_route_drops_out_of_range_ids(pkg, oracle_mod, dev):
     assert np.array_equal(s.cpu().numpy()[:n], rs[:n])
 
 
-@pytest.mark.parametrize("T,topk,H", [(7, 2, 256), (2048, 8, 2048)])
+@pytest.mark.parametrize("T,topk,H", [(7, 2, 256), (2048, 8, 2048), (33, 1, 128), (5, 10, 512)])
 def test_reduce_bit_exact(pkg, oracle_mod, dev, T, topk, H):
     g = torch.Generator().manual_seed(12035)
     y = torch.randn(T * topk, H, generator=g).bfloat16()
