@@ -9,7 +9,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("T,topk,E", [(7, 2, 4), (1, 8, 256), (128, 8, 256), (2048, 8, 256), (3000, 4, 64),
-                                     (1, 1, 1), (100, 4, 1024), (129, 8, 256)])  # one-chunk and two-chunk edges
+                                     (1, 1, 1), (100, 4, 1024), (129, 8, 256),  # one-chunk and two-chunk edges
+                                     (4096, 8, 512), (300, 8, 2048)])  # histograms past LDS: three launches
 def test_route_bit_exact(pkg, oracle_mod, dev, T, topk, E):
     g = torch.Generator().manual_seed(T + E)
     logits = torch.randn(T, E, generator=g)

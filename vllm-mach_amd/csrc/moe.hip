@@ -6,7 +6,8 @@
 //   sorted_routes[pos]     route at each sorted position
 //   inverse[r]             sorted position of each route (-1 if dropped)
 // Three passes over 1024-route chunks: per-chunk histograms (LDS atomics,
-// order free), one workgroup scanning chunks and experts, then a pass that
+// order free), one workgroup scanning chunks and experts (the two in one
+// workgroup when the histograms fit in LDS), then a pass that
 // ranks each route inside its chunk (shuffle count inside the wavefront plus
 // an LDS prefix over the chunk's 16 wavefronts) and scatters.  A single chunk
 // (decode-sized steps) runs all three in one workgroup.
@@ -101,6 +102,58 @@ __global__ __launch_bounds__(kChunk) void route_scatter_kernel(const int32_t* __
   const int64_t pos = expert_offsets[e] + chunk_base[c * E + e] + whist[w * E + e] + rank;
   sorted_routes[pos] = (int32_t)r;
   inverse[r] = (int32_t)pos;
+}
+
+// Count and scan in one workgroup when the per-chunk histograms fit in LDS
+// (C x E <= kCountScanMaxEntries, E <= 1024): the chunk histograms of route_hist_kernel
+// (route ids loaded eight at a time, LDS atomics), then per expert the running chunk
+// bases in chunk order and the exclusive offsets -- the values route_scan_kernel writes,
+// in one launch instead of two and without its serial walk through global memory.
+constexpr int kCountScanMaxEntries = 14336;
+__global__ __launch_bounds__(kChunk) void route_count_scan_kernel(const int32_t* __restrict__ ids, int64_t R,
+                                                                  int64_t C, int E,
+                                                                  int32_t* __restrict__ chunk_base,
+                                                                  int64_t* __restrict__ expert_offsets) {
+  extern __shared__ int32_t lds[];
+  int32_t* hist = lds;              // [C][E]
+  int32_t* tot = lds + C * E;       // [2][E]
+  const int t = threadIdx.x;
+  for (int64_t i = t; i < C * E; i += kChunk) hist[i] = 0;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < C; c0 += 8) {
+    int32_t e[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int64_t r = (c0 + k) * kChunk + t;
+      e[k] = (c0 + k < C && r < R) ? ids[r] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (e[k] >= 0 && e[k] < E) atomicAdd(&hist[(c0 + k) * E + e[k]], 1);
+  }
+  __syncthreads();
+  for (int x = t; x < E; x += kChunk) {
+    int32_t run = 0;
+    for (int64_t c = 0; c < C; ++c) {
+      const int32_t n = hist[c * E + x];
+      chunk_base[c * E + x] = run;
+      run += n;
+    }
+    tot[x] = run;
+  }
+  __syncthreads();
+  int src = 0;  // inclusive scan of the totals (ping-pong)
+  for (int d = 1; d < E; d <<= 1) {
+    for (int x = t; x < E; x += kChunk) {
+      int32_t v = tot[src * E + x];
+      if (x >= d) v += tot[src * E + x - d];
+      tot[(1 - src) * E + x] = v;
+    }
+    __syncthreads();
+    src = 1 - src;
+  }
+  for (int x = t; x < E; x += kChunk) expert_offsets[x + 1] = tot[src * E + x];
+  if (t == 0) expert_offsets[0] = 0;
 }
 
 // All routes in one chunk (R <= 1024, E <= 1024): the three passes in one
@@ -217,12 +270,18 @@ extern "C" int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, i
     return MXL_OK;
   }
   int32_t* counts = (int32_t*)workspace;
-  if (C > 0) {
-    route_hist_kernel<<<dim3((unsigned)C), kChunk, E * sizeof(int32_t), s>>>(topk_ids, R, (int)E, counts);
-    MXL_CHECK_LAUNCH("mxl_moe_route(hist)");
+  if (C > 0 && C * E <= kCountScanMaxEntries && E <= 1024) {
+    route_count_scan_kernel<<<1, kChunk, (C * E + 2 * E) * sizeof(int32_t), s>>>(topk_ids, R, C, (int)E, counts,
+                                                                                  expert_offsets);
+    MXL_CHECK_LAUNCH("mxl_moe_route(count_scan)");
+  } else {
+    if (C > 0) {
+      route_hist_kernel<<<dim3((unsigned)C), kChunk, E * sizeof(int32_t), s>>>(topk_ids, R, (int)E, counts);
+      MXL_CHECK_LAUNCH("mxl_moe_route(hist)");
+    }
+    route_scan_kernel<<<1, 1024, 2 * E * sizeof(int64_t), s>>>(counts, C, (int)E, expert_offsets);
+    MXL_CHECK_LAUNCH("mxl_moe_route(scan)");
   }
-  route_scan_kernel<<<1, 1024, 2 * E * sizeof(int64_t), s>>>(counts, C, (int)E, expert_offsets);
-  MXL_CHECK_LAUNCH("mxl_moe_route(scan)");
   if (C > 0) {
     route_scatter_kernel<<<dim3((unsigned)C), kChunk, (kChunk / 64) * E * sizeof(int32_t), s>>>(
         topk_ids, R, (int)E, counts, expert_offsets, sorted_routes, inverse);
