@@ -224,6 +224,41 @@ def test_swiglu_row_fused_is_bit_identical(pkg, oracle_mod, dev, fmt, rule, N, K
     _check(y.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("fmt", [0, 2])
+def test_swiglu_row_fused_graph_replay(pkg, oracle_mod, dev, fmt):
+    """The one-launch SwiGLU down projection captured in a graph: each replay with a new
+    gate/up row equals the eager call bit for bit and the oracle within the GEMM bar."""
+    ops = pkg.ops
+    N, K = 2560, 9216  # the decode MLP down projection of the reference's dense model
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 410 + fmt)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    gu = torch.randn(1, 2 * K, device=dev).bfloat16()
+    assert ops.swiglu_row_fusable(1, K, 2)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        ops.swiglu_mx_down(gu, tiled, tiled_s, N, fmt, 2)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y = ops.swiglu_mx_down(gu, tiled, tiled_s, N, fmt, 2)
+        gen = torch.Generator(device=dev).manual_seed(411)
+        for scale in (2.0, 0.5, 0.0):
+            gu.normal_(generator=gen).mul_(scale)
+            graph.replay()
+            stream.synchronize()
+            replayed = y.clone()
+            eager = ops.swiglu_mx_down(gu, tiled, tiled_s, N, fmt, 2)
+            stream.synchronize()
+            assert torch.equal(replayed.view(torch.int16), eager.view(torch.int16))
+            if scale == 0.0:
+                assert not replayed.float().any()
+                continue
+            rc, rs = oracle_mod.swiglu_mxfp8(gu.cpu(), 2)
+            ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)))
+            _check(replayed.float().cpu().numpy(), ref)
+    torch.cuda.current_stream().wait_stream(stream)
+
+
 def test_swiglu_row_fused_rejects_other_shapes(pkg, dev):
     ops = pkg.ops
     w = torch.zeros(16 * 512, dtype=torch.uint8, device=dev)

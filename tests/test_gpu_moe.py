@@ -123,10 +123,15 @@ def test_moe_layer_matches_oracle(pkg, oracle_mod, dev, E, H, I, T, topk, fmt):
         np.testing.assert_allclose(got, ref, rtol=0.03, atol=0.03)  # tests/native_mxfp6/test_moe.py:248
 
 
-def test_moe_graph_replay_changing_routes(pkg, oracle_mod, dev):
+@pytest.mark.parametrize("E,H,I,T", [
+    (4, 256, 128, 7),      # the reference's case
+    (16, 512, 256, 700),   # about 88 routes per expert: both GEMMs on 96-row streaming units,
+                           # routing over six token chunks in one count-and-scan launch
+])
+def test_moe_graph_replay_changing_routes(pkg, oracle_mod, dev, E, H, I, T):
     """Captured layer replayed with new hidden states and rotated expert ids
     (tests/native_mxfp6/test_moe.py:216-248)."""
-    E, H, I, T, topk = 4, 256, 128, 7, 2
+    topk = 2
     c13, s13, c2, s2, x, wts, ids = _moe_case(oracle_mod, E, H, I, T, topk, 12035)
     experts = pkg.Mxfp6Experts(fmt=2)
     w1, w2 = experts.process_weights_after_loading(
