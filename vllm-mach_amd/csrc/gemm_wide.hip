@@ -10,14 +10,16 @@
 // registers) into a ring of K128 stage slots (four, or three for NT = 4 whose
 // 53 KiB stages would not fit four times), issued two or three stages ahead of
 // the MFMAs.  A slot holds
-//   A    8 m-tiles x 2 KiB: chunk (m-tile i, half h) holds the 16 rows x 64 bytes
-//        K [64 h, +64) of rows 16 i .. 16 i + 15 row by row, the four 16-byte
-//        pieces of row r permuted by piece ^ a_swz(r).  The copy is row-major
-//        because the memory pipeline coalesces neighbouring lanes: four lanes
-//        reading one row's 64 bytes move them in one access, while lanes on
+//   A    8 m-tiles x 2 KiB: chunk (m-tile i, half h) holds rows 16 i + 8 h ..
+//        + 7 whole (the slice's 128 bytes per row), the eight 16-byte pieces of
+//        row r permuted by piece ^ a_swz(r).  The copy is row-major because the
+//        memory pipeline coalesces neighbouring lanes: eight lanes reading one
+//        row's 128 bytes move a whole cache line in one request, while lanes on
 //        sixteen different rows (MFMA fragment order) cost one access each --
-//        measured 10.8 vs 3.0 TB/s for this 16 x 64 B pattern.  The permutation
-//        keeps the fragment reads (lane 16 q + r: row r, piece q) free of LDS
+//        measured 10.8 vs 3.0 TB/s for a 16 x 64 B pattern -- and half-line
+//        pieces (16 rows x 64 bytes per copy) cost two requests per line: whole
+//        rows took 3-7 % off every wide shape.  The permutation keeps the
+//        fragment reads (lane 16 q + r: row r, pieces q and 4 + q) free of LDS
 //        bank conflicts;
 //   B    per wave, its NT n-tiles' 2 KiB of the MFMA-tiled weight (copied
 //        verbatim: the tiled layout already is fragment order);
@@ -70,11 +72,13 @@ struct WideSlot {
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-// Piece permutation of row r (0..15) of an A chunk: for every piece q the LDS
-// offsets 64 r + 16 (q ^ a_swz(r)) of rows 0..7 (8..15) are distinct modulo
-// 128 bytes, and those of rows 0..15 distinct modulo 256 bytes, so a 16-byte
-// fragment read meets no bank conflict with either 32 or 64 banks.
-__device__ __forceinline__ int a_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+// Piece permutation of row r (0..15) of an m-tile, whose rows are stored whole
+// (128 bytes: rows 0..7 in the first 1 KiB chunk, 8..15 in the second): piece p
+// of row r sits at 128 (r % 8) + 16 (p ^ a_swz(r)) of its chunk.  For every
+// piece p the offsets of rows 0..7 (8..15) are distinct modulo 128 bytes and
+// those of rows 0..15 distinct modulo 256 bytes, so a 16-byte fragment read
+// meets no bank conflict with either 32 or 64 banks.
+__device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) { return (uint32_t)(uintptr_t)(const lds_u8*)p; }
 
@@ -101,7 +105,9 @@ __device__ __forceinline__ void wide_barrier() { asm volatile("s_barrier" ::: "m
 
 template <int MT, int NT>
 struct WideLanes {
-  uint32_t a_off[MT / 4];  // copy lane l of m-tile (MT / 4) wv + i: row (l / 4) * lda + 16 (l % 4 ^ a_swz(l / 4))
+  // copy lane l of m-tile (MT / 4) wv + u / 2, rows 8 (u % 2) .. + 7: row 8 (u % 2) + l / 8, piece
+  // (l % 8) ^ a_swz(row), as row * lda + 16 piece
+  uint32_t a_off[MT / 2];
   uint32_t sa_off;    // MX: row * K/32; block-FP8: 4 row  (row = t % 16 MT)
   uint32_t sa_piece[4];  // scale ring: lane l of scale wave w reads dword l % 4 of row 4 MT j + 16 w + l / 4
   uint32_t sa_last[4];   // the same for the last super-tile when it is half (K % 512 = 256), from p.sa and
@@ -123,9 +129,9 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
   const int64_t kt = t >> 2;
   const int j = (int)(t & 3);
 #pragma unroll
-  for (int u = 0; u < 2 * AW; ++u) {  // A: m-tile AW wv + u / 2, half u % 2
-    const int i = AW * wv + (u >> 1), hl = u & 1;
-    copy16(p.a + t * 128 + 64 * hl, L.a_off[u >> 1], lds_addr(slot + S::A + (i * 2 + hl) * 1024));
+  for (int u = 0; u < 2 * AW; ++u) {  // A: m-tile AW wv + u / 2, rows 8 (u % 2) .. + 7, whole 128-byte rows
+    const int i = AW * wv + (u >> 1);
+    copy16(p.a + t * 128, L.a_off[u], lds_addr(slot + S::A + (i * 2 + (u & 1)) * 1024));
   }
   // B: the two 1 KiB chunks of the tile that hold slice j (FP6: its 24 bytes per lane
   // straddle two chunks)
@@ -194,9 +200,10 @@ __device__ __forceinline__ void wide_read(const uint8_t* slot, const uint8_t* sa
   }
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
-    const uint8_t* fr = slot + S::A + i * 2048 + 16 * (4 * r + (q ^ a_swz(r)));
-    const uint4 lo = *reinterpret_cast<const uint4*>(fr);
-    const uint4 hi = *reinterpret_cast<const uint4*>(fr + 1024);
+    const uint8_t* row = slot + S::A + i * 2048 + (r >> 3) * 1024 + (r & 7) * 128;
+    const int sw = a_swz(r);
+    const uint4 lo = *reinterpret_cast<const uint4*>(row + 16 * (q ^ sw));        // K 16 q ..
+    const uint4 hi = *reinterpret_cast<const uint4*>(row + 16 * ((q + 4) ^ sw));  // K 64 + 16 q ..
     x.a[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     if (S::SA_RING) x.sa[i] = sa_entry[(16 * i + r) * 16 + 4 * j + q];
     else if (!BLOCK) x.sa[i] = slot[S::SA + (16 * i + r) * 4 + q];
@@ -311,9 +318,9 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
   constexpr int CH = FmtTraits<FMT>::CH;
   WideLanes<MT, NT> L;
 #pragma unroll
-  for (int i = 0; i < AW; ++i) {
-    const int cr = lane >> 2;  // the row this lane copies (row-major chunk order)
-    L.a_off[i] = (uint32_t)(a_row(row_base + (AW * wv + i) * 16 + cr) * p.lda + 16 * ((lane & 3) ^ a_swz(cr)));
+  for (int u = 0; u < 2 * AW; ++u) {
+    const int cr = 8 * (u & 1) + (lane >> 3);  // the m-tile row this lane copies
+    L.a_off[u] = (uint32_t)(a_row(row_base + (AW * wv + (u >> 1)) * 16 + cr) * p.lda + 16 * ((lane & 7) ^ a_swz(cr)));
   }
   // the scale waves' threads t < BM copy row t
   L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & (BM - 1))) : a_row(row_base + (t & (BM - 1))) * (p.K / 32));
