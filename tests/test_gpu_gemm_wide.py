@@ -135,14 +135,16 @@ def test_wide_block_fp8_64_row_tiles(pkg, oracle_mod, dev, monkeypatch, M, N, K,
 
 @pytest.mark.parametrize("mt", [None, "4", "8"])
 @pytest.mark.parametrize("fmt", [0, 2])
-def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, monkeypatch, fmt, mt):
-    """Expert 0 takes 300 routes (three 128-row blocks or five 64-row blocks), expert 1
-    none, the rest a few dozen each; rows are gathered through the sorted route list
-    (row_div = topk)."""
+@pytest.mark.parametrize("T", [400, 340])
+def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, monkeypatch, fmt, mt, T):
+    """Expert 0 takes 300 routes (three 128-row blocks, the last of 44 rows on the 64-row
+    path, or five 64-row blocks), expert 1 none, the rest about 83 (T = 400) or 63 (T =
+    340) each, so 128-row blocks of both paths meet in one launch; rows are gathered
+    through the sorted route list (row_div = topk)."""
     if mt:
         monkeypatch.setenv("MXL_WIDE_MT", mt)
     ops = pkg.ops
-    E, N, K, T, topk = 8, 384, 1024, 400, 2
+    E, N, K, topk = 8, 384, 1024, 2
     g = torch.Generator().manual_seed(5)
     ids = torch.randint(2, E, (T, topk), generator=g, dtype=torch.int32)
     ids[:300, 0] = 0

@@ -568,10 +568,17 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
       if (sh_pre[e] <= mb && mb < sh_pre[e + 1]) sh_hit = e;
     __syncthreads();
     const int e = __builtin_amdgcn_readfirstlane(sh_hit);
-    wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, sh_row[e] + (mb - sh_pre[e]) * BM, sh_row[e + 1],
-                                       p.w + e * p.w_expert_stride,
-                                       static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride, nb, 0, nullptr,
-                                       0, ring, sa_ring, t, lane, wv, r, q);
+    const int64_t rb = sh_row[e] + (mb - sh_pre[e]) * BM, rhi = sh_row[e + 1];
+    const uint8_t* we = p.w + e * p.w_expert_stride;
+    const uint8_t* swe = static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride;
+    // a 128-row block with at most 64 routed rows (an expert's last block) runs the
+    // 64-row tile path in the same ring: half the activation copies and MFMAs
+    if (MT == 8 && __builtin_amdgcn_readfirstlane((int)(rhi - rb)) <= 64)
+      wide_tile<FMT, (MT == 8 ? 4 : MT), NT, BLOCK, GROUPED>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring,
+                                                             sa_ring, t, lane, wv, r, q);
+    else
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring, sa_ring, t, lane,
+                                             wv, r, q);
     __syncthreads();  // the epilogue's LDS reads are done before the next tile's copies
   }
 }
