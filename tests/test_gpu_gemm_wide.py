@@ -179,6 +179,8 @@ def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, monkeypatch, fmt
     (3, 200, 384, 3),        # ragged N, three K128 slices over eight waves
     (16, 4096, 10240, 0),
     (16, 1000, 128, 2),      # a single slice
+    (16, 2048, 2048, 0),     # c1's shape: 128 n-tiles, four super-tiles
+    (5, 18408, 2560, 3),     # 1151 n-tiles, the last 8 columns wide
 ])
 def test_stream_decode_gemm(pkg, oracle_mod, dev, M, N, K, fmt):
     """The weight-streaming decode kernel (M <= 16) against the oracle."""
