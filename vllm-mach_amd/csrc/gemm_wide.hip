@@ -523,9 +523,9 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
 
   // Grouped: persistent workgroups.  The experts' BM-row block counts are
   // prefix-summed once per workgroup into LDS; each workgroup then walks the
-  // tiles L = blockIdx, blockIdx + grid, ... of the (m-block bound x n-block)
-  // grid (the same XCD remap, so a workgroup stays on its XCD's tiles) and
-  // finds its expert by a parallel search of the prefix.
+  // tiles L = blockIdx, blockIdx + grid, ... of the routed (m-block x n-block)
+  // grid, n-blocks fastest (the same XCD remap, so a workgroup stays on its XCD's
+  // tiles), and finds its expert by a parallel search of the prefix.
   __shared__ int32_t sh_pre[kWideMaxExperts + 1];   // m-blocks before expert e
   __shared__ int32_t sh_row[kWideMaxExperts + 1];   // expert_offsets
   __shared__ int32_t sh_hit;
@@ -554,13 +554,17 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   if (t == 255) sh_pre[E] = sh_scan[255];
   __syncthreads();
   const int64_t total_mb = sh_pre[E];
-  const int64_t Gt = g.mblocks * g.nblocks;  // the launch bound on tiles
+  // the routed tiles only (the launch's m-block count is a bound): the XCD remap then
+  // spreads them evenly, whatever the tile order
+  const int64_t Gt = (total_mb < g.mblocks ? total_mb : g.mblocks) * g.nblocks;
   const int64_t per = Gt >> 3, extra = Gt & 7;
   for (int64_t Lid = blockIdx.x; Lid < Gt; Lid += gridDim.x) {
     const int64_t xcd = Lid & 7;
     const int64_t logical = xcd * per + (xcd < extra ? xcd : extra) + (Lid >> 3);
-    const int64_t mb = logical % g.mblocks;
-    const int64_t nb = logical / g.mblocks;
+    // n-blocks fastest: an expert block's n-blocks are consecutive, so they run on one
+    // XCD and its gathered activation rows are fetched into that L2 once
+    const int64_t nb = logical % g.nblocks;
+    const int64_t mb = logical / g.nblocks;
     if (mb >= total_mb) continue;  // beyond the routed m-blocks (uniform)
     if (t == 0) sh_hit = 0;
     __syncthreads();
