@@ -127,6 +127,8 @@ def test_moe_layer_matches_oracle(pkg, oracle_mod, dev, E, H, I, T, topk, fmt):
     (4, 256, 128, 7),      # the reference's case
     (16, 512, 256, 700),   # about 88 routes per expert: both GEMMs on 96-row streaming units,
                            # routing over six token chunks in one count-and-scan launch
+    (8, 1024, 512, 256),   # gate_up (K = 1024) on the wide grouped kernel: 64 rows per expert
+                           # under the rotated ids (the 64-row path), mixed sizes at first
 ])
 def test_moe_graph_replay_changing_routes(pkg, oracle_mod, dev, E, H, I, T):
     """Captured layer replayed with new hidden states and rotated expert ids
