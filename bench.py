@@ -375,43 +375,164 @@ def make_workload(pkg, name, dev, gen, sweep=None):
 
 # ------------------------------------------------------------------ CPU leg
 
-def cpu_baseline(budget_s: float = 15.0):
-    """The oracle's CPU path (C SwiGLU->MXFP8 producer + exact dequantize + BLAS matmul)
-    on a bounded sample of the c2 workload: M = 16 rows.  Median of >= 5 runs after one
-    warmup, with all host threads and with one thread; about `budget_s` each."""
-    import statistics
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+class _RowPool:
+    """Runs a row-wise oracle stage (C through ctypes, which releases the GIL) over row
+    chunks on `threads` host threads, so "all threads" covers the quantizers too."""
+
+    def __init__(self, threads: int):
+        from concurrent.futures import ThreadPoolExecutor
+        self.threads = threads
+        self.pool = ThreadPoolExecutor(max_workers=threads) if threads > 1 else None
+
+    def map(self, fn, x, *args):
+        """fn(x[rows], *args) -> tuple of arrays with rows first; concatenated."""
+        import numpy as np
+        n = x.shape[0]
+        if self.pool is None or n < 2:
+            return fn(x, *args)
+        k = min(self.threads, n)
+        bounds = [n * i // k for i in range(k + 1)]
+        parts = list(self.pool.map(lambda i: fn(x[bounds[i]:bounds[i + 1]], *args), range(k)))
+        if isinstance(parts[0], tuple):
+            return tuple(np.concatenate([p[j] for p in parts]) for j in range(len(parts[0])))
+        return np.concatenate(parts)
+
+
+def _cpu_case(name: str, M: int, g, pool: "_RowPool", cache: dict):
+    """(callable running one CPU step of config `name` at M rows, flops).  The oracle's
+    restatement of the reference's CPU path: quantize / produce the activation in C,
+    dequantize exactly, fp32 matmul against the exactly dequantized (pre-computed)
+    weights, one bf16 rounding (tests/native_mxfp6/test_mxfp8_sm120.py:53-57); block-FP8
+    folds the per-K128 partials in ascending group order (fp8/ordered.py:8-64); the MoE
+    runs the per-expert reference (tests/native_mxfp6/test_moe.py:230-247)."""
+    import numpy as np
     import oracle
-    N, K = SwigluDown.N, SwigluDown.K
+    if name in ("c1", "c2", "c4"):
+        N, K, fmt, std = {"c1": (2048, 2048, 0, 0.02), "c2": (2560, 9216, 0, 0.02),
+                          "c4": (17408, 5120, 2, 0.015)}[name]
+        if "w" not in cache:
+            w = (torch.randn(N, K, generator=g) * std).bfloat16()
+            wc, ws = (oracle.quant_mxfp8(w, 0) if fmt == 0 else oracle.quant_mxfp6(w, fmt))
+            cache["w"] = torch.from_numpy(pool.map(lambda c, s: oracle.dequant_mx(c, s, fmt), wc, ws))
+        wdq = cache["w"]
+        if name == "c2":
+            x = torch.randn(M, 2 * K, generator=g).bfloat16()
+            xb = oracle.bf16_bits(x)
+            produce = lambda: pool.map(oracle.swiglu_mxfp8, xb, oracle.RULE_CEIL_DIV448)
+        else:
+            x = torch.randn(M, K, generator=g)
+            x[:, torch.randperm(K, generator=g)[: max(1, K // 100)]] *= 20
+            xb = oracle.bf16_bits(x.bfloat16())
+            produce = lambda: pool.map(oracle.quant_mxfp8, xb, 0)
+
+        def run():
+            c, sc = produce()
+            a = torch.from_numpy(pool.map(lambda cc, ss: oracle.dequant_mx(cc, ss, 0), c, sc))
+            return (a @ wdq.T).bfloat16()
+        return run, 2.0 * M * N * K
+    if name == "c3":
+        N, K = 18432, 2560
+        G = K // 128
+        if "w" not in cache:
+            wb = (torch.randn(N, K, generator=g) * 0.02).view(N // 128, 128, G, 128)
+            sb = (wb.abs().amax(dim=(1, 3)) / 448.0).clamp_min(1e-12)
+            q = (wb / sb[:, None, :, None]).view(N, K).to(torch.float8_e4m3fn)
+            cache["w"] = (q.float(), sb.float().repeat_interleave(128, dim=0))  # [N, K], [N, G]
+        wq, sbn = cache["w"]
+        xb = oracle.bf16_bits(torch.randn(M, K, generator=g).bfloat16())
+
+        def run():
+            q, s = pool.map(lambda xx: tuple(np.ascontiguousarray(t) for t in oracle.quant_block_fp8(xx)), xb)
+            a = torch.from_numpy(oracle.e4m3_to_f32(q))
+            sa = torch.from_numpy(s)
+            acc = torch.zeros(M, N)
+            for gi in range(G):  # ascending-group fold of the exact K128 partials
+                raw = a[:, gi * 128:(gi + 1) * 128] @ wq[:, gi * 128:(gi + 1) * 128].T
+                acc += raw * (sa[:, gi:gi + 1] * sbn[:, gi][None, :])
+            return acc.bfloat16()
+        return run, 2.0 * M * N * K
+    if name == "c5":
+        E, H, I, topk = 256, 2048, 512, 8
+        if "w" not in cache:
+            w13 = (torch.randn(E * 2 * I, H, generator=g) * 0.015).bfloat16()
+            c13, s13 = oracle.quant_mxfp6(w13, 2)
+            w2 = (torch.randn(E * H, I, generator=g) * 0.015).bfloat16()
+            c2, s2 = oracle.quant_mxfp6(w2, 2)
+            deq = lambda c, s: oracle.dequant_mx(c, s, 2)
+            cache["w"] = (torch.from_numpy(pool.map(deq, c13, s13)).view(E, 2 * I, H),
+                          torch.from_numpy(pool.map(deq, c2, s2)).view(E, H, I))
+        W13, W2 = cache["w"]
+        T = M
+        xb = oracle.bf16_bits(torch.randn(T, H, generator=g).bfloat16())
+        wts, ids = torch.topk(torch.softmax(torch.randn(T, E, generator=g), -1), topk, -1)
+        wts = (wts / wts.sum(-1, keepdim=True)).float().numpy()
+        ids = ids.int().numpy()
+
+        def run():
+            c, sc = pool.map(oracle.quant_mxfp8, xb, 0)
+            a = torch.from_numpy(pool.map(lambda cc, ss: oracle.dequant_mx(cc, ss, 0), c, sc))
+            routes, offs, inv = oracle.moe_route(ids, E)
+            y = np.zeros((T * topk, H), np.uint16)
+            for e in range(E):
+                lo, hi = int(offs[e]), int(offs[e + 1])
+                if lo == hi:
+                    continue
+                gu = (a[torch.from_numpy(routes[lo:hi] // topk).long()] @ W13[e].T).bfloat16()
+                c2_, s2_ = oracle.swiglu_mxfp8(oracle.bf16_bits(gu), oracle.RULE_CEIL_DIV448)
+                y[lo:hi] = oracle.bf16_bits((torch.from_numpy(oracle.dequant_mx(c2_, s2_, 0)) @ W2[e].T).bfloat16())
+            return oracle.moe_reduce(y, wts, inv)
+        return run, 2.0 * T * topk * (2 * I * H + H * I)
+    raise ValueError(name)
+
+
+def cpu_baseline(name: str, sweep, budget_s: float = 2.0):
+    """The reference's CPU path (the oracle's restatement) timed on this host at every M
+    of the config's sweep: median of >= 3 runs after one warmup (more within `budget_s`
+    per M), with all the job's host threads and with one thread."""
+    import statistics
     avail = len(os.sched_getaffinity(0))
-    threads = min(avail, int(os.environ.get("OMP_NUM_THREADS", "0") or avail))  # the job's CPU share
-    g = torch.Generator().manual_seed(0)
-    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
-    wc, ws = oracle.quant_mxfp8(w, 0)
-    wdq = torch.from_numpy(oracle.dequant_mx(wc, ws, 0))
-    M = 16
-    gu = torch.randn(M, 2 * K, generator=g).bfloat16()
-    flops = 2.0 * M * N * K
-
-    def timed(n_threads):
+    env = int(os.environ.get("OMP_NUM_THREADS") or 0)
+    threads = min(avail, env) if env > 0 else avail  # the job's CPU share
+    cache: dict = {}
+    per_m, tot = {}, {threads: [0.0, 0.0], 1: [0.0, 0.0]}
+    for n_threads in (threads, 1):
         torch.set_num_threads(n_threads)
-        times = []
-        t_start = time.perf_counter()
-        while len(times) < 6 or (time.perf_counter() - t_start < budget_s and len(times) < 1000):
-            t0 = time.perf_counter()
-            c, sc = oracle.swiglu_mxfp8(gu, oracle.RULE_CEIL_DIV448)
-            a = torch.from_numpy(oracle.dequant_mx(c, sc, 0))
-            _ = (a @ wdq.T).bfloat16()
-            times.append(time.perf_counter() - t0)
-        return statistics.median(times[1:]), len(times) - 1
-
-    dt_all, n_all = timed(threads)
-    dt_one, n_one = timed(1)
+        pool = _RowPool(n_threads)
+        g = torch.Generator().manual_seed(0)
+        for M in sweep:
+            run, flops = _cpu_case(name, M, g, pool, cache)
+            run()
+            times = []
+            t_start = time.perf_counter()
+            while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
+                t0 = time.perf_counter()
+                run()
+                times.append(time.perf_counter() - t0)
+            dt = statistics.median(times)
+            key = "ms" if n_threads == threads else "ms_1thread"
+            per_m.setdefault(str(M), {})[key] = round(dt * 1e3, 3)
+            per_m[str(M)]["tflops" if n_threads == threads else "tflops_1thread"] = round(flops / dt / 1e12, 4)
+            tot[n_threads][0] += flops
+            tot[n_threads][1] += dt
     torch.set_num_threads(threads)
-    return {"value": flops / dt_all / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "value_1thread": flops / dt_one / 1e12,
-            "sample": f"c2 at M={M}: oracle SwiGLU->MXFP8 (C, 1 thread) + exact dequant + torch fp32 matmul "
-                      f"+ bf16, weights pre-dequantized; median of {n_all} runs with {threads} threads "
-                      f"({dt_all * 1e3:.2f} ms) and of {n_one} runs with 1 thread ({dt_one * 1e3:.2f} ms)"}
+    return {"value": round(tot[threads][0] / tot[threads][1] / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "value_1thread": round(tot[1][0] / tot[1][1] / 1e12, 4), "cpu_model": _cpu_model(),
+            "host_threads_available": avail, "per_m": per_m,
+            "sample": f"{name}, the whole sweep M={list(sweep)} (one CPU step = the oracle's quantizer or "
+                      f"producer in C over {threads} threads by row chunks, exact dequantization and a torch fp32 "
+                      f"matmul on {threads} threads against pre-dequantized weights, bf16 out); median of >= 3 "
+                      f"runs per M after one warmup; value = total flops / summed medians"}
 
 
 # ------------------------------------------------------------- profiling mode
@@ -550,8 +671,8 @@ def main():
     out["roofline"]["traffic"] = measured_traffic(args.config, dom[2], dom[0])
     out["roofline"]["traffic_source"] = ("profiles/hbm_traffic.md (rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, "
                                          "calibrated on a 256 MiB device copy)")
-    if args.config == "c2" and not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline()
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.config, wl.sweep)
     print(json.dumps(out))
 
 

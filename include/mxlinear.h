@@ -50,6 +50,16 @@ int mxl_device_supported(int device);
 int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t ldx, int rule,
                        void* codes, void* scales, void* stream);
 
+/* The same quantization with the scales in the reference's swizzled layout
+ * (128-row x 4-group tiles: byte (r, g) at (((r/128 T + g/4) 32 + r%32) 4 +
+ * (r%128)/32) 4 + g%4, T = ceil(K/128), padding bytes zeroed;
+ * mxl_swizzled_scale_bytes(M, K) bytes), the layout the reference's GEMMs read.
+ * Replaces vLLM's mxfp8_e4m3_quantize(x, is_sf_swizzled_layout=True)
+ * (src/vllm_mach/mxfp8/native_backend.py:287-293) and the packed-scale
+ * torch.ops.mxfp6.quantize_mxfp8 (src/vllm_mach/mxfp6/moe_utils.py:285-317). */
+int mxl_quantize_mxfp8_swizzled(const void* x, int64_t M, int64_t K, int64_t ldx, int rule, void* codes,
+                                void* scales, void* stream);
+
 /* MXFP6 weight quantization (OCP MX v1.0 floor rule): bf16 x [M, K] (row
  * stride ldx elements) -> packed FP6 [M, 3K/4] (fmt 2 = E2M3, 3 = E3M2) + E8M0
  * [M, K/32].  Replaces the offline MXFP6 quantizer the reference's checkpoints
@@ -60,6 +70,12 @@ int mxl_quantize_mxfp6(const void* x, int64_t M, int64_t K, int64_t ldx, int fmt
 
 /* Bytes of the swizzled scale buffer for [M, K] (mxfp8_mlp.py:122). */
 int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K);
+
+/* Logical E8M0 scales [R, K/32] -> the swizzled layout (padding zeroed).
+ * Replaces pack_scales (src/vllm_mach/mxfp6/moe_utils.py:162-164,
+ * src/vllm_mach/mxfp6/dense_mxfp8.py:150-151), whose output this library's
+ * GEMMs read as swizzled scales. */
+int mxl_swizzle_scales(const void* logical, int64_t R, int64_t K, void* swizzled, void* stream);
 
 /* SwiGLU -> MXFP8 producer: gate_up bf16 [M, 2K] (gate = cols [0, K), up =
  * [K, 2K)) -> codes [M, K] + scales, logical [M, K/32] (swizzled = 0) or the
@@ -118,9 +134,39 @@ int64_t mxl_tiled_scale_bytes(int64_t N, int64_t K);
 int mxl_pack_weight(const void* codes, const void* scales, int64_t N, int64_t K, int fmt,
                     void* tiled_codes, void* tiled_scales, void* stream);
 
-/* Scratch bytes the GEMMs may use for split-K partials at (M, N, K); with a
- * smaller workspace they run unsplit. */
+/* The same repack with the E8M0 scales given in the swizzled layout
+ * (scale_layout 1, as mxl_quantize_mxfp8_swizzled writes them for N rows) or
+ * logical (0).  Replaces the weight-side pack_scales input of the reference's
+ * MXFP8 GEMMs, whose weight scales arrive swizzled
+ * (src/vllm_mach/mxfp8/native_backend.py:266-281). */
+int mxl_pack_weight_ex(const void* codes, const void* scales, int scale_layout, int64_t N, int64_t K, int fmt,
+                       void* tiled_codes, void* tiled_scales, void* stream);
+
+/* Per-call GEMM options: the activation-scale layout and the tuning overrides
+ * of the reference's native GEMM (tactic, splits: _DEFAULT_CONFIG,
+ * src/vllm_mach/mxfp8/native_backend.py:29).  A NULL options pointer means
+ * {0, -1, 0, 0, 0, 0}: logical scales, everything chosen by the cost model. */
+typedef struct mxl_gemm_options {
+  int sa_layout; /* MX activation scales: 0 logical [M, K/32], 1 swizzled */
+  int kernel;    /* -1 automatic; 0 weight-streaming (M <= 16), 1 wide (M >= 64,
+                    K % 256 == 0), 2 generic; grouped GEMMs also 3 (96-row
+                    weight-streaming units).  A kernel the shape does not admit
+                    returns MXL_EUNSUPPORTED. */
+  int splits;    /* 0 automatic, else the K split (wide with tile_n, generic) */
+  int tile_n;    /* wide: 64-column groups per workgroup tile, 1, 2 or 4; 0 automatic */
+  int tile_m;    /* wide: 16-row tiles per workgroup tile, 4 or 8; 0 automatic */
+  int hybrid;    /* wide, splits == 1: whole-K full rounds, the remainder split */
+} mxl_gemm_options;
+
+/* Scratch bytes the GEMMs may use for split-K partials at (M, N, K) (the
+ * largest over weight formats and block-FP8); with a smaller workspace they
+ * run unsplit. */
 int64_t mxl_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/* Exactly the split-K bytes mxl_mx_gemm_ex (block = 0) or
+ * mxl_block_fp8_gemm_ex (block = 1) uses for this shape, format and options. */
+int64_t mxl_gemm_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, int w_fmt, int block,
+                                    const mxl_gemm_options* options);
 
 /* Two-limb MX GEMM for M <= 64: y = bf16(hi . W^T + res . W^T) with the limbs
  * accumulated separately in fp32 (each limb's partial goes to the workspace,
@@ -140,6 +186,14 @@ int mxl_mx_gemm_dual(const void* hi, const void* s_hi, const void* res, const vo
 int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,
                 int64_t N, int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc,
                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* mxl_mx_gemm with per-call options (NULL: the defaults); sa is read in
+ * options->sa_layout.  Replaces mxfp8_sm120::gemm's tactic / splits arguments
+ * and its swizzled activation scales (src/vllm_mach/mxfp8/native_backend.py:77-89,
+ * 193-205). */
+int mxl_mx_gemm_ex(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled, int64_t N,
+                   int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc, void* workspace,
+                   int64_t workspace_bytes, const mxl_gemm_options* options, void* stream);
 
 /* SwiGLU -> MXFP8 -> MX GEMM for one activation row, in one launch: the weight-
  * streaming GEMM computes the row's codes and scales from gate_up bf16 [1, 2K]
@@ -161,6 +215,12 @@ int mxl_block_fp8_gemm(const void* a, const void* sa_colmajor, int64_t M, const 
                        const void* sb, int64_t N, int64_t K, const void* bias, void* out, int64_t ldc,
                        void* workspace, int64_t workspace_bytes, void* stream);
 
+/* mxl_block_fp8_gemm with per-call options (kernel, splits, tiles; sa_layout
+ * must be 0). */
+int mxl_block_fp8_gemm_ex(const void* a, const void* sa_colmajor, int64_t M, const void* w_tiled, const void* sb,
+                          int64_t N, int64_t K, const void* bias, void* out, int64_t ldc, void* workspace,
+                          int64_t workspace_bytes, const mxl_gemm_options* options, void* stream);
+
 /* Grouped MX GEMM over experts: output row p (bf16 [routed_rows, N]) of expert
  * e, expert_offsets[e] <= p < expert_offsets[e+1], is A[row_index[p] / row_div]
  * . W[e]^T (A[p] when row_index is NULL).  W: num_experts tiled weights laid
@@ -171,9 +231,17 @@ int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, const int32_
                      const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
                      void* out, void* stream);
 
+/* mxl_grouped_gemm with a per-call schedule (options->kernel: -1 automatic,
+ * 0 16-row weight-streaming units, 3 96-row units, 1 wide 128-row tiles
+ * (tile_m 4: 64-row), 2 per-expert generic). */
+int mxl_grouped_gemm_ex(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index, int row_div,
+                        const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
+                        const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, void* out,
+                        const mxl_gemm_options* options, void* stream);
+
 /* Token sort by expert (stable): topk_ids int32 [T, topk] -> sorted_routes
  * int32 [T*topk], expert_offsets int64 [E+1], inverse int32 [T*topk] (-1 for
- * ids outside [0, E)).  Replaces route_mxfp8_out's routing outputs
+ * ids outside [0, E)).  1 <= E <= 2560.  Replaces route_mxfp8_out's routing outputs
  * (src/vllm_mach/mxfp6/moe_utils.py:205-255, src/vllm_mach/mxfp6/moe.py:651-669). */
 int64_t mxl_moe_route_workspace_bytes(int64_t T, int64_t topk, int64_t E);
 int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, int64_t E, int32_t* sorted_routes,

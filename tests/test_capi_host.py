@@ -62,6 +62,9 @@ def test_invalid_arguments_fail_before_any_launch(pkg):
         _lib.call("mxl_pack_weight", 16, 16, 16, 100, 0, 16, 16, None)
     with pytest.raises(_lib.MxlError, match="workspace too small"):
         _lib.call("mxl_moe_route", 16, 4096, 8, 256, 16, 16, 16, None, 0, None)
+    # the scatter's per-wavefront histograms bound the expert count (160 KiB of LDS)
+    with pytest.raises(_lib.MxlError, match="at most 2560 experts"):
+        _lib.call("mxl_moe_route", 16, 4096, 8, 2561, 16, 16, 16, 16, 1 << 30, None)
 
 
 def test_missing_library_fails_loudly(tmp_path, monkeypatch, pkg):
@@ -136,11 +139,74 @@ def test_workspace_capture_miss_raises(pkg, monkeypatch):
     from vllm_mach_amd import ops
     monkeypatch.setattr(ops, "stream_handle", lambda device: 0x1234)
     monkeypatch.setattr(ops, "_workspaces", {})
+    monkeypatch.setattr(ops, "_planned", {})
+    monkeypatch.setattr(ops, "_retired", [])
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
-    cpu = torch.device("cpu")
+    cpu = torch.device("cpu", 0)
     buf = ops.workspace(cpu, 100)
     assert buf.numel() >= 100 and ops.workspace(cpu, 50) is buf
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
     assert ops.workspace(cpu, 80) is buf
     with pytest.raises(RuntimeError, match="before graph capture"):
         ops.workspace(cpu, 10_000)
+
+
+def test_workspace_growth_keeps_captured_buffers(pkg, monkeypatch):
+    """A buffer handed to a call during capture stays alive after a larger shape replaces
+    it (a captured graph writes through its address on replay); one never captured is
+    released."""
+    from vllm_mach_amd import ops
+    monkeypatch.setattr(ops, "stream_handle", lambda device: 0x77)
+    monkeypatch.setattr(ops, "_workspaces", {})
+    monkeypatch.setattr(ops, "_planned", {})
+    monkeypatch.setattr(ops, "_retired", [])
+    cpu = torch.device("cpu", 0)
+    capturing = [False]
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: capturing[0])
+    a = ops.workspace(cpu, 1000)
+    b = ops.workspace(cpu, 5000)          # grows: a was never captured, so it is not kept
+    assert b is not a and ops._retired == []
+    capturing[0] = True
+    assert ops.workspace(cpu, 4000) is b  # a graph now holds b's address
+    capturing[0] = False
+    c = ops.workspace(cpu, 20000)
+    assert c is not b and len(ops._retired) == 1 and ops._retired[0] is b
+    assert c.numel() >= 20000
+    info = ops.inspect()
+    assert info["workspaces"] == {"0:0x77:gemm": c.numel()}
+    assert info["planned"] == {"0:gemm": 20000} and info["retired_bytes"] == b.numel()
+
+
+def test_reserve_workspaces_sizes_a_new_stream(pkg, monkeypatch):
+    from vllm_mach_amd import ops
+    stream = [0x10]
+    monkeypatch.setattr(ops, "stream_handle", lambda device: stream[0])
+    monkeypatch.setattr(ops, "_workspaces", {})
+    monkeypatch.setattr(ops, "_planned", {})
+    monkeypatch.setattr(ops, "_retired", [])
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    cpu = torch.device("cpu", 0)
+    ops.workspace(cpu, 300, "gemm")
+    ops.workspace(cpu, 9000, "gemm")
+    ops.workspace(cpu, 64, "route")
+    stream[0] = 0x20                       # the capture stream
+    ops.reserve_workspaces(cpu)
+    ws = ops.inspect()["workspaces"]
+    assert ws["0:0x20:gemm"] >= 9000 and ws["0:0x20:route"] >= 64
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    assert ops.workspace(cpu, 9000, "gemm").numel() >= 9000   # no allocation during capture
+
+
+def test_warmup_collects_distinct_problems(pkg):
+    from vllm_mach_amd import linear as L, warmup as W
+    layers = []
+    for n in (256, 256, 384):
+        layer = torch.nn.Module()
+        layer.mxl_shape = (n, 512)
+        layer.mxl_format = 0
+        layer.mxl_kernel = L.Mxfp8LinearKernel()
+        layers.append(layer)
+    dense, moe = W.collect_problems(layers)
+    assert sorted((k[1], k[2]) for k in dense) == [(256, 512), (384, 512)] and moe == {}
+    assert W._sizes([1, 16, 300]) == [300, 256, 128, 64, 16, 1]
+    assert W._sizes([]) == []

@@ -13,6 +13,24 @@ from test_gpu_gemm import _act, _check, _weights
 pytestmark = pytest.mark.gpu
 
 
+def force(monkeypatch, ops, cfg=None, **changes):
+    """Pin the kernel selection for this test (``ops._tuning``), merged with any pin already
+    set: ``cfg`` is a wide-tile spec "NT,S" or "NT,1,h"; keywords set other fields."""
+    cur = ops._tuning
+    f = {k: getattr(cur, k) for k in ("kernel", "splits", "tile_n", "tile_m", "hybrid")} if cur is not None else \
+        {"kernel": -1, "splits": 0, "tile_n": 0, "tile_m": 0, "hybrid": 0}
+    if cfg:
+        parts = cfg.split(",")
+        f.update(tile_n=int(parts[0]), splits=int(parts[1]), hybrid=int(len(parts) > 2 and parts[2] == "h"))
+    f.update(changes)
+    monkeypatch.setattr(ops, "_tuning", pkg_options(ops, **f))
+
+
+def pkg_options(ops, kernel, splits, tile_n, tile_m, hybrid):
+    from vllm_mach_amd import _lib
+    return _lib.GemmOptions(0, kernel, splits, tile_n, tile_m, hybrid)
+
+
 @pytest.mark.parametrize("M,N,K,fmt,cfg,bias", [
     (64, 256, 512, 0, None, False),
     (200, 1000, 768, 0, "2,1", True),     # K = 1.5 super-tiles, ragged M
@@ -26,9 +44,9 @@ pytestmark = pytest.mark.gpu
     (256, 700, 1280, 3, "4,3", False),    # N not a multiple of 256
 ])
 def test_wide_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias):
-    if cfg:
-        monkeypatch.setenv("MXL_WIDE_CONFIG", cfg)
     ops = pkg.ops
+    if cfg:
+        force(monkeypatch, ops, cfg)
     wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 11 + N + K)
     tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
     x = _act(M, K, 7 + M)
@@ -50,9 +68,9 @@ def test_wide_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias
     (512, 18432, 2560, None),
 ])
 def test_wide_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
-    if cfg:
-        monkeypatch.setenv("MXL_WIDE_CONFIG", cfg)
     ops = pkg.ops
+    if cfg:
+        force(monkeypatch, ops, cfg)
     g = torch.Generator().manual_seed(91 + M + K)
     w = torch.randn(N, K, generator=g) * 0.02
     wb = w.reshape(N // 128, 128, K // 128, 128)
@@ -77,8 +95,8 @@ def test_wide_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
 def test_wide_hybrid_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias):
     """More tiles than CUs: full rounds of whole-K tiles write bf16, the remainder is split
     in K into compact partials and summed by the tile reduce; repeated calls agree."""
-    monkeypatch.setenv("MXL_WIDE_CONFIG", cfg)
     ops = pkg.ops
+    force(monkeypatch, ops, cfg)
     wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 5 + N + K)
     tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
     x = _act(M, K, 9 + M)
@@ -95,8 +113,8 @@ def test_wide_hybrid_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cf
 
 @pytest.mark.parametrize("M,N,K,cfg", [(512, 8320, 1280, "2,1,h"), (512, 16640, 1024, "4,1,h")])
 def test_wide_hybrid_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
-    monkeypatch.setenv("MXL_WIDE_CONFIG", cfg)
     ops = pkg.ops
+    force(monkeypatch, ops, cfg)
     g = torch.Generator().manual_seed(33 + K)
     wb = (torch.randn(N, K, generator=g) * 0.02).reshape(N // 128, 128, K // 128, 128)
     sb = (wb.abs().amax(dim=(1, 3)) / 448.0).float()
@@ -123,13 +141,13 @@ def test_wide_hybrid_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, 
 def test_wide_mx_gemm_64_row_tiles(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias):
     """The 64-row workgroup tile (four m-tiles, one activation-scale wave) on the edge
     shapes of the 128-row tests."""
-    monkeypatch.setenv("MXL_WIDE_MT", "4")
+    force(monkeypatch, pkg.ops, tile_m=4)
     test_wide_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias)
 
 
 @pytest.mark.parametrize("M,N,K,cfg", [(100, 384, 1280, "2,2"), (200, 1024, 1280, "4,1"), (300, 8320, 1280, "2,1,h")])
 def test_wide_block_fp8_64_row_tiles(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
-    monkeypatch.setenv("MXL_WIDE_MT", "4")
+    force(monkeypatch, pkg.ops, tile_m=4)
     test_wide_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg)
 
 
@@ -141,9 +159,9 @@ def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, monkeypatch, fmt
     path, or five 64-row blocks), expert 1 none, the rest about 83 (T = 400) or 63 (T =
     340) each, so 128-row blocks of both paths meet in one launch; rows are gathered
     through the sorted route list (row_div = topk)."""
-    if mt:
-        monkeypatch.setenv("MXL_WIDE_MT", mt)
     ops = pkg.ops
+    if mt:
+        force(monkeypatch, ops, tile_m=int(mt))
     E, N, K, topk = 8, 384, 1024, 2
     g = torch.Generator().manual_seed(5)
     ids = torch.randint(2, E, (T, topk), generator=g, dtype=torch.int32)
@@ -202,7 +220,7 @@ def test_wide_split_repeat_and_replay(pkg, oracle_mod, dev, monkeypatch):
     the same bits, since the partials are summed in split order."""
     ops = pkg.ops
     M, N, K = 300, 1024, 2304
-    monkeypatch.setenv("MXL_WIDE_CONFIG", "2,3")
+    force(monkeypatch, ops, "2,3")
     wc, ws, stored = _weights(oracle_mod, N, K, 0, 0.02, 17)
     tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), 0)
     a, sa = torch.ops.mach_amd.quantize_mxfp8(_act(M, K, 5).to(dev), 0)

@@ -8,6 +8,11 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
+def _lib_options(**kw):
+    from vllm_mach_amd import _lib
+    return _lib.GemmOptions(**kw)
+
+
 @pytest.mark.parametrize("T,topk,E", [(7, 2, 4), (1, 8, 256), (128, 8, 256), (2048, 8, 256), (3000, 4, 64),
                                      (1, 1, 1), (100, 4, 1024), (129, 8, 256),  # one-chunk and two-chunk edges
                                      (4096, 8, 512), (300, 8, 2048)])  # histograms past LDS: three launches
@@ -199,7 +204,7 @@ def test_grouped_stream_small_batch(pkg, oracle_mod, dev, monkeypatch, E, N, K, 
     a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
     args = (a, sa, routes, topk) if gathered else (a, sa, None, 1)
     y = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
-    monkeypatch.setenv("MXL_GROUPED_MT", "0")
+    monkeypatch.setattr(ops, "_tuning", _lib_options(kernel=ops.KERNEL_GENERIC))
     y_ref_kernel = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
     if K <= 2048:
         assert torch.equal(y, y_ref_kernel)
@@ -242,13 +247,13 @@ def test_grouped_stream_96_row_units(pkg, oracle_mod, dev, monkeypatch, E, N, K,
     a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
     args = (a, sa, routes, topk) if gathered else (a, sa, None, 1)
     y_default = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
-    monkeypatch.setenv("MXL_GROUPED_MT", "m")
+    monkeypatch.setattr(ops, "_tuning", _lib_options(kernel=ops.KERNEL_STREAM_WIDE))
     y = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
-    monkeypatch.setenv("MXL_GROUPED_MT", "1")
+    monkeypatch.setattr(ops, "_tuning", _lib_options(kernel=ops.KERNEL_STREAM))
     assert torch.equal(y, torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt))
     if K <= 512:
         assert torch.equal(y, y_default)
-    monkeypatch.setenv("MXL_GROUPED_MT", "w")
+    monkeypatch.setattr(ops, "_tuning", _lib_options(kernel=ops.KERNEL_WIDE))
     y_wide = torch.ops.mach_amd.grouped_gemm(*args, offsets, R, w_t, s_t, N, K, fmt)
     _check(y.float().cpu().numpy(), y_wide.float().cpu().numpy())
     _check(y_default.float().cpu().numpy(), y.float().cpu().numpy())

@@ -28,8 +28,10 @@ SIGNATURES = {
     "mxl_last_error": (ctypes.c_char_p, []),
     "mxl_device_supported": (_I, [_I]),
     "mxl_quantize_mxfp8": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "mxl_quantize_mxfp8_swizzled": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "mxl_quantize_mxfp6": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P]),
     "mxl_swizzled_scale_bytes": (_I64, [_I64, _I64]),
+    "mxl_swizzle_scales": (_I, [_P, _I64, _I64, _P, _P]),
     "mxl_swiglu_mxfp8": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P]),
     "mxl_quantize_mxfp8_dual": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P]),
     "mxl_mx_gemm_dual": (_I, [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P]),
@@ -40,8 +42,13 @@ SIGNATURES = {
     "mxl_tiled_weight_bytes": (_I64, [_I64, _I64, _I]),
     "mxl_tiled_scale_bytes": (_I64, [_I64, _I64]),
     "mxl_pack_weight": (_I, [_P, _P, _I64, _I64, _I, _P, _P, _P]),
+    "mxl_pack_weight_ex": (_I, [_P, _P, _I, _I64, _I64, _I, _P, _P, _P]),
     "mxl_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "mxl_gemm_workspace_bytes_ex": (_I64, [_I64, _I64, _I64, _I, _I, _P]),
     "mxl_mx_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P]),
+    "mxl_mx_gemm_ex": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P, _P]),
+    "mxl_block_fp8_gemm_ex": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _P]),
+    "mxl_grouped_gemm_ex": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P, _P]),
     "mxl_swiglu_mx_gemm": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P]),
     "mxl_block_fp8_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "mxl_grouped_gemm": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P]),
@@ -49,6 +56,19 @@ SIGNATURES = {
     "mxl_moe_route": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "mxl_moe_reduce": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
 }
+
+class GemmOptions(ctypes.Structure):
+    """``mxl_gemm_options``: activation-scale layout and tuning overrides of one GEMM call."""
+    _fields_ = [("sa_layout", _I), ("kernel", _I), ("splits", _I), ("tile_n", _I), ("tile_m", _I),
+                ("hybrid", _I)]
+
+    def __init__(self, sa_layout=0, kernel=-1, splits=0, tile_n=0, tile_m=0, hybrid=0):
+        super().__init__(sa_layout, kernel, splits, tile_n, tile_m, hybrid)
+
+
+def options_ptr(opts: "GemmOptions | None"):
+    return None if opts is None else ctypes.byref(opts)
+
 
 _lib = None
 _lock = threading.Lock()

@@ -38,6 +38,34 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+TORCH_OPS_SRC = CSRC / "torch_ops.cpp"
+TORCH_OPS_OUT = HERE / "libmxlinear_torch.so"
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """The torch operator library (host C++ over the C ABI): registers the reference's
+    native op names, loadable with ``torch.ops.load_library``."""
+    import torch
+    import torch.utils.cpp_extension as ext
+
+    inc = ext.include_paths(device_type="cuda") + [str(HERE.parent / "include")]
+    libdir = Path(torch.__file__).parent / "lib"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = TORCH_OPS_OUT.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+           "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *[f"-I{d}" for d in inc], str(TORCH_OPS_SRC), "-o", str(tmp),
+           f"-L{libdir}", f"-L{HERE}", "-lmxlinear", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip",
+           "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch op library build failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, TORCH_OPS_OUT)
+    if verbose:
+        print(f"built {TORCH_OPS_OUT}")
+    return TORCH_OPS_OUT
+
+
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
@@ -52,6 +80,7 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, OUT)
     if verbose:
         print(f"built {OUT}")
+    build_torch_ops(verbose)
     return OUT
 
 

@@ -39,8 +39,6 @@
 // cannot fill 256 CUs, S workgroups split K further and write fp32 partials
 // that a second kernel sums in split order: both orders are fixed, so every
 // result is deterministic.
-#include <cstdlib>
-
 #include "gemm_common.h"
 
 namespace mxl {
@@ -84,9 +82,10 @@ __global__ void pack_weight_kernel(const uint8_t* __restrict__ src, int64_t ld_s
   *reinterpret_cast<uint4*>(dst + tile * (CH * 1024) + c * 1024 + lane * 16) = w;
 }
 
-// One thread writes one lane's scale dword of one tile.
+// One thread writes one lane's scale dword of one tile.  The source is the logical
+// [N, K/32] layout, or (swizzled) the reference's 128-row x 4-group tiles.
 __global__ void pack_scale_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t N,
-                                  int64_t K, int64_t KT, int64_t total) {
+                                  int64_t K, int64_t KT, int64_t total, int swizzled) {
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= total) return;
   const int lane = (int)(id & 63);
@@ -98,7 +97,12 @@ __global__ void pack_scale_kernel(const uint8_t* __restrict__ src, uint8_t* __re
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t blk = kt * 16 + 4 * j + q;
-    if (row < N && blk * 32 < K) w |= (uint32_t)src[row * (K / 32) + blk] << (8 * j);
+    if (row < N && blk * 32 < K) {
+      const int64_t off = swizzled ? (((row >> 7) * ((K / 32 + 3) / 4) + (blk >> 2)) * 32 + (row & 31)) * 16 +
+                                         ((row & 127) >> 5) * 4 + (blk & 3)
+                                   : row * (K / 32) + blk;
+      w |= (uint32_t)src[off] << (8 * j);
+    }
   }
   *reinterpret_cast<uint32_t*>(dst + tile * 256 + lane * 4) = w;
 }
@@ -402,8 +406,22 @@ extern "C" int64_t mxl_tiled_scale_bytes(int64_t N, int64_t K) {
   return NTl * KT * 256;
 }
 
+static int pack_common(const void* codes, const void* scales, int scale_layout, int64_t N, int64_t K, int fmt,
+                       void* tiled_codes, void* tiled_scales, void* stream);
+
 extern "C" int mxl_pack_weight(const void* codes, const void* scales, int64_t N, int64_t K, int fmt,
                                void* tiled_codes, void* tiled_scales, void* stream) {
+  return pack_common(codes, scales, 0, N, K, fmt, tiled_codes, tiled_scales, stream);
+}
+
+extern "C" int mxl_pack_weight_ex(const void* codes, const void* scales, int scale_layout, int64_t N, int64_t K,
+                                  int fmt, void* tiled_codes, void* tiled_scales, void* stream) {
+  MXL_CHECK_ARG(scale_layout == 0 || scale_layout == 1, "mxl_pack_weight_ex: unknown scale layout %d", scale_layout);
+  return pack_common(codes, scales, scale_layout, N, K, fmt, tiled_codes, tiled_scales, stream);
+}
+
+static int pack_common(const void* codes, const void* scales, int scale_layout, int64_t N, int64_t K, int fmt,
+                       void* tiled_codes, void* tiled_scales, void* stream) {
   MXL_CHECK_ARG(valid_wfmt(fmt), "mxl_pack_weight: unknown weight format %d", fmt);
   MXL_CHECK_ARG(N > 0 && K > 0 && K % 128 == 0, "mxl_pack_weight: need N > 0 and K %% 128 == 0 (N=%lld K=%lld)",
                 (long long)N, (long long)K);
@@ -419,35 +437,80 @@ extern "C" int mxl_pack_weight(const void* codes, const void* scales, int64_t N,
   MXL_CHECK_LAUNCH("mxl_pack_weight(codes)");
   if (scales) {
     const int64_t ts = NTl * KT * 64;
-    pack_scale_kernel<<<dim3((unsigned)((ts + 255) / 256)), 256, 0, s>>>((const uint8_t*)scales,
-                                                                         (uint8_t*)tiled_scales, N, K, KT, ts);
+    pack_scale_kernel<<<dim3((unsigned)((ts + 255) / 256)), 256, 0, s>>>(
+        (const uint8_t*)scales, (uint8_t*)tiled_scales, N, K, KT, ts, scale_layout);
     MXL_CHECK_LAUNCH("mxl_pack_weight(scales)");
   }
   return MXL_OK;
 }
 
+static GemmOptions options_of(const void* opts) {
+  GemmOptions o;
+  if (opts) {
+    const int* v = static_cast<const int*>(opts);  // mxl_gemm_options: six ints in declaration order
+    o.sa_layout = v[0]; o.kernel = v[1]; o.splits = v[2]; o.tile_n = v[3]; o.tile_m = v[4]; o.hybrid = v[5];
+  }
+  return o;
+}
+
+// The dense kernel and split a call runs with (shared by the launch and the workspace
+// query, so that the bytes the query reports are the bytes the launch uses).
+struct DensePlan {
+  int kernel;  // kStream, kWide or kGeneric
+  WideConfig wide{2, 1, 1};
+  GemmConfig gen{};
+  int64_t need = 0;  // split-K workspace bytes of the plan
+};
+
+static bool plan_dense(int64_t M, int64_t N, int64_t K, int fmt, bool block, const GemmOptions& o, DensePlan& d) {
+  const bool stream_ok = stream_gemm_eligible(M, K, block);
+  const bool wide_ok = wide_gemm_eligible(M, K);
+  d.kernel = o.kernel == kAuto ? (stream_ok ? kStream : wide_ok ? kWide : kGeneric) : o.kernel;
+  if ((d.kernel == kStream && !stream_ok) || (d.kernel == kWide && !wide_ok) ||
+      (d.kernel != kStream && d.kernel != kWide && d.kernel != kGeneric))
+    return false;
+  if (d.kernel == kWide) {
+    d.wide = wide_config(M, N, K, fmt, o);
+    d.need = wide_workspace_bytes(d.wide, M, N);
+  } else if (d.kernel == kGeneric) {
+    d.gen = choose_config(M, N, K);
+    if (o.splits >= 1 && o.kernel == kGeneric) d.gen.S = o.splits;
+    d.need = d.gen.S > 1 ? (int64_t)d.gen.S * M * N * 4 : 0;
+  }
+  return true;
+}
+
 static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw, int64_t N,
                        int64_t K, int fmt, bool block, const void* bias, void* out, int64_t ldc, void* workspace,
-                       int64_t workspace_bytes, void* stream, const char* who) {
+                       int64_t workspace_bytes, const GemmOptions& o, void* stream, const char* who) {
   MXL_CHECK_ARG(M >= 0 && N > 0 && K > 0 && K % 128 == 0, "%s: need N > 0, K %% 128 == 0 (M=%lld N=%lld K=%lld)", who,
                 (long long)M, (long long)N, (long long)K);
   MXL_CHECK_ARG(ldc >= N, "%s: ldc < N", who);
   MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0, "%s: a and w must be 16-byte aligned", who);
+  MXL_CHECK_ARG(o.sa_layout == 0 || (o.sa_layout == 1 && !block), "%s: unknown activation scale layout %d", who,
+                o.sa_layout);
+  MXL_CHECK_ARG(o.splits >= 0 && o.splits <= 64, "%s: splits must be 0 (automatic) .. 64", who);
   if (M == 0) return MXL_OK;
+  DensePlan d;
+  if (!plan_dense(M, N, K, fmt, block, o, d)) {
+    set_error("%s: kernel %d does not run (M=%lld, K=%lld)", who, o.kernel, (long long)M, (long long)K);
+    return MXL_EUNSUPPORTED;
+  }
   GemmParams p{};
   p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw;
   p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out; p.partial = (float*)workspace;
   p.lda = K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
   p.row_div = 1;
+  set_sa_layout(p, o.sa_layout);
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
-  if (stream_gemm_eligible(M, K, block)) {
+  const bool room = d.need == 0 || (workspace != nullptr && d.need <= workspace_bytes);
+  if (d.kernel == kStream) {
     p.S = 1;
     e = launch_gemm_stream(fmt, block, p, s);
-  } else if (wide_gemm_eligible(M, K)) {
-    WideConfig wc = wide_config(M, N, K, fmt);
-    const int64_t need = wide_workspace_bytes(wc, M, N);
-    if (need > 0 && (need > workspace_bytes || workspace == nullptr)) {
+  } else if (d.kernel == kWide) {
+    WideConfig wc = d.wide;
+    if (!room) {
       const int mt = wc.MT;
       wc = WideConfig{wc.NT, 1, (K + kTileK - 1) / kTileK};  // no room: skip the K split
       wc.MT = mt;
@@ -455,9 +518,8 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
     p.S = wc.S;
     e = launch_gemm_wide(fmt, block, wc, p, 0, s);
   } else {
-    GemmConfig c = choose_config(M, N, K);
-    const int64_t need = c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
-    if (need > workspace_bytes || (need > 0 && workspace == nullptr)) c.S = 1;
+    GemmConfig c = d.gen;
+    if (!room) c.S = 1;
     p.S = c.S;
     const int64_t n_groups = ((N + 15) / 16 + c.NT - 1) / c.NT;
     const int64_t m_groups = (M + 16 * c.MT - 1) / (16 * c.MT);
@@ -479,17 +541,23 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
 }
 
 extern "C" int64_t mxl_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0) return 0;
-  int S = choose_config(M, N, K).S;
-  int64_t bytes = S > 1 ? (int64_t)S * M * N * 4 : 0;
-  if (wide_gemm_eligible(M, K)) {
-    bytes = 0;
-    for (int fmt : {kE4M3, kE2M3}) {
-      const int64_t b = wide_workspace_bytes(wide_config(M, N, K, fmt), M, N);
-      if (b > bytes) bytes = b;
-    }
+  if (M <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
+  // the largest need over the weight formats and the block-FP8 mode
+  int64_t bytes = 0;
+  for (int fmt : {kE4M3, kE2M3}) {
+    DensePlan d;
+    if (plan_dense(M, N, K, fmt, false, GemmOptions(), d) && d.need > bytes) bytes = d.need;
   }
+  DensePlan d;
+  if (plan_dense(M, N, K, kE4M3, true, GemmOptions(), d) && d.need > bytes) bytes = d.need;
   return bytes;
+}
+
+extern "C" int64_t mxl_gemm_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, int w_fmt, int block,
+                                               const void* options) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 128 || !valid_wfmt(w_fmt)) return 0;
+  DensePlan d;
+  return plan_dense(M, N, K, w_fmt, block != 0, options_of(options), d) ? d.need : 0;
 }
 
 extern "C" int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,
@@ -497,7 +565,15 @@ extern "C" int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void*
                            void* workspace, int64_t workspace_bytes, void* stream) {
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm: unknown weight format %d", w_fmt);
   return gemm_common(a, sa, M, w_tiled, sw_tiled, N, K, w_fmt, false, bias, out, ldc, workspace, workspace_bytes,
-                     stream, "mxl_mx_gemm");
+                     GemmOptions(), stream, "mxl_mx_gemm");
+}
+
+extern "C" int mxl_mx_gemm_ex(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,
+                              int64_t N, int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc,
+                              void* workspace, int64_t workspace_bytes, const void* options, void* stream) {
+  MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm_ex: unknown weight format %d", w_fmt);
+  return gemm_common(a, sa, M, w_tiled, sw_tiled, N, K, w_fmt, false, bias, out, ldc, workspace, workspace_bytes,
+                     options_of(options), stream, "mxl_mx_gemm_ex");
 }
 
 extern "C" int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
@@ -569,13 +645,41 @@ extern "C" int mxl_block_fp8_gemm(const void* a, const void* sa_colmajor, int64_
                                   const void* sb, int64_t N, int64_t K, const void* bias, void* out, int64_t ldc,
                                   void* workspace, int64_t workspace_bytes, void* stream) {
   return gemm_common(a, sa_colmajor, M, w_tiled, sb, N, K, kE4M3, true, bias, out, ldc, workspace, workspace_bytes,
-                     stream, "mxl_block_fp8_gemm");
+                     GemmOptions(), stream, "mxl_block_fp8_gemm");
 }
+
+extern "C" int mxl_block_fp8_gemm_ex(const void* a, const void* sa_colmajor, int64_t M, const void* w_tiled,
+                                     const void* sb, int64_t N, int64_t K, const void* bias, void* out, int64_t ldc,
+                                     void* workspace, int64_t workspace_bytes, const void* options, void* stream) {
+  return gemm_common(a, sa_colmajor, M, w_tiled, sb, N, K, kE4M3, true, bias, out, ldc, workspace, workspace_bytes,
+                     options_of(options), stream, "mxl_block_fp8_gemm_ex");
+}
+
+static int grouped_common(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index, int row_div,
+                          const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
+                          const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, void* out,
+                          const GemmOptions& o, void* stream);
 
 extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index, int row_div,
                                 const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
                                 const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
                                 void* out, void* stream) {
+  return grouped_common(a, sa, a_rows, row_index, row_div, expert_offsets, num_experts, routed_rows, w_tiled,
+                        sw_tiled, N, K, w_fmt, out, GemmOptions(), stream);
+}
+
+extern "C" int mxl_grouped_gemm_ex(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index,
+                                   int row_div, const int64_t* expert_offsets, int64_t num_experts,
+                                   int64_t routed_rows, const void* w_tiled, const void* sw_tiled, int64_t N,
+                                   int64_t K, int w_fmt, void* out, const void* options, void* stream) {
+  return grouped_common(a, sa, a_rows, row_index, row_div, expert_offsets, num_experts, routed_rows, w_tiled,
+                        sw_tiled, N, K, w_fmt, out, options_of(options), stream);
+}
+
+static int grouped_common(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index, int row_div,
+                          const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
+                          const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, void* out,
+                          const GemmOptions& o, void* stream) {
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_grouped_gemm: unknown weight format %d", w_fmt);
   MXL_CHECK_ARG(N > 0 && K > 0 && K % 128 == 0 && num_experts > 0 && row_div >= 1,
                 "mxl_grouped_gemm: need N > 0, K %% 128 == 0, experts > 0");
@@ -586,20 +690,21 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
   // units, one per expert (each expert's weights read once); otherwise the wide kernel's
   // 128-row tiles.  (With K split over waves the many-row units run one 16-column n-tile
   // per round and measured 274 against the wide kernel's 143 us at c5's gate_up.)
-  // MXL_GROUPED_MT (tuning runs and tests): 1 forces the 16-row units, m the many-row units
-  // (where they apply), 0 the per-expert kernel, w the wide kernel.
-  const char* mt_force = std::getenv("MXL_GROUPED_MT");
-  const char force = mt_force ? mt_force[0] : '\0';
+  // options.kernel (tuning runs and tests): kStream forces the 16-row units, kStreamWide the
+  // many-row units (where they apply), kGeneric the per-expert kernel, kWide the wide kernel.
+  MXL_CHECK_ARG(o.kernel >= kAuto && o.kernel <= kStreamWide, "mxl_grouped_gemm: unknown kernel %d", o.kernel);
+  MXL_CHECK_ARG(o.sa_layout == 0, "mxl_grouped_gemm: grouped activations take logical scales");
+  const int force = o.kernel;
   int stream_mt = 0;
-  if (force == '1' || force == 'm') {
-    stream_mt = force == '1' ? 1 : kGroupedStreamWideMT;
-  } else if (force == '\0') {
+  if (force == kStream || force == kStreamWide) {
+    stream_mt = force == kStream ? 1 : kGroupedStreamWideMT;
+  } else if (force == kAuto) {
     if (routed_rows < 32 * num_experts) stream_mt = 1;
     else if (routed_rows <= 96 * num_experts && K <= kTileK) stream_mt = kGroupedStreamWideMT;
   }
   if (stream_mt && !stream_grouped_eligible(K, num_experts, w_fmt, stream_mt)) stream_mt = 0;
   const bool wide_ok = K % 256 == 0 && a_rows * K < (int64_t(1) << 32) && num_experts <= kWideGroupedMaxExperts;
-  if (!stream_mt && force != '0' && wide_ok && (force == 'w' || routed_rows >= 32 * num_experts)) {
+  if (!stream_mt && force != kGeneric && wide_ok && (force == kWide || routed_rows >= 32 * num_experts)) {
     // enough rows per expert on average for 128-row blocks: the wide kernel
     GemmParams p{};
     p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;
@@ -611,9 +716,7 @@ extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, c
     WideConfig wc{2, 1, (K + kTileK - 1) / kTileK};
     // 128-row blocks: with 64 rows per expert on average (c5, T = 2048) 64-row blocks
     // measured 8-10 % slower, since experts past 64 rows then copy their weights twice
-    wc.MT = 8;
-    const char* mt_env = std::getenv("MXL_WIDE_MT");  // tuning runs and tests
-    if (mt_env && (std::atoi(mt_env) == 4 || std::atoi(mt_env) == 8)) wc.MT = std::atoi(mt_env);
+    wc.MT = o.tile_m == 4 ? 4 : 8;
     hipError_t e = launch_gemm_wide(w_fmt, false, wc, p, num_experts, (hipStream_t)stream);
     if (e != hipSuccess) {
       set_error("mxl_grouped_gemm: launch failed: %s", hipGetErrorString(e));

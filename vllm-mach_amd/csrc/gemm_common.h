@@ -33,6 +33,36 @@ struct GemmParams {
   int64_t lda, ldc, M, N, K, KT, a_rows;
   int64_t w_expert_stride, sw_expert_stride;
   int row_div, S;
+  int sa_swz = 0;     // MX activation scales: 0 logical [rows, K/32], 1 swizzled 128 x 4 tiles
+  int64_t sa_ss = 4;  // bytes between the scale dwords of consecutive K128 slices of a row (4 or 512)
+};
+
+// Byte offset of row `row`'s scale dword of K128 slice 0; slice s is sa_ss bytes further.
+// Logical: row * K/32.  Swizzled (the reference's activation layout, 128-row x 4-group
+// tiles of 512 bytes, groups padded to a multiple of 4): byte (r, g) sits at
+// (((r / 128) T + g / 4) 32 + r % 32) 16 + ((r % 128) / 32) 4 + g % 4, T = ceil(K / 128).
+__host__ __device__ inline int64_t sa_row_offset(const GemmParams& p, int64_t row) {
+  if (!p.sa_swz) return row * (p.K / 32);
+  const int64_t T = (p.K / 32 + 3) / 4;
+  return (row >> 7) * T * 512 + (row & 31) * 16 + ((row & 127) >> 5) * 4;
+}
+
+inline void set_sa_layout(GemmParams& p, int swizzled) {
+  p.sa_swz = swizzled ? 1 : 0;
+  p.sa_ss = swizzled ? 512 : 4;
+}
+
+// Per-call selection: the scale layout of A and the tuning overrides (the reference's
+// tactic / splits overrides, src/vllm_mach/mxfp8/native_backend.py:29).  Same layout
+// as mxl_gemm_options in include/mxlinear.h.
+enum KernelChoice : int { kAuto = -1, kStream = 0, kWide = 1, kGeneric = 2, kStreamWide = 3 };
+struct GemmOptions {
+  int sa_layout = 0;  // 0 logical, 1 swizzled
+  int kernel = kAuto;
+  int splits = 0;     // 0: the cost model's; else the K split (wide, generic)
+  int tile_n = 0;     // wide: NT in {1, 2, 4}; 0 auto
+  int tile_m = 0;     // wide: MT in {4, 8}; 0 auto
+  int hybrid = 0;     // wide, splits == 1: full rounds whole-K, the remainder split
 };
 
 template <int MT>
@@ -58,11 +88,11 @@ __device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const uint8_t* base = p.a + arow[mt] * p.lda;
-    const uint8_t* sbase = static_cast<const uint8_t*>(p.sa) + arow[mt] * (p.K / 32);
+    const uint8_t* sbase = static_cast<const uint8_t*>(p.sa) + (BLOCK ? 0 : sa_row_offset(p, arow[mt]));
     uint32_t sd = 0;
     if (!BLOCK) {  // scale dword of slice cp (clamped inside K; slices past K are zeroed below)
       const int64_t ks = kt * kTileK + 128 * cp;
-      sd = *reinterpret_cast<const uint32_t*>(sbase + (ks < p.K ? ks : p.K - 128) / 32);
+      sd = *reinterpret_cast<const uint32_t*>(sbase + ((ks < p.K ? ks : p.K - 128) / 128) * p.sa_ss);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -151,7 +181,8 @@ struct WideConfig {
   int64_t kt2 = 0;
   int MT = 8;  // 16-row m-tiles per workgroup tile: 8 (128 rows) or 4 (64 rows)
 };
-WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt);
+// The cost model's choice, or the options' tile / split overrides where given.
+WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptions& o = GemmOptions());
 // Workspace bytes a configuration needs (split partials), 0 when none.
 int64_t wide_workspace_bytes(const WideConfig& c, int64_t M, int64_t N);
 bool wide_gemm_eligible(int64_t M, int64_t K);

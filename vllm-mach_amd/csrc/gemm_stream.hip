@@ -285,7 +285,7 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
     const int cr = lane >> 2, cp = lane & 3;
     const int64_t row = cr < p.M ? cr : p.M - 1;
     // (block-FP8 has no E8M0 scales: any valid address, the dword is unused)
-    const uint8_t* srow = BLOCK ? p.a : static_cast<const uint8_t*>(p.sa) + row * (p.K / 32);
+    const uint8_t* srow = BLOCK ? p.a : static_cast<const uint8_t*>(p.sa) + sa_row_offset(p, row);
     const uint8_t* arow = p.a + row * p.lda;
     const int from = 4 * (4 * r + q);  // byte address of the source lane (4 r + q)
 #pragma unroll
@@ -300,7 +300,8 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
       }
       // scale dword of slice cp (E8M0 of blocks 4 cp .. 4 cp + 3 of the super-tile)
       const int64_t ks = kt[u] * kTileK + 128 * cp;
-      const uint32_t sd = BLOCK ? 0u : *reinterpret_cast<const uint32_t*>(srow + (ks < p.K ? ks : p.K - 128) / 32);
+      const uint32_t sd =
+          BLOCK ? 0u : *reinterpret_cast<const uint32_t*>(srow + ((ks < p.K ? ks : p.K - 128) / 128) * p.sa_ss);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t x[8] = {lo[j].x, lo[j].y, lo[j].z, lo[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
@@ -464,7 +465,7 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
       int64_t row = lo + 16 * i + cr;
       if (row >= hi) row = hi - 1;  // padding rows read a valid row and are not stored
       const int64_t arow = p.row_index ? (int64_t)(p.row_index[row] / p.row_div) : row;
-      const uint8_t* srow = static_cast<const uint8_t*>(p.sa) + arow * (p.K / 32);
+      const uint8_t* srow = static_cast<const uint8_t*>(p.sa) + sa_row_offset(p, arow);
       const uint8_t* ap = p.a + arow * p.lda;
       const int from = 4 * (4 * r + q);
       uint4 lo4[4], hi4[4];
@@ -476,7 +477,7 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
         hi4[j] = *reinterpret_cast<const uint4*>(ap + kc + 64 + 16 * cp);
       }
       const int64_t ks = kt1[0] * kTileK + 128 * cp;
-      const uint32_t sd = *reinterpret_cast<const uint32_t*>(srow + (ks < p.K ? ks : p.K - 128) / 32);
+      const uint32_t sd = *reinterpret_cast<const uint32_t*>(srow + ((ks < p.K ? ks : p.K - 128) / 128) * p.sa_ss);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t x[8] = {lo4[j].x, lo4[j].y, lo4[j].z, lo4[j].w, hi4[j].x, hi4[j].y, hi4[j].z, hi4[j].w};

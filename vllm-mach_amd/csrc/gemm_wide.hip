@@ -39,9 +39,6 @@
 // fp32 partials that a second kernel sums in split order.  The grouped variant
 // walks experts' row ranges (expert_offsets) on device, so the launch needs no
 // host-side counts.
-#include <cstdio>
-#include <cstdlib>
-
 #include "gemm_common.h"
 
 // the copies set M0 (the LDS base of a global->LDS load) themselves
@@ -148,11 +145,11 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
       const int64_t ks = kt + 1 < p.KT ? kt + 1 : p.KT - 1;
       const uint32_t dst = lds_addr(sa_ring + ((kt + 1) % 3) * S::RING_ENTRY + (4 * MT * j + 16 * wv) * 16);
       if (ks == p.KT - 1 && p.K % kTileK != 0) copy4(static_cast<const uint8_t*>(p.sa), L.sa_last[j], dst);
-      else copy4(static_cast<const uint8_t*>(p.sa) + ks * 16, L.sa_piece[j], dst);
+      else copy4(static_cast<const uint8_t*>(p.sa) + ks * 4 * p.sa_ss, L.sa_piece[j], dst);
     }
   } else if (wv < S::SW) {  // activation scales of the 16 MT rows (row = t of the scale waves)
     if (!BLOCK)  // E8M0 bytes of blocks 4t .. 4t + 3
-      copy4(static_cast<const uint8_t*>(p.sa) + t * 4, L.sa_off, lds_addr(slot + S::SA + wv * 256));
+      copy4(static_cast<const uint8_t*>(p.sa) + t * p.sa_ss, L.sa_off, lds_addr(slot + S::SA + wv * 256));
     else  // fp32 scale of K128 group t (column-major [K/128, M])
       copy4(static_cast<const uint8_t*>(p.sa) + t * 4 * p.M, L.sa_off, lds_addr(slot + S::SA + wv * 256));
   }
@@ -323,13 +320,15 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     L.a_off[u] = (uint32_t)(a_row(row_base + (AW * wv + (u >> 1)) * 16 + cr) * p.lda + 16 * ((lane & 7) ^ a_swz(cr)));
   }
   // the scale waves' threads t < BM copy row t
-  L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & (BM - 1))) : a_row(row_base + (t & (BM - 1))) * (p.K / 32));
+  L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & (BM - 1))) : sa_row_offset(p, a_row(row_base + (t & (BM - 1)))));
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t srow = a_row(row_base + 4 * MT * j + 16 * (wv % S::SW) + (lane >> 2)) * (p.K / 32);
-    L.sa_piece[j] = (uint32_t)(srow + 4 * (lane & 3));
-    const int64_t last = 16 * (p.KT - 1) + 4 * (lane & 3);
-    L.sa_last[j] = (uint32_t)(srow + (last < p.K / 32 - 4 ? last : p.K / 32 - 4));
+    // dword (lane % 4) of the super-tile's four slice dwords of its row; a half last
+    // super-tile (K % 512 = 256) clamps the slice inside K
+    const int64_t srow = sa_row_offset(p, a_row(row_base + 4 * MT * j + 16 * (wv % S::SW) + (lane >> 2)));
+    L.sa_piece[j] = (uint32_t)(srow + (lane & 3) * p.sa_ss);
+    const int64_t last = 4 * (p.KT - 1) + (lane & 3);
+    L.sa_last[j] = (uint32_t)(srow + (last < p.K / 128 - 1 ? last : p.K / 128 - 1) * p.sa_ss);
   }
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
@@ -363,7 +362,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
       for (int j = 0; j < 4; ++j) {
         const uint32_t dst = lds_addr(sa_ring + ((tb >> 2) % 3) * S::RING_ENTRY + (4 * MT * j + 16 * wv) * 16);
         if (half) copy4(static_cast<const uint8_t*>(p.sa), L.sa_last[j], dst);
-        else copy4(static_cast<const uint8_t*>(p.sa) + (tb >> 2) * 16, L.sa_piece[j], dst);
+        else copy4(static_cast<const uint8_t*>(p.sa) + (tb >> 2) * 4 * p.sa_ss, L.sa_piece[j], dst);
       }
     }
 #pragma unroll
@@ -633,27 +632,6 @@ __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __re
 
 namespace {
 
-// Optional m-tile count override (tuning runs and tests): MXL_WIDE_MT=4 or 8.
-int wide_mt_override() {
-  const char* v = std::getenv("MXL_WIDE_MT");
-  const int mt = v ? std::atoi(v) : 0;
-  return mt == 4 || mt == 8 ? mt : 0;
-}
-
-// Optional override "NT,S" or "NT,1,h" (hybrid) for tuning runs and tests, e.g.
-// MXL_WIDE_CONFIG=4,3.
-bool wide_override(int& nt, int& s, bool& hybrid) {
-  const char* v = std::getenv("MXL_WIDE_CONFIG");
-  int o_nt = 0, o_s = 0;
-  char h = 0;
-  const int got = v ? std::sscanf(v, "%d,%d,%c", &o_nt, &o_s, &h) : 0;
-  if (got < 2 || (o_nt != 1 && o_nt != 2 && o_nt != 4) || o_s < 1) return false;
-  nt = o_nt;
-  s = o_s;
-  hybrid = got == 3 && h == 'h' && o_s == 1;
-  return true;
-}
-
 // The hybrid split of `tiles` whole-K tiles over `cus` workgroup slots: full
 // rounds first, the remainder split in K as evenly as the CUs allow.  Returns
 // false when there is no partial last round to balance.
@@ -680,17 +658,16 @@ static double wide_stage_cycles(int mt, int nt) { return mt == 8 ? 1200.0 + 900.
 // Pick the workgroup tile (MT, NT), the K split and the hybrid split from the
 // stage model; weights stream at ~5 TB/s; split partials cost a write and a
 // read of their bytes at ~3 TB/s.
-WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
+WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptions& o) {
   const int64_t KT = (K + kTileK - 1) / kTileK;
-  const int mt_force = wide_mt_override();
-  int o_nt, o_s;
-  bool o_h = false;
-  if (wide_override(o_nt, o_s, o_h)) {
+  const int mt_force = o.tile_m == 4 || o.tile_m == 8 ? o.tile_m : 0;
+  if ((o.tile_n == 1 || o.tile_n == 2 || o.tile_n == 4) && o.splits >= 1) {  // explicit tile and split
     const int mt = mt_force ? mt_force : 8;
-    const int64_t per = (KT + o_s - 1) / o_s;
-    WideConfig c{o_nt, (int)((KT + per - 1) / per), per};
+    const int64_t per = (KT + o.splits - 1) / o.splits;
+    WideConfig c{o.tile_n, (int)((KT + per - 1) / per), per};
     c.MT = mt;
-    if (o_h) wide_hybrid(((M + 16 * mt - 1) / (16 * mt)) * ((N + 64 * o_nt - 1) / (64 * o_nt)), KT, cu_count(), c);
+    if (o.hybrid && o.splits == 1)
+      wide_hybrid(((M + 16 * mt - 1) / (16 * mt)) * ((N + 64 * o.tile_n - 1) / (64 * o.tile_n)), KT, cu_count(), c);
     return c;
   }
   const int64_t cus = cu_count();
@@ -707,12 +684,15 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
     const int64_t MB = (M + 16 * mt - 1) / (16 * mt);
     for (int nt : nts) {
       if (mt == 4 && nt == 1) continue;  // not instantiated
+      if (o.tile_n && nt != o.tile_n) continue;
       const int64_t NBk = (N + 64 * nt - 1) / (64 * nt);
       const int64_t tiles = MB * NBk;
       const double t_stage = wide_stage_cycles(mt, nt);
+      // a forced split count is rounded to the admissible one of its super-tiles per split
+      const int64_t s_only = o.splits >= 1 ? (KT + (KT + o.splits - 1) / o.splits - 1) / ((KT + o.splits - 1) / o.splits) : 0;
       for (int64_t s = 1; s <= KT; ++s) {
         const int64_t per = (KT + s - 1) / s;
-        if ((KT + per - 1) / per != s) continue;
+        if ((KT + per - 1) / per != s || (s_only && s != s_only)) continue;
         const double rounds = (double)((tiles * s + cus - 1) / cus);
         const double compute = rounds * per * 4 * t_stage + 3000.0;
         const double partial = s > 1 ? ((double)M * N * 4 * s * 2 + (double)M * N * 2) / (3.0e12 / 2.4e9) : 0.0;
@@ -724,6 +704,7 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt) {
         }
         WideConfig h{nt, 1, KT};
         h.MT = mt;
+        if (s_only > 1 || (o.splits == 1 && !o.hybrid)) continue;  // a forced split excludes the hybrid
         // (64-wide tiles re-read the activations too often for extra rounds to pay off)
         if (s == 1 && nt >= 2 && wide_hybrid(tiles, KT, cus, h)) {
           // full rounds, then the split remainder, its partials' round trip and two more launches
@@ -752,10 +733,7 @@ int64_t wide_workspace_bytes(const WideConfig& c, int64_t M, int64_t N) {
   return c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
 }
 
-bool wide_gemm_eligible(int64_t M, int64_t K) {
-  const char* v = std::getenv("MXL_WIDE_DISABLE");  // tuning runs only: compare with the older kernels
-  return !(v && v[0] == '1') && M >= 64 && K % 256 == 0 && M * K < (int64_t(1) << 32);
-}
+bool wide_gemm_eligible(int64_t M, int64_t K) { return M >= 64 && K % 256 == 0 && M * K < (int64_t(1) << 32); }
 
 template <int FMT, int MT, bool BLOCK, bool GROUPED>
 static hipError_t launch_wide_mt(const WideConfig& c, const GemmParams& p, const WideGrid& g, int64_t grid,

@@ -161,6 +161,10 @@ __global__ __launch_bounds__(kChunk) void route_count_scan_kernel(const int32_t*
 // the offsets, then the same rank and scatter -- so a decode-sized step pays one
 // launch.  The result is the multi-chunk path's (chunk base 0).
 constexpr int kSingleMaxExperts = 1024;
+// Largest expert count any route schedule launches: the scatter's (kChunk / 64) * E
+// ints of LDS must fit gfx950's 160 KiB per workgroup.
+constexpr int kRouteMaxExperts = 160 * 1024 / ((kChunk / 64) * (int)sizeof(int32_t));
+static_assert(kRouteMaxExperts == 2560, "the documented expert limit");
 
 __global__ __launch_bounds__(kChunk) void route_single_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
                                                              int64_t* __restrict__ expert_offsets,
@@ -257,7 +261,9 @@ extern "C" int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, i
                              int64_t* expert_offsets, int32_t* inverse, void* workspace, int64_t workspace_bytes,
                              void* stream) {
   MXL_CHECK_ARG(T >= 0 && topk > 0 && E > 0, "mxl_moe_route: need T >= 0, topk > 0, E > 0");
-  MXL_CHECK_ARG(E <= 4096, "mxl_moe_route: at most 4096 experts (E=%lld)", (long long)E);
+  // route_scatter_kernel keeps one histogram per wavefront of a chunk in LDS:
+  // (kChunk / 64) * E ints must fit gfx950's 160 KiB per workgroup
+  MXL_CHECK_ARG(E <= kRouteMaxExperts, "mxl_moe_route: at most %d experts (E=%lld)", kRouteMaxExperts, (long long)E);
   const int64_t R = T * topk;
   const int64_t C = (R + kChunk - 1) / kChunk;
   MXL_CHECK_ARG(workspace_bytes >= mxl_moe_route_workspace_bytes(T, topk, E) && (C == 0 || workspace),

@@ -37,7 +37,9 @@ struct BlockLane {
 
 // Four lanes own one 32-element block (8 values, one 16-byte load each), so a
 // decode-sized launch still spreads over enough lanes to hide latency.
-template <int RULE>
+__device__ __forceinline__ int64_t swizzle_offset(int64_t r, int64_t g, int64_t K);
+
+template <int RULE, bool SWIZZLED = false>
 __global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                           uint8_t* __restrict__ codes,
                                                           uint8_t* __restrict__ scales, int64_t M,
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __rest
   const uint32_t s = quant8x4<RULE>(v, packed);
   if (!live) return;
   *reinterpret_cast<uint2*>(codes + row * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
-  if (sub == 0) scales[row * blocks_per_row + blk] = (uint8_t)s;
+  if (sub == 0) scales[SWIZZLED ? swizzle_offset(row, blk, K) : row * blocks_per_row + blk] = (uint8_t)s;
 }
 
 // ------------------------------------------------------------ MXFP6 weights
@@ -182,6 +184,22 @@ __global__ void swizzle_pad_kernel(uint8_t* __restrict__ scales, int64_t M, int6
   const int64_t gt = t % T, rt = t / T;
   const int64_t r = rt * 128 + r4 * 32 + r32, g = gt * 4 + g4;
   if (r >= M || g >= K / 32) scales[off] = 0;
+}
+
+// Logical [R, K/32] E8M0 -> the swizzled layout, padding zeroed: one thread per
+// byte of the swizzled buffer (the inverse map of swizzle_offset).
+__global__ void swizzle_scales_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t R,
+                                      int64_t K, int64_t total) {
+  const int64_t off = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (off >= total) return;
+  const int64_t T = (K / 32 + 3) / 4;
+  int64_t t = off;
+  const int64_t g4 = t % 4; t /= 4;
+  const int64_t r4 = t % 4; t /= 4;
+  const int64_t r32 = t % 32; t /= 32;
+  const int64_t gt = t % T, rt = t / T;
+  const int64_t r = rt * 128 + r4 * 32 + r32, g = gt * 4 + g4;
+  dst[off] = (r < R && g < K / 32) ? src[r * (K / 32) + g] : (uint8_t)0;
 }
 
 // ------------------------------------------------------- block-FP8 quantizer
@@ -366,6 +384,36 @@ extern "C" int mxl_quantize_mxfp8(const void* x, int64_t M, int64_t K, int64_t l
   return MXL_OK;
 }
 
+extern "C" int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K);
+
+extern "C" int mxl_quantize_mxfp8_swizzled(const void* x, int64_t M, int64_t K, int64_t ldx, int rule, void* codes,
+                                           void* scales, void* stream) {
+  MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_quantize_mxfp8_swizzled: need K > 0, K %% 32 == 0 (K=%lld)",
+                (long long)K);
+  MXL_CHECK_ARG(ldx >= K && ldx % 8 == 0, "mxl_quantize_mxfp8_swizzled: ldx must be >= K and a multiple of 8");
+  MXL_CHECK_ARG(rule == kFloorCarry175 || rule == kCeilDiv448 || rule == kRpUe8m0,
+                "mxl_quantize_mxfp8_swizzled: unknown rule %d", rule);
+  MXL_CHECK_ARG(aligned16(x) && aligned16(codes), "mxl_quantize_mxfp8_swizzled: x and codes must be 16-byte aligned");
+  MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_quantize_mxfp8_swizzled: too large (M=%lld, K=%lld)", (long long)M,
+                (long long)K);
+  if (M == 0) return MXL_OK;
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* sc = (uint8_t*)scales;
+  if (M % 128 || (K / 32) % 4) {  // the layout has padding bytes: zero them
+    const int64_t total = mxl_swizzled_scale_bytes(M, K);
+    swizzle_pad_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, s>>>(sc, M, K, total);
+  }
+  const int64_t n = M * (K / 32) * 4;
+  dim3 grid((unsigned)((n + 255) / 256));
+  const uint16_t* in = (const uint16_t*)x;
+  uint8_t* c = (uint8_t*)codes;
+  if (rule == kFloorCarry175) quant_mxfp8_kernel<kFloorCarry175, true><<<grid, 256, 0, s>>>(in, ldx, c, sc, M, K);
+  else if (rule == kCeilDiv448) quant_mxfp8_kernel<kCeilDiv448, true><<<grid, 256, 0, s>>>(in, ldx, c, sc, M, K);
+  else quant_mxfp8_kernel<kRpUe8m0, true><<<grid, 256, 0, s>>>(in, ldx, c, sc, M, K);
+  MXL_CHECK_LAUNCH("mxl_quantize_mxfp8_swizzled");
+  return MXL_OK;
+}
+
 extern "C" int mxl_quantize_mxfp6(const void* x, int64_t M, int64_t K, int64_t ldx, int fmt, void* packed,
                                   void* scales, void* stream) {
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_quantize_mxfp6: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
@@ -414,6 +462,16 @@ extern "C" int64_t mxl_swizzled_scale_bytes(int64_t M, int64_t K) {
   return (M + 127) / 128 * 128 * ((K / 32 + 3) / 4) * 4;
 }
 
+extern "C" int mxl_swizzle_scales(const void* logical, int64_t R, int64_t K, void* swizzled, void* stream) {
+  MXL_CHECK_ARG(R >= 0 && K > 0 && K % 32 == 0, "mxl_swizzle_scales: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
+  if (R == 0) return MXL_OK;
+  const int64_t total = mxl_swizzled_scale_bytes(R, K);
+  swizzle_scales_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)logical, (uint8_t*)swizzled, R, K, total);
+  MXL_CHECK_LAUNCH("mxl_swizzle_scales");
+  return MXL_OK;
+}
+
 extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int rule, int swizzled,
                                 void* codes, void* scales, void* stream) {
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_swiglu_mxfp8: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
@@ -428,8 +486,10 @@ extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int r
   uint8_t* c = (uint8_t*)codes;
   uint8_t* sc = (uint8_t*)scales;
   if (swizzled) {
-    const int64_t total = mxl_swizzled_scale_bytes(M, K);
-    swizzle_pad_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, s>>>(sc, M, K, total);
+    if (M % 128 || (K / 32) % 4) {  // the layout has padding bytes: zero them
+      const int64_t total = mxl_swizzled_scale_bytes(M, K);
+      swizzle_pad_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, s>>>(sc, M, K, total);
+    }
     if (rule == kFloorCarry175) swiglu_mxfp8_kernel<kFloorCarry175, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
     else if (rule == kCeilDiv448) swiglu_mxfp8_kernel<kCeilDiv448, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
     else swiglu_mxfp8_kernel<kRpUe8m0, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);

@@ -139,6 +139,7 @@ class Mxfp8LinearKernel(_Kernel):
         _replace(layer, "weight_scale", tiled_s)
         layer.mxl_shape = (n, k)
         layer.mxl_format = ops.E4M3
+        layer.mxl_kernel = self
 
     def apply_weights(self, layer: torch.nn.Module, x: torch.Tensor,
                       bias: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -197,6 +198,7 @@ class Mxfp6LinearKernel(_Kernel):
         _replace(layer, "weight_scale", tiled_s)
         layer.mxl_shape = (n, k)
         layer.mxl_format = fmt
+        layer.mxl_kernel = self
 
     def apply_weights(self, layer: torch.nn.Module, x: torch.Tensor,
                       bias: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -242,6 +244,7 @@ class BlockFp8LinearKernel(_Kernel):
         _replace(layer, "weight", tiled)
         layer.mxl_block_scale = scale.data.contiguous()
         layer.mxl_shape = (n, k)
+        layer.mxl_kernel = self
 
     def apply_weights(self, layer: torch.nn.Module, x: torch.Tensor,
                       bias: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -32,11 +32,14 @@ class Mxfp6Experts:
     """Routed experts over packed MXFP6 weights.
 
     Checkpoint layout (Quark OCP-MX): w13 u8 [E, 2I, 3H/4] + E8M0 [E, 2I, H/32] (gate rows
-    [0, I), up rows [I, 2I)); w2 u8 [E, H, 3I/4] + E8M0 [E, H, I/32].
+    [0, I), up rows [I, 2I)); w2 u8 [E, H, 3I/4] + E8M0 [E, H, I/32].  The weight format
+    defaults to E3M2, the reference's (``Mxfp6Sm120Experts``); E2M3 is selected explicitly.
     """
 
-    def __init__(self, fmt: int = ops.E2M3, act_rule: int = ops.FLOOR_CARRY175,
+    def __init__(self, fmt: int = ops.E3M2, act_rule: int = ops.FLOOR_CARRY175,
                  mid_rule: int = ops.CEIL_DIV448):
+        if fmt not in (ops.E2M3, ops.E3M2):
+            raise ValueError("MXFP6 MoE weights are E2M3 or E3M2")
         self.fmt = fmt
         self.act_rule = act_rule
         self.mid_rule = mid_rule
@@ -175,6 +178,7 @@ class Mxfp6MoEMethod:
             layer.w13_weight.data, layer.w13_weight_scale.data, layer.w2_weight.data, layer.w2_weight_scale.data)
         for name, value in zip(_MOE_PARAMS, (w1, self.experts.w1_scale, w2, self.experts.w2_scale)):
             setattr(layer, name, torch.nn.Parameter(value, requires_grad=False))
+        layer.mxl_experts = self.experts  # found by warmup()
 
     def apply(self, layer: torch.nn.Module, x: torch.Tensor, topk_weights: torch.Tensor,
               topk_ids: torch.Tensor, expert_map: Optional[torch.Tensor] = None,

@@ -5,12 +5,18 @@ allocates a fresh output per call, and is registered as a ``torch.library``
 custom op whose fake implementation keeps the row count symbolic (the
 contract of the reference's ``direct_register_custom_op`` ops, e.g.
 src/vllm_mach/mxfp6/dense_mxfp8.py:99-111 and mxfp8/native_backend.py:208-220).
-Scratch memory (split-K partials, routing counts) lives in per-(device, stream)
-workspaces that grow outside graph capture and raise inside it when a shape
-was not warmed (mxfp8/native_backend.py:159-189).
+Scratch memory (split-K partials, routing counts) lives in per-(device, stream, kind)
+workspaces that grow outside graph capture and raise inside it when a shape was not
+warmed (mxfp8/native_backend.py:159-189).  A workspace handed to a call made during
+graph capture is never freed: when a later shape outgrows it, the old buffer is kept
+alive, because a captured graph still writes through its address on every replay.
+``warmup`` (below) sizes every workspace to the largest shape of a model before
+capture, as the reference's planning pass does (mxfp6/dense_mxfp8.py:177-220,
+mxfp6/warmup.py:75-147).
 """
 from __future__ import annotations
 
+import contextlib
 import threading
 from typing import Optional
 
@@ -24,7 +30,22 @@ FLOOR_CARRY175, CEIL_DIV448, RP_UE8M0 = 0, 1, 2
 FORMATS = {"e4m3": E4M3, "e2m3": E2M3, "e3m2": E3M2}
 
 _ws_lock = threading.RLock()
-_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+class _Workspace:
+    __slots__ = ("buf", "captured")
+
+    def __init__(self, buf: torch.Tensor):
+        self.buf = buf
+        self.captured = False  # handed to a call during graph capture: a graph may hold its address
+
+
+# (device index, stream handle, kind) -> the current workspace
+_workspaces: dict[tuple[int, int, str], _Workspace] = {}
+# superseded workspaces that a captured graph may still reference (kept until exit)
+_retired: list[torch.Tensor] = []
+# (device index, kind) -> planned bytes: the high-water mark of the shapes warmed so far
+_planned: dict[tuple[int, str], int] = {}
 _COUNTS: dict[str, int] = {}
 
 
@@ -33,30 +54,93 @@ def _count(key: str) -> None:
 
 
 def inspect() -> dict:
-    """Call counters (eager/capture invocations, not graph replays) and workspace sizes."""
+    """Call counters (eager/capture invocations, not graph replays), workspace sizes per
+    (device, stream, kind), planned high-water marks, and the retired buffers kept for
+    captured graphs."""
     with _ws_lock:
         return {"counts": dict(_COUNTS),
-                "workspaces": {f"{d}:{s:#x}": t.numel() for (d, s), t in _workspaces.items()}}
+                "workspaces": {f"{d}:{s:#x}:{kind}": w.buf.numel() for (d, s, kind), w in _workspaces.items()},
+                "planned": {f"{d}:{kind}": n for (d, kind), n in _planned.items()},
+                "retired_bytes": sum(t.numel() for t in _retired)}
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def workspace(device: torch.device, nbytes: int, kind: str = "gemm") -> Optional[torch.Tensor]:
-    """Per-(device, stream, kind) scratch of at least ``nbytes``; never reallocated during
-    capture."""
+    """Per-(device, stream, kind) scratch of at least ``nbytes``.
+
+    Outside capture a workspace that is too small is replaced by one of at least the
+    planned size (``warmup``) and twice the old one; the old buffer is freed only if no
+    captured graph can reference it.  During capture a workspace is never reallocated:
+    a shape that needs more raises (warm it first)."""
     if nbytes <= 0:
         return None
-    key = (device.index, stream_handle(device), kind)
+    di = _device_index(device)
+    key = (di, stream_handle(device), kind)
+    capturing = torch.cuda.is_current_stream_capturing()
     with _ws_lock:
-        buf = _workspaces.get(key)
-        if buf is None or buf.numel() < nbytes:
-            if torch.cuda.is_current_stream_capturing():
+        _planned[(di, kind)] = max(_planned.get((di, kind), 0), nbytes)
+        ws = _workspaces.get(key)
+        if ws is None or ws.buf.numel() < nbytes:
+            if capturing:
+                _count("capture_cache_miss")
                 raise RuntimeError(
-                    f"mach_amd workspace for stream {key[1]:#x} holds "
-                    f"{0 if buf is None else buf.numel()} bytes but this shape needs {nbytes}; "
+                    f"mach_amd {kind} workspace for stream {key[1]:#x} holds "
+                    f"{0 if ws is None else ws.buf.numel()} bytes but this shape needs {nbytes}; "
                     "run the shape once (warmup) before graph capture")
-            size = max(nbytes, 0 if buf is None else 2 * buf.numel())
-            buf = torch.empty(size, dtype=torch.uint8, device=device)
-            _workspaces[key] = buf
-        return buf
+            size = max(nbytes, _planned[(di, kind)], 0 if ws is None else 2 * ws.buf.numel())
+            if ws is not None and ws.captured:
+                _retired.append(ws.buf)
+            ws = _Workspace(torch.empty(size, dtype=torch.uint8, device=device))
+            _workspaces[key] = ws
+            _count("workspace_miss")
+        if capturing:
+            ws.captured = True
+        return ws.buf
+
+
+def reserve_workspaces(device: torch.device) -> None:
+    """Give the current stream of ``device`` every planned workspace at its planned size
+    (the capture-stream registration of ``warmup_mxfp6_sm120_stream``,
+    src/vllm_mach/mxfp6/warmup.py:119-147); call outside capture."""
+    di = _device_index(device)
+    with _ws_lock:
+        for (d, kind), n in list(_planned.items()):
+            if d == di:
+                workspace(device, n, kind)
+
+
+# Kernel-selection override for tuning runs and tests (None: the library's cost model).
+# Set through ``tuning()``; read once per GEMM call, never from the environment.
+_tuning: Optional[_lib.GemmOptions] = None
+
+KERNEL_AUTO, KERNEL_STREAM, KERNEL_WIDE, KERNEL_GENERIC, KERNEL_STREAM_WIDE = -1, 0, 1, 2, 3
+
+
+@contextlib.contextmanager
+def tuning(kernel: int = KERNEL_AUTO, splits: int = 0, tile_n: int = 0, tile_m: int = 0, hybrid: bool = False):
+    """Force the GEMM kernel / wide tile / K split of every GEMM call inside the block
+    (``mxl_gemm_options``; the reference's tactic and splits overrides,
+    src/vllm_mach/mxfp8/native_backend.py:29).  Grouped GEMMs read ``kernel`` (their
+    schedule) and ``tile_m``.  For tuning runs and tests."""
+    global _tuning
+    old = _tuning
+    _tuning = _lib.GemmOptions(0, kernel, splits, tile_n, tile_m, int(hybrid))
+    try:
+        yield _tuning
+    finally:
+        _tuning = old
+
+
+def wide_tuning(cfg: Optional[str] = None, tile_m: int = 0):
+    """``tuning`` from a wide-tile spec "NT,S" or "NT,1,h" (hybrid) and an m-tile count."""
+    if not cfg:
+        return tuning(tile_m=tile_m)
+    parts = cfg.split(",")
+    return tuning(tile_n=int(parts[0]), splits=int(parts[1]), tile_m=tile_m,
+                  hybrid=len(parts) > 2 and parts[2] == "h")
 
 
 def _u8(t: torch.Tensor) -> torch.Tensor:
@@ -270,8 +354,9 @@ def silu_and_mul_per_block_quant(out: torch.Tensor, input: torch.Tensor, scales:
             or tuple(out.shape) != (rows, H) or tuple(scales.shape) != (rows, H // 128) or H % 128
             or not input.is_contiguous() or not out.is_contiguous()):
         raise ValueError("silu_and_mul_per_block_quant: unexpected dtype/shape/layout")
+    # the kernel writes scale (r, g) at g * rows + r (transposed) or r * H/128 + g
     if is_scale_transposed:
-        if rows > 1 and scales.stride() != (1, rows):
+        if (rows > 1 and scales.stride() != (1, rows)) or (rows == 1 and H > 128 and scales.stride(1) != 1):
             raise ValueError("transposed scales need stride (1, rows)")
     elif not scales.is_contiguous():
         raise ValueError("scales must be contiguous")
@@ -318,10 +403,28 @@ def pack_weight(codes: torch.Tensor, scales: Optional[torch.Tensor], fmt: int) -
 
 # -------------------------------------------------------------------- GEMMs
 
-def _gemm_ws(device, M, N, K):
-    nbytes = query("mxl_gemm_workspace_bytes", M, N, K)
+def _gemm_ws(device, M, N, K, fmt=E4M3, block=False, opts=None):
+    if opts is None:
+        nbytes = query("mxl_gemm_workspace_bytes", M, N, K)
+    else:
+        nbytes = query("mxl_gemm_workspace_bytes_ex", M, N, K, fmt, int(block), _lib.options_ptr(opts))
     buf = workspace(device, nbytes)
     return (ptr(buf), nbytes) if buf is not None else (None, 0)
+
+
+def _mx_gemm_call(a8, sa8, M, w, sw, n, k, w_fmt, bias, out, ldc, opts, sa_layout=0):
+    """mxl_mx_gemm (defaults) or mxl_mx_gemm_ex (a scale layout or a tuning override)."""
+    dev = a8.device
+    if opts is None and sa_layout == 0:
+        ws, wsb = _gemm_ws(dev, M, n, k)
+        call("mxl_mx_gemm", ptr(a8), ptr(sa8), M, ptr(w), ptr(sw), n, k, w_fmt, ptr(bias), ptr(out), ldc,
+             ws, wsb, stream_handle(dev))
+        return
+    o = _lib.GemmOptions(sa_layout) if opts is None else _lib.GemmOptions(
+        sa_layout, opts.kernel, opts.splits, opts.tile_n, opts.tile_m, opts.hybrid)
+    ws, wsb = _gemm_ws(dev, M, n, k, w_fmt, False, o)
+    call("mxl_mx_gemm_ex", ptr(a8), ptr(sa8), M, ptr(w), ptr(sw), n, k, w_fmt, ptr(bias), ptr(out), ldc,
+         ws, wsb, _lib.options_ptr(o), stream_handle(dev))
 
 
 @torch.library.custom_op("mach_amd::mx_gemm", mutates_args=())
@@ -345,9 +448,7 @@ def mx_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sw: torch.Tensor
         raise ValueError(f"activation scales must be [M, K/32] = [{M}, {k // 32}]")
     out = torch.empty((M, n), dtype=torch.bfloat16, device=a.device)
     if M:
-        ws, wsb = _gemm_ws(a.device, M, n, k)
-        call("mxl_mx_gemm", ptr(a8), ptr(sa8), M, ptr(w), ptr(sw), n, k, w_fmt, ptr(bias), ptr(out), n,
-             ws, wsb, stream_handle(a.device))
+        _mx_gemm_call(a8, sa8, M, w, sw, n, k, w_fmt, bias, out, n, _tuning)
     _count("mx_gemm")
     return out
 
@@ -507,14 +608,21 @@ def block_fp8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sb: torch
         raise ValueError("activation K does not match weight K")
     if tuple(sa.shape) != (M, k // 128) or sa.dtype != torch.float32:
         raise ValueError("sa must be fp32 [M, K/128]")
-    if M > 1 and sa.stride() != (1, M):
+    # the kernels read sa[m, g] at g * M + m: column-major, which for one row means
+    # consecutive groups (a row view of a wider column-major tensor is not)
+    if (M > 1 and sa.stride() != (1, M)) or (M == 1 and k > 128 and sa.stride(1) != 1):
         sa = sa.t().contiguous().t()
     sb = sb.contiguous()
     out = torch.empty((M, n), dtype=torch.bfloat16, device=a.device)
     if M:
-        ws, wsb = _gemm_ws(a.device, M, n, k)
-        call("mxl_block_fp8_gemm", ptr(a8), ptr(sa), M, ptr(w), ptr(sb), n, k, ptr(bias), ptr(out), n, ws, wsb,
-             stream_handle(a.device))
+        opts = _tuning
+        ws, wsb = _gemm_ws(a.device, M, n, k, E4M3, True, opts)
+        if opts is None:
+            call("mxl_block_fp8_gemm", ptr(a8), ptr(sa), M, ptr(w), ptr(sb), n, k, ptr(bias), ptr(out), n, ws, wsb,
+                 stream_handle(a.device))
+        else:
+            call("mxl_block_fp8_gemm_ex", ptr(a8), ptr(sa), M, ptr(w), ptr(sb), n, k, ptr(bias), ptr(out), n, ws,
+                 wsb, _lib.options_ptr(opts), stream_handle(a.device))
     _count("block_fp8_gemm")
     return out
 
@@ -573,8 +681,14 @@ def grouped_gemm(a: torch.Tensor, sa: torch.Tensor, row_index: Optional[torch.Te
     E = expert_offsets.shape[0] - 1
     out = torch.empty((routed_rows, n), dtype=torch.bfloat16, device=a.device)
     if routed_rows:
-        call("mxl_grouped_gemm", ptr(a8), ptr(sa8), a8.shape[0], ptr(row_index), row_div, ptr(expert_offsets), E,
-             routed_rows, ptr(w), ptr(sw), n, k, w_fmt, ptr(out), stream_handle(a.device))
+        opts = _tuning
+        if opts is None:
+            call("mxl_grouped_gemm", ptr(a8), ptr(sa8), a8.shape[0], ptr(row_index), row_div, ptr(expert_offsets),
+                 E, routed_rows, ptr(w), ptr(sw), n, k, w_fmt, ptr(out), stream_handle(a.device))
+        else:
+            call("mxl_grouped_gemm_ex", ptr(a8), ptr(sa8), a8.shape[0], ptr(row_index), row_div,
+                 ptr(expert_offsets), E, routed_rows, ptr(w), ptr(sw), n, k, w_fmt, ptr(out),
+                 _lib.options_ptr(opts), stream_handle(a.device))
     _count("grouped_gemm")
     return out
 
