@@ -195,6 +195,19 @@ int mxl_mx_gemm_ex(const void* a, const void* sa, int64_t M, const void* w_tiled
                    int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc, void* workspace,
                    int64_t workspace_bytes, const mxl_gemm_options* options, void* stream);
 
+/* mxl_mx_gemm that allocates nothing: its split-K partials live in a
+ * library-owned device array of mxl_noalloc_scratch_bytes() (32 MiB) per GPU,
+ * so the call needs no workspace argument.  No counterpart in the reference: for
+ * callers that cannot allocate (HIP graph capture, tight serving loops).  The
+ * plan (kernel, tile, split) is mxl_mx_gemm's, so the result is bit-identical to
+ * mxl_mx_gemm with a large enough workspace; a shape whose plan needs more
+ * scratch than the array holds returns MXL_EINVAL.  `stream` must belong to the
+ * current device.  All calls on one GPU share the array: calls that overlap on
+ * one GPU (concurrent streams) race; every call overwrites what it reads. */
+int64_t mxl_noalloc_scratch_bytes(void);
+int mxl_mx_gemm_noalloc(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,
+                        int64_t N, int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc, void* stream);
+
 /* SwiGLU -> MXFP8 -> MX GEMM for one activation row, in one launch: the weight-
  * streaming GEMM computes the row's codes and scales from gate_up bf16 [1, 2K]
  * itself, with the producer's arithmetic (mxl_swiglu_mxfp8, rule 1 or 2), so y is

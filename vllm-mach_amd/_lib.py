@@ -46,6 +46,8 @@ SIGNATURES = {
     "mxl_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "mxl_gemm_workspace_bytes_ex": (_I64, [_I64, _I64, _I64, _I, _I, _P]),
     "mxl_mx_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P]),
+    "mxl_noalloc_scratch_bytes": (_I64, []),
+    "mxl_mx_gemm_noalloc": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P]),
     "mxl_mx_gemm_ex": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P, _P]),
     "mxl_block_fp8_gemm_ex": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _P]),
     "mxl_grouped_gemm_ex": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P, _P]),

@@ -39,6 +39,8 @@
 // cannot fill 256 CUs, S workgroups split K further and write fp32 partials
 // that a second kernel sums in split order: both orders are fixed, so every
 // result is deterministic.
+#include <mutex>
+
 #include "gemm_common.h"
 
 namespace mxl {
@@ -574,6 +576,79 @@ extern "C" int mxl_mx_gemm_ex(const void* a, const void* sa, int64_t M, const vo
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm_ex: unknown weight format %d", w_fmt);
   return gemm_common(a, sa, M, w_tiled, sw_tiled, N, K, w_fmt, false, bias, out, ldc, workspace, workspace_bytes,
                      options_of(options), stream, "mxl_mx_gemm_ex");
+}
+
+// ------------------------------------------------------ no-allocation entry point
+
+// Split-K scratch of mxl_mx_gemm_noalloc.  Every GPU that loads this code object
+// holds its own copy until the process ends.  On the host `scratch` names a
+// stand-in, not a device address: host code uses only the per-device address that
+// hipGetSymbolAddress returns (g_scratch_ptr), never the array's name.
+constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, queried once per device (with that
+// device current) and kept.
+int scratch_address(const char* who, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no current HIP device (%s)", who, hipGetErrorString(e));
+    return MXL_EHIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev, hipGetErrorString(e));
+      return MXL_EHIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MXL_OK;
+}
+}  // namespace
+
+extern "C" int64_t mxl_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int mxl_mx_gemm_noalloc(const void* a, const void* sa, int64_t M, const void* w_tiled,
+                                   const void* sw_tiled, int64_t N, int64_t K, int w_fmt, const void* bias, void* out,
+                                   int64_t ldc, void* stream) {
+  const char* who = "mxl_mx_gemm_noalloc";
+  MXL_CHECK_ARG(valid_wfmt(w_fmt), "%s: unknown weight format %d", who, w_fmt);
+  MXL_CHECK_ARG(M >= 0 && N > 0 && K > 0 && K % 128 == 0, "%s: need N > 0, K %% 128 == 0 (M=%lld N=%lld K=%lld)", who,
+                (long long)M, (long long)N, (long long)K);
+  if (M == 0) return MXL_OK;
+  // the plan mxl_mx_gemm makes for this shape; its split-K partials must fit the scratch
+  DensePlan d;
+  if (!plan_dense(M, N, K, w_fmt, false, GemmOptions(), d)) {
+    set_error("%s: no kernel runs this shape (M=%lld, K=%lld)", who, (long long)M, (long long)K);
+    return MXL_EUNSUPPORTED;
+  }
+  MXL_CHECK_ARG(d.need <= kNoAllocScratchBytes,
+                "%s: this shape needs %lld bytes of split-K scratch, more than the %lld this entry point holds "
+                "(M=%lld N=%lld K=%lld); use mxl_mx_gemm with a workspace",
+                who, (long long)d.need, (long long)kNoAllocScratchBytes, (long long)M, (long long)N, (long long)K);
+  if (stream) {  // the scratch is the current device's: the stream must belong to it
+    int cur = -1, sdev = -1;
+    if (hipGetDevice(&cur) != hipSuccess || hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess ||
+        cur != sdev) {
+      set_error("%s: the stream's device (%d) is not the current device (%d)", who, sdev, cur);
+      return MXL_EINVAL;
+    }
+  }
+  void* ws = nullptr;
+  const int rc = scratch_address(who, &ws);
+  if (rc != MXL_OK) return rc;
+  return gemm_common(a, sa, M, w_tiled, sw_tiled, N, K, w_fmt, false, bias, out, ldc, ws, kNoAllocScratchBytes,
+                     GemmOptions(), stream, who);
 }
 
 extern "C" int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
