@@ -342,19 +342,36 @@ class MoeLayer(Workload):
         a2, sa2 = self.mid[T]
         active = int((offs[1:] > offs[:-1]).sum().item())
         routes = T * k
-        g1 = [lambda ex=ex, w1=w1: torch.ops.mach_amd.grouped_gemm(a, sa, sr, k, offs, routes, w1, ex.w1_scale,
-                                                                   2 * I, H, ops.E2M3)
-              for ex, w1, _ in self.copies]
-        g2 = [lambda ex=ex, w2=w2: torch.ops.mach_amd.grouped_gemm(a2, sa2, None, 1, offs, routes, w2, ex.w2_scale,
-                                                                   H, I, ops.E2M3)
-              for ex, _, w2 in self.copies]
+        x = self.inputs[T][0]
+        gate_up = torch.ops.mach_amd.grouped_gemm(a, sa, sr, k, offs, routes, self.copies[0][1],
+                                                  self.copies[0][0].w1_scale, 2 * I, H, ops.E2M3)
+        # the kernels the step runs: with a fused producer (bf16 rows in) where the grouped
+        # weight-streaming schedule admits it, else the MXFP8 operands of the separate producer
+        if ops.grouped_fused_supported(routes, self.E, H, ops.E2M3):
+            g1 = [lambda ex=ex, w1=w1: torch.ops.mach_amd.grouped_gemm_quant(x, sr, k, offs, routes, w1, ex.w1_scale,
+                                                                             2 * I, H, ops.E2M3, ops.FLOOR_CARRY175)
+                  for ex, w1, _ in self.copies]
+            n1, in1 = "grouped w13 + MXFP8 quant", routes * H * 2
+        else:
+            g1 = [lambda ex=ex, w1=w1: torch.ops.mach_amd.grouped_gemm(a, sa, sr, k, offs, routes, w1, ex.w1_scale,
+                                                                       2 * I, H, ops.E2M3)
+                  for ex, w1, _ in self.copies]
+            n1, in1 = "grouped w13", routes * H * (1 + 1 / 32)
+        if ops.grouped_fused_supported(routes, self.E, I, ops.E2M3):
+            g2 = [lambda ex=ex, w2=w2: torch.ops.mach_amd.grouped_gemm_swiglu(gate_up, offs, routes, w2, ex.w2_scale,
+                                                                              H, I, ops.E2M3, ops.CEIL_DIV448)
+                  for ex, _, w2 in self.copies]
+            n2, in2 = "grouped w2 + SwiGLU->MXFP8", routes * 2 * I * 2
+        else:
+            g2 = [lambda ex=ex, w2=w2: torch.ops.mach_amd.grouped_gemm(a2, sa2, None, 1, offs, routes, w2,
+                                                                       ex.w2_scale, H, I, ops.E2M3)
+                  for ex, _, w2 in self.copies]
+            n2, in2 = "grouped w2", routes * I * (1 + 1 / 32)
         return {
-            f"grouped w13 T={T} ({active} active experts) N={2 * I} K={H}": (
-                g1, 2.0 * routes * 2 * I * H,
-                active * mx_weight_bytes(2 * I, H, 2) + routes * H * (1 + 1 / 32) + routes * 2 * I * 2),
-            f"grouped w2 T={T} ({active} active experts) N={H} K={I}": (
-                g2, 2.0 * routes * H * I,
-                active * mx_weight_bytes(H, I, 2) + routes * I * (1 + 1 / 32) + routes * H * 2),
+            f"{n1} T={T} ({active} active experts) N={2 * I} K={H}": (
+                g1, 2.0 * routes * 2 * I * H, active * mx_weight_bytes(2 * I, H, 2) + in1 + routes * 2 * I * 2),
+            f"{n2} T={T} ({active} active experts) N={H} K={I}": (
+                g2, 2.0 * routes * H * I, active * mx_weight_bytes(H, I, 2) + in2 + routes * H * 2),
         }
 
 

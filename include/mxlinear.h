@@ -252,6 +252,30 @@ int mxl_grouped_gemm_ex(const void* a, const void* sa, int64_t a_rows, const int
                         const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, void* out,
                         const mxl_gemm_options* options, void* stream);
 
+/* Grouped GEMMs with the activation producer fused (one launch instead of two):
+ * each workgroup computes its rows' MXFP8 operands in LDS with the standalone
+ * producers' arithmetic, so the output is bit-identical to the two-call path.
+ *   _quant:  A = MXFP8(x[row_index[p] / row_div]) under `rule` (x bf16, row stride
+ *            ldx), as mxl_quantize_mxfp8 then mxl_grouped_gemm;
+ *   _swiglu: A = SwiGLU -> MXFP8 of gate_up bf16 [routed_rows, 2K] (gate columns
+ *            [0, K), up [K, 2K)) under `rule`, as mxl_swiglu_mxfp8 then
+ *            mxl_grouped_gemm; replaces silu_and_mul_mxfp8_grouped +
+ *            grouped_gemm_w6a8_out (mxfp6_sm120_silu_grouped_gemm,
+ *            src/vllm_mach/mxfp6/moe_utils.py:383-442).
+ * They run the weight-streaming grouped schedule of 16-row units (below 32
+ * routed rows per expert on average, the operands of a unit within 64 KiB of
+ * LDS); mxl_grouped_fused_supported says whether a shape has one, and the entry
+ * points return MXL_EUNSUPPORTED otherwise.  Replace the fused
+ * router/quant and SiLU schedules of src/vllm_mach/mxfp6/moe.py:126-190. */
+int mxl_grouped_fused_supported(int64_t routed_rows, int64_t num_experts, int64_t K, int w_fmt);
+int mxl_grouped_gemm_quant(const void* x, int64_t ldx, const int32_t* row_index, int row_div,
+                           const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
+                           const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, int rule,
+                           void* out, void* stream);
+int mxl_grouped_gemm_swiglu(const void* gate_up, const int64_t* expert_offsets, int64_t num_experts,
+                            int64_t routed_rows, const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K,
+                            int w_fmt, int rule, void* out, void* stream);
+
 /* Token sort by expert (stable): topk_ids int32 [T, topk] -> sorted_routes
  * int32 [T*topk], expert_offsets int64 [E+1], inverse int32 [T*topk] (-1 for
  * ids outside [0, E)).  1 <= E <= 2560.  Replaces route_mxfp8_out's routing outputs

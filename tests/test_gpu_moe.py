@@ -77,6 +77,7 @@ def _check_gemm(got, ref):
     (4, 256, 128, 7, 2, 3),
     (32, 2048, 512, 128, 8, 2),
     (16, 2048, 512, 512, 8, 3),
+    (256, 2048, 512, 128, 8, 2),   # c5 at T = 128: every expert checked
 ])
 def test_moe_layer_matches_oracle(pkg, oracle_mod, dev, E, H, I, T, topk, fmt):
     """Each stage against the oracle on the GPU's own inputs to that stage (quantizers and
@@ -266,3 +267,54 @@ def test_grouped_stream_96_row_units(pkg, oracle_mod, dev, monkeypatch, E, N, K,
         rows = rt[lo:hi] // topk if gathered else np.arange(lo, hi)
         ref = oracle_mod.mx_gemm_ref(rc[rows], rs[rows], parts[e][0], parts[e][1], fmt)
         _check(got[lo:hi], oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref)))
+
+
+@pytest.mark.parametrize("E,H,I,T,topk,fmt,mapped", [
+    (4, 256, 128, 7, 2, 2, False),
+    (256, 2048, 512, 128, 8, 2, False),    # c5, T = 128: both GEMMs fused (16-row units)
+    (256, 2048, 512, 2048, 8, 2, False),   # c5, T = 2048: 64 rows per expert, separate producers
+    (16, 512, 256, 100, 4, 3, True),       # E3M2 experts, an expert_map dropping half the experts
+    (64, 1024, 384, 100, 8, 3, False),     # ragged: 12.5 rows per expert, K = 1024 / 384 (three K waves)
+])
+def test_moe_fused_producers_bit_identical(pkg, oracle_mod, dev, E, H, I, T, topk, fmt, mapped):
+    """The grouped GEMMs with fused producers (quantization in w13, SwiGLU in w2) give the
+    same bits as the separate quantize / SwiGLU launches; at T = 128 the layer is four
+    launches (route, w13, w2, combine); an expert_map's dropped routes contribute nothing."""
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(E + T + H)
+    Eg = 2 * E if mapped else E
+    def wg(n, k):  # random codes: every packed FP6 pattern is a number
+        return torch.randint(0, 256, (E, n, k * 3 // 4), generator=g, dtype=torch.uint8).to(dev)
+    w13, w2 = wg(2 * I, H), wg(H, I)
+    s13 = torch.randint(118, 124, (E, 2 * I, H // 32), generator=g, dtype=torch.uint8).to(dev)
+    s2 = torch.randint(118, 124, (E, H, I // 32), generator=g, dtype=torch.uint8).to(dev)
+    x = torch.randn(T, H, generator=g).bfloat16().to(dev)
+    wts, ids = torch.topk(torch.softmax(torch.randn(T, Eg, generator=g), -1), topk, -1)
+    wts = (wts / wts.sum(-1, keepdim=True)).float().to(dev)
+    ids = ids.int().to(dev)
+    emap = None
+    if mapped:
+        gm = torch.full((Eg,), -1, dtype=torch.int32)
+        gm[0::2] = torch.arange(E, dtype=torch.int32)
+        emap = gm.to(dev)
+    experts = pkg.Mxfp6Experts(fmt=fmt)
+    e1, e2 = experts.process_weights_after_loading(w13, s13, w2, s2)
+    routes = T * topk
+    fused = (ops.grouped_fused_supported(routes, E, H, fmt), ops.grouped_fused_supported(routes, E, I, fmt))
+    # the fused producers serve the 16-row-unit schedule (below 32 routed rows per expert)
+    assert fused == ((routes < 32 * E),) * 2, fused
+    out_f = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    before = dict(ops._COUNTS)
+    experts.apply(out_f, x, e1, e2, wts, ids, "silu", Eg, emap, None, None, None, None, None, False)
+    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items() if v != before.get(k, 0)}
+    if (E, T) == (256, 128):
+        assert fused[0] and calls == {"moe_route": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu": 1,
+                                      "moe_reduce": 1}, calls
+    experts.fuse = False
+    out_u = torch.empty_like(out_f)
+    experts.apply(out_u, x, e1, e2, wts, ids, "silu", Eg, emap, None, None, None, None, None, False)
+    assert torch.equal(out_f, out_u)
+    if mapped:  # tokens whose routes all left the node get exactly zero
+        gone = (emap[ids.long()] < 0).all(dim=1)
+        if gone.any():
+            assert (out_f[gone] == 0).all()

@@ -54,6 +54,9 @@ SIGNATURES = {
     "mxl_swiglu_mx_gemm": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P]),
     "mxl_block_fp8_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "mxl_grouped_gemm": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P]),
+    "mxl_grouped_fused_supported": (_I, [_I64, _I64, _I64, _I]),
+    "mxl_grouped_gemm_quant": (_I, [_P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _P, _P]),
+    "mxl_grouped_gemm_swiglu": (_I, [_P, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _P, _P]),
     "mxl_moe_route_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "mxl_moe_route": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "mxl_moe_reduce": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),

@@ -208,6 +208,13 @@ hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hip
 // Grouped (MoE) variant: persistent workgroups over (expert, up to 16 mt rows) units,
 // each streaming the expert's weights; mt = 1 (few rows per expert) or 8.
 bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt, int mt);
-hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, int mt, hipStream_t s);
+// With prod = 1 (MXFP8 quantization of gathered bf16 rows) or 2 (SwiGLU of bf16 gate/up
+// rows then MXFP8) each workgroup produces its unit's operands into LDS itself, rule
+// `rule`; p.a then holds the bf16 input.  The unit's produced operands must fit
+// kGroupedStageMaxBytes of LDS beside the kernel's own.
+constexpr int64_t kGroupedStageMaxBytes = 64 * 1024;
+bool stream_grouped_fused_eligible(int64_t K, int64_t num_experts, int fmt, int mt);
+hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, int mt, hipStream_t s,
+                                      int prod = 0, int rule = 0);
 
 }  // namespace mxl

@@ -389,10 +389,71 @@ constexpr int kStreamGroupedDepth = 4;
 template <int FMT, int MT>
 constexpr int stream_grouped_waves() { return MT > 1 ? 4 : (FMT == kE4M3 ? 8 : 16); }
 
-template <int FMT, int MT>
+// Activation producers fused into the grouped kernel (prod != 0): the workgroup
+// computes its unit's MXFP8 operands -- codes [ROWS][K] then E8M0 [ROWS][K/32], rows
+// past the unit repeating its last row -- into LDS with the standalone producers'
+// arithmetic and lane mapping (four lanes per 32-element block), so the codes are
+// those quant_mxfp8_kernel / swiglu_mxfp8_kernel would write:
+//   prod 1: MXFP8 quantization of the gathered bf16 rows A[row_index[r] / row_div]
+//           (row stride lda), rule `rule`;
+//   prod 2: SwiGLU of the unit's bf16 gate/up rows (gate columns [0, K), up [K, 2K),
+//           row stride lda) then MXFP8, rule `rule`.
+template <int ROWS>
+__device__ __forceinline__ void grouped_produce(const GemmParams& p, int prod, int rule, int64_t lo, int64_t hi,
+                                                uint8_t* stage, int t, int nthreads) {
+  const int64_t K = p.K;
+  const int bpr = (int)(K / 32);
+  // only the unit's rows: the gather reads its padding rows from the last one
+  const int items = (int)(hi - lo) * bpr * 4;
+  uint8_t* codes = stage;
+  uint8_t* scales = stage + ROWS * K;
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(p.a);
+  // items and nthreads are multiples of four: the four lanes of a block are live together
+  for (int base = 0; base < items; base += nthreads) {
+    const int c = base + t < items ? base + t : items - 4 + (t & 3);
+    const int sub = c & 3, blk = (c >> 2) % bpr, rloc = (c >> 2) / bpr;
+    int64_t row = lo + rloc;
+    if (row >= hi) row = hi - 1;
+    float v[8];
+    uint32_t packed[2], sc;
+    if (prod == 1) {
+      const int64_t arow = p.row_index ? (int64_t)(p.row_index[row] / p.row_div) : row;
+      bf16x8_to_f32(*reinterpret_cast<const uint4*>(src + arow * p.lda + blk * 32 + sub * 8), v);
+      quiet8(v);
+      sc = rule == kFloorCarry175 ? quant8x4<kFloorCarry175>(v, packed)
+           : rule == kCeilDiv448  ? quant8x4<kCeilDiv448>(v, packed)
+                                  : quant8x4<kRpUe8m0>(v, packed);
+    } else {
+      const uint16_t* gp = src + row * p.lda + blk * 32 + sub * 8;
+      float g[8], u[8];
+      bf16x8_to_f32(*reinterpret_cast<const uint4*>(gp), g);
+      bf16x8_to_f32(*reinterpret_cast<const uint4*>(gp + K), u);
+      if (rule == kFloorCarry175) {
+        swiglu8<kFloorCarry175>(g, u, v);
+        sc = quant8x4<kFloorCarry175, true>(v, packed);
+      } else if (rule == kCeilDiv448) {
+        swiglu8<kCeilDiv448>(g, u, v);
+        sc = quant8x4<kCeilDiv448, true>(v, packed);
+      } else {
+        swiglu8<kRpUe8m0>(g, u, v);
+        sc = quant8x4<kRpUe8m0, true>(v, packed);
+      }
+    }
+    if (base + t < items) {
+      *reinterpret_cast<uint2*>(codes + rloc * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
+      if (sub == 0) scales[rloc * bpr + blk] = (uint8_t)sc;
+    }
+  }
+}
+
+template <int FMT, int MT, int PROD>
 __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_stream_grouped_kernel(GemmParams p, int E,
-                                                                                                int WK, int NW) {
+                                                                                                int WK, int NW,
+                                                                                                int rule) {
+  constexpr int prod = PROD;
   constexpr int WAVES = stream_grouped_waves<FMT, MT>();
+  // prod != 0: the unit's produced operands (grouped_produce), sized at launch
+  extern __shared__ __attribute__((aligned(16))) uint8_t stage_act[];
   constexpr int ROWS = 16 * MT;
   __shared__ float red[2][WAVES][MT][4][64];
   // MT > 1, one super-tile: each wave's 16 MT x 16 bf16 output block, staged so that the
@@ -456,6 +517,12 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
       return nt < ntiles ? nt : ntiles - 1;
     };
     stream_load_b<FMT, 1, false>(p, w, sw, nt_of(0), kt1, lane, b0);
+    if constexpr (prod != 0) {
+      // every wave has read the previous unit's operands (the s_barrier below the gather
+      // orders that); produce this unit's into LDS, then hand them over
+      grouped_produce<ROWS>(p, prod, rule, lo, hi, stage_act, t, nthreads);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
     v8i a[MT][1][4];
     uint32_t sa[MT > 1 ? 1 : MT][1][4];  // MT = 1: one byte per slice
     uint32_t spk[MT];                    // MT > 1: the four bytes packed (byte j: slice j)
@@ -465,8 +532,9 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
       int64_t row = lo + 16 * i + cr;
       if (row >= hi) row = hi - 1;  // padding rows read a valid row and are not stored
       const int64_t arow = p.row_index ? (int64_t)(p.row_index[row] / p.row_div) : row;
-      const uint8_t* srow = static_cast<const uint8_t*>(p.sa) + sa_row_offset(p, arow);
-      const uint8_t* ap = p.a + arow * p.lda;
+      const uint8_t* srow = prod ? stage_act + ROWS * p.K + (row - lo) * (p.K / 32)
+                                 : static_cast<const uint8_t*>(p.sa) + sa_row_offset(p, arow);
+      const uint8_t* ap = prod ? stage_act + (row - lo) * p.K : p.a + arow * p.lda;
       const int from = 4 * (4 * r + q);
       uint4 lo4[4], hi4[4];
 #pragma unroll
@@ -477,7 +545,8 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
         hi4[j] = *reinterpret_cast<const uint4*>(ap + kc + 64 + 16 * cp);
       }
       const int64_t ks = kt1[0] * kTileK + 128 * cp;
-      const uint32_t sd = *reinterpret_cast<const uint32_t*>(srow + ((ks < p.K ? ks : p.K - 128) / 128) * p.sa_ss);
+      const uint32_t sd = *reinterpret_cast<const uint32_t*>(
+          srow + ((ks < p.K ? ks : p.K - 128) / 128) * (prod ? 4 : p.sa_ss));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t x[8] = {lo4[j].x, lo4[j].y, lo4[j].z, lo4[j].w, hi4[j].x, hi4[j].y, hi4[j].z, hi4[j].w};
@@ -493,6 +562,7 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
         if (!in) a[i][0][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
       }
     }
+    if constexpr (prod != 0) asm volatile("s_waitcnt lgkmcnt(0) vmcnt(0)\n\ts_barrier" ::: "memory");
 
     // the m-tiles' products of one n-tile (m-tiles without rows are skipped)
     auto mma = [&](const StreamB<FMT, 1>& b, v4f (&acc)[MT]) {
@@ -682,8 +752,11 @@ template <int MT>
 int grouped_waves(int fmt) {
   return fmt == kE4M3 ? stream_grouped_waves<kE4M3, MT>() : stream_grouped_waves<kE2M3, MT>();
 }
+// LDS bytes of a unit's produced operands (codes + E8M0), 16-byte rounded
+int64_t grouped_stage_bytes(int mt, int64_t K) { return ((16 * mt * K * 33 / 32) + 15) / 16 * 16; }
+
 template <int MT>
-hipError_t launch_grouped_mt(int fmt, const GemmParams& p, int64_t num_experts, hipStream_t s) {
+hipError_t launch_grouped_mt(int fmt, const GemmParams& p, int64_t num_experts, int prod, int rule, hipStream_t s) {
   const int waves = grouped_waves<MT>(fmt);
   const int WK = (int)p.KT;
   if (WK < 1 || WK > waves) return hipErrorInvalidValue;
@@ -693,10 +766,27 @@ hipError_t launch_grouped_mt(int fmt, const GemmParams& p, int64_t num_experts, 
   const int64_t G = bound < cu_count() ? bound : cu_count();
   const dim3 grid((unsigned)G), blk((unsigned)(64 * WK * NW));
   const int E = (int)num_experts;
-  if (fmt == kE4M3) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE4M3, MT>), grid, blk, 0, s, p, E, WK, NW);
-  else if (fmt == kE2M3) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE2M3, MT>), grid, blk, 0, s, p, E, WK, NW);
-  else if (fmt == kE3M2) hipLaunchKernelGGL((gemm_stream_grouped_kernel<kE3M2, MT>), grid, blk, 0, s, p, E, WK, NW);
+  const size_t shmem = prod ? (size_t)grouped_stage_bytes(MT, p.K) : 0;
+  // the fused producers are instantiated for the 16-row units only (the schedule that uses them)
+  if (prod && MT != 1) return hipErrorInvalidValue;
+#define MXL_GROUPED_LAUNCH(F_, P_) \
+  hipLaunchKernelGGL((gemm_stream_grouped_kernel<F_, MT, (MT == 1 ? P_ : 0)>), grid, blk, shmem, s, p, E, WK, NW, rule)
+#define MXL_GROUPED_PROD(F_)                    \
+  if (prod == 0) MXL_GROUPED_LAUNCH(F_, 0);     \
+  else if (prod == 1) MXL_GROUPED_LAUNCH(F_, 1); \
+  else if (prod == 2) MXL_GROUPED_LAUNCH(F_, 2); \
   else return hipErrorInvalidValue;
+  if (fmt == kE4M3) {
+    MXL_GROUPED_PROD(kE4M3)
+  } else if (fmt == kE2M3) {
+    MXL_GROUPED_PROD(kE2M3)
+  } else if (fmt == kE3M2) {
+    MXL_GROUPED_PROD(kE3M2)
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef MXL_GROUPED_PROD
+#undef MXL_GROUPED_LAUNCH
   return hipGetLastError();
 }
 }  // namespace
@@ -707,9 +797,15 @@ bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt, int mt) {
          (K + kTileK - 1) / kTileK <= waves && num_experts >= 1 && num_experts <= kStreamGroupedMaxExperts;
 }
 
-hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, int mt, hipStream_t s) {
-  if (mt == 1) return launch_grouped_mt<1>(fmt, p, num_experts, s);
-  if (mt == kGroupedStreamWideMT) return launch_grouped_mt<kGroupedStreamWideMT>(fmt, p, num_experts, s);
+bool stream_grouped_fused_eligible(int64_t K, int64_t num_experts, int fmt, int mt) {
+  return stream_grouped_eligible(K, num_experts, fmt, mt) && grouped_stage_bytes(mt, K) <= kGroupedStageMaxBytes;
+}
+
+hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, int mt, hipStream_t s,
+                                      int prod, int rule) {
+  if (prod && grouped_stage_bytes(mt, p.K) > kGroupedStageMaxBytes) return hipErrorInvalidValue;
+  if (mt == 1) return launch_grouped_mt<1>(fmt, p, num_experts, prod, rule, s);
+  if (mt == kGroupedStreamWideMT) return launch_grouped_mt<kGroupedStreamWideMT>(fmt, p, num_experts, prod, rule, s);
   return hipErrorInvalidValue;
 }
 

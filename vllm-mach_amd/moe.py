@@ -6,7 +6,10 @@ quantize hidden states to MXFP8 -> stable token sort by expert -> grouped
 W6A8 GEMM (w13) -> SwiGLU (bf16 SiLU) + MXFP8 -> grouped W6A8 GEMM (w2) ->
 fp32 weighted combine into ``output``.  The grouped GEMMs gather activation
 rows through the sorted route list, so no permuted copy of the activations is
-written, and experts that receive no rows read no weights.
+written, and experts that receive no rows read no weights.  Where the grouped
+weight-streaming schedules run (below ~96 routed rows per expert), they produce
+their own MXFP8 operands -- the quantization inside w13, the SwiGLU inside w2 --
+so a small-batch layer is four launches (route, w13, w2, combine).
 """
 from __future__ import annotations
 
@@ -43,6 +46,7 @@ class Mxfp6Experts:
         self.fmt = fmt
         self.act_rule = act_rule
         self.mid_rule = mid_rule
+        self.fuse = True  # fused producers where the grouped schedule admits them (False: separate launches)
         self.w1_scale: Optional[torch.Tensor] = None
         self.w2_scale: Optional[torch.Tensor] = None
         self.shapes: Optional[tuple[int, int, int]] = None  # (E, H, I)
@@ -90,13 +94,25 @@ class Mxfp6Experts:
         topk = ids.shape[1]
         if T == 0:
             return
-        a, sa = torch.ops.mach_amd.quantize_mxfp8(hidden_states, self.act_rule)
         sorted_routes, offsets, inverse = torch.ops.mach_amd.moe_route(ids, E)
         routes = T * topk
-        gate_up = torch.ops.mach_amd.grouped_gemm(a, sa, sorted_routes, topk, offsets, routes, w1,
-                                                  self.w1_scale, 2 * I, H, self.fmt)
-        a2, sa2 = torch.ops.mach_amd.swiglu_mxfp8(gate_up, self.mid_rule, False)
-        y = torch.ops.mach_amd.grouped_gemm(a2, sa2, None, 1, offsets, routes, w2, self.w2_scale, H, I, self.fmt)
+        # Below ~96 routed rows per expert the grouped GEMMs stream each expert's weights
+        # past its rows and produce their own MXFP8 operands (the activation quantization in
+        # w13, the SwiGLU in w2) in LDS: route, w13, w2, combine -- four launches, the same
+        # bits as the separate producers.
+        if self.fuse and ops.grouped_fused_supported(routes, E, H, self.fmt) and hidden_states.stride(1) == 1:
+            gate_up = torch.ops.mach_amd.grouped_gemm_quant(hidden_states, sorted_routes, topk, offsets, routes, w1,
+                                                            self.w1_scale, 2 * I, H, self.fmt, self.act_rule)
+        else:
+            a, sa = torch.ops.mach_amd.quantize_mxfp8(hidden_states, self.act_rule)
+            gate_up = torch.ops.mach_amd.grouped_gemm(a, sa, sorted_routes, topk, offsets, routes, w1,
+                                                      self.w1_scale, 2 * I, H, self.fmt)
+        if self.fuse and ops.grouped_fused_supported(routes, E, I, self.fmt):
+            y = torch.ops.mach_amd.grouped_gemm_swiglu(gate_up, offsets, routes, w2, self.w2_scale, H, I, self.fmt,
+                                                       self.mid_rule)
+        else:
+            a2, sa2 = torch.ops.mach_amd.swiglu_mxfp8(gate_up, self.mid_rule, False)
+            y = torch.ops.mach_amd.grouped_gemm(a2, sa2, None, 1, offsets, routes, w2, self.w2_scale, H, I, self.fmt)
         torch.ops.mach_amd.moe_reduce(output, y, topk_weights, inverse)
 
     def __call__(self, hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,

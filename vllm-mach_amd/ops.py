@@ -698,6 +698,59 @@ def _(a, sa, row_index, row_div, expert_offsets, routed_rows, w, sw, n, k, w_fmt
     return a.new_empty((routed_rows, n), dtype=torch.bfloat16)
 
 
+def grouped_fused_supported(routed_rows: int, num_experts: int, k: int, w_fmt: int) -> bool:
+    """Whether the grouped GEMMs with a fused activation producer run this shape."""
+    return bool(query("mxl_grouped_fused_supported", routed_rows, num_experts, k, w_fmt))
+
+
+@torch.library.custom_op("mach_amd::grouped_gemm_quant", mutates_args=())
+def grouped_gemm_quant(x: torch.Tensor, row_index: Optional[torch.Tensor], row_div: int,
+                       expert_offsets: torch.Tensor, routed_rows: int, w: torch.Tensor, sw: torch.Tensor,
+                       n: int, k: int, w_fmt: int, rule: int = FLOOR_CARRY175) -> torch.Tensor:
+    """MXFP8 quantization of the gathered bf16 rows fused into the grouped GEMM: bit-identical to
+    ``quantize_mxfp8`` then ``grouped_gemm`` (the fused router-quant schedule's role,
+    src/vllm_mach/mxfp6/moe.py:142-152)."""
+    _check_cuda(x, row_index, expert_offsets, w, sw)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.shape[1] != k or x.stride(1) != 1:
+        raise ValueError("grouped_gemm_quant needs bf16 rows [T, K] with unit column stride")
+    E = expert_offsets.shape[0] - 1
+    out = torch.empty((routed_rows, n), dtype=torch.bfloat16, device=x.device)
+    if routed_rows:
+        call("mxl_grouped_gemm_quant", ptr(x), x.stride(0), ptr(row_index), row_div, ptr(expert_offsets), E,
+             routed_rows, ptr(w), ptr(sw), n, k, w_fmt, rule, ptr(out), stream_handle(x.device))
+    _count("grouped_gemm_quant")
+    return out
+
+
+@grouped_gemm_quant.register_fake
+def _(x, row_index, row_div, expert_offsets, routed_rows, w, sw, n, k, w_fmt, rule=FLOOR_CARRY175):
+    return x.new_empty((routed_rows, n), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("mach_amd::grouped_gemm_swiglu", mutates_args=())
+def grouped_gemm_swiglu(gate_up: torch.Tensor, expert_offsets: torch.Tensor, routed_rows: int, w: torch.Tensor,
+                        sw: torch.Tensor, n: int, k: int, w_fmt: int, rule: int = CEIL_DIV448) -> torch.Tensor:
+    """SwiGLU -> MXFP8 of the routed gate/up rows fused into the grouped GEMM: bit-identical to
+    ``swiglu_mxfp8`` then ``grouped_gemm`` (``mxfp6_sm120_silu_grouped_gemm``,
+    src/vllm_mach/mxfp6/moe_utils.py:383-442)."""
+    _check_cuda(gate_up, expert_offsets, w, sw)
+    if gate_up.dtype != torch.bfloat16 or gate_up.ndim != 2 or gate_up.shape[1] != 2 * k:
+        raise ValueError("grouped_gemm_swiglu needs bf16 gate/up rows [R, 2K]")
+    gate_up = gate_up.contiguous()
+    E = expert_offsets.shape[0] - 1
+    out = torch.empty((routed_rows, n), dtype=torch.bfloat16, device=gate_up.device)
+    if routed_rows:
+        call("mxl_grouped_gemm_swiglu", ptr(gate_up), ptr(expert_offsets), E, routed_rows, ptr(w), ptr(sw), n, k,
+             w_fmt, rule, ptr(out), stream_handle(gate_up.device))
+    _count("grouped_gemm_swiglu")
+    return out
+
+
+@grouped_gemm_swiglu.register_fake
+def _(gate_up, expert_offsets, routed_rows, w, sw, n, k, w_fmt, rule=CEIL_DIV448):
+    return gate_up.new_empty((routed_rows, n), dtype=torch.bfloat16)
+
+
 @torch.library.custom_op("mach_amd::moe_reduce", mutates_args=("output",))
 def moe_reduce(output: torch.Tensor, routed_output: torch.Tensor, topk_weights: torch.Tensor,
                inverse: torch.Tensor) -> None:
