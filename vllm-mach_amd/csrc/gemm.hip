@@ -466,7 +466,7 @@ struct DensePlan {
 
 static bool plan_dense(int64_t M, int64_t N, int64_t K, int fmt, bool block, const GemmOptions& o, DensePlan& d) {
   const bool stream_ok = stream_gemm_eligible(M, K, block);
-  const bool wide_ok = wide_gemm_eligible(M, K);
+  const bool wide_ok = wide_gemm_eligible(M, K) && (!block || K <= int64_t(128) * kWideBlockStages);
   d.kernel = o.kernel == kAuto ? (stream_ok ? kStream : wide_ok ? kWide : kGeneric) : o.kernel;
   if ((d.kernel == kStream && !stream_ok) || (d.kernel == kWide && !wide_ok) ||
       (d.kernel != kStream && d.kernel != kWide && d.kernel != kGeneric))

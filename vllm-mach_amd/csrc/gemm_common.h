@@ -188,6 +188,9 @@ int64_t wide_workspace_bytes(const WideConfig& c, int64_t M, int64_t N);
 bool wide_gemm_eligible(int64_t M, int64_t K);
 // Grouped wide kernel: at most this many experts (their prefix lives in LDS).
 constexpr int64_t kWideGroupedMaxExperts = 1024;
+// Block-FP8 wide kernel: at most this many K128 stages per K split (each wave keeps
+// its weight block scales of the split in LDS), so K <= 32768.
+constexpr int kWideBlockStages = 256;
 // m-tiles per unit of the grouped weight-streaming variant for tens of rows per expert
 // (96 rows: one unit per expert at 64 rows per expert on average; with 80-row units the
 // few experts past 80 rows made some CUs run two units, 107 against 74 us at c5)

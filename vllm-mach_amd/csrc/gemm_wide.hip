@@ -301,8 +301,8 @@ struct WideGrid {
 template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED>
 __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g, int64_t mb, int64_t row_base,
                                           int64_t hi, const uint8_t* w, const uint8_t* sw, int64_t nb, int64_t split,
-                                          float* pdst, int64_t pld, uint8_t* ring, uint8_t* sa_ring, int t, int lane,
-                                          int wv, int r, int q) {
+                                          float* pdst, int64_t pld, uint8_t* ring, uint8_t* sa_ring, float* sb_stage,
+                                          int t, int lane, int wv, int r, int q) {
   using S = WideSlot<MT, NT, BLOCK>;
   constexpr int C = S::COPIES;
   constexpr int AW = MT / 4, BM = 16 * MT;
@@ -336,15 +336,19 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     L.w_tile[n] = w + nt * p.KT * (CH * 1024);
     L.sw_tile[n] = sw + nt * p.KT * 256;
   }
-  const float* sbp = nullptr;
-  if (BLOCK) {
-    const int64_t nt0 = nt_wave < ntiles_total ? nt_wave : ntiles_total - 1;
-    sbp = static_cast<const float*>(p.sw) + (nt0 * 16 / 128) * (p.K / 128);
-  }
-
   const int64_t T = p.K / 128;
   const int64_t tb = split * g.kt_per_split * 4;
   const int64_t te = tb + g.kt_per_split * 4 < T ? tb + g.kt_per_split * 4 : T;
+
+  if (BLOCK) {
+    // The wave's weight block scales of this split, staged in its LDS row before any
+    // copy is issued.  Read inside the loop from global memory they would be the
+    // compiler's own vector loads, and the compiler waits for its loads with vmcnt,
+    // which counts the stage copies too: every step would drain the whole ring.
+    const int64_t nt0 = nt_wave < ntiles_total ? nt_wave : ntiles_total - 1;
+    const float* sbp = static_cast<const float*>(p.sw) + (nt0 * 16 / 128) * (p.K / 128);
+    for (int64_t i = lane; i < te - tb; i += 64) sb_stage[i] = sbp[tb + i];
+  }
 
   v4f acc[MT][NT];
 #pragma unroll
@@ -373,7 +377,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     WideRegs<MT, NT, BLOCK> x0, x1;
     wide_read<FMT, MT, NT, BLOCK>(ring, sa_ring + ((tb >> 2) % 3) * S::RING_ENTRY, (int)(tb & 3), wv, lane, q, r,
                                   x0);
-    if (BLOCK) x0.sbv = sbp[tb];
+    if (BLOCK) x0.sbv = sb_stage[0];
 
 // Step tt = t0 + I (ring slot I % R): wait for stage tt + 1 and for this wave's
 // reads of stage tt, barrier (every wave holds stage tt in registers, so its slot
@@ -396,7 +400,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
       wide_read<FMT, MT, NT, BLOCK>(ring + ((I_ + 1) % R) * S::BYTES,                               \
                                     sa_ring + (((tt + 1) >> 2) % 3) * S::RING_ENTRY,            \
                                 (int)((tt + 1) & 3), wv, lane, q, r, NXT_);                         \
-      if (BLOCK) NXT_.sbv = sbp[tt + 1 < te ? tt + 1 : tt];                                         \
+      if (BLOCK) NXT_.sbv = sb_stage[(tt + 1 < te ? tt + 1 : tt) - tb];                             \
       wide_mfma<FMT, MT, NT, BLOCK>(CUR_, acc);                                                     \
       wide_interleave<FMT, MT, NT, BLOCK>();                                                        \
     }                                                                                               \
@@ -497,6 +501,8 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
   // stage it holds the output tile of the epilogue
   __shared__ __attribute__((aligned(16))) uint8_t ring[S::SLOTS * S::BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t sa_ring[S::SA_RING ? 3 * S::RING_ENTRY : 16];
+  // block-FP8: each wave's weight block scales of the tile's K range
+  __shared__ float sb_lds[BLOCK ? 4 * kWideBlockStages : 1];
   const int t = threadIdx.x, lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
   const int r = lane & 15, q = lane >> 4;
@@ -516,7 +522,8 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
                                     : p.partial + (split * p.M + mb * BM) * p.N + nb * TW;
     const int64_t pld = g.compact ? TW : p.N;
     wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, mb * BM, p.M, p.w, static_cast<const uint8_t*>(p.sw), nb,
-                                           split, pdst, pld, ring, sa_ring, t, lane, wv, r, q);
+                                           split, pdst, pld, ring, sa_ring, sb_lds + (BLOCK ? wv * kWideBlockStages : 0),
+                                           t, lane, wv, r, q);
     return;
   }
 
@@ -578,10 +585,10 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
     // 64-row tile path in the same ring: half the activation copies and MFMAs
     if (MT == 8 && __builtin_amdgcn_readfirstlane((int)(rhi - rb)) <= 64)
       wide_tile<FMT, (MT == 8 ? 4 : MT), NT, BLOCK, GROUPED>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring,
-                                                             sa_ring, t, lane, wv, r, q);
+                                                             sa_ring, sb_lds, t, lane, wv, r, q);
     else
-      wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring, sa_ring, t, lane,
-                                             wv, r, q);
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring, sa_ring, sb_lds,
+                                             t, lane, wv, r, q);
     __syncthreads();  // the epilogue's LDS reads are done before the next tile's copies
   }
 }
@@ -764,6 +771,7 @@ static hipError_t launch_wide_fmt(const WideConfig& c, const GemmParams& p, cons
 hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const GemmParams& p, int64_t num_experts,
                             hipStream_t s) {
   const int64_t bm = 16 * c.MT;
+  if (block && (c.kt_per_split * 4 > kWideBlockStages || c.kt2 * 4 > kWideBlockStages)) return hipErrorInvalidValue;
   WideGrid g{};
   g.nblocks = (p.N + 64 * c.NT - 1) / (64 * c.NT);
   g.kt_per_split = c.kt_per_split;
