@@ -177,6 +177,15 @@ int mxl_mx_gemm_dual(const void* hi, const void* s_hi, const void* res, const vo
                      const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, const void* bias,
                      void* out, int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* mxl_mx_gemm_dual with per-call options (NULL: the defaults); s_hi and s_res are
+ * read in options->sa_layout (the other fields are unused).  Replaces
+ * mxfp8_sm120::dual_gemm_out(hi, weight, s_hi, s_weight, res, s_res, out), whose
+ * scales are swizzled (src/vllm_mach/mxfp8/native_backend.py:90-93). */
+int mxl_mx_gemm_dual_ex(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
+                        const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
+                        const void* bias, void* out, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                        const mxl_gemm_options* options, void* stream);
+
 /* MX block-scaled GEMM: y[M, N] (bf16, row stride ldc) = A . W^T, A = E4M3
  * codes [M, K] + E8M0 [M, K/32]; W tiled (fmt 0/2/3); bias bf16 [N] or NULL
  * (added after the bf16 rounding, as y + bias in bf16).  Replaces

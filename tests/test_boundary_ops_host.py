@@ -20,7 +20,14 @@ MXFP8_FRAGMENTS = {
              "int tactic", "int splits", "int swizzle", "int sms"),
     "allocate_workspace": ("Tensor a", "Tensor b", "Tensor sa", "Tensor sb", "Tensor out", "int tactic",
                            "int splits", "int swizzle", "int sms"),
+    # the two-limb path's operator, checked when dual dispatch is enabled (native_backend.py:90-93)
+    "dual_gemm_out": ("Tensor hi", "Tensor weight", "Tensor s_hi", "Tensor s_weight", "Tensor res",
+                      "Tensor s_res", "Tensor(a!) out"),
 }
+# src/vllm_mach/moe_utils.py:15-26: the names is_mxfp6_sm120_available() requires of the package
+MXFP6_REQUIRED_API = ("MXFP8Tensor", "PackedMXFP6Tensor", "autotune_w6a8", "begin_workspace_planning",
+                      "finalize_workspace_planning", "gemm_w6a8", "is_available", "load_library", "pack_scales",
+                      "workspace_stats")
 
 
 @pytest.fixture(scope="module")
@@ -45,6 +52,12 @@ def test_mxfp8_schema_fragments(loaded):
     assert "bool use_pdl=False" in str(torch.ops.mxfp8_sm120.gemm.default._schema)
     assert "mxfp8_sm120::gemm_from_float(Tensor x, Tensor w, Tensor ws) -> Tensor" == \
         str(torch.ops.mxfp8_sm120.gemm_from_float.default._schema)
+    # the PDL entry points _require_pdl_runtime() looks for (dense_mxfp8.py:63-67)
+    for name in ("gemm_pdl", "gemm_from_float_pdl"):
+        assert hasattr(torch.ops.mxfp8_sm120, name), name
+    assert hasattr(torch.ops.mxfp6, "quantize_mxfp8_pdl")
+    assert str(torch.ops.mxfp8_sm120.gemm_from_float_pdl.default._schema) == \
+        "mxfp8_sm120::gemm_from_float_pdl(Tensor x, Tensor w, Tensor ws) -> Tensor"
 
 
 def test_mxfp6_op_signatures(loaded):
@@ -69,3 +82,20 @@ def test_moe_api_names(loaded):
         assert callable(getattr(loaded, name)), name
     if not torch.cuda.is_available():
         assert loaded.is_available() is False
+
+
+def test_dense_api_and_runtime_modules(loaded):
+    """The package names the reference's availability check requires (moe_utils.py:15-26,
+    139-146), the dense MXFP8 runtime module's names (dense_mxfp8.py:120-125, 151) and the
+    two-limb module's (mxfp8/dual.py:42-45, 109-111)."""
+    for name in MXFP6_REQUIRED_API + ("gemm_from_float", "warmup_w6a8", "quantize_mxfp8"):
+        assert hasattr(loaded, name), name
+    for name in ("load_library", "gemm_from_float", "begin_workspace_planning", "finalize_workspace_planning",
+                 "warmup", "MXFP8Tensor", "pack_scales"):
+        assert hasattr(loaded.mxfp8, name), name
+    for name in ("load_library", "quantize", "gemm_out"):
+        assert hasattr(loaded.mxfp8_dual, name), name
+    t = loaded.PackedMXFP6Tensor(values=torch.zeros(8, 96, dtype=torch.uint8), scales=torch.zeros(4),
+                                 rows=8, k=128)
+    assert (t.rows, t.k) == (8, 128)
+    assert loaded.MXFP8Tensor(torch.zeros(2, 32), torch.zeros(4), 2, 32).k == 32

@@ -227,3 +227,54 @@ def test_moe_api_sequence(api, oracle_mod, dev, E, T, topk, mapped):
     got = out.float().cpu().numpy()
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
     np.testing.assert_allclose(got, ref, rtol=0.03, atol=0.03)
+
+
+@pytest.mark.parametrize("M,N,K", [(32, 2048, 2560), (64, 1024, 4096), (7, 512, 1024)])
+def test_dual_gemm_out(api, oracle_mod, dev, pkg, M, N, K):
+    """mxfp6.mxfp8_dual.quantize + gemm_out (mxfp8/dual.py:42-45) with swizzled scales:
+    bit-identical to this package's two-limb GEMM on logical scales, within the GEMM bar
+    of the oracle's exact two-limb sum."""
+    wc, ws, _ = _weights(oracle_mod, N, K, 0, 0.02, 41 + M)
+    w = torch.from_numpy(wc).to(dev).view(torch.float8_e4m3fn)
+    wsw = api.pack_scales(torch.from_numpy(ws).to(dev))
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[: K // 50]] *= 30
+    x = x.bfloat16()
+    hi, s_hi, res, s_res = api.mxfp8_dual.quantize(x.to(dev))
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    api.mxfp8_dual.gemm_out(hi, w, s_hi, wsw.view(-1), res, s_res, out)
+    ops = pkg.ops
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(wc).to(dev), torch.from_numpy(ws).to(dev), 0)
+    assert torch.equal(out, ops.mx_gemm_from_float_dual(x.to(dev), tiled, tiled_s, N, 0))
+    rh, rsh, rr, rsr = oracle_mod.quant_mxfp8_dual(x, 0)
+    ref = oracle_mod.mx_gemm_ref(rh, rsh, wc, ws, 0) + oracle_mod.mx_gemm_ref(rr, rsr, wc, ws, 0)
+    _check(out.float().cpu().numpy(), _ref_bf16(oracle_mod, ref))
+    # the PDL-named entry points are the same work
+    y = torch.ops.mxfp8_sm120.gemm_from_float(x.to(dev), w, wsw)
+    assert torch.equal(torch.ops.mxfp8_sm120.gemm_from_float_pdl(x.to(dev), w, wsw), y)
+    q, sq = torch.ops.mxfp6.quantize_mxfp8(x.to(dev))
+    q2, sq2 = torch.ops.mxfp6.quantize_mxfp8_pdl(x.to(dev))
+    assert torch.equal(q, q2) and torch.equal(sq, sq2)
+    assert torch.equal(torch.ops.mxfp8_sm120.gemm_pdl(q.view(torch.float8_e4m3fn), w, sq, wsw), y)
+    # the dense runtime module (mxfp6.mxfp8)
+    assert torch.equal(api.mxfp8.gemm_from_float(x.to(dev), api.mxfp8.MXFP8Tensor(w, wsw, N, K)), y)
+
+
+@pytest.mark.parametrize("M", [1, 16, 200])
+def test_dense_w6a8_api(api, oracle_mod, dev, M):
+    """PackedMXFP6Tensor / gemm_from_float / gemm_w6a8 / warmup_w6a8 of the mxfp6 package
+    (warmup.py:55-67, sm120_owner_prefill.py:56-63, tests/native_mxfp6/test_moe.py:232)."""
+    N, K = 1024, 2048
+    wc, ws, stored = _weights(oracle_mod, N, K, 3, 0.015, 90 + M)
+    weight = api.PackedMXFP6Tensor(torch.from_numpy(stored).to(dev), api.pack_scales(torch.from_numpy(ws).to(dev)),
+                                   N, K)
+    x = _act(M, K, 7 + M).to(dev)
+    api.warmup_w6a8(x, weight, out_dtype=torch.bfloat16, iterations=1)
+    y = api.gemm_from_float(x, weight, out_dtype=torch.bfloat16)
+    rc, rs = oracle_mod.quant_mxfp8(x.cpu(), 0)
+    _check(y.float().cpu().numpy(), _ref_bf16(oracle_mod, oracle_mod.mx_gemm_ref(rc, rs, wc, ws, 3)))
+    operand = api.quantize_mxfp8(x)
+    assert (operand.rows, operand.k) == (M, K)
+    assert torch.equal(api.gemm_w6a8(operand, weight, out_dtype=torch.bfloat16), y)
+    assert api.gemm_from_float(x, weight, out_dtype=torch.float16).dtype == torch.float16

@@ -35,6 +35,7 @@ SIGNATURES = {
     "mxl_swiglu_mxfp8": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P]),
     "mxl_quantize_mxfp8_dual": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P]),
     "mxl_mx_gemm_dual": (_I, [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P]),
+    "mxl_mx_gemm_dual_ex": (_I, [_P, _P, _P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P, _P]),
     "mxl_rmsnorm_mxfp8": (_I, [_P, _P, _P, _I64, _I64, _F, _I, _I, _P, _P, _P, _P]),
     "mxl_gemma_rmsnorm": (_I, [_P, _P, _P, _I64, _I64, _F, _P, _P, _P]),
     "mxl_quantize_block_fp8": (_I, [_P, _I64, _I64, _P, _P, _P]),

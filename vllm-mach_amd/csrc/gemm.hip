@@ -676,11 +676,12 @@ extern "C" int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int
   return MXL_OK;
 }
 
-extern "C" int mxl_mx_gemm_dual(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
-                                const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
-                                const void* bias, void* out, int64_t ldc, void* workspace, int64_t workspace_bytes,
-                                void* stream) {
+static int gemm_dual_common(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
+                            const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
+                            const void* bias, void* out, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                            const GemmOptions& o, void* stream) {
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm_dual: unknown weight format %d", w_fmt);
+  MXL_CHECK_ARG(o.sa_layout == 0 || o.sa_layout == 1, "mxl_mx_gemm_dual: sa_layout must be 0 or 1");
   MXL_CHECK_ARG(M >= 0 && M <= 64 && N > 0 && K > 0 && K % 128 == 0,
                 "mxl_mx_gemm_dual: need M <= 64, N > 0, K %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
                 (long long)N, (long long)K);
@@ -697,6 +698,7 @@ extern "C" int mxl_mx_gemm_dual(const void* hi, const void* s_hi, const void* re
   p.partial = (float*)workspace;
   p.lda = K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
   p.row_div = 1;
+  set_sa_layout(p, o.sa_layout);
   p.S = 2;  // the two limbs' fp32 partials
   GemmConfig c = choose_config(M, N, K);
   c.S = 1;
@@ -714,6 +716,22 @@ extern "C" int mxl_mx_gemm_dual(const void* hi, const void* s_hi, const void* re
     return MXL_EHIP;
   }
   return MXL_OK;
+}
+
+extern "C" int mxl_mx_gemm_dual(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
+                                const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
+                                const void* bias, void* out, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  return gemm_dual_common(hi, s_hi, res, s_res, M, w_tiled, sw_tiled, N, K, w_fmt, bias, out, ldc, workspace,
+                          workspace_bytes, GemmOptions(), stream);
+}
+
+extern "C" int mxl_mx_gemm_dual_ex(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
+                                   const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
+                                   const void* bias, void* out, int64_t ldc, void* workspace, int64_t workspace_bytes,
+                                   const void* options, void* stream) {
+  return gemm_dual_common(hi, s_hi, res, s_res, M, w_tiled, sw_tiled, N, K, w_fmt, bias, out, ldc, workspace,
+                          workspace_bytes, options_of(options), stream);
 }
 
 extern "C" int mxl_block_fp8_gemm(const void* a, const void* sa_colmajor, int64_t M, const void* w_tiled,

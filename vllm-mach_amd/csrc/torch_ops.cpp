@@ -4,6 +4,8 @@
 //
 //   torch.ops.load_library(VLLM_MACH_BLOCK_FP8_LIBRARY)   src/vllm_mach/fp8/block_native.py:22-44
 //   torch.ops.load_library(MXFP8_LIBRARY_PATH)            src/vllm_mach/mxfp8/native_backend.py:100-125
+//   torch.ops.mxfp8_sm120.{gemm,gemm_from_float}_pdl,     src/vllm_mach/mxfp6/dense_mxfp8.py:54-95
+//     mxfp6.quantize_mxfp8_pdl, mxfp8_sm120.dual_gemm_out native_backend.py:90-93
 //   torch.ops.mach_fp8_activation.run                     native/fp8_activation/activation.cu:98-104
 //   torch.ops.mxfp6.*                                     src/vllm_mach/mxfp6/dense.py:113-129,
 //                                                         dense_mxfp8.py:40, fused_mlp.py:16-19,
@@ -315,6 +317,45 @@ at::Tensor mxfp8_gemm_from_float(const at::Tensor& x, const at::Tensor& w, const
   return mx_gemm(std::get<0>(q), std::get<1>(q), 0, t, kE4M3, N, K, options(0, -1, 0), at::Tensor(), at::Tensor(), s);
 }
 
+// Two-limb MXFP8 GEMM (M <= 64): out = bf16(hi . W^T + res . W^T), the limbs' fp32
+// products summed before the one rounding.  hi / res E4M3 [M, K] with swizzled scales
+// s_hi / s_res; weight E4M3 [N, K] with swizzled s_weight (flat, as the reference
+// passes scale.view(-1)).
+void mxfp8_dual_gemm_out(const at::Tensor& hi, const at::Tensor& weight, const at::Tensor& s_hi,
+                         const at::Tensor& s_weight, const at::Tensor& res, const at::Tensor& s_res, at::Tensor& out) {
+  TORCH_CHECK(weight.dim() == 2 && weight.scalar_type() == at::kFloat8_e4m3fn,
+              "mxfp8_sm120::dual_gemm_out: weight must be E4M3 [N, K]");
+  const int64_t N = weight.size(0), K = weight.size(1);
+  TORCH_CHECK(is_byte_dtype(hi) && hi.element_size() == 1 && is_byte_dtype(res) && res.element_size() == 1,
+              "mxfp8_sm120::dual_gemm_out: hi and res must hold E4M3 codes");
+  check_act(hi, K, "mxfp8_sm120::dual_gemm_out");
+  check_act(res, K, "mxfp8_sm120::dual_gemm_out");
+  const int64_t M = hi.size(0);
+  TORCH_CHECK(res.size(0) == M && M <= 64, "mxfp8_sm120::dual_gemm_out: hi and res must be [M, K] with M <= 64");
+  TORCH_CHECK(N % 16 == 0 && K % 128 == 0, "mxfp8_sm120::dual_gemm_out: need N % 16 == 0 and K % 128 == 0");
+  TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.dim() == 2 && out.size(0) == M && out.size(1) == N &&
+                  out.stride(1) == 1 && out.stride(0) >= N,
+              "mxfp8_sm120::dual_gemm_out: out must be bf16 [M, N] with unit column stride");
+  const int64_t need_s = mxl_swizzled_scale_bytes(M, K);
+  for (const at::Tensor* t : {&s_hi, &s_res})
+    TORCH_CHECK(t->is_cuda() && t->is_contiguous() && t->numel() * t->element_size() >= need_s,
+                "mxfp8_sm120::dual_gemm_out: activation scales hold ", t->numel() * t->element_size(),
+                " bytes, need ", need_s);
+  hipStream_t s = stream_of(hi);
+  const Tiled& t = tiled_mx(weight, s_weight, kE4M3, N, K, 1, s);
+  if (M == 0) return;
+  // the two limbs' partials: a workspace that must grow during capture cannot run unsplit here
+  const int64_t nbytes = 2 * M * N * 4;
+  auto w = workspace(hi, nbytes, s);
+  TORCH_CHECK(w.second >= nbytes, "mxfp8_sm120::dual_gemm_out: run this shape once before graph capture (its ",
+              nbytes, "-byte workspace would grow during capture)");
+  const mxl_gemm_options o{1, -1, 0, 0, 0, 0};
+  check(mxl_mx_gemm_dual_ex(hi.data_ptr(), s_hi.data_ptr(), res.data_ptr(), s_res.data_ptr(), M, t.tiled.data_ptr(),
+                            t.tiled_s.data_ptr(), N, K, kE4M3, nullptr, out.data_ptr(), out.stride(0), w.first,
+                            w.second, &o, s),
+        "mxl_mx_gemm_dual_ex");
+}
+
 // ================================================================== mxfp6
 
 std::tuple<at::Tensor, at::Tensor> mxfp6_quantize_mxfp8(const at::Tensor& x) {
@@ -426,16 +467,27 @@ TORCH_LIBRARY(mxfp8_sm120, m) {
   m.def("allocate_workspace(Tensor a, Tensor b, Tensor sa, Tensor sb, Tensor out, int tactic, int splits, "
         "int swizzle, int sms) -> Tensor");
   m.def("gemm_from_float(Tensor x, Tensor w, Tensor ws) -> Tensor");
+  // the programmatic-dependent-launch entry points of the reference's PDL build
+  // (dense_mxfp8.py:54-70): the same work here, where a HIP graph carries the overlap
+  m.def("gemm_pdl(Tensor a, Tensor b, Tensor sa, Tensor sb, Tensor(a!)? out=None, Tensor? workspace=None, "
+        "int tactic=-1, int splits=1, int swizzle=1, int sms=0, bool use_pdl=False) -> Tensor");
+  m.def("gemm_from_float_pdl(Tensor x, Tensor w, Tensor ws) -> Tensor");
+  m.def("dual_gemm_out(Tensor hi, Tensor weight, Tensor s_hi, Tensor s_weight, Tensor res, Tensor s_res, "
+        "Tensor(a!) out) -> ()");
 }
 TORCH_LIBRARY_IMPL(mxfp8_sm120, CUDA, m) {
   m.impl("gemm", &mxfp8_gemm);
   m.impl("allocate_workspace", &mxfp8_allocate_workspace);
   m.impl("gemm_from_float", &mxfp8_gemm_from_float);
+  m.impl("gemm_pdl", &mxfp8_gemm);
+  m.impl("gemm_from_float_pdl", &mxfp8_gemm_from_float);
+  m.impl("dual_gemm_out", &mxfp8_dual_gemm_out);
 }
 
 TORCH_LIBRARY(mxfp6, m) {
   m.def("quantize_mxfp8(Tensor x) -> (Tensor, Tensor)");
   m.def("quantize_mxfp8_logical(Tensor x) -> (Tensor, Tensor)");
+  m.def("quantize_mxfp8_pdl(Tensor x) -> (Tensor, Tensor)");
   m.def("pack_scales(Tensor scales) -> Tensor");
   m.def("gemm_from_float(Tensor x, Tensor w, Tensor ws, int N, float alpha, ScalarType dtype) -> Tensor");
   m.def("gemm_from_swiglu(Tensor gate_up, Tensor w, Tensor ws, int N, float alpha, ScalarType dtype) -> Tensor");
@@ -445,6 +497,7 @@ TORCH_LIBRARY(mxfp6, m) {
 TORCH_LIBRARY_IMPL(mxfp6, CUDA, m) {
   m.impl("quantize_mxfp8", &mxfp6_quantize_mxfp8);
   m.impl("quantize_mxfp8_logical", &mxfp6_quantize_mxfp8_logical);
+  m.impl("quantize_mxfp8_pdl", &mxfp6_quantize_mxfp8);
   m.impl("pack_scales", &mxfp6_pack_scales);
   m.impl("gemm_from_float", &mxfp6_gemm_from_float);
   m.impl("gemm_from_swiglu", &mxfp6_gemm_from_swiglu);

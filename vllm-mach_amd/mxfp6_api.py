@@ -10,12 +10,19 @@ The reference binds its MX kernels through two kinds of native entry points:
   those names and schemas over this library's C ABI; ``library_path()`` is the file a
   maintainer points ``MXFP8_LIBRARY_PATH`` / ``VLLM_MACH_BLOCK_FP8_LIBRARY`` at, and
   ``load_library()`` opens it.
-* the Python API of the ``mxfp6`` package that the MoE path calls
-  (src/vllm_mach/mxfp6/moe_utils.py:15-44, 162-488): ``quantize_mxfp8_logical``,
-  ``quantize_mxfp8``, ``pack_scales``, ``to_mma_k64_weight``, ``route_mxfp8_out``,
-  ``grouped_gemm_w6a8_out``, ``silu_and_mul_mxfp8_grouped``, ``moe_reduce_out`` and
-  the workspace-planning calls.  This module provides them with the same names,
-  argument order and mutation contracts.
+* the Python API of the ``mxfp6`` package that the dense and MoE paths call
+  (src/vllm_mach/mxfp6/moe_utils.py:15-44, 162-488; warmup.py:46-147;
+  sm120_owner_prefill.py:50-63): ``MXFP8Tensor``, ``PackedMXFP6Tensor``,
+  ``gemm_w6a8``, ``gemm_from_float``, ``warmup_w6a8``, ``autotune_w6a8``,
+  ``quantize_mxfp8_logical``, ``quantize_mxfp8``, ``pack_scales``, ``to_mma_k64_weight``,
+  ``route_mxfp8_out``, ``grouped_gemm_w6a8_out``, ``silu_and_mul_mxfp8_grouped``,
+  ``moe_reduce_out`` and the workspace-planning calls, plus its runtime modules
+  ``mxfp6.mxfp8`` (dense MXFP8, dense_mxfp8.py:45-220) and ``mxfp6.mxfp8_dual``
+  (two-limb MXFP8, mxfp8/dual.py:40-50, 109-111) as the attributes ``mxfp8`` and
+  ``mxfp8_dual``.  This module provides them with the same names, argument order and
+  mutation contracts.  The Qwen3.5 TP2 schedules (``qwen35_*``,
+  ``array_gemm_w6a8_reduce_out``, ``Qwen35GroupedWorkspace``) are multi-GPU and are
+  not provided.
 
 Layouts at this boundary are the reference's: weights stay in their checkpoint form
 (E4M3 [N, K], packed FP6 [E, N, 3K/4]); weight scales are ``pack_scales`` output,
@@ -80,9 +87,23 @@ def is_available() -> bool:
 
 # ------------------------------------------------------------- quantizers
 
-class MXFP8Operand(NamedTuple):
-    values: torch.Tensor  # E4M3 codes as uint8 [M, K]
-    scales: torch.Tensor  # swizzled E8M0 bytes
+class MXFP8Tensor(NamedTuple):
+    """An MXFP8 operand: E4M3 codes [rows, k] and its swizzled E8M0 scales
+    (``mxfp6.MXFP8Tensor(values, scales, rows, k)``, sm120_owner_prefill.py:502,
+    dense_mxfp8.py:214)."""
+    values: torch.Tensor
+    scales: torch.Tensor
+    rows: int
+    k: int
+
+
+class PackedMXFP6Tensor(NamedTuple):
+    """A packed MXFP6 (E3M2) weight: bytes [rows, 3k/4] and its swizzled E8M0 scales
+    (``mxfp6.PackedMXFP6Tensor(values, scales, rows, k)``, warmup.py:55-60)."""
+    values: torch.Tensor
+    scales: torch.Tensor
+    rows: int
+    k: int
 
 
 def quantize_mxfp8_logical(input: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -90,12 +111,47 @@ def quantize_mxfp8_logical(input: torch.Tensor) -> tuple[torch.Tensor, torch.Ten
     return torch.ops.mach_amd.quantize_mxfp8(input, ops.FLOOR_CARRY175)
 
 
-def quantize_mxfp8(input: torch.Tensor) -> MXFP8Operand:
+def quantize_mxfp8(input: torch.Tensor) -> MXFP8Tensor:
     """bf16 [M, K] -> codes and swizzled scales (``operand.values`` / ``.scales``,
     moe_utils.py:285-317)."""
     load_library()
     codes, scales = torch.ops.mxfp6.quantize_mxfp8(input)
-    return MXFP8Operand(codes, scales)
+    return MXFP8Tensor(codes, scales, int(input.shape[0]), int(input.shape[1]))
+
+
+# ----------------------------------------------------------- dense W6A8
+
+def _dtype(out_dtype) -> torch.dtype:
+    return out_dtype if out_dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+
+
+def gemm_from_float(x: torch.Tensor, weight: PackedMXFP6Tensor, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """bf16 [M, K] quantized on the fly (floor_carry175) times a packed MXFP6 weight
+    (tests/native_mxfp6/test_moe.py:232-241)."""
+    load_library()
+    return torch.ops.mxfp6.gemm_from_float(x, weight.values, weight.scales, int(weight.rows), 1.0, _dtype(out_dtype))
+
+
+def gemm_w6a8(activation: MXFP8Tensor, weight: PackedMXFP6Tensor, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """A quantized MXFP8 activation (``quantize_mxfp8`` output) times a packed MXFP6
+    weight (sm120_owner_prefill.py:61-63)."""
+    load_library()
+    codes = activation.values.view(torch.uint8) if activation.values.dtype != torch.uint8 else activation.values
+    return torch.ops.mxfp6.gemm_w6a8_pdl(codes, weight.values, activation.scales, weight.scales, int(activation.rows),
+                                         int(weight.rows), int(weight.k), 1.0, _dtype(out_dtype))
+
+
+def warmup_w6a8(x: torch.Tensor, weight: PackedMXFP6Tensor, out_dtype=torch.bfloat16, iterations: int = 1) -> None:
+    """Run the GEMM at x's shape (warmup.py:67): prepares the weight's tiled copy and
+    grows this stream's workspace outside graph capture."""
+    for _ in range(max(1, int(iterations))):
+        gemm_from_float(x, weight, out_dtype=out_dtype)
+
+
+def autotune_w6a8(x: torch.Tensor, weight: PackedMXFP6Tensor, out_dtype=torch.bfloat16, **_unused) -> None:
+    """The reference tunes CUTLASS tactics per shape; here a cost model picks the kernel,
+    so tuning is a warmup of the shape."""
+    warmup_w6a8(x, weight, out_dtype=out_dtype)
 
 
 def pack_scales(logical_scales: torch.Tensor) -> torch.Tensor:
@@ -219,3 +275,8 @@ def workspace_stats(device) -> dict:
     (stream, kind) workspaces held."""
     info = ops.inspect()
     return {"lanes": len(info["workspaces"]), **info}
+
+
+# the package's runtime submodules (``mxfp6.mxfp8``, ``mxfp6.mxfp8_dual``)
+from . import mxfp8_api as mxfp8  # noqa: E402
+from . import mxfp8_dual_api as mxfp8_dual  # noqa: E402
