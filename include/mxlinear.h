@@ -145,7 +145,7 @@ int mxl_pack_weight_ex(const void* codes, const void* scales, int scale_layout, 
 /* Per-call GEMM options: the activation-scale layout and the tuning overrides
  * of the reference's native GEMM (tactic, splits: _DEFAULT_CONFIG,
  * src/vllm_mach/mxfp8/native_backend.py:29).  A NULL options pointer means
- * {0, -1, 0, 0, 0, 0}: logical scales, everything chosen by the cost model. */
+ * {0, -1, 0, 0, 0, 0, 0}: logical scales, everything chosen by the cost model. */
 typedef struct mxl_gemm_options {
   int sa_layout; /* MX activation scales: 0 logical [M, K/32], 1 swizzled */
   int kernel;    /* -1 automatic; 0 weight-streaming (M <= 16), 1 wide (M >= 64,
@@ -156,6 +156,8 @@ typedef struct mxl_gemm_options {
   int tile_n;    /* wide: 64-column groups per workgroup tile, 1, 2 or 4; 0 automatic */
   int tile_m;    /* wide: 16-row tiles per workgroup tile, 4 or 8; 0 automatic */
   int hybrid;    /* wide, splits == 1: whole-K full rounds, the remainder split */
+  int waves;     /* wide MX dense with 128-row tiles: 4 waves per workgroup (each all
+                    128 rows) or 8 (two per SIMD, each 64 rows); 0 automatic */
 } mxl_gemm_options;
 
 /* Scratch bytes the GEMMs may use for split-K partials at (M, N, K) (the

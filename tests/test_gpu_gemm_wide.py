@@ -17,8 +17,8 @@ def force(monkeypatch, ops, cfg=None, **changes):
     """Pin the kernel selection for this test (``ops._tuning``), merged with any pin already
     set: ``cfg`` is a wide-tile spec "NT,S" or "NT,1,h"; keywords set other fields."""
     cur = ops._tuning
-    f = {k: getattr(cur, k) for k in ("kernel", "splits", "tile_n", "tile_m", "hybrid")} if cur is not None else \
-        {"kernel": -1, "splits": 0, "tile_n": 0, "tile_m": 0, "hybrid": 0}
+    f = {k: getattr(cur, k) for k in ("kernel", "splits", "tile_n", "tile_m", "hybrid", "waves")} \
+        if cur is not None else {"kernel": -1, "splits": 0, "tile_n": 0, "tile_m": 0, "hybrid": 0, "waves": 0}
     if cfg:
         parts = cfg.split(",")
         f.update(tile_n=int(parts[0]), splits=int(parts[1]), hybrid=int(len(parts) > 2 and parts[2] == "h"))
@@ -26,9 +26,9 @@ def force(monkeypatch, ops, cfg=None, **changes):
     monkeypatch.setattr(ops, "_tuning", pkg_options(ops, **f))
 
 
-def pkg_options(ops, kernel, splits, tile_n, tile_m, hybrid):
+def pkg_options(ops, kernel, splits, tile_n, tile_m, hybrid, waves=0):
     from vllm_mach_amd import _lib
-    return _lib.GemmOptions(0, kernel, splits, tile_n, tile_m, hybrid)
+    return _lib.GemmOptions(0, kernel, splits, tile_n, tile_m, hybrid, waves)
 
 
 @pytest.mark.parametrize("M,N,K,fmt,cfg,bias", [
@@ -58,6 +58,38 @@ def test_wide_mx_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias
     if bias:
         ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().numpy()[None, :]))
     _check(y.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,fmt,cfg,bias", [
+    (200, 1000, 768, 0, "2,1", True),      # ragged M, K = 1.5 super-tiles
+    (300, 640, 2304, 2, "2,3", False),     # 3 K splits over 4.5 super-tiles
+    (130, 384, 1280, 3, "1,2", False),     # one n-tile per group: both waves copy its scales
+    (384, 1024, 2560, 0, "4,2", True),     # 3-slot ring
+    (256, 700, 1280, 3, "4,3", False),     # N not a multiple of 256
+    (512, 8320, 1024, 0, "2,1,h", True),   # hybrid: whole-K rounds then the split remainder
+    (512, 2560, 9216, 0, "2,3", False),    # c2 M = 512
+    (256, 17408, 5120, 2, "2,1,h", False), # c4 M = 256
+])
+def test_wide_eight_waves(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, bias):
+    """Eight waves per workgroup (two per SIMD, each half the tile's rows): bit-identical to
+    the four-wave kernel (the same MFMA chain per 16 x 16 output tile) and within the bar."""
+    ops = pkg.ops
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 13 + N + K)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    x = _act(M, K, 5 + M)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    b = (torch.randn(N, generator=torch.Generator().manual_seed(6)) * 0.5).bfloat16().to(dev) if bias else None
+    force(monkeypatch, ops, cfg, waves=4)
+    y4 = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, b)
+    force(monkeypatch, ops, cfg, waves=8)
+    y8 = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, b)
+    assert torch.equal(y8, y4)
+    assert torch.equal(torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, b), y8)
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)))
+    if bias:
+        ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().cpu().numpy()[None, :]))
+    _check(y8.float().cpu().numpy(), ref)
 
 
 @pytest.mark.parametrize("M,N,K,cfg", [

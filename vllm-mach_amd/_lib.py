@@ -66,10 +66,10 @@ SIGNATURES = {
 class GemmOptions(ctypes.Structure):
     """``mxl_gemm_options``: activation-scale layout and tuning overrides of one GEMM call."""
     _fields_ = [("sa_layout", _I), ("kernel", _I), ("splits", _I), ("tile_n", _I), ("tile_m", _I),
-                ("hybrid", _I)]
+                ("hybrid", _I), ("waves", _I)]
 
-    def __init__(self, sa_layout=0, kernel=-1, splits=0, tile_n=0, tile_m=0, hybrid=0):
-        super().__init__(sa_layout, kernel, splits, tile_n, tile_m, hybrid)
+    def __init__(self, sa_layout=0, kernel=-1, splits=0, tile_n=0, tile_m=0, hybrid=0, waves=0):
+        super().__init__(sa_layout, kernel, splits, tile_n, tile_m, hybrid, waves)
 
 
 def options_ptr(opts: "GemmOptions | None"):

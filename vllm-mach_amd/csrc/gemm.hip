@@ -449,8 +449,9 @@ static int pack_common(const void* codes, const void* scales, int scale_layout, 
 static GemmOptions options_of(const void* opts) {
   GemmOptions o;
   if (opts) {
-    const int* v = static_cast<const int*>(opts);  // mxl_gemm_options: six ints in declaration order
+    const int* v = static_cast<const int*>(opts);  // mxl_gemm_options: seven ints in declaration order
     o.sa_layout = v[0]; o.kernel = v[1]; o.splits = v[2]; o.tile_n = v[3]; o.tile_m = v[4]; o.hybrid = v[5];
+    o.waves = v[6];
   }
   return o;
 }
@@ -473,6 +474,7 @@ static bool plan_dense(int64_t M, int64_t N, int64_t K, int fmt, bool block, con
     return false;
   if (d.kernel == kWide) {
     d.wide = wide_config(M, N, K, fmt, o);
+    if (block) d.wide.WM = 1;  // eight-wave tiles are MX only
     d.need = wide_workspace_bytes(d.wide, M, N);
   } else if (d.kernel == kGeneric) {
     d.gen = choose_config(M, N, K);

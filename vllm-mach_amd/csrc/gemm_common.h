@@ -63,6 +63,7 @@ struct GemmOptions {
   int tile_n = 0;     // wide: NT in {1, 2, 4}; 0 auto
   int tile_m = 0;     // wide: MT in {4, 8}; 0 auto
   int hybrid = 0;     // wide, splits == 1: full rounds whole-K, the remainder split
+  int waves = 0;      // wide MX dense, 128-row tiles: 4 or 8 waves per workgroup; 0 auto
 };
 
 template <int MT>
@@ -180,6 +181,7 @@ struct WideConfig {
   int S2 = 1;
   int64_t kt2 = 0;
   int MT = 8;  // 16-row m-tiles per workgroup tile: 8 (128 rows) or 4 (64 rows)
+  int WM = 1;  // m-groups of four waves: 1, or 2 (eight waves, each half the tile's rows)
 };
 // The cost model's choice, or the options' tile / split overrides where given.
 WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptions& o = GemmOptions());

@@ -48,9 +48,10 @@ namespace mxl {
 
 namespace {
 
-template <int MT, int NT, bool BLOCK>
+template <int MT, int NT, bool BLOCK, int WM = 1>
 struct WideSlot {
   static_assert(MT == 4 || MT == 8, "64- or 128-row workgroup tiles");
+  static_assert(WM == 1 || (WM == 2 && !BLOCK && MT == 8), "two m-groups of waves: MX 128-row tiles only");
   // MX with NT <= 2: the activation scales live in a separate ring of three
   // super-tile entries (16 MT rows x 16 bytes), filled a super-tile ahead, so a
   // copy moves 16 bytes per row instead of one dword from each row.
@@ -63,8 +64,16 @@ struct WideSlot {
   static constexpr int SLOTS = NT == 4 ? 3 : 4;             // 4 x 53 KiB would not fit the LDS
   static constexpr int SW = MT / 4;                         // scale waves: 0 .. SW - 1, 64 rows each
   static constexpr int RING_ENTRY = 256 * MT;               // scale ring entry: 16 MT rows x 16 bytes
-  // copies per wave per stage (the scale waves also copy the activation scales)
-  static constexpr int COPIES = MT / 2 + 2 * NT + (BLOCK ? 0 : NT);
+  // WM m-groups of four waves: wave w owns m-tiles (w / 4) MT / WM .. + MT / WM - 1 and the
+  // n-tiles of n-group w % 4.  Copies per wave per stage: its share of the A chunks, of its
+  // n-group's B chunks (one of the two per n-tile when WM = 2) and of their E8M0 scales (with
+  // one n-tile both waves of the group copy it: the same bytes to the same place); the scale
+  // waves also copy the activation scales.
+  static constexpr int WAVES = 4 * WM;
+  static constexpr int ACH = 2 * MT / WAVES;
+  static constexpr int BCH = 2 / WM;
+  static constexpr int SBC = BLOCK ? 0 : (WM == 1 ? NT : (NT >= 2 ? NT / 2 : 1));
+  static constexpr int COPIES = ACH + BCH * NT + SBC;
 };
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -100,11 +109,11 @@ __device__ __forceinline__ void wait_vm() {
 // outstanding load): LDS data is handed over by the explicit waits.
 __device__ __forceinline__ void wide_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <int MT, int NT>
+template <int MT, int NT, int WM = 1>
 struct WideLanes {
-  // copy lane l of m-tile (MT / 4) wv + u / 2, rows 8 (u % 2) .. + 7: row 8 (u % 2) + l / 8, piece
-  // (l % 8) ^ a_swz(row), as row * lda + 16 piece
-  uint32_t a_off[MT / 2];
+  // A chunk c = ACH wv + u (m-tile c / 2, rows 8 (c % 2) .. + 7): copy lane l reads row
+  // 8 (c % 2) + l / 8, piece (l % 8) ^ a_swz(row), as row * lda + 16 piece
+  uint32_t a_off[2 * MT / (4 * WM)];
   uint32_t sa_off;    // MX: row * K/32; block-FP8: 4 row  (row = t % 16 MT)
   uint32_t sa_piece[4];  // scale ring: lane l of scale wave w reads dword l % 4 of row 4 MT j + 16 w + l / 4
   uint32_t sa_last[4];   // the same for the last super-tile when it is half (K % 512 = 256), from p.sa and
@@ -117,18 +126,18 @@ struct WideLanes {
 // the scale ring, waves 0 and 1 also copy piece j (32 rows) of the next
 // super-tile's activation scales (clamped inside K: a piece past the last
 // super-tile is never read).
-template <int FMT, int MT, int NT, bool BLOCK>
+template <int FMT, int MT, int NT, bool BLOCK, int WM>
 __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, int64_t t, int wv, int lane,
-                                          const WideLanes<MT, NT>& L, uint8_t* sa_ring) {
-  using S = WideSlot<MT, NT, BLOCK>;
+                                          const WideLanes<MT, NT, WM>& L, uint8_t* sa_ring) {
+  using S = WideSlot<MT, NT, BLOCK, WM>;
   constexpr int CH = FmtTraits<FMT>::CH;
-  constexpr int AW = MT / 4;  // m-tiles copied per wave
+  const int wn = wv & 3, wm = wv >> 2;
   const int64_t kt = t >> 2;
   const int j = (int)(t & 3);
 #pragma unroll
-  for (int u = 0; u < 2 * AW; ++u) {  // A: m-tile AW wv + u / 2, rows 8 (u % 2) .. + 7, whole 128-byte rows
-    const int i = AW * wv + (u >> 1);
-    copy16(p.a + t * 128, L.a_off[u], lds_addr(slot + S::A + (i * 2 + (u & 1)) * 1024));
+  for (int u = 0; u < S::ACH; ++u) {  // A chunk ACH wv + u: m-tile c / 2, rows 8 (c % 2) .. + 7, whole rows
+    const int c = S::ACH * wv + u;
+    copy16(p.a + t * 128, L.a_off[u], lds_addr(slot + S::A + c * 1024));
   }
   // B: the two 1 KiB chunks of the tile that hold slice j (FP6: its 24 bytes per lane
   // straddle two chunks)
@@ -137,8 +146,10 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
   for (int n = 0; n < NT; ++n) {
     const uint8_t* tile = L.w_tile[n] + kt * (CH * 1024) + c0 * 1024;
 #pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2)
-      copy16(tile + c2 * 1024, (uint32_t)(lane * 16), lds_addr(slot + S::B + ((wv * NT + n) * 2 + c2) * 1024));
+    for (int h = 0; h < S::BCH; ++h) {
+      const int c2 = WM == 1 ? h : wm;
+      copy16(tile + c2 * 1024, (uint32_t)(lane * 16), lds_addr(slot + S::B + ((wn * NT + n) * 2 + c2) * 1024));
+    }
   }
   if (S::SA_RING) {
     if (wv < S::SW) {
@@ -156,7 +167,8 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
   if (!BLOCK) {
 #pragma unroll
     for (int n = 0; n < NT; ++n)
-      copy4(L.sw_tile[n] + kt * 256, (uint32_t)(lane * 4), lds_addr(slot + S::SB + (wv * NT + n) * 256));
+      if (WM == 1 || NT == 1 || (n & 1) == wm)
+        copy4(L.sw_tile[n] + kt * 256, (uint32_t)(lane * 4), lds_addr(slot + S::SB + (wn * NT + n) * 256));
   }
 }
 
@@ -173,16 +185,18 @@ struct WideRegs {
 
 // Read stage operands (slice j of its super-tile) from a slot: B fragments
 // and scales first, then the MT A fragments in MFMA order.
-template <int FMT, int MT, int NT, bool BLOCK>
+template <int FMT, int MT, int NT, bool BLOCK, int WM>
 __device__ __forceinline__ void wide_read(const uint8_t* slot, const uint8_t* sa_entry, int j, int wv, int lane,
-                                          int q, int r, WideRegs<MT, NT, BLOCK>& x) {
-  using S = WideSlot<MT, NT, BLOCK>;
+                                          int q, int r, WideRegs<MT / WM, NT, BLOCK>& x) {
+  using S = WideSlot<MT, NT, BLOCK, WM>;
+  constexpr int MTW = MT / WM;
+  const int wn = wv & 3, i0 = (wv >> 2) * MTW;
   // FP6: the slice's 24 bytes start at byte 0 (even j) or 8 (odd j) of the first chunk
   const int odd = j & 1;
   const int o0 = 8 * odd, o1 = odd ? 1024 : 8, o2 = odd ? 1032 : 1024;
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
-    const uint8_t* base = slot + S::B + (wv * NT + n) * 2048 + lane * 16;
+    const uint8_t* base = slot + S::B + (wn * NT + n) * 2048 + lane * 16;
     if (FMT == kE4M3) {
       const uint4 lo = *reinterpret_cast<const uint4*>(base);
       const uint4 hi = *reinterpret_cast<const uint4*>(base + 1024);
@@ -193,18 +207,19 @@ __device__ __forceinline__ void wide_read(const uint8_t* slot, const uint8_t* sa
       const uint2 d2 = *reinterpret_cast<const uint2*>(base + o2);
       x.b[n] = v8i{(int)d0.x, (int)d0.y, (int)d1.x, (int)d1.y, (int)d2.x, (int)d2.y, 0, 0};
     }
-    if (!BLOCK) x.sb[n] = slot[S::SB + (wv * NT + n) * 256 + lane * 4 + j];  // byte j: slice j
+    if (!BLOCK) x.sb[n] = slot[S::SB + (wn * NT + n) * 256 + lane * 4 + j];  // byte j: slice j
   }
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    const uint8_t* row = slot + S::A + i * 2048 + (r >> 3) * 1024 + (r & 7) * 128;
+  for (int i = 0; i < MTW; ++i) {
+    const int gi = i0 + i;  // the wave's i-th m-tile within the workgroup tile
+    const uint8_t* row = slot + S::A + gi * 2048 + (r >> 3) * 1024 + (r & 7) * 128;
     const int sw = a_swz(r);
     const uint4 lo = *reinterpret_cast<const uint4*>(row + 16 * (q ^ sw));        // K 16 q ..
     const uint4 hi = *reinterpret_cast<const uint4*>(row + 16 * ((q + 4) ^ sw));  // K 64 + 16 q ..
     x.a[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    if (S::SA_RING) x.sa[i] = sa_entry[(16 * i + r) * 16 + 4 * j + q];
-    else if (!BLOCK) x.sa[i] = slot[S::SA + (16 * i + r) * 4 + q];
-    else x.s4[i] = *reinterpret_cast<const float4*>(slot + S::SA + (16 * i + 4 * q) * 4);
+    if (S::SA_RING) x.sa[i] = sa_entry[(16 * gi + r) * 16 + 4 * j + q];
+    else if (!BLOCK) x.sa[i] = slot[S::SA + (16 * gi + r) * 4 + q];
+    else x.s4[i] = *reinterpret_cast<const float4*>(slot + S::SA + (16 * gi + 4 * q) * 4);
   }
 }
 
@@ -298,26 +313,28 @@ struct WideGrid {
 // One output tile: rows [row_base, hi) of m-block rows (hi bounds the valid rows
 // of a grouped expert), n-block nb, K split `split`; w / sw are the expert's
 // weights.  The ring and the scale ring are the workgroup's LDS.
-template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED>
+template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED, int WM>
 __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g, int64_t mb, int64_t row_base,
                                           int64_t hi, const uint8_t* w, const uint8_t* sw, int64_t nb, int64_t split,
                                           float* pdst, int64_t pld, uint8_t* ring, uint8_t* sa_ring, float* sb_stage,
                                           int t, int lane, int wv, int r, int q) {
-  using S = WideSlot<MT, NT, BLOCK>;
+  using S = WideSlot<MT, NT, BLOCK, WM>;
   constexpr int C = S::COPIES;
-  constexpr int AW = MT / 4, BM = 16 * MT;
+  constexpr int BM = 16 * MT, MTW = MT / WM;
+  const int wn = wv & 3, wm = wv >> 2;
   auto a_row = [&](int64_t row) -> int64_t {
     if (row >= hi) row = hi - 1;  // padding rows copy a valid row; their outputs are not stored
     return (GROUPED && p.row_index) ? (int64_t)(p.row_index[row] / p.row_div) : row;
   };
   const int64_t ntiles_total = (p.N + 15) / 16;
-  const int64_t nt_wave = (nb * 4 + wv) * NT;
+  const int64_t nt_wave = (nb * 4 + wn) * NT;
   constexpr int CH = FmtTraits<FMT>::CH;
-  WideLanes<MT, NT> L;
+  WideLanes<MT, NT, WM> L;
 #pragma unroll
-  for (int u = 0; u < 2 * AW; ++u) {
-    const int cr = 8 * (u & 1) + (lane >> 3);  // the m-tile row this lane copies
-    L.a_off[u] = (uint32_t)(a_row(row_base + (AW * wv + (u >> 1)) * 16 + cr) * p.lda + 16 * ((lane & 7) ^ a_swz(cr)));
+  for (int u = 0; u < S::ACH; ++u) {
+    const int c = S::ACH * wv + u;               // the A chunk: m-tile c / 2, rows 8 (c % 2) .. + 7
+    const int cr = 8 * (c & 1) + (lane >> 3);  // the m-tile row this lane copies
+    L.a_off[u] = (uint32_t)(a_row(row_base + (c >> 1) * 16 + cr) * p.lda + 16 * ((lane & 7) ^ a_swz(cr)));
   }
   // the scale waves' threads t < BM copy row t
   L.sa_off = (uint32_t)(BLOCK ? 4 * a_row(row_base + (t & (BM - 1))) : sa_row_offset(p, a_row(row_base + (t & (BM - 1)))));
@@ -350,9 +367,9 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     for (int64_t i = lane; i < te - tb; i += 64) sb_stage[i] = sbp[tb + i];
   }
 
-  v4f acc[MT][NT];
+  v4f acc[MTW][NT];
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+  for (int i = 0; i < MTW; ++i)
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
 
@@ -371,11 +388,11 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     }
 #pragma unroll
     for (int k = 0; k < R; ++k)
-      if (tb + k < te) wide_copy<FMT, MT, NT, BLOCK>(p, ring + k * S::BYTES, tb + k, wv, lane, L, sa_ring);
+      if (tb + k < te) wide_copy<FMT, MT, NT, BLOCK, WM>(p, ring + k * S::BYTES, tb + k, wv, lane, L, sa_ring);
     wide_wait<C, R - 1>((int)(te - 1 - tb < R - 1 ? te - 1 - tb : R - 1), wv < S::SW);
     wide_barrier();
-    WideRegs<MT, NT, BLOCK> x0, x1;
-    wide_read<FMT, MT, NT, BLOCK>(ring, sa_ring + ((tb >> 2) % 3) * S::RING_ENTRY, (int)(tb & 3), wv, lane, q, r,
+    WideRegs<MTW, NT, BLOCK> x0, x1;
+    wide_read<FMT, MT, NT, BLOCK, WM>(ring, sa_ring + ((tb >> 2) % 3) * S::RING_ENTRY, (int)(tb & 3), wv, lane, q, r,
                                   x0);
     if (BLOCK) x0.sbv = sb_stage[0];
 
@@ -395,14 +412,14 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
         wide_wait<C, R - 2>((int)later, wv < S::SW);                                                  \
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                          \
         wide_barrier();                                                                             \
-        if (tt + R < te) wide_copy<FMT, MT, NT, BLOCK>(p, ring + ((I_) % R) * S::BYTES, tt + R, wv, lane, L, sa_ring); \
+        if (tt + R < te) wide_copy<FMT, MT, NT, BLOCK, WM>(p, ring + ((I_) % R) * S::BYTES, tt + R, wv, lane, L, sa_ring); \
       }                                                                                             \
-      wide_read<FMT, MT, NT, BLOCK>(ring + ((I_ + 1) % R) * S::BYTES,                               \
+      wide_read<FMT, MT, NT, BLOCK, WM>(ring + ((I_ + 1) % R) * S::BYTES,                           \
                                     sa_ring + (((tt + 1) >> 2) % 3) * S::RING_ENTRY,            \
                                 (int)((tt + 1) & 3), wv, lane, q, r, NXT_);                         \
       if (BLOCK) NXT_.sbv = sb_stage[(tt + 1 < te ? tt + 1 : tt) - tb];                             \
-      wide_mfma<FMT, MT, NT, BLOCK>(CUR_, acc);                                                     \
-      wide_interleave<FMT, MT, NT, BLOCK>();                                                        \
+      wide_mfma<FMT, MTW, NT, BLOCK>(CUR_, acc);                                                    \
+      wide_interleave<FMT, MTW, NT, BLOCK>();                                                       \
     }                                                                                               \
   }
 
@@ -439,14 +456,15 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MTW; ++i)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) tile[(16 * i + 4 * q + e) * ST + 16 * (wv * NT + n) + r] = acc[i][n][e];
+      for (int e = 0; e < 4; ++e)
+        tile[(16 * (wm * MTW + i) + 4 * q + e) * ST + 16 * (wn * NT + n) + r] = acc[i][n][e];
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const int64_t col0 = nb * TW;
   if (p.S > 1) {  // fp32 partials, 4 columns per piece, row rr of the tile at pdst + rr * pld
     const bool vec = pld % 4 == 0 && (reinterpret_cast<uintptr_t>(pdst) & 15) == 0;
-    for (int c = t; c < BM * (TW / 4); c += 256) {
+    for (int c = t; c < BM * (TW / 4); c += 64 * S::WAVES) {
       const int rr = c / (TW / 4), cc = (c % (TW / 4)) * 4;
       const int64_t row = row_base + rr, col = col0 + cc;
       if (row >= hi || col >= p.N) continue;
@@ -461,7 +479,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     }
   } else {  // bf16 out (bias added in bf16), 8 columns per piece
     const bool vec = p.ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
-    for (int c = t; c < BM * (TW / 8); c += 256) {
+    for (int c = t; c < BM * (TW / 8); c += 64 * S::WAVES) {
       const int rr = c / (TW / 8), cc = (c % (TW / 8)) * 8;
       const int64_t row = row_base + rr, col = col0 + cc;
       if (row >= hi || col >= p.N) continue;
@@ -493,9 +511,10 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
 // Largest number of experts the grouped variant keeps in LDS.
 constexpr int kWideMaxExperts = (int)kWideGroupedMaxExperts;
 
-template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED>
-__global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g) {
-  using S = WideSlot<MT, NT, BLOCK>;
+template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED, int WM = 1>
+__global__ __launch_bounds__(256 * WM) void gemm_wide_kernel(GemmParams p, WideGrid g) {
+  static_assert(WM == 1 || !GROUPED, "the grouped variant runs four waves");
+  using S = WideSlot<MT, NT, BLOCK, WM>;
   constexpr int BM = 16 * MT;
   // the stage ring (the LDS budget of one workgroup per CU); after the last
   // stage it holds the output tile of the epilogue
@@ -521,7 +540,7 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
                         : g.compact ? p.partial + (split * g.tiles + local) * BM * TW
                                     : p.partial + (split * p.M + mb * BM) * p.N + nb * TW;
     const int64_t pld = g.compact ? TW : p.N;
-    wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, mb * BM, p.M, p.w, static_cast<const uint8_t*>(p.sw), nb,
+    wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g, mb, mb * BM, p.M, p.w, static_cast<const uint8_t*>(p.sw), nb,
                                            split, pdst, pld, ring, sa_ring, sb_lds + (BLOCK ? wv * kWideBlockStages : 0),
                                            t, lane, wv, r, q);
     return;
@@ -584,10 +603,10 @@ __global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, WideGrid g
     // a 128-row block with at most 64 routed rows (an expert's last block) runs the
     // 64-row tile path in the same ring: half the activation copies and MFMAs
     if (MT == 8 && __builtin_amdgcn_readfirstlane((int)(rhi - rb)) <= 64)
-      wide_tile<FMT, (MT == 8 ? 4 : MT), NT, BLOCK, GROUPED>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring,
+      wide_tile<FMT, (MT == 8 ? 4 : MT), NT, BLOCK, GROUPED, 1>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring,
                                                              sa_ring, sb_lds, t, lane, wv, r, q);
     else
-      wide_tile<FMT, MT, NT, BLOCK, GROUPED>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring, sa_ring, sb_lds,
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED, 1>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring, sa_ring, sb_lds,
                                              t, lane, wv, r, q);
     __syncthreads();  // the epilogue's LDS reads are done before the next tile's copies
   }
@@ -673,6 +692,7 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptio
     const int64_t per = (KT + o.splits - 1) / o.splits;
     WideConfig c{o.tile_n, (int)((KT + per - 1) / per), per};
     c.MT = mt;
+    c.WM = o.waves == 8 && mt == 8 ? 2 : 1;
     if (o.hybrid && o.splits == 1)
       wide_hybrid(((M + 16 * mt - 1) / (16 * mt)) * ((N + 64 * o.tile_n - 1) / (64 * o.tile_n)), KT, cu_count(), c);
     return c;
@@ -728,6 +748,7 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptio
       }
     }
   }
+  if (o.waves == 8 && best.MT == 8) best.WM = 2;
   return best;
 }
 
@@ -746,6 +767,18 @@ template <int FMT, int MT, bool BLOCK, bool GROUPED>
 static hipError_t launch_wide_mt(const WideConfig& c, const GemmParams& p, const WideGrid& g, int64_t grid,
                                  hipStream_t s) {
   const dim3 gr((unsigned)grid), blk(256);
+  if (c.WM == 2) {  // eight waves: MX dense 128-row tiles
+    if constexpr (BLOCK || GROUPED || MT != 8) {
+      return hipErrorInvalidValue;
+    } else {
+      const dim3 blk8(512);
+      if (c.NT == 4) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 4, false, false, 2>), gr, blk8, 0, s, p, g);
+      else if (c.NT == 2) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 2, false, false, 2>), gr, blk8, 0, s, p, g);
+      else if (c.NT == 1) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 1, false, false, 2>), gr, blk8, 0, s, p, g);
+      else return hipErrorInvalidValue;
+      return hipGetLastError();
+    }
+  }
   if (c.NT == 4) {
     if constexpr (GROUPED) return hipErrorInvalidValue;  // the grouped variant runs NT <= 2 (LDS)
     else hipLaunchKernelGGL((gemm_wide_kernel<FMT, MT, 4, BLOCK, GROUPED>), gr, blk, 0, s, p, g);

@@ -120,14 +120,16 @@ KERNEL_AUTO, KERNEL_STREAM, KERNEL_WIDE, KERNEL_GENERIC, KERNEL_STREAM_WIDE = -1
 
 
 @contextlib.contextmanager
-def tuning(kernel: int = KERNEL_AUTO, splits: int = 0, tile_n: int = 0, tile_m: int = 0, hybrid: bool = False):
+def tuning(kernel: int = KERNEL_AUTO, splits: int = 0, tile_n: int = 0, tile_m: int = 0, hybrid: bool = False,
+           waves: int = 0):
     """Force the GEMM kernel / wide tile / K split of every GEMM call inside the block
     (``mxl_gemm_options``; the reference's tactic and splits overrides,
     src/vllm_mach/mxfp8/native_backend.py:29).  Grouped GEMMs read ``kernel`` (their
-    schedule) and ``tile_m``.  For tuning runs and tests."""
+    schedule) and ``tile_m``; ``waves`` (4 or 8) picks the wide MX kernel's workgroup size.
+    For tuning runs and tests."""
     global _tuning
     old = _tuning
-    _tuning = _lib.GemmOptions(0, kernel, splits, tile_n, tile_m, int(hybrid))
+    _tuning = _lib.GemmOptions(0, kernel, splits, tile_n, tile_m, int(hybrid), waves)
     try:
         yield _tuning
     finally:
