@@ -47,6 +47,14 @@ __host__ __device__ inline int64_t sa_row_offset(const GemmParams& p, int64_t ro
   return (row >> 7) * T * 512 + (row & 31) * 16 + ((row & 127) >> 5) * 4;
 }
 
+// Byte offset, from a row's slice-0 scale dword, of the dword of the K128 slice holding
+// K index ks (clamped to the last slice).  32-bit arithmetic: the slice count and the
+// stride (4 or 512) keep the product far below 2^32, and the narrower math keeps the
+// decode kernels inside their register budgets.
+__host__ __device__ inline uint32_t scale_slice_offset(const GemmParams& p, int64_t ks) {
+  return (uint32_t)((ks < p.K ? ks : p.K - 128) >> 7) * (uint32_t)p.sa_ss;
+}
+
 inline void set_sa_layout(GemmParams& p, int swizzled) {
   p.sa_swz = swizzled ? 1 : 0;
   p.sa_ss = swizzled ? 512 : 4;
@@ -93,7 +101,7 @@ __device__ __forceinline__ void load_a(const GemmParams& p, const int64_t (&arow
     uint32_t sd = 0;
     if (!BLOCK) {  // scale dword of slice cp (clamped inside K; slices past K are zeroed below)
       const int64_t ks = kt * kTileK + 128 * cp;
-      sd = *reinterpret_cast<const uint32_t*>(sbase + ((ks < p.K ? ks : p.K - 128) / 128) * p.sa_ss);
+      sd = *reinterpret_cast<const uint32_t*>(sbase + scale_slice_offset(p, ks));
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

@@ -285,7 +285,9 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
     const int cr = lane >> 2, cp = lane & 3;
     const int64_t row = cr < p.M ? cr : p.M - 1;
     // (block-FP8 has no E8M0 scales: any valid address, the dword is unused)
-    const uint8_t* srow = BLOCK ? p.a : static_cast<const uint8_t*>(p.sa) + sa_row_offset(p, row);
+    // rows < 16: in the swizzled layout row r's dword of slice 0 sits at 16 r (one 128-row tile)
+    const int64_t srs = p.sa_swz ? 16 : p.K / 32;
+    const uint8_t* srow = BLOCK ? p.a : static_cast<const uint8_t*>(p.sa) + row * srs;
     const uint8_t* arow = p.a + row * p.lda;
     const int from = 4 * (4 * r + q);  // byte address of the source lane (4 r + q)
 #pragma unroll
@@ -301,7 +303,7 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
       // scale dword of slice cp (E8M0 of blocks 4 cp .. 4 cp + 3 of the super-tile)
       const int64_t ks = kt[u] * kTileK + 128 * cp;
       const uint32_t sd =
-          BLOCK ? 0u : *reinterpret_cast<const uint32_t*>(srow + ((ks < p.K ? ks : p.K - 128) / 128) * p.sa_ss);
+          BLOCK ? 0u : *reinterpret_cast<const uint32_t*>(srow + scale_slice_offset(p, ks));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t x[8] = {lo[j].x, lo[j].y, lo[j].z, lo[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
@@ -398,59 +400,97 @@ constexpr int stream_grouped_waves() { return MT > 1 ? 4 : (FMT == kE4M3 ? 8 : 1
 //           (row stride lda), rule `rule`;
 //   prod 2: SwiGLU of the unit's bf16 gate/up rows (gate columns [0, K), up [K, 2K),
 //           row stride lda) then MXFP8, rule `rule`.
-template <int ROWS>
-__device__ __forceinline__ void grouped_produce(const GemmParams& p, int prod, int rule, int64_t lo, int64_t hi,
-                                                uint8_t* stage, int t, int nthreads) {
+// One producer item is the 8 values lane c % 4 of 32-block (c / 4) % (K / 32) of unit row
+// (c / 4) / (K / 32) owns.  Its loads are split from its arithmetic so that the kernel can
+// issue the first item's loads ahead of the unit's first weight loads: vector loads
+// complete in issue order, so the arithmetic then waits for these loads only, not for the
+// weights behind them.
+struct ProduceIn {
+  uint4 x, y;  // prod 1: the 8 bf16 values (x); prod 2: gate (x) and up (y)
+};
+
+__device__ __forceinline__ void produce_load(const GemmParams& p, int prod, int64_t lo, int64_t hi, int c,
+                                             ProduceIn& in) {
+  const int bpr = (int)(p.K / 32);
+  const int sub = c & 3, blk = (c >> 2) % bpr, rloc = (c >> 2) / bpr;
+  int64_t row = lo + rloc;
+  if (row >= hi) row = hi - 1;
+  const uint16_t* src = reinterpret_cast<const uint16_t*>(p.a);
+  if (prod == 1) {
+    const int64_t arow = p.row_index ? (int64_t)(p.row_index[row] / p.row_div) : row;
+    in.x = *reinterpret_cast<const uint4*>(src + arow * p.lda + blk * 32 + sub * 8);
+  } else {
+    const uint16_t* gp = src + row * p.lda + blk * 32 + sub * 8;
+    in.x = *reinterpret_cast<const uint4*>(gp);
+    in.y = *reinterpret_cast<const uint4*>(gp + p.K);
+  }
+}
+
+template <int ROWS, int PRODUCER, int RULE>
+__device__ __forceinline__ void produce_store(const GemmParams& p, int c, bool live, const ProduceIn& in,
+                                              uint8_t* stage) {
   const int64_t K = p.K;
   const int bpr = (int)(K / 32);
-  // only the unit's rows: the gather reads its padding rows from the last one
-  const int items = (int)(hi - lo) * bpr * 4;
-  uint8_t* codes = stage;
-  uint8_t* scales = stage + ROWS * K;
-  const uint16_t* src = reinterpret_cast<const uint16_t*>(p.a);
-  // items and nthreads are multiples of four: the four lanes of a block are live together
-  for (int base = 0; base < items; base += nthreads) {
+  const int sub = c & 3, blk = (c >> 2) % bpr, rloc = (c >> 2) / bpr;
+  float v[8];
+  uint32_t packed[2], sc;
+  if constexpr (PRODUCER == 1) {
+    bf16x8_to_f32(in.x, v);
+    quiet8(v);
+    sc = quant8x4<RULE>(v, packed);
+  } else {
+    float g[8], u[8];
+    bf16x8_to_f32(in.x, g);
+    bf16x8_to_f32(in.y, u);
+    // two halves, so that the scheduler does not interleave all eight exp sequences: the
+    // sixteen-wave kernel has 128 registers, and a spill reload here would wait (vmcnt)
+    // for the unit's first weights as well
+    swiglu8<RULE, 4>(g, u, v);
+    __builtin_amdgcn_sched_barrier(0);
+    swiglu8<RULE, 4>(g + 4, u + 4, v + 4);
+    sc = quant8x4<RULE, true>(v, packed);
+  }
+  if (live) {
+    *reinterpret_cast<uint2*>(stage + rloc * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
+    if (sub == 0) stage[ROWS * K + rloc * bpr + blk] = (uint8_t)sc;
+  }
+}
+
+// Activation producers fused into the grouped kernel (prod != 0): the workgroup
+// computes its unit's MXFP8 operands -- codes [ROWS][K] then E8M0 [ROWS][K/32], rows
+// past the unit repeating its last row -- into LDS with the standalone producers'
+// arithmetic and lane mapping (four lanes per 32-element block), so the codes are
+// those quant_mxfp8_kernel / swiglu_mxfp8_kernel would write:
+//   producer 1: MXFP8 quantization of the gathered bf16 rows A[row_index[r] / row_div]
+//               (row stride lda), scale rule RULE;
+//   producer 2: SwiGLU of the unit's bf16 gate/up rows (gate columns [0, K), up [K, 2K),
+//               row stride lda) then MXFP8, rule RULE.
+// (Each producer and rule is its own instantiation: one kernel holding all three rules'
+// code needed more than the 128 registers of its sixteen waves.)
+// Only the unit's rows are produced (the gather reads its padding rows from the last
+// one): items = rows x K/32 x 4.  Items and thread counts are multiples of four, so the
+// four lanes of a block are live together; threads past the end redo the last block
+// without storing.  With EARLY, `first` holds item t's loads, issued by the caller.
+template <int ROWS, int PRODUCER, int RULE, bool EARLY>
+__device__ __forceinline__ void grouped_produce(const GemmParams& p, int64_t lo, int64_t hi, uint8_t* stage, int t,
+                                                int nthreads, ProduceIn first) {
+  const int items = (int)(hi - lo) * (int)(p.K / 32) * 4;
+  if constexpr (!EARLY) produce_load(p, PRODUCER, lo, hi, t < items ? t : items - 4 + (t & 3), first);
+  produce_store<ROWS, PRODUCER, RULE>(p, t < items ? t : items - 4 + (t & 3), t < items, first, stage);
+  for (int base = nthreads; base < items; base += nthreads) {
     const int c = base + t < items ? base + t : items - 4 + (t & 3);
-    const int sub = c & 3, blk = (c >> 2) % bpr, rloc = (c >> 2) / bpr;
-    int64_t row = lo + rloc;
-    if (row >= hi) row = hi - 1;
-    float v[8];
-    uint32_t packed[2], sc;
-    if (prod == 1) {
-      const int64_t arow = p.row_index ? (int64_t)(p.row_index[row] / p.row_div) : row;
-      bf16x8_to_f32(*reinterpret_cast<const uint4*>(src + arow * p.lda + blk * 32 + sub * 8), v);
-      quiet8(v);
-      sc = rule == kFloorCarry175 ? quant8x4<kFloorCarry175>(v, packed)
-           : rule == kCeilDiv448  ? quant8x4<kCeilDiv448>(v, packed)
-                                  : quant8x4<kRpUe8m0>(v, packed);
-    } else {
-      const uint16_t* gp = src + row * p.lda + blk * 32 + sub * 8;
-      float g[8], u[8];
-      bf16x8_to_f32(*reinterpret_cast<const uint4*>(gp), g);
-      bf16x8_to_f32(*reinterpret_cast<const uint4*>(gp + K), u);
-      if (rule == kFloorCarry175) {
-        swiglu8<kFloorCarry175>(g, u, v);
-        sc = quant8x4<kFloorCarry175, true>(v, packed);
-      } else if (rule == kCeilDiv448) {
-        swiglu8<kCeilDiv448>(g, u, v);
-        sc = quant8x4<kCeilDiv448, true>(v, packed);
-      } else {
-        swiglu8<kRpUe8m0>(g, u, v);
-        sc = quant8x4<kRpUe8m0, true>(v, packed);
-      }
-    }
-    if (base + t < items) {
-      *reinterpret_cast<uint2*>(codes + rloc * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
-      if (sub == 0) scales[rloc * bpr + blk] = (uint8_t)sc;
-    }
+    ProduceIn in;
+    produce_load(p, PRODUCER, lo, hi, c, in);
+    produce_store<ROWS, PRODUCER, RULE>(p, c, base + t < items, in, stage);
   }
 }
 
 template <int FMT, int MT, int PROD>
 __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_stream_grouped_kernel(GemmParams p, int E,
-                                                                                                int WK, int NW,
-                                                                                                int rule) {
-  constexpr int prod = PROD;
+                                                                                                int WK, int NW) {
+  // PROD = 4 producer + rule: producer 0 (none), 1 (quantization) or 2 (SwiGLU), rule the
+  // MXFP8 scale rule of the produced operands
+  constexpr int prod = PROD >> 2, RULE = PROD & 3;
   constexpr int WAVES = stream_grouped_waves<FMT, MT>();
   // prod != 0: the unit's produced operands (grouped_produce), sized at launch
   extern __shared__ __attribute__((aligned(16))) uint8_t stage_act[];
@@ -516,11 +556,20 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
       const int64_t nt = nl + round * NW;
       return nt < ntiles ? nt : ntiles - 1;
     };
+    // the SwiGLU producer's first loads go out ahead of the weights (see ProduceIn); the
+    // quantizing producer's rows are gathered through row_index, a dependent load, so its
+    // loads follow the weights
+    ProduceIn first{};
+    if constexpr (prod == 2) {
+      const int items = (int)(hi - lo) * (int)(p.K / 32) * 4;
+      produce_load(p, prod, lo, hi, t < items ? t : items - 4 + (t & 3), first);
+      __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
+    }
     stream_load_b<FMT, 1, false>(p, w, sw, nt_of(0), kt1, lane, b0);
     if constexpr (prod != 0) {
       // every wave has read the previous unit's operands (the s_barrier below the gather
       // orders that); produce this unit's into LDS, then hand them over
-      grouped_produce<ROWS>(p, prod, rule, lo, hi, stage_act, t, nthreads);
+      grouped_produce<ROWS, prod, RULE, prod == 2>(p, lo, hi, stage_act, t, nthreads, first);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
     v8i a[MT][1][4];
@@ -546,7 +595,7 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
       }
       const int64_t ks = kt1[0] * kTileK + 128 * cp;
       const uint32_t sd = *reinterpret_cast<const uint32_t*>(
-          srow + ((ks < p.K ? ks : p.K - 128) / 128) * (prod ? 4 : p.sa_ss));
+          srow + (prod ? (uint32_t)((ks < p.K ? ks : p.K - 128) >> 7) * 4u : scale_slice_offset(p, ks)));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t x[8] = {lo4[j].x, lo4[j].y, lo4[j].z, lo4[j].w, hi4[j].x, hi4[j].y, hi4[j].z, hi4[j].w};
@@ -770,12 +819,20 @@ hipError_t launch_grouped_mt(int fmt, const GemmParams& p, int64_t num_experts, 
   // the fused producers are instantiated for the 16-row units only (the schedule that uses them)
   if (prod && MT != 1) return hipErrorInvalidValue;
 #define MXL_GROUPED_LAUNCH(F_, P_) \
-  hipLaunchKernelGGL((gemm_stream_grouped_kernel<F_, MT, (MT == 1 ? P_ : 0)>), grid, blk, shmem, s, p, E, WK, NW, rule)
-#define MXL_GROUPED_PROD(F_)                    \
-  if (prod == 0) MXL_GROUPED_LAUNCH(F_, 0);     \
-  else if (prod == 1) MXL_GROUPED_LAUNCH(F_, 1); \
-  else if (prod == 2) MXL_GROUPED_LAUNCH(F_, 2); \
-  else return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_stream_grouped_kernel<F_, MT, (MT == 1 ? P_ : 0)>), grid, blk, shmem, s, p, E, WK, NW)
+  if (prod && (rule < kFloorCarry175 || rule > kRpUe8m0)) return hipErrorInvalidValue;
+  const int code = prod ? 4 * prod + rule : 0;
+#define MXL_GROUPED_PROD(F_)                       \
+  switch (code) {                                  \
+    case 0: MXL_GROUPED_LAUNCH(F_, 0); break;      \
+    case 4: MXL_GROUPED_LAUNCH(F_, 4); break;      \
+    case 5: MXL_GROUPED_LAUNCH(F_, 5); break;      \
+    case 6: MXL_GROUPED_LAUNCH(F_, 6); break;      \
+    case 8: MXL_GROUPED_LAUNCH(F_, 8); break;      \
+    case 9: MXL_GROUPED_LAUNCH(F_, 9); break;      \
+    case 10: MXL_GROUPED_LAUNCH(F_, 10); break;    \
+    default: return hipErrorInvalidValue;          \
+  }
   if (fmt == kE4M3) {
     MXL_GROUPED_PROD(kE4M3)
   } else if (fmt == kE2M3) {

@@ -131,7 +131,7 @@ __device__ __forceinline__ void wide_copy(const GemmParams& p, uint8_t* slot, in
                                           const WideLanes<MT, NT, WM>& L, uint8_t* sa_ring) {
   using S = WideSlot<MT, NT, BLOCK, WM>;
   constexpr int CH = FmtTraits<FMT>::CH;
-  const int wn = wv & 3, wm = wv >> 2;
+  const int wn = WM == 1 ? wv : wv & 3, wm = WM == 1 ? 0 : wv >> 2;
   const int64_t kt = t >> 2;
   const int j = (int)(t & 3);
 #pragma unroll
@@ -190,7 +190,7 @@ __device__ __forceinline__ void wide_read(const uint8_t* slot, const uint8_t* sa
                                           int q, int r, WideRegs<MT / WM, NT, BLOCK>& x) {
   using S = WideSlot<MT, NT, BLOCK, WM>;
   constexpr int MTW = MT / WM;
-  const int wn = wv & 3, i0 = (wv >> 2) * MTW;
+  const int wn = WM == 1 ? wv : wv & 3, i0 = WM == 1 ? 0 : (wv >> 2) * MTW;
   // FP6: the slice's 24 bytes start at byte 0 (even j) or 8 (odd j) of the first chunk
   const int odd = j & 1;
   const int o0 = 8 * odd, o1 = odd ? 1024 : 8, o2 = odd ? 1032 : 1024;
@@ -321,7 +321,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
   using S = WideSlot<MT, NT, BLOCK, WM>;
   constexpr int C = S::COPIES;
   constexpr int BM = 16 * MT, MTW = MT / WM;
-  const int wn = wv & 3, wm = wv >> 2;
+  const int wn = WM == 1 ? wv : wv & 3, wm = WM == 1 ? 0 : wv >> 2;
   auto a_row = [&](int64_t row) -> int64_t {
     if (row >= hi) row = hi - 1;  // padding rows copy a valid row; their outputs are not stored
     return (GROUPED && p.row_index) ? (int64_t)(p.row_index[row] / p.row_div) : row;

@@ -169,10 +169,10 @@ __device__ __forceinline__ float mx_exp(float x) {
 // (mxfp8_mlp.py:96-97), or for the rp_ue8m0 rule v = bf16((g / (1 + exp(-g))) * u)
 // (swiglu_quant.py:56-57).  A NaN act makes a NaN v, and quant8x4<RULE, true> codes every
 // NaN v as the canonical one, so the pair roundings leave NaN sign and payload as they come.
-template <int RULE>
+template <int RULE, int N = 8>
 __device__ __forceinline__ void swiglu8(const float* g, const float* u, float* v) {
 #pragma unroll
-  for (int i = 0; i < 8; i += 2) {
+  for (int i = 0; i < N; i += 2) {
     float a0 = g[i] / (1.0f + mx_exp(-g[i])), a1 = g[i + 1] / (1.0f + mx_exp(-g[i + 1]));
     if (RULE != kRpUe8m0) bf16_round2_nan_any(a0, a1);
     v[i] = a0 * u[i];
