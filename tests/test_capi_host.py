@@ -65,6 +65,15 @@ def test_invalid_arguments_fail_before_any_launch(pkg):
     # the scatter's per-wavefront histograms bound the expert count (160 KiB of LDS)
     with pytest.raises(_lib.MxlError, match="at most 2560 experts"):
         _lib.call("mxl_moe_route", 16, 4096, 8, 2561, 16, 16, 16, 16, 1 << 30, None)
+    # mxl_gemm_options fields outside their ranges are argument errors, not defaults
+    for bad in ({"tile_n": 3}, {"tile_m": 2}, {"waves": 6}, {"hybrid": 2}, {"kernel": 9}, {"sa_layout": 2}):
+        opts = _lib.GemmOptions(**bad)
+        with pytest.raises(_lib.MxlError, match="sa_layout|invalid options|unknown"):
+            _lib.call("mxl_mx_gemm_ex", 16, 16, 1, 16, 16, 16, 128, 0, None, 16, 16, None, 0,
+                      _lib.options_ptr(opts), None)
+    with pytest.raises(_lib.MxlError, match="invalid options"):
+        _lib.call("mxl_mx_gemm_dual_ex", 16, 16, 16, 16, 1, 16, 16, 16, 128, 0, None, 16, 16, 16, 1 << 20,
+                  _lib.options_ptr(_lib.GemmOptions(waves=5)), None)
 
 
 def test_missing_library_fails_loudly(tmp_path, monkeypatch, pkg):

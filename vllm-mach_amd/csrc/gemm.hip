@@ -446,6 +446,18 @@ static int pack_common(const void* codes, const void* scales, int scale_layout, 
   return MXL_OK;
 }
 
+// The option fields a call may set: anything else is an argument error, not a default.
+static bool options_valid(const GemmOptions& o, const char* who) {
+  const bool ok = (o.sa_layout == 0 || o.sa_layout == 1) && o.kernel >= kAuto && o.kernel <= kStreamWide &&
+                  o.splits >= 0 && o.splits <= 64 && (o.tile_n == 0 || o.tile_n == 1 || o.tile_n == 2 ||
+                  o.tile_n == 4) && (o.tile_m == 0 || o.tile_m == 4 || o.tile_m == 8) &&
+                  (o.hybrid == 0 || o.hybrid == 1) && (o.waves == 0 || o.waves == 4 || o.waves == 8);
+  if (!ok)
+    set_error("%s: invalid options {sa_layout %d, kernel %d, splits %d, tile_n %d, tile_m %d, hybrid %d, waves %d}",
+              who, o.sa_layout, o.kernel, o.splits, o.tile_n, o.tile_m, o.hybrid, o.waves);
+  return ok;
+}
+
 static GemmOptions options_of(const void* opts) {
   GemmOptions o;
   if (opts) {
@@ -494,6 +506,7 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
   MXL_CHECK_ARG(o.sa_layout == 0 || (o.sa_layout == 1 && !block), "%s: unknown activation scale layout %d", who,
                 o.sa_layout);
   MXL_CHECK_ARG(o.splits >= 0 && o.splits <= 64, "%s: splits must be 0 (automatic) .. 64", who);
+  if (!options_valid(o, who)) return MXL_EINVAL;
   if (M == 0) return MXL_OK;
   DensePlan d;
   if (!plan_dense(M, N, K, fmt, block, o, d)) {
@@ -684,6 +697,7 @@ static int gemm_dual_common(const void* hi, const void* s_hi, const void* res, c
                             const GemmOptions& o, void* stream) {
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm_dual: unknown weight format %d", w_fmt);
   MXL_CHECK_ARG(o.sa_layout == 0 || o.sa_layout == 1, "mxl_mx_gemm_dual: sa_layout must be 0 or 1");
+  if (!options_valid(o, "mxl_mx_gemm_dual")) return MXL_EINVAL;
   MXL_CHECK_ARG(M >= 0 && M <= 64 && N > 0 && K > 0 && K % 128 == 0,
                 "mxl_mx_gemm_dual: need M <= 64, N > 0, K %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
                 (long long)N, (long long)K);
@@ -854,6 +868,7 @@ static int grouped_common(const void* a, const void* sa, int64_t a_rows, const i
   // many-row units (where they apply), kGeneric the per-expert kernel, kWide the wide kernel.
   MXL_CHECK_ARG(o.kernel >= kAuto && o.kernel <= kStreamWide, "mxl_grouped_gemm: unknown kernel %d", o.kernel);
   MXL_CHECK_ARG(o.sa_layout == 0, "mxl_grouped_gemm: grouped activations take logical scales");
+  if (!options_valid(o, "mxl_grouped_gemm")) return MXL_EINVAL;
   const int force = o.kernel;
   int stream_mt = 0;
   if (force == kStream || force == kStreamWide) {
