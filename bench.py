@@ -225,11 +225,19 @@ class MxLinear(Workload):
                 for wt, st in self.copies]
         quant = [lambda: torch.ops.mach_amd.quantize_mxfp8(self.inputs[M], ops.FLOOR_CARRY175)] * 8
         tag = "mxfp8" if fmt == ops.E4M3 else "mxfp6"
-        return {
+        out = {
             f"{tag} gemm M={M} N={N} K={K}": (gemm, self.flops(M),
                                               mx_weight_bytes(N, K, fmt) + M * K * (1 + 1 / 32) + M * N * 2),
             f"quantize_mxfp8 M={M} K={K}": (quant, 0.0, M * K * 2 + M * K * (1 + 1 / 32)),
         }
+        if ops.quant_row_fusable(M, K, ops.FLOOR_CARRY175):
+            # the step's path for one row: the quantizer inside the weight-streaming GEMM
+            fused = [lambda wt=wt, st=st: torch.ops.mach_amd.quant_mx_gemm(self.inputs[M], wt, st, N, fmt,
+                                                                           ops.FLOOR_CARRY175, None)
+                     for wt, st in self.copies]
+            out[f"quantize->{tag} gemm, one launch, M={M} N={N} K={K}"] = (
+                fused, self.flops(M), mx_weight_bytes(N, K, fmt) + M * K * 2 + M * N * 2)
+        return out
 
 
 class BlockFp8Linear(Workload):

@@ -229,6 +229,16 @@ int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, cons
                        const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
                        void* stream);
 
+/* MXFP8 quantization -> MX GEMM for one bf16 activation row, in one launch: the weight-
+ * streaming GEMM computes the row's codes and scales from x bf16 [1, K] itself, with the
+ * activation quantizer's arithmetic (mxl_quantize_mxfp8, rule 0, 1 or 2), so y is
+ * bit-identical to mxl_quantize_mxfp8 followed by mxl_mx_gemm.  K % 128 == 0,
+ * K <= 12288; other shapes return MXL_EUNSUPPORTED (use the two calls).  Replaces
+ * mxfp8_sm120::gemm_from_float and mxfp6::gemm_from_float at M = 1
+ * (src/vllm_mach/mxfp6/dense_mxfp8.py:89-96, src/vllm_mach/mxfp6/dense.py:122-129). */
+int mxl_quant_mx_gemm(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled, const void* sw_tiled,
+                      int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc, void* stream);
+
 /* Block-FP8 GEMM: y[m, n] = sum_g sa[g*M + m] * sb[(n/128) * (K/128) + g] *
  * (A_g . W_g) with fp32 FMA per K128 block, bf16 out.  A E4M3 [M, K]; W tiled
  * E4M3 (fmt 0, no scales); sb fp32 [ceil(N/128), K/128].  Replaces

@@ -224,6 +224,70 @@ def test_swiglu_row_fused_is_bit_identical(pkg, oracle_mod, dev, fmt, rule, N, K
     _check(y.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("fmt", [0, 2, 3])
+@pytest.mark.parametrize("rule", [0, 1, 2])
+@pytest.mark.parametrize("N,K", [(160, 128), (200, 640), (2560, 9216), (96, 12288), (17408, 5120)])
+def test_quant_row_fused_is_bit_identical(pkg, oracle_mod, dev, fmt, rule, N, K):
+    """One bf16 row quantized inside the weight-streaming GEMM (one launch) equals the
+    quantizer followed by the GEMM bit for bit -- infinite, NaN and subnormal inputs and
+    outlier channels included -- and the oracle within the GEMM bar."""
+    ops = pkg.ops
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 500 + N + K)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    x = _act(1, K, 501 + K)
+    special = x.clone()
+    special[0, 3] = float("inf")
+    special[0, 40] = float("nan")
+    special[0, 70] = -float("inf")
+    special[0, 100] = 1e-40
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(7)).bfloat16().to(dev) if N == 200 else None
+    for row in (x, special):
+        xd = row.to(dev)
+        a, sa = torch.ops.mach_amd.quantize_mxfp8(xd, rule)
+        y_ref = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, bias)
+        y = torch.ops.mach_amd.quant_mx_gemm(xd, tiled, tiled_s, N, fmt, rule, bias)
+        assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    # mx_gemm_from_float takes the one-launch path for one row
+    before = dict(ops._COUNTS)
+    y = ops.mx_gemm_from_float(x.to(dev), tiled, tiled_s, N, fmt, rule)
+    assert ops._COUNTS.get("quant_mx_gemm", 0) == before.get("quant_mx_gemm", 0) + 1
+    if N >= 160:  # the Frobenius bar needs more than a few dozen outputs to be meaningful
+        rc, rs = oracle_mod.quant_mxfp8(x, rule)
+        ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(rc, rs, wc, ws, fmt)))
+        _check(y.float().cpu().numpy(), ref)
+
+
+def test_quant_row_fused_graph_replay_and_limits(pkg, oracle_mod, dev):
+    """The one-launch quantized row under graph capture (each replay with a new row equals
+    the eager call), and the shapes it refuses."""
+    ops = pkg.ops
+    N, K = 17408, 5120  # the W6A8 decode shape
+    wc, ws, stored = _weights(oracle_mod, N, K, 2, 0.02, 77)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), 2)
+    x = torch.randn(1, K, device=dev).bfloat16()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        ops.mx_gemm_from_float(x, tiled, tiled_s, N, 2)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y = ops.mx_gemm_from_float(x, tiled, tiled_s, N, 2)
+        gen = torch.Generator(device=dev).manual_seed(78)
+        for scale in (3.0, 0.25):
+            x.normal_(generator=gen).mul_(scale)
+            graph.replay()
+            stream.synchronize()
+            replayed = y.clone()
+            a, sa = torch.ops.mach_amd.quantize_mxfp8(x, 0)
+            eager = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, 2, None)
+            stream.synchronize()
+            assert torch.equal(replayed.view(torch.int16), eager.view(torch.int16))
+    torch.cuda.current_stream().wait_stream(stream)
+    assert not ops.quant_row_fusable(2, K, 0) and not ops.quant_row_fusable(1, 12416, 0)
+    with pytest.raises(ValueError):
+        torch.ops.mach_amd.quant_mx_gemm(torch.zeros(2, K, dtype=torch.bfloat16, device=dev), tiled, tiled_s, N, 2)
+
+
 @pytest.mark.parametrize("fmt", [0, 2])
 def test_swiglu_row_fused_graph_replay(pkg, oracle_mod, dev, fmt):
     """The one-launch SwiGLU down projection captured in a graph: each replay with a new

@@ -53,6 +53,7 @@ SIGNATURES = {
     "mxl_block_fp8_gemm_ex": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _P]),
     "mxl_grouped_gemm_ex": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P, _P]),
     "mxl_swiglu_mx_gemm": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P]),
+    "mxl_quant_mx_gemm": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P]),
     "mxl_block_fp8_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "mxl_grouped_gemm": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P]),
     "mxl_grouped_fused_supported": (_I, [_I64, _I64, _I64, _I]),

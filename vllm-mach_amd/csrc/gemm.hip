@@ -691,6 +691,31 @@ extern "C" int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int
   return MXL_OK;
 }
 
+extern "C" int mxl_quant_mx_gemm(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled,
+                                 const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
+                                 void* stream) {
+  MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_quant_mx_gemm: unknown weight format %d", w_fmt);
+  MXL_CHECK_ARG(N > 0 && ldc >= N, "mxl_quant_mx_gemm: need N > 0 and ldc >= N");
+  MXL_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
+                "mxl_quant_mx_gemm: x and w must be 16-byte aligned");
+  if (!stream_quant_row_eligible(M, K, rule)) {
+    set_error("mxl_quant_mx_gemm: unsupported (one row, K %% 128 == 0, K <= 12288, rule 0, 1 or 2; "
+              "M=%lld K=%lld rule=%d)", (long long)M, (long long)K, rule);
+    return MXL_EUNSUPPORTED;
+  }
+  GemmParams p{};
+  p.a = (const uint8_t*)x;
+  p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled; p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out;
+  p.lda = K; p.ldc = ldc; p.M = 1; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = 1;
+  p.row_div = 1; p.S = 1;
+  const hipError_t e = launch_gemm_stream_quant_row(w_fmt, rule, p, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    set_error("mxl_quant_mx_gemm: launch failed: %s", hipGetErrorString(e));
+    return MXL_EHIP;
+  }
+  return MXL_OK;
+}
+
 static int gemm_dual_common(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
                             const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
                             const void* bias, void* out, int64_t ldc, void* workspace, int64_t workspace_bytes,

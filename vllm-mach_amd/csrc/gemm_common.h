@@ -218,6 +218,10 @@ hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStrea
 // GEMM (p.a = gate_up, M = 1, SwiGLU rule 1 or 2)
 bool stream_swiglu_eligible(int64_t M, int64_t K, int rule);
 hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hipStream_t s);
+// One bf16 activation row (p.a, M = 1) quantized to MXFP8 inside the weight-streaming GEMM
+// (the activation quantizer's arithmetic, rule 0, 1 or 2)
+bool stream_quant_row_eligible(int64_t M, int64_t K, int rule);
+hipError_t launch_gemm_stream_quant_row(int fmt, int rule, const GemmParams& p, hipStream_t s);
 // Grouped (MoE) variant: persistent workgroups over (expert, up to 16 mt rows) units,
 // each streaming the expert's weights; mt = 1 (few rows per expert) or 8.
 bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt, int mt);

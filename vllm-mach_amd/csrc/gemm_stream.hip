@@ -184,13 +184,18 @@ __device__ __forceinline__ v4f stream_mfma_packed(const v8i (&a)[4], uint32_t sa
 
 }  // namespace
 
-// SWIGLU >= 0 (one activation row): p.a is the bf16 gate/up row [2K] and each wave
-// computes its own super-tiles' MXFP8 codes and scales from it with the producer's
-// arithmetic (swiglu8 + quant8x4 under rule SWIGLU) while its weights are in flight.
-template <int FMT, int RUN, bool DB, bool BLOCK, int SWIGLU = -1>
+// ROWP >= 0 (one activation row): each wave computes its own super-tiles' MXFP8 codes
+// and scales from the bf16 row p.a while its weights are in flight, with the standalone
+// producers' arithmetic:
+//   ROWP = rule (0..2): p.a is the gate/up row [2K], swiglu8 + quant8x4 under the rule;
+//   ROWP = 4 + rule:    p.a is the row [K], quiet8 + quant8x4 under the rule (the
+//                       activation quantizer's).
+template <int FMT, int RUN, bool DB, bool BLOCK, int ROWP = -1>
 __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_stream_kernel(GemmParams p) {
   static_assert(!BLOCK || FMT == kE4M3, "block-FP8 weights are E4M3");
-  static_assert(SWIGLU < 0 || !BLOCK, "the fused SwiGLU row feeds MX GEMMs");
+  static_assert(ROWP < 0 || !BLOCK, "the fused producer row feeds MX GEMMs");
+  constexpr bool ROW = ROWP >= 0, SWI = ROWP >= 0 && ROWP < 4;
+  constexpr int RRULE = ROWP & 3;
   __shared__ float red[2][kStreamMaxWaves][4][64];
   const int t = threadIdx.x, lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -215,18 +220,18 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
   // fragments and scales, kept in registers for every n-tile (rows >= M read row
   // M - 1 and are never stored; loads are clamped inside K so all are unconditional)
   const int64_t count = g < ntiles ? (ntiles - g + G - 1) / G : 0;  // n-tiles of this workgroup
-  // The fused SwiGLU row's bf16 gate/up pieces are requested before the weights: vector
-  // loads complete in issue order, so the SiLU arithmetic then waits for these loads only
-  // and runs while the weights stream in.
-  uint4 gu_raw[SWIGLU >= 0 ? RUN : 1][2];
-  if constexpr (SWIGLU >= 0) {
+  // The fused row's bf16 pieces (gate and up for SwiGLU) are requested before the weights:
+  // vector loads complete in issue order, so the producer arithmetic then waits for these
+  // loads only and runs while the weights stream in.
+  uint4 gu_raw[ROW ? RUN : 1][SWI ? 2 : 1];
+  if constexpr (ROW) {
     const uint16_t* gu = reinterpret_cast<const uint16_t*>(p.a);
 #pragma unroll
     for (int u = 0; u < RUN; ++u) {
       const int64_t k0 = kt[u] * kTileK + (lane >> 2) * 32 + (lane & 3) * 8;
       const int64_t kc = k0 < p.K ? k0 : p.K - 8;  // blocks past K: any valid data, zeroed below
       gu_raw[u][0] = *reinterpret_cast<const uint4*>(gu + kc);
-      gu_raw[u][1] = *reinterpret_cast<const uint4*>(gu + p.K + kc);
+      if constexpr (SWI) gu_raw[u][SWI ? 1 : 0] = *reinterpret_cast<const uint4*>(gu + p.K + kc);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
   }
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
                           sa[gi * p.M + rows[3]]};
       }
   }
-  if constexpr (SWIGLU >= 0) {
+  if constexpr (ROW) {
     // lanes 4 b .. 4 b + 3 own 32-block b of the super-tile (8 values each, the producer's
     // lane mapping).  Fragment lane 16 q + r of slice j holds K values 16 q .. 16 q + 15
     // (dwords 0-3) and 64 + 16 q .. 64 + 16 q + 15 (dwords 4-7) of the slice, the layout the
@@ -263,12 +268,19 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
     // scale dword of the unfused path has it.
 #pragma unroll
     for (int u = 0; u < RUN; ++u) {
-      float g[8], up[8], v[8];
-      bf16x8_to_f32(gu_raw[u][0], g);
-      bf16x8_to_f32(gu_raw[u][1], up);
-      swiglu8<SWIGLU>(g, up, v);
-      uint32_t pk[2];
-      const uint32_t sc = quant8x4<SWIGLU, true>(v, pk);
+      float v[8];
+      uint32_t pk[2], sc;
+      if constexpr (SWI) {
+        float g[8], up[8];
+        bf16x8_to_f32(gu_raw[u][0], g);
+        bf16x8_to_f32(gu_raw[u][SWI ? 1 : 0], up);
+        swiglu8<RRULE>(g, up, v);
+        sc = quant8x4<RRULE, true>(v, pk);
+      } else {
+        bf16x8_to_f32(gu_raw[u][0], v);
+        quiet8(v);
+        sc = quant8x4<RRULE>(v, pk);
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         int y[8];
@@ -766,21 +778,27 @@ hipError_t launch_stream_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
 }  // namespace
 
 namespace {
-template <int FMT, int RULE>
-hipError_t launch_swiglu_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
+// ROWP: the row producer of gemm_stream_kernel (rule of the SwiGLU row, or 4 + rule of
+// the quantized row)
+template <int FMT, int ROWP>
+hipError_t launch_row_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
   if (p.KT <= kStreamMaxWaves)
-    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, false, RULE>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, false, ROWP>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 2, false, false, RULE>), grid,
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 2, false, false, ROWP>), grid,
                        dim3((unsigned)((p.KT + 1) / 2 * 64)), 0, s, p);
   return hipGetLastError();
 }
-template <int RULE>
-hipError_t launch_swiglu_rule(int fmt, const GemmParams& p, dim3 grid, hipStream_t s) {
-  if (fmt == kE4M3) return launch_swiglu_fmt<kE4M3, RULE>(p, grid, s);
-  if (fmt == kE2M3) return launch_swiglu_fmt<kE2M3, RULE>(p, grid, s);
-  if (fmt == kE3M2) return launch_swiglu_fmt<kE3M2, RULE>(p, grid, s);
+template <int ROWP>
+hipError_t launch_row(int fmt, const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (fmt == kE4M3) return launch_row_fmt<kE4M3, ROWP>(p, grid, s);
+  if (fmt == kE2M3) return launch_row_fmt<kE2M3, ROWP>(p, grid, s);
+  if (fmt == kE3M2) return launch_row_fmt<kE3M2, ROWP>(p, grid, s);
   return hipErrorInvalidValue;
+}
+dim3 row_grid(const GemmParams& p) {
+  const int64_t ntiles = (p.N + 15) / 16;
+  return dim3((unsigned)(ntiles < cu_count() ? ntiles : cu_count()));
 }
 }  // namespace
 
@@ -789,10 +807,19 @@ bool stream_swiglu_eligible(int64_t M, int64_t K, int rule) {
 }
 
 hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hipStream_t s) {
-  const int64_t ntiles = (p.N + 15) / 16;
-  const dim3 grid((unsigned)(ntiles < cu_count() ? ntiles : cu_count()));
-  if (rule == kCeilDiv448) return launch_swiglu_rule<kCeilDiv448>(fmt, p, grid, s);
-  if (rule == kRpUe8m0) return launch_swiglu_rule<kRpUe8m0>(fmt, p, grid, s);
+  if (rule == kCeilDiv448) return launch_row<kCeilDiv448>(fmt, p, row_grid(p), s);
+  if (rule == kRpUe8m0) return launch_row<kRpUe8m0>(fmt, p, row_grid(p), s);
+  return hipErrorInvalidValue;
+}
+
+bool stream_quant_row_eligible(int64_t M, int64_t K, int rule) {
+  return M == 1 && stream_gemm_eligible(1, K, false) && rule >= kFloorCarry175 && rule <= kRpUe8m0;
+}
+
+hipError_t launch_gemm_stream_quant_row(int fmt, int rule, const GemmParams& p, hipStream_t s) {
+  if (rule == kFloorCarry175) return launch_row<4 + kFloorCarry175>(fmt, p, row_grid(p), s);
+  if (rule == kCeilDiv448) return launch_row<4 + kCeilDiv448>(fmt, p, row_grid(p), s);
+  if (rule == kRpUe8m0) return launch_row<4 + kRpUe8m0>(fmt, p, row_grid(p), s);
   return hipErrorInvalidValue;
 }
 

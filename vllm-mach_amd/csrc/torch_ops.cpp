@@ -207,6 +207,19 @@ std::tuple<at::Tensor, at::Tensor> quantize_logical(const at::Tensor& x, int rul
   return {codes, scales};
 }
 
+// One bf16 row quantized inside the weight-streaming GEMM (one launch, the same bits as
+// quantize + GEMM); nullopt for shapes that take the two calls.
+std::optional<at::Tensor> quant_row(const at::Tensor& x, const Tiled& t, int fmt, int64_t N, int64_t K,
+                                    hipStream_t s) {
+  if (x.size(0) != 1 || K % 128 != 0 || K > 12288 || x.scalar_type() != at::kBFloat16 || !x.is_cuda()) return {};
+  at::Tensor xc = x.contiguous();
+  at::Tensor out = at::empty({1, N}, xc.options().dtype(at::kBFloat16));
+  check(mxl_quant_mx_gemm(xc.data_ptr(), 1, K, kFloorCarry175, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N, fmt,
+                          nullptr, out.data_ptr(), N, s),
+        "mxl_quant_mx_gemm");
+  return out;
+}
+
 // ================================================== vllm_mach_block_fp8::mm
 
 // a E4M3 [M, K]; b = weight.T (E4M3 [K, N], stride (1, K)); sa fp32 [M, K/128],
@@ -313,6 +326,7 @@ at::Tensor mxfp8_gemm_from_float(const at::Tensor& x, const at::Tensor& w, const
   TORCH_CHECK(x.dim() == 2 && x.size(1) == K, "mxfp8_sm120::gemm_from_float: x must be [M, K]");
   hipStream_t s = stream_of(x);
   const Tiled& t = tiled_mx(w, ws, kE4M3, N, K, 1, s);
+  if (auto y = quant_row(x, t, kE4M3, N, K, s)) return *y;
   auto q = quantize_logical(x, kFloorCarry175, s);
   return mx_gemm(std::get<0>(q), std::get<1>(q), 0, t, kE4M3, N, K, options(0, -1, 0), at::Tensor(), at::Tensor(), s);
 }
@@ -403,6 +417,7 @@ at::Tensor mxfp6_gemm_from_float(const at::Tensor& x, const at::Tensor& w, const
   TORCH_CHECK(x.dim() == 2 && x.size(1) == K && K % 128 == 0, "mxfp6::gemm_from_float: x must be [M, K], K % 128 == 0");
   hipStream_t s = stream_of(x);
   const Tiled& t = tiled_mx(w, ws, kE3M2, N, K, 1, s);
+  if (auto y = quant_row(x, t, kE3M2, N, K, s)) return finish(*y, alpha, dtype);
   auto q = quantize_logical(x, kFloorCarry175, s);
   return finish(mx_gemm(std::get<0>(q), std::get<1>(q), 0, t, kE3M2, N, K, options(0, -1, 0), at::Tensor(),
                         at::Tensor(), s),

@@ -466,6 +466,37 @@ def swiglu_row_fusable(m: int, k: int, rule: int) -> bool:
     return m == 1 and k % 128 == 0 and 128 <= k <= 12288 and rule in (CEIL_DIV448, RP_UE8M0)
 
 
+def quant_row_fusable(m: int, k: int, rule: int) -> bool:
+    """Shapes ``mxl_quant_mx_gemm`` runs in one launch (one row, the weight-streaming GEMM's
+    K range, every MXFP8 scale rule)."""
+    return m == 1 and k % 128 == 0 and 128 <= k <= 12288 and rule in (FLOOR_CARRY175, CEIL_DIV448, RP_UE8M0)
+
+
+@torch.library.custom_op("mach_amd::quant_mx_gemm", mutates_args=())
+def quant_mx_gemm(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
+                  rule: int = FLOOR_CARRY175, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """MXFP8 quantization -> MX GEMM of one bf16 row in one launch, bit-identical to
+    ``quantize_mxfp8`` then ``mx_gemm`` (``mxfp8_sm120::gemm_from_float`` /
+    ``mxfp6::gemm_from_float`` at M = 1, src/vllm_mach/mxfp6/dense_mxfp8.py:89-96)."""
+    _check_cuda(x, w, sw, bias)
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise ValueError("quant_mx_gemm needs bf16 [1, K]")
+    x = x.contiguous()
+    M, K = x.shape
+    if not quant_row_fusable(M, K, rule):
+        raise ValueError(f"quant_mx_gemm runs one row with K % 128 == 0, K <= 12288 (M={M}, K={K}, rule={rule})")
+    out = torch.empty((1, n), dtype=torch.bfloat16, device=x.device)
+    call("mxl_quant_mx_gemm", ptr(x), 1, K, rule, ptr(w), ptr(sw), n, w_fmt, ptr(bias), ptr(out), n,
+         stream_handle(x.device))
+    _count("quant_mx_gemm")
+    return out
+
+
+@quant_mx_gemm.register_fake
+def _(x, w, sw, n, w_fmt, rule=FLOOR_CARRY175, bias=None):
+    return x.new_empty((x.shape[0], n), dtype=torch.bfloat16)
+
+
 @torch.library.custom_op("mach_amd::swiglu_mx_gemm", mutates_args=())
 def swiglu_mx_gemm(gate_up: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
                    rule: int = CEIL_DIV448, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -563,8 +594,11 @@ def mx_gemm_from_float(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: in
     """Quantize bf16 activations to MXFP8 and run the MX GEMM.
 
     Replaces ``mxfp8_sm120::gemm_from_float`` / ``mxfp6::gemm_from_float``
-    (src/vllm_mach/mxfp6/dense_mxfp8.py:96, src/vllm_mach/mxfp6/dense.py:122-129).
+    (src/vllm_mach/mxfp6/dense_mxfp8.py:96, src/vllm_mach/mxfp6/dense.py:122-129).  One
+    row runs as one launch (``quant_mx_gemm``, the same bits).
     """
+    if quant_row_fusable(x.shape[0], x.shape[1], rule):
+        return torch.ops.mach_amd.quant_mx_gemm(x, w, sw, n, w_fmt, rule, bias)
     a, sa = torch.ops.mach_amd.quantize_mxfp8(x, rule)
     return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, x.shape[1], w_fmt, bias)
 
