@@ -101,8 +101,13 @@ def _torch_dequant(codes_u8: torch.Tensor, scales_u8: torch.Tensor, fmt: int, or
 
 @pytest.mark.parametrize("name,M,N,K,fmt,std", [
     ("c1", 16, 2048, 2048, 0, 0.02),
+    ("c2", 1, 2560, 9216, 0, 0.02),
+    ("c2", 16, 2560, 9216, 0, 0.02),
+    ("c2", 128, 2560, 9216, 0, 0.02),
     ("c2", 512, 2560, 9216, 0, 0.02),
+    ("c4", 1, 17408, 5120, 2, 0.015),
     ("c4", 16, 17408, 5120, 2, 0.015),
+    ("c4", 128, 17408, 5120, 2, 0.015),
     ("c4", 256, 17408, 5120, 2, 0.015),
 ])
 def test_full_size_configs(pkg, oracle_mod, dev, name, M, N, K, fmt, std):
