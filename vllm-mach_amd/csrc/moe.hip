@@ -8,8 +8,8 @@
 // Three passes over 1024-route chunks: per-chunk histograms (LDS atomics,
 // order free), one workgroup scanning chunks and experts (the two in one
 // workgroup when the histograms fit in LDS), then a pass that
-// ranks each route inside its chunk (shuffle count inside the wavefront plus
-// an LDS prefix over the chunk's 16 wavefronts) and scatters.  A single chunk
+// ranks each route inside its chunk (a ballot match of the expert id's bits inside the
+// wavefront plus an LDS prefix over the chunk's 16 wavefronts) and scatters.  A single chunk
 // (decode-sized steps) runs all three in one workgroup.
 //
 // Combine: out[t, h] = bf16(sum_k y[inverse[t*topk + k], h] * w[t, k]),
@@ -19,6 +19,24 @@
 namespace mxl {
 
 constexpr int kChunk = 1024;
+
+// Routes of the same key in the earlier lanes of this wavefront (the rank of the lane's
+// route among its expert's routes in the wavefront); key = the expert id, or E for a
+// route whose expert is outside [0, E).  The lanes holding the same key are found one key
+// bit at a time with a ballot -- a bit's ballot, or its complement where the lane's bit
+// is 0, keeps the lanes that agree on it -- bit_width(E) ballots (9 for 256 experts)
+// instead of 64 lane-by-lane comparisons; only wavefront-uniform control flow, so every
+// lane takes part in every ballot.
+__device__ __forceinline__ int same_expert_rank(int key, int E, int lane) {
+  const int bits = 32 - __builtin_clz((unsigned)E);
+  uint64_t same = ~0ull;
+  for (int b = 0; b < bits; ++b) {
+    const bool bit = (key >> b) & 1;
+    const uint64_t on = __ballot(bit);
+    same &= bit ? on : ~on;
+  }
+  return __popcll(same & ((1ull << lane) - 1ull));
+}
 
 __global__ __launch_bounds__(kChunk) void route_hist_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
                                                            int32_t* __restrict__ chunk_counts) {
@@ -77,11 +95,7 @@ __global__ __launch_bounds__(kChunk) void route_scatter_kernel(const int32_t* __
   const int64_t r = c * kChunk + t;
   const int32_t e = r < R ? ids[r] : -1;
   const bool valid = e >= 0 && e < E;
-  int rank = 0;  // routes of the same expert in earlier lanes of this wavefront
-  for (int l = 0; l < 64; ++l) {
-    const int32_t el = __shfl(e, l);
-    rank += (l < lane && el == e) ? 1 : 0;
-  }
+  const int rank = same_expert_rank(valid ? e : E, E, lane);
   __syncthreads();
   if (valid) atomicAdd(&whist[w * E + e], 1);
   __syncthreads();
@@ -177,11 +191,7 @@ __global__ __launch_bounds__(kChunk) void route_single_kernel(const int32_t* __r
   for (int i = t; i < W * E; i += kChunk) whist[i] = 0;
   const int32_t e = t < R ? ids[t] : -1;
   const bool valid = e >= 0 && e < E;
-  int rank = 0;  // routes of the same expert in earlier lanes of this wavefront
-  for (int l = 0; l < 64; ++l) {
-    const int32_t el = __shfl(e, l);
-    rank += (l < lane && el == e) ? 1 : 0;
-  }
+  const int rank = same_expert_rank(valid ? e : E, E, lane);
   __syncthreads();
   if (valid) atomicAdd(&whist[w * E + e], 1);
   __syncthreads();
