@@ -297,14 +297,8 @@ __global__ __launch_bounds__(256) void splitk_reduce8_kernel(const float* __rest
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= M * n8) return;
   const int64_t m = id / n8, n = (id - m * n8) * 8;
-  const float* src = partial + m * N + n;
-  float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
-  for (int k = 1; k < S; ++k) {
-    const float* p = src + (int64_t)k * M * N;
-    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
-    lo.x += a.x; lo.y += a.y; lo.z += a.z; lo.w += a.w;
-    hi.x += b.x; hi.y += b.y; hi.z += b.z; hi.w += b.w;
-  }
+  float4 lo, hi;
+  sum_splits8(partial + m * N + n, M * N, S, lo, hi);
   const float f[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   uint32_t h[4];
 #pragma unroll

@@ -60,6 +60,33 @@ inline void set_sa_layout(GemmParams& p, int swizzled) {
   p.sa_ss = swizzled ? 512 : 4;
 }
 
+// Sum of S fp32 split partials of 8 consecutive columns (split k at src + k * stride,
+// 16-byte aligned), added in split order starting from split 0 itself.  The loads of
+// up to eight splits are issued before their adds, so a thread waits on memory once
+// per eight splits instead of once per split.
+__device__ __forceinline__ void sum_splits8(const float* src, int64_t stride, int S, float4& lo, float4& hi) {
+  lo = *reinterpret_cast<const float4*>(src);
+  hi = *reinterpret_cast<const float4*>(src + 4);
+  for (int k0 = 1; k0 < S; k0 += 8) {
+    float4 a[8], b[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (k0 + u < S) {
+        const float* p = src + (int64_t)(k0 + u) * stride;
+        a[u] = *reinterpret_cast<const float4*>(p);
+        b[u] = *reinterpret_cast<const float4*>(p + 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (k0 + u < S) {
+        lo.x += a[u].x; lo.y += a[u].y; lo.z += a[u].z; lo.w += a[u].w;
+        hi.x += b[u].x; hi.y += b[u].y; hi.z += b[u].z; hi.w += b[u].w;
+      }
+    }
+  }
+}
+
 // Per-call selection: the scale layout of A and the tuning overrides (the reference's
 // tactic / splits overrides, src/vllm_mach/mxfp8/native_backend.py:29).  Same layout
 // as mxl_gemm_options in include/mxlinear.h.

@@ -36,7 +36,10 @@
 // Grid: one workgroup per (m-block, n-block, K split), remapped so that the
 // m-blocks sharing a weight slice are consecutive on one XCD (workgroup L runs
 // on XCD L % 8) and hit its L2.  K splits (whole 512-wide super-tiles) write
-// fp32 partials that a second kernel sums in split order.  The grouped variant
+// fp32 partials that a second kernel sums in split order.  When the whole-K tiles
+// leave a partial last round (more tiles than CUs), the same launch runs the
+// leftover tiles split in K: workgroup L computes whole-K tile L and then unit L
+// of the split leftovers, so no CU waits for a second launch.  The grouped variant
 // walks experts' row ranges (expert_offsets) on device, so the launch needs no
 // host-side counts.
 #include "gemm_common.h"
@@ -308,14 +311,19 @@ struct WideGrid {
   int64_t num_experts;   // grouped only
   int64_t tile0, tiles;  // dense: this launch covers output tiles [tile0, tile0 + tiles) (tile = nb * mblocks + mb)
   int compact;           // dense, split: partials as [split][tile - tile0][16 MT][64 NT] instead of [split][M][N]
+  // dense, one-launch hybrid: after its whole-K tile (tiles [0, tiles), bf16 out) workgroup
+  // L also runs unit L < rem_tiles * S2 of the remainder: tile rem_tile0 + L % rem_tiles,
+  // K split L / rem_tiles of kt2 super-tiles, into compact partials
+  int64_t rem_tile0, rem_tiles, kt2;
+  int S2;
 };
 
 // One output tile: rows [row_base, hi) of m-block rows (hi bounds the valid rows
 // of a grouped expert), n-block nb, K split `split`; w / sw are the expert's
 // weights.  The ring and the scale ring are the workgroup's LDS.
 template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED, int WM>
-__device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g, int64_t mb, int64_t row_base,
-                                          int64_t hi, const uint8_t* w, const uint8_t* sw, int64_t nb, int64_t split,
+__device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int64_t row_base, int64_t hi,
+                                          const uint8_t* w, const uint8_t* sw, int64_t nb, int64_t split,
                                           float* pdst, int64_t pld, uint8_t* ring, uint8_t* sa_ring, float* sb_stage,
                                           int t, int lane, int wv, int r, int q) {
   using S = WideSlot<MT, NT, BLOCK, WM>;
@@ -354,8 +362,8 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
     L.sw_tile[n] = sw + nt * p.KT * 256;
   }
   const int64_t T = p.K / 128;
-  const int64_t tb = split * g.kt_per_split * 4;
-  const int64_t te = tb + g.kt_per_split * 4 < T ? tb + g.kt_per_split * 4 : T;
+  const int64_t tb = split * kps * 4;
+  const int64_t te = tb + kps * 4 < T ? tb + kps * 4 : T;
 
   if (BLOCK) {
     // The wave's weight block scales of this split, staged in its LDS row before any
@@ -462,7 +470,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, const WideGrid& g
         tile[(16 * (wm * MTW + i) + 4 * q + e) * ST + 16 * (wn * NT + n) + r] = acc[i][n][e];
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const int64_t col0 = nb * TW;
-  if (p.S > 1) {  // fp32 partials, 4 columns per piece, row rr of the tile at pdst + rr * pld
+  if (pdst) {  // fp32 partials, 4 columns per piece, row rr of the tile at pdst + rr * pld
     const bool vec = pld % 4 == 0 && (reinterpret_cast<uintptr_t>(pdst) & 15) == 0;
     for (int c = t; c < BM * (TW / 4); c += 64 * S::WAVES) {
       const int rr = c / (TW / 4), cc = (c % (TW / 4)) * 4;
@@ -532,17 +540,36 @@ __global__ __launch_bounds__(256 * WM) void gemm_wide_kernel(GemmParams p, WideG
     const int64_t G = gridDim.x, Lid = blockIdx.x;
     const int64_t xcd = Lid & 7, per = G >> 3, extra = G & 7;
     const int64_t logical = xcd * per + (xcd < extra ? xcd : extra) + (Lid >> 3);
-    const int64_t local = logical % g.tiles, split = logical / g.tiles;
-    const int64_t tile = g.tile0 + local;
-    const int64_t mb = tile % g.mblocks, nb = tile / g.mblocks;
     constexpr int TW = 64 * NT;
-    float* const pdst = p.S == 1 ? nullptr
-                        : g.compact ? p.partial + (split * g.tiles + local) * BM * TW
-                                    : p.partial + (split * p.M + mb * BM) * p.N + nb * TW;
-    const int64_t pld = g.compact ? TW : p.N;
-    wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g, mb, mb * BM, p.M, p.w, static_cast<const uint8_t*>(p.sw), nb,
-                                           split, pdst, pld, ring, sa_ring, sb_lds + (BLOCK ? wv * kWideBlockStages : 0),
-                                           t, lane, wv, r, q);
+    float* const sbw = sb_lds + (BLOCK ? wv * kWideBlockStages : 0);
+    const uint8_t* const sw = static_cast<const uint8_t*>(p.sw);
+    if (g.rem_tiles == 0) {
+      const int64_t local = logical % g.tiles, split = logical / g.tiles;
+      const int64_t tile = g.tile0 + local;
+      const int64_t mb = tile % g.mblocks, nb = tile / g.mblocks;
+      float* const pdst = p.S == 1 ? nullptr
+                          : g.compact ? p.partial + (split * g.tiles + local) * BM * TW
+                                      : p.partial + (split * p.M + mb * BM) * p.N + nb * TW;
+      const int64_t pld = g.compact ? TW : p.N;
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g.kt_per_split, mb * BM, p.M, p.w, sw, nb, split, pdst, pld, ring,
+                                                 sa_ring, sbw, t, lane, wv, r, q);
+      return;
+    }
+    // one-launch hybrid: the whole-K tile, then the remainder unit (if any)
+    if (logical < g.tiles) {
+      const int64_t mb = logical % g.mblocks, nb = logical / g.mblocks;
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g.kt_per_split, mb * BM, p.M, p.w, sw, nb, 0, nullptr, 0, ring,
+                                                 sa_ring, sbw, t, lane, wv, r, q);
+    }
+    if (logical < g.rem_tiles * g.S2) {
+      const int64_t local = logical % g.rem_tiles, split = logical / g.rem_tiles;
+      const int64_t tile = g.rem_tile0 + local;
+      const int64_t mb = tile % g.mblocks, nb = tile / g.mblocks;
+      __syncthreads();  // the first tile's epilogue reads of the ring are done
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g.kt2, mb * BM, p.M, p.w, sw, nb, split,
+                                                 p.partial + (split * g.rem_tiles + local) * BM * TW, TW, ring, sa_ring,
+                                                 sbw, t, lane, wv, r, q);
+    }
     return;
   }
 
@@ -603,11 +630,11 @@ __global__ __launch_bounds__(256 * WM) void gemm_wide_kernel(GemmParams p, WideG
     // a 128-row block with at most 64 routed rows (an expert's last block) runs the
     // 64-row tile path in the same ring: half the activation copies and MFMAs
     if (MT == 8 && __builtin_amdgcn_readfirstlane((int)(rhi - rb)) <= 64)
-      wide_tile<FMT, (MT == 8 ? 4 : MT), NT, BLOCK, GROUPED, 1>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring,
-                                                             sa_ring, sb_lds, t, lane, wv, r, q);
+      wide_tile<FMT, (MT == 8 ? 4 : MT), NT, BLOCK, GROUPED, 1>(p, g.kt_per_split, rb, rhi, we, swe, nb, 0, nullptr,
+                                                             0, ring, sa_ring, sb_lds, t, lane, wv, r, q);
     else
-      wide_tile<FMT, MT, NT, BLOCK, GROUPED, 1>(p, g, mb, rb, rhi, we, swe, nb, 0, nullptr, 0, ring, sa_ring, sb_lds,
-                                             t, lane, wv, r, q);
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED, 1>(p, g.kt_per_split, rb, rhi, we, swe, nb, 0, nullptr, 0, ring, sa_ring,
+                                             sb_lds, t, lane, wv, r, q);
     __syncthreads();  // the epilogue's LDS reads are done before the next tile's copies
   }
 }
@@ -628,15 +655,8 @@ __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __re
   const int64_t tile = tile0 + local, mb = tile % mblocks, nb = tile / mblocks;
   const int64_t row = mb * BM + rr, col = nb * TW + cc;
   if (row >= M || col >= N) return;
-  const float* src = partial + (local * BM + rr) * TW + cc;
-  const int64_t split_stride = tiles * BM * TW;
-  float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
-  for (int k = 1; k < S; ++k) {
-    const float4 a = *reinterpret_cast<const float4*>(src + k * split_stride);
-    const float4 b = *reinterpret_cast<const float4*>(src + k * split_stride + 4);
-    lo.x += a.x; lo.y += a.y; lo.z += a.z; lo.w += a.w;
-    hi.x += b.x; hi.y += b.y; hi.z += b.z; hi.w += b.w;
-  }
+  float4 lo, hi;
+  sum_splits8(partial + (local * BM + rr) * TW + cc, tiles * BM * TW, S, lo, hi);
   const float f[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   uint16_t h[8];
 #pragma unroll
@@ -734,10 +754,11 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptio
         if (s_only > 1 || (o.splits == 1 && !o.hybrid)) continue;  // a forced split excludes the hybrid
         // (64-wide tiles re-read the activations too often for extra rounds to pay off)
         if (s == 1 && nt >= 2 && wide_hybrid(tiles, KT, cus, h)) {
-          // full rounds, then the split remainder, its partials' round trip and two more launches
+          // full rounds with one remainder unit after the tile, its partials' round trip and
+          // the reduce launch
           const double rem = (double)(tiles - h.dp_tiles);
           const double compute_h =
-              (double)(h.dp_tiles / cus) * KT * 4 * t_stage + (double)h.kt2 * 4 * t_stage + 9000.0;
+              (double)(h.dp_tiles / cus) * KT * 4 * t_stage + (double)h.kt2 * 4 * t_stage + 6000.0;
           const double partial_h = rem * 16 * mt * 64 * nt * 4 * h.S2 * 2 / (3.0e12 / 2.4e9);
           const double cost_h = (compute_h > hbm ? compute_h : hbm) + partial_h;
           if (cost_h < best_cost) {
@@ -831,25 +852,24 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
     return hipErrorInvalidValue;
   };
   if (c.dp_tiles <= 0 || c.dp_tiles >= g.tiles) return dense(p, g, g.tiles * c.S);
-  // hybrid: whole-K tiles in full rounds (bf16 out), then the remainder split in K
-  // into compact partials (p.partial), then their reduce
+  // hybrid, one launch: workgroup L runs whole-K tile L (full rounds, bf16 out) and then
+  // unit L of the remainder, split in K into compact partials (p.partial); their reduce
+  // follows.  (With more than one full round some units run in later rounds' workgroups;
+  // the last round still ends one unit after its tiles.)
   GemmParams q = p;
   q.S = 1;
   WideGrid gd = g;
   gd.tiles = c.dp_tiles;
-  hipError_t e = dense(q, gd, gd.tiles);
+  gd.rem_tile0 = c.dp_tiles;
+  gd.rem_tiles = g.tiles - c.dp_tiles;
+  gd.kt2 = c.kt2;
+  gd.S2 = c.S2;
+  const int64_t units = gd.rem_tiles * c.S2;
+  hipError_t e = dense(q, gd, c.dp_tiles > units ? c.dp_tiles : units);
   if (e != hipSuccess) return e;
-  q.S = c.S2;
-  WideGrid gs = g;
-  gs.tile0 = c.dp_tiles;
-  gs.tiles = g.tiles - c.dp_tiles;
-  gs.kt_per_split = c.kt2;
-  gs.compact = 1;
-  e = dense(q, gs, gs.tiles * c.S2);
-  if (e != hipSuccess) return e;
-  const int64_t items = gs.tiles * bm * (64 * c.NT / 8);
+  const int64_t items = gd.rem_tiles * bm * (64 * c.NT / 8);
   wide_tile_reduce_kernel<<<dim3((unsigned)((items + 255) / 256)), 256, 0, s>>>(
-      p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, gs.tile0, gs.tiles, c.S2, (int)bm, 64 * c.NT);
+      p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, gd.rem_tile0, gd.rem_tiles, c.S2, (int)bm, 64 * c.NT);
   return hipGetLastError();
 }
 
