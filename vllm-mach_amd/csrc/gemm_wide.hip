@@ -366,13 +366,19 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
   const int64_t te = tb + kps * 4 < T ? tb + kps * 4 : T;
 
   if (BLOCK) {
-    // The wave's weight block scales of this split, staged in its LDS row before any
-    // copy is issued.  Read inside the loop from global memory they would be the
-    // compiler's own vector loads, and the compiler waits for its loads with vmcnt,
-    // which counts the stage copies too: every step would drain the whole ring.
+    // The wave's weight block scales of this split, copied into its LDS row (64 per
+    // global->LDS copy) ahead of the stage copies, so the first stage's wait covers them.
+    // Read inside the loop from global memory they would be the compiler's own vector
+    // loads, which it waits for with vmcnt counts that include the stage copies (every
+    // step would drain the ring); loaded into registers here, they cost a memory round
+    // trip before the first copy is issued.
     const int64_t nt0 = nt_wave < ntiles_total ? nt_wave : ntiles_total - 1;
-    const float* sbp = static_cast<const float*>(p.sw) + (nt0 * 16 / 128) * (p.K / 128);
-    for (int64_t i = lane; i < te - tb; i += 64) sb_stage[i] = sbp[tb + i];
+    const float* sbp = static_cast<const float*>(p.sw) + (nt0 * 16 / 128) * (p.K / 128) + tb;
+    const int n_sb = (int)(te - tb);
+    for (int c = 0; c < n_sb; c += 64) {  // lanes past the split re-read its last scale
+      const int i = c + lane < n_sb ? c + lane : n_sb - 1;
+      copy4(reinterpret_cast<const uint8_t*>(sbp), (uint32_t)(i * 4), lds_addr(reinterpret_cast<uint8_t*>(sb_stage + c)));
+    }
   }
 
   v4f acc[MTW][NT];
@@ -470,8 +476,32 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
         tile[(16 * (wm * MTW + i) + 4 * q + e) * ST + 16 * (wn * NT + n) + r] = acc[i][n][e];
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const int64_t col0 = nb * TW;
+  // Tiles whose columns all lie inside N (rows are checked per piece) take batched
+  // passes: a thread issues the LDS reads of up to eight pieces before their stores, so it
+  // waits on LDS once per batch instead of once per piece.
+  constexpr int kThreads = 64 * S::WAVES;
+  static_assert((BM * TW / 4) % kThreads == 0 && (BM * TW / 8) % kThreads == 0, "epilogue pieces per thread");
   if (pdst) {  // fp32 partials, 4 columns per piece, row rr of the tile at pdst + rr * pld
     const bool vec = pld % 4 == 0 && (reinterpret_cast<uintptr_t>(pdst) & 15) == 0;
+    if (vec && col0 + TW <= p.N) {
+      constexpr int P = BM * (TW / 4) / kThreads;
+#pragma unroll
+      for (int k0 = 0; k0 < P; k0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8 && k0 + k < P; ++k) {
+          const int c = t + (k0 + k) * kThreads;
+          v[k] = *reinterpret_cast<const float4*>(tile + (c / (TW / 4)) * ST + (c % (TW / 4)) * 4);
+        }
+#pragma unroll
+        for (int k = 0; k < 8 && k0 + k < P; ++k) {
+          const int c = t + (k0 + k) * kThreads;
+          const int rr = c / (TW / 4);
+          if (row_base + rr < hi) *reinterpret_cast<float4*>(pdst + rr * pld + (c % (TW / 4)) * 4) = v[k];
+        }
+      }
+      return;
+    }
     for (int c = t; c < BM * (TW / 4); c += 64 * S::WAVES) {
       const int rr = c / (TW / 4), cc = (c % (TW / 4)) * 4;
       const int64_t row = row_base + rr, col = col0 + cc;
@@ -487,6 +517,41 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
     }
   } else {  // bf16 out (bias added in bf16), 8 columns per piece
     const bool vec = p.ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+    if (vec && col0 + TW <= p.N) {
+      constexpr int P = BM * (TW / 8) / kThreads;
+#pragma unroll
+      for (int k0 = 0; k0 < P; k0 += 8) {
+        float4 v[8][2];
+#pragma unroll
+        for (int k = 0; k < 8 && k0 + k < P; ++k) {
+          const int c = t + (k0 + k) * kThreads;
+          const float* src = tile + (c / (TW / 8)) * ST + (c % (TW / 8)) * 8;
+          v[k][0] = *reinterpret_cast<const float4*>(src);
+          v[k][1] = *reinterpret_cast<const float4*>(src + 4);
+        }
+#pragma unroll
+        for (int k = 0; k < 8 && k0 + k < P; ++k) {
+          const int c = t + (k0 + k) * kThreads;
+          const int rr = c / (TW / 8), cc = (c % (TW / 8)) * 8;
+          float f[8] = {v[k][0].x, v[k][0].y, v[k][0].z, v[k][0].w, v[k][1].x, v[k][1].y, v[k][1].z, v[k][1].w};
+          uint32_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+          if (p.bias) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float y = u2f(e & 1 ? h[e >> 1] & 0xFFFF0000u : h[e >> 1] << 16);
+              f[e] = y + bf16_to_f32(p.bias[col0 + cc + e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+          }
+          if (row_base + rr < hi)
+            *reinterpret_cast<uint4*>(p.out + (row_base + rr) * p.ldc + col0 + cc) = uint4{h[0], h[1], h[2], h[3]};
+        }
+      }
+      return;
+    }
     for (int c = t; c < BM * (TW / 8); c += 64 * S::WAVES) {
       const int rr = c / (TW / 8), cc = (c % (TW / 8)) * 8;
       const int64_t row = row_base + rr, col = col0 + cc;
