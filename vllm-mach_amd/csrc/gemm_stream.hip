@@ -383,7 +383,7 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
   }
 }
 
-// rounds of weight fragments in flight per wave in the grouped variant with MT > 1
+// rounds of weight fragments in each wave's register ring in the grouped variant
 constexpr int kStreamGroupedDepth = 4;
 
 // Grouped (MoE) weight-streaming GEMM.  A persistent workgroup owns one unit -- up to
@@ -396,12 +396,13 @@ constexpr int kStreamGroupedDepth = 4;
 // directly).  Units are numbered expert by expert (a block scan of the experts' unit
 // counts in LDS), so the launch needs no host-side counts.  Every m-tile's product is
 // the same MFMA chain whatever MT is, so the MT variants give identical bits.
-// Waves per workgroup: MT = 1 (a few rows per expert): sixteen for FP6 weights, eight
-// for E4M3, whose double-buffered fragments need more than the 128 registers a
-// sixteen-wave workgroup leaves a wave.  MT > 1: four, whose activation fragments
+// Waves per workgroup: MT = 1 (a few rows per expert): eight, each keeping
+// kStreamGroupedDepth - 1 rounds of weight fragments in flight in a register ring (a
+// round's tiles arrive one HBM latency after their request, so with one round ahead a
+// round costs a whole latency under load).  MT > 1: four, whose activation fragments
 // (32 MT registers per super-tile) need the registers of a whole SIMD.
 template <int FMT, int MT>
-constexpr int stream_grouped_waves() { return MT > 1 ? 4 : (FMT == kE4M3 ? 8 : 16); }
+constexpr int stream_grouped_waves() { return MT > 1 ? 4 : 8; }
 
 // Activation producers fused into the grouped kernel (prod != 0): the workgroup
 // computes its unit's MXFP8 operands -- codes [ROWS][K] then E8M0 [ROWS][K/32], rows
@@ -454,9 +455,8 @@ __device__ __forceinline__ void produce_store(const GemmParams& p, int c, bool l
     float g[8], u[8];
     bf16x8_to_f32(in.x, g);
     bf16x8_to_f32(in.y, u);
-    // two halves, so that the scheduler does not interleave all eight exp sequences: the
-    // sixteen-wave kernel has 128 registers, and a spill reload here would wait (vmcnt)
-    // for the unit's first weights as well
+    // two halves, so that the scheduler does not interleave all eight exp sequences: a
+    // spill reload here would wait (vmcnt) for the unit's first weights as well
     swiglu8<RULE, 4>(g, u, v);
     __builtin_amdgcn_sched_barrier(0);
     swiglu8<RULE, 4>(g + 4, u + 4, v + 4);
@@ -478,7 +478,7 @@ __device__ __forceinline__ void produce_store(const GemmParams& p, int c, bool l
 //   producer 2: SwiGLU of the unit's bf16 gate/up rows (gate columns [0, K), up [K, 2K),
 //               row stride lda) then MXFP8, rule RULE.
 // (Each producer and rule is its own instantiation: one kernel holding all three rules'
-// code needed more than the 128 registers of its sixteen waves.)
+// code would hold every rule's registers.)
 // Only the unit's rows are produced (the gather reads its padding rows from the last
 // one): items = rows x K/32 x 4.  Items and thread counts are multiples of four, so the
 // four lanes of a block are live together; threads past the end redo the last block
@@ -508,9 +508,9 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
   extern __shared__ __attribute__((aligned(16))) uint8_t stage_act[];
   constexpr int ROWS = 16 * MT;
   __shared__ float red[2][WAVES][MT][4][64];
-  // MT > 1, one super-tile: each wave's 16 MT x 16 bf16 output block, staged so that the
-  // stores move 16-byte row pieces (row stride 24 halfwords: 48 bytes keeps pieces aligned)
-  __shared__ __attribute__((aligned(16))) uint16_t stage[MT > 1 ? WAVES : 1][MT > 1 ? ROWS : 1][24];
+  // one super-tile: each wave's 16 MT x 16 bf16 output block, staged so that the stores
+  // move 16-byte row pieces (row stride 24 halfwords: 48 bytes keeps pieces aligned)
+  __shared__ __attribute__((aligned(16))) uint16_t stage[WAVES][ROWS][24];
   __shared__ int32_t sh_pre[kStreamGroupedMaxExperts + 1];  // units before expert e
   __shared__ int32_t sh_off[kStreamGroupedMaxExperts + 1];  // expert_offsets
   __shared__ int32_t sh_scan[64 * WAVES];
@@ -563,7 +563,7 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
     const bool valid[1] = {kw < p.KT};
 
     // the first round's weights first, then the unit's gathered activation fragments
-    StreamB<FMT, 1> b0, b1;  // (b1: MT = 1 only)
+    StreamB<FMT, 1> b0;
     auto nt_of = [&](int64_t round) -> int64_t {
       const int64_t nt = nl + round * NW;
       return nt < ntiles ? nt : ntiles - 1;
@@ -639,10 +639,10 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
         }
       }
     };
-    // store the round's NW n-tiles: one super-tile per wave stores its own product; else
-    // the WK partials of each n-tile are summed in LDS in K order
+    // store the round's NW n-tiles: one super-tile per wave stores its own product (no
+    // workgroup barrier); else the WK partials of each n-tile are summed in LDS in K order
     auto finish = [&](const v4f (&acc)[MT], int64_t round) {
-      if (MT > 1 && WK == 1) {
+      if (WK == 1) {
         const int64_t nt = nl + round * NW;
         if (nt >= ntiles) return;
         if (p.N % 8 == 0 && p.ldc % 8 == 0 && ((uintptr_t)p.out & 15) == 0) {
@@ -704,21 +704,10 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
 
     const int64_t rounds = (ntiles + NW - 1) / NW;
     v4f acc[MT];
-    if constexpr (MT == 1) {
-      for (int64_t rd = 0; rd < rounds; rd += 2) {
-        stream_load_b<FMT, 1, false>(p, w, sw, nt_of(rd + 1 < rounds ? rd + 1 : rd), kt1, lane, b1);
-        mma(b0, acc);
-        finish(acc, rd);
-        stream_load_b<FMT, 1, false>(p, w, sw, nt_of(rd + 2 < rounds ? rd + 2 : rd), kt1, lane, b0);
-        if (rd + 1 < rounds) {
-          mma(b1, acc);
-          finish(acc, rd + 1);
-        }
-      }
-    } else {
-      // four waves keep kStreamGroupedDepth rounds of weights in flight: a register ring,
-      // round rd + D - 1 requested before round rd is used (past the end: the last round
-      // is re-read, and nothing is stored for it)
+    {
+      // a register ring of kStreamGroupedDepth rounds of weights: round rd + D - 1 requested
+      // before round rd is used (past the end: the last round is re-read, and nothing is
+      // stored for it)
       constexpr int D = kStreamGroupedDepth;
       StreamB<FMT, 1> ring[D];
       ring[0] = b0;
