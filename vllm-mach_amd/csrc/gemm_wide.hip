@@ -9,7 +9,8 @@
 // of a wave writes 4 or 16 bytes at LDS base + 4i / 16i, no staging
 // registers) into a ring of K128 stage slots (four, or three for NT = 4 whose
 // 53 KiB stages would not fit four times), issued two or three stages ahead of
-// the MFMAs.  A slot holds
+// the MFMAs; the grouped variant runs two workgroups per CU with two slots each,
+// one stage ahead.  A slot holds
 //   A    8 m-tiles x 2 KiB: chunk (m-tile i, half h) holds rows 16 i + 8 h ..
 //        + 7 whole (the slice's 128 bytes per row), the eight 16-byte pieces of
 //        row r permuted by piece ^ a_swz(r).  The copy is row-major because the
@@ -78,6 +79,9 @@ struct WideSlot {
   static constexpr int SBC = BLOCK ? 0 : (WM == 1 ? NT : (NT >= 2 ? NT / 2 : 1));
   static constexpr int COPIES = ACH + BCH * NT + SBC;
 };
+
+// Ring slots of the grouped variant, which runs two workgroups per CU.
+constexpr int kWideGroupedSlots = 2;
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
@@ -387,19 +391,54 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  if (tb < te) {
-    constexpr int R = S::SLOTS;
-    // prologue: the scale ring entry of the first super-tile; stages tb .. tb + R - 1
-    // fill the ring; stage tb is read into registers
-    if (S::SA_RING && wv < S::SW) {
-      const bool half = (tb >> 2) == p.KT - 1 && p.K % kTileK != 0;
+  // prologue: the scale ring entry of the first super-tile
+  if (S::SA_RING && tb < te && wv < S::SW) {
+    const bool half = (tb >> 2) == p.KT - 1 && p.K % kTileK != 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t dst = lds_addr(sa_ring + ((tb >> 2) % 3) * S::RING_ENTRY + (4 * MT * j + 16 * wv) * 16);
-        if (half) copy4(static_cast<const uint8_t*>(p.sa), L.sa_last[j], dst);
-        else copy4(static_cast<const uint8_t*>(p.sa) + (tb >> 2) * 4 * p.sa_ss, L.sa_piece[j], dst);
-      }
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t dst = lds_addr(sa_ring + ((tb >> 2) % 3) * S::RING_ENTRY + (4 * MT * j + 16 * wv) * 16);
+      if (half) copy4(static_cast<const uint8_t*>(p.sa), L.sa_last[j], dst);
+      else copy4(static_cast<const uint8_t*>(p.sa) + (tb >> 2) * 4 * p.sa_ss, L.sa_piece[j], dst);
     }
+  }
+  if constexpr (GROUPED) {
+    // Two workgroups per CU, each with a two-slot ring and one register set: step tt
+    // waits for its own copies of stage tt (issued in the step before, the last ones
+    // in flight), a barrier hands stage tt to every wave and frees the slot read in
+    // the step before, stage tt + 1 is copied into it, then stage tt is read and
+    // multiplied.  The other workgroup's steps run while this one waits on LDS
+    // reads, copies or its prologue and epilogue.
+    constexpr int R = kWideGroupedSlots;
+    static_assert(4 % R == 0, "the four steps below rotate the slots");
+    if (tb < te) wide_copy<FMT, MT, NT, BLOCK, WM>(p, ring, tb, wv, lane, L, sa_ring);
+    WideRegs<MTW, NT, BLOCK> x;
+#define MXL_WIDE_STEP2(I_)                                                                              \
+  {                                                                                                   \
+    const int64_t tt = t0 + I_;                                                                       \
+    if (tt < te) {                                                                                    \
+      wait_vm<0>();                                                                                   \
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                            \
+      wide_barrier();                                                                                 \
+      if (tt + 1 < te)                                                                                \
+        wide_copy<FMT, MT, NT, BLOCK, WM>(p, ring + ((I_ + 1) % R) * S::BYTES, tt + 1, wv, lane, L, sa_ring); \
+      wide_read<FMT, MT, NT, BLOCK, WM>(ring + (I_ % R) * S::BYTES, sa_ring + ((tt >> 2) % 3) * S::RING_ENTRY, \
+                                        (int)(tt & 3), wv, lane, q, r, x);                           \
+      if (BLOCK) x.sbv = sb_stage[tt - tb];                                                           \
+      wide_mfma<FMT, MTW, NT, BLOCK>(x, acc);                                                         \
+    }                                                                                                 \
+  }
+    // four steps per iteration: tb is a multiple of 4, so each step's slice index
+    // (tt & 3) is a compile-time value and the per-slice lane offsets stay in registers
+    for (int64_t t0 = tb; t0 < te; t0 += 4) {
+      MXL_WIDE_STEP2(0)
+      MXL_WIDE_STEP2(1)
+      MXL_WIDE_STEP2(2)
+      MXL_WIDE_STEP2(3)
+    }
+#undef MXL_WIDE_STEP2
+  } else if (tb < te) {
+    constexpr int R = S::SLOTS;
+    // prologue: stages tb .. tb + R - 1 fill the ring; stage tb is read into registers
 #pragma unroll
     for (int k = 0; k < R; ++k)
       if (tb + k < te) wide_copy<FMT, MT, NT, BLOCK, WM>(p, ring + k * S::BYTES, tb + k, wv, lane, L, sa_ring);
@@ -464,7 +503,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
   // stores straight from the accumulator layout would cost a store instruction
   // per 64 values with 64-bit address arithmetic for each.
   constexpr int TW = 64 * NT, ST = TW + 4;
-  static_assert(BM * ST * 4 <= S::SLOTS * S::BYTES, "epilogue tile exceeds the ring");
+  static_assert(BM * ST * 4 <= (GROUPED ? kWideGroupedSlots : S::SLOTS) * S::BYTES, "epilogue tile exceeds the ring");
   float* const tile = reinterpret_cast<float*>(ring);
   wide_barrier();  // every wave is past its last fragment reads
 #pragma unroll
@@ -584,14 +623,16 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
 // Largest number of experts the grouped variant keeps in LDS.
 constexpr int kWideMaxExperts = (int)kWideGroupedMaxExperts;
 
+// The grouped variant runs two workgroups per CU (at most 256 registers per lane and
+// half the LDS each).
 template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED, int WM = 1>
-__global__ __launch_bounds__(256 * WM) void gemm_wide_kernel(GemmParams p, WideGrid g) {
+__global__ __launch_bounds__(256 * WM, GROUPED ? 2 : 1) void gemm_wide_kernel(GemmParams p, WideGrid g) {
   static_assert(WM == 1 || !GROUPED, "the grouped variant runs four waves");
   using S = WideSlot<MT, NT, BLOCK, WM>;
   constexpr int BM = 16 * MT;
-  // the stage ring (the LDS budget of one workgroup per CU); after the last
-  // stage it holds the output tile of the epilogue
-  __shared__ __attribute__((aligned(16))) uint8_t ring[S::SLOTS * S::BYTES];
+  // the stage ring (dense: the LDS budget of one workgroup per CU; grouped: two slots);
+  // after the last stage it holds the output tile of the epilogue
+  __shared__ __attribute__((aligned(16))) uint8_t ring[(GROUPED ? kWideGroupedSlots : S::SLOTS) * S::BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t sa_ring[S::SA_RING ? 3 * S::RING_ENTRY : 16];
   // block-FP8: each wave's weight block scales of the tile's K range
   __shared__ float sb_lds[BLOCK ? 4 * kWideBlockStages : 1];
@@ -642,19 +683,20 @@ __global__ __launch_bounds__(256 * WM) void gemm_wide_kernel(GemmParams p, WideG
   // prefix-summed once per workgroup into LDS; each workgroup then walks the
   // tiles L = blockIdx, blockIdx + grid, ... of the routed (m-block x n-block)
   // grid, n-blocks fastest (the same XCD remap, so a workgroup stays on its XCD's
-  // tiles), and finds its expert by a parallel search of the prefix.
+  // tiles), and finds its expert by a parallel search of the prefix.  Only the prefix
+  // stays in LDS (two workgroups share a CU's LDS); a tile reads its expert's row range
+  // from expert_offsets.
   __shared__ int32_t sh_pre[kWideMaxExperts + 1];   // m-blocks before expert e
-  __shared__ int32_t sh_row[kWideMaxExperts + 1];   // expert_offsets
   __shared__ int32_t sh_hit;
   const int E = (int)g.num_experts;
-  for (int e = t; e <= E; e += 256) sh_row[e] = (int32_t)p.expert_offsets[e];
-  __syncthreads();
   // block counts per thread chunk, then a block-wide inclusive scan of the chunk sums
+  // (in the ring, which holds no stage yet)
   const int chunk = (E + 255) / 256;
   const int e0 = t * chunk < E ? t * chunk : E, e1 = e0 + chunk < E ? e0 + chunk : E;
   int cnt = 0;
-  for (int e = e0; e < e1; ++e) cnt += (sh_row[e + 1] - sh_row[e] + BM - 1) / BM;
-  __shared__ int32_t sh_scan[256];
+  for (int e = e0; e < e1; ++e)
+    cnt += (int)((p.expert_offsets[e + 1] - p.expert_offsets[e] + BM - 1) / BM);
+  int32_t* const sh_scan = reinterpret_cast<int32_t*>(ring);
   sh_scan[t] = cnt;
   __syncthreads();
   for (int off = 1; off < 256; off <<= 1) {
@@ -666,7 +708,7 @@ __global__ __launch_bounds__(256 * WM) void gemm_wide_kernel(GemmParams p, WideG
   int base = sh_scan[t] - cnt;  // exclusive prefix of this thread's chunk
   for (int e = e0; e < e1; ++e) {
     sh_pre[e] = base;
-    base += (sh_row[e + 1] - sh_row[e] + BM - 1) / BM;
+    base += (int)((p.expert_offsets[e + 1] - p.expert_offsets[e] + BM - 1) / BM);
   }
   if (t == 255) sh_pre[E] = sh_scan[255];
   __syncthreads();
@@ -689,7 +731,7 @@ __global__ __launch_bounds__(256 * WM) void gemm_wide_kernel(GemmParams p, WideG
       if (sh_pre[e] <= mb && mb < sh_pre[e + 1]) sh_hit = e;
     __syncthreads();
     const int e = __builtin_amdgcn_readfirstlane(sh_hit);
-    const int64_t rb = sh_row[e] + (mb - sh_pre[e]) * BM, rhi = sh_row[e + 1];
+    const int64_t rb = p.expert_offsets[e] + (mb - sh_pre[e]) * BM, rhi = p.expert_offsets[e + 1];
     const uint8_t* we = p.w + e * p.w_expert_stride;
     const uint8_t* swe = static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride;
     // a 128-row block with at most 64 routed rows (an expert's last block) runs the
@@ -899,7 +941,7 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
   if (num_experts > 0) {
     g.mblocks = (p.M + bm - 1) / bm + num_experts;  // bound on the routed m-blocks
     grid = g.mblocks * g.nblocks;
-    if (grid > cu_count()) grid = cu_count();     // persistent workgroups walk the tiles
+    if (grid > 2 * cu_count()) grid = 2 * cu_count();  // persistent workgroups (two per CU) walk the tiles
     if (fmt == kE4M3) return launch_wide_fmt<kE4M3, false, true>(c, p, g, grid, s);
     if (fmt == kE2M3) return launch_wide_fmt<kE2M3, false, true>(c, p, g, grid, s);
     if (fmt == kE3M2) return launch_wide_fmt<kE3M2, false, true>(c, p, g, grid, s);
