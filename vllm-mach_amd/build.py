@@ -5,7 +5,9 @@ Each ``csrc/*.hip`` is compiled to an object in parallel, then linked.
 """
 from __future__ import annotations
 
+import json
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -16,6 +18,8 @@ CSRC = HERE / "csrc"
 OUT = HERE / "libmxlinear.so"
 BUILD = HERE / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# per-kernel register, scratch and LDS figures of the last build (compiler remarks)
+RESOURCES = BUILD / "kernel_resources.json"
 
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -35,13 +39,36 @@ FILE_FLAGS: dict[str, list[str]] = {
 }
 
 
-def _compile(src: Path) -> Path:
+_REMARK_FIELDS = {
+    "VGPRs": "vgpr", "AGPRs": "agpr", "TotalSGPRs": "sgpr", "ScratchSize [bytes/lane]": "scratch",
+    "VGPRs Spill": "vgpr_spill", "SGPRs Spill": "sgpr_spill", "LDS Size [bytes/block]": "lds",
+    "Occupancy [waves/SIMD]": "occupancy",
+}
+
+
+def parse_resource_remarks(text: str) -> dict[str, dict[str, int]]:
+    """Kernel name -> figures from hipcc's ``-Rpass-analysis=kernel-resource-usage`` remarks."""
+    kernels: dict[str, dict[str, int]] = {}
+    cur = None
+    for line in text.splitlines():
+        m = re.search(r"remark:\s+Function Name: (\S+)", line)
+        if m:
+            cur = kernels.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([A-Za-z ]+(?:\[[^\]]*\])?): (\d+) \[", line)
+        if m and cur is not None and m.group(1).strip() in _REMARK_FIELDS:
+            cur[_REMARK_FIELDS[m.group(1).strip()]] = int(m.group(2))
+    return kernels
+
+
+def _compile(src: Path) -> tuple[Path, dict[str, dict[str, int]]]:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-Rpass-analysis=kernel-resource-usage",
+           "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
-    return obj
+    return obj, parse_resource_remarks(r.stderr)
 
 
 TORCH_OPS_SRC = CSRC / "torch_ops.cpp"
@@ -77,7 +104,12 @@ def build(verbose: bool = False) -> Path:
     sources = sorted(CSRC.glob("*.hip"))
     jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-        objs = list(pool.map(_compile, sources))
+        done = list(pool.map(_compile, sources))
+    objs = [o for o, _ in done]
+    resources: dict[str, dict[str, int]] = {}
+    for _, k in done:
+        resources.update(k)
+    RESOURCES.write_text(json.dumps(resources, indent=1, sort_keys=True))
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -368,9 +368,12 @@ static hipError_t launch_gemm(const GemmConfig& c, dim3 grid, const GemmParams& 
     return hipGetLastError();                                                                       \
   }
   MXL_LAUNCH(1, 1)
-  MXL_LAUNCH(2, 1)
-  MXL_LAUNCH(4, 1)
-  MXL_LAUNCH(2, 2)
+  // grouped launches use 16-row tiles only (mxl_grouped_gemm's generic schedule)
+  if constexpr (!GROUPED) {
+    MXL_LAUNCH(2, 1)
+    MXL_LAUNCH(4, 1)
+    MXL_LAUNCH(2, 2)
+  }
 #undef MXL_LAUNCH
   return hipErrorInvalidValue;
 }
