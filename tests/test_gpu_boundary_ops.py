@@ -5,6 +5,8 @@ E8M0 activation and weight scales, the 64-row duplicated block-FP8 scales passed
 transposed (src/vllm_mach/fp8/block_native.py:61-65), and the MoE route -> grouped
 GEMM -> SwiGLU grouped GEMM -> reduce sequence of src/vllm_mach/mxfp6/moe.py:652-702.
 Codes and scales must match bit for bit; GEMMs meet the north-star bar."""
+import warnings
+
 import numpy as np
 import pytest
 import torch
@@ -129,9 +131,11 @@ def test_mxfp8_sm120_gemm_from_float_and_capture(api, oracle_mod, dev):
             assert torch.equal(out, y)
             assert torch.equal(torch.ops.mxfp8_sm120.gemm_from_float(x, w, wsw), y)
     torch.cuda.current_stream().wait_stream(stream)
-    # an unprepared weight is refused during capture
+    # an unprepared weight is refused during capture (the aborted capture records nothing,
+    # which torch reports as an empty graph)
     w2 = w.clone()
-    with torch.cuda.stream(stream):
+    with torch.cuda.stream(stream), warnings.catch_warnings():
+        warnings.filterwarnings("ignore", message="The CUDA Graph is empty")
         g2 = torch.cuda.CUDAGraph()
         with pytest.raises(RuntimeError, match="before graph capture"):
             with torch.cuda.graph(g2, stream=stream):
