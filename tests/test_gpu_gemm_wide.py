@@ -222,6 +222,40 @@ def test_wide_grouped_gemm_skewed_experts(pkg, oracle_mod, dev, monkeypatch, fmt
         _check(got[lo:hi], oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref)))
 
 
+def test_wide_grouped_gemm_max_experts(pkg, oracle_mod, dev, monkeypatch):
+    """The most experts the grouped wide kernel takes (1024: its expert prefix shares the
+    LDS with the second workgroup on each CU), about 32 routed rows per expert, forced onto
+    the wide kernel: within the bar of the 96-row streaming schedule on every route and of
+    the oracle on the first, the last and the largest expert."""
+    ops = pkg.ops
+    E, N, K, T, topk, fmt = 1024, 256, 512, 4096, 8, 2
+    g = torch.Generator().manual_seed(2024)
+    ids = torch.randint(0, E, (T, topk), generator=g, dtype=torch.int32)
+    packed = torch.randint(0, 256, (E, N, K * 3 // 4), generator=g, dtype=torch.uint8)  # every FP6 pattern is a number
+    scales = torch.randint(118, 124, (E, N, K // 32), generator=g, dtype=torch.uint8)
+    w_t, s_t = ops.pack_weight(packed.to(dev), scales.to(dev), fmt)
+    routes, offsets, _ = torch.ops.mach_amd.moe_route(ids.to(dev), E)
+    R = T * topk
+    x = _act(T, K, 31)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    force(monkeypatch, ops, kernel=ops.KERNEL_WIDE)
+    y = torch.ops.mach_amd.grouped_gemm(a, sa, routes, topk, offsets, R, w_t, s_t, N, K, fmt)
+    force(monkeypatch, ops, kernel=ops.KERNEL_STREAM_WIDE)
+    y_s = torch.ops.mach_amd.grouped_gemm(a, sa, routes, topk, offsets, R, w_t, s_t, N, K, fmt)
+    got = y.float().cpu().numpy()
+    _check(got, y_s.float().cpu().numpy())
+    rc, rs = oracle_mod.quant_mxfp8(x, 0)
+    off, rt = offsets.cpu().numpy(), routes.cpu().numpy()
+    for e in sorted({0, E - 1, int(np.argmax(off[1:] - off[:-1]))}):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if lo == hi:
+            continue
+        rows = rt[lo:hi] // topk
+        ref = oracle_mod.mx_gemm_ref(rc[rows], rs[rows], oracle_mod.unpack_fp6(packed[e].numpy()),
+                                     scales[e].numpy(), fmt)
+        _check(got[lo:hi], oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref)))
+
+
 @pytest.mark.parametrize("M,N,K,fmt", [
     (1, 2560, 9216, 0),      # sixteen single-buffered waves
     (16, 2560, 9216, 0),
