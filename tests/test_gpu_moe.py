@@ -224,6 +224,8 @@ def test_grouped_stream_small_batch(pkg, oracle_mod, dev, monkeypatch, E, N, K, 
     (256, 2048, 512, 2048, 8, False, 2, False),  # the MoE down projection at T = 2048 (c5): the default
     (256, 1024, 2048, 2048, 8, True, 2, False),  # the MoE gate_up at T = 2048 (c5): forced, four K waves
     (8, 384, 512, 200, 2, True, 0, True),        # E4M3: an expert with > 96 rows (two units), empty experts
+    (8, 200, 512, 200, 2, True, 2, True),        # 13 n-tiles over four wave lanes: each unit's partial
+                                                 # round lands at its own rotated position
     (16, 200, 1280, 400, 2, True, 3, True),      # forced: ragged N, K % 512 != 0 (three K waves)
 ])
 def test_grouped_stream_96_row_units(pkg, oracle_mod, dev, monkeypatch, E, N, K, T, topk, gathered, fmt, skew):
