@@ -508,14 +508,12 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
   extern __shared__ __attribute__((aligned(16))) uint8_t stage_act[];
   constexpr int ROWS = 16 * MT;
   __shared__ float red[2][WAVES][MT][4][64];
-  // one super-tile, MT = 1: each wave's 16 x 16 bf16 output block, staged so that the stores
-  // move 16-byte row pieces (row stride 24 halfwords: 48 bytes keeps pieces aligned)
-  __shared__ __attribute__((aligned(16))) uint16_t stage[WAVES][ROWS][24];
-  // MT > 1: the round's NW adjacent n-tiles of all waves side by side, so that each row's
-  // 16 NW columns (whole 128-byte lines) are stored together (double-buffered by round;
-  // per-wave 32-byte row pieces left the lines to be merged in L2 between the weight reads:
-  // 68.9 -> 64.9 us at c5 T = 2048)
-  __shared__ __attribute__((aligned(16))) uint16_t wstage[MT > 1 ? 2 : 1][MT > 1 ? ROWS : 1][MT > 1 ? 16 * WAVES + 8 : 8];
+  // one super-tile: the round's NW adjacent n-tiles of all waves side by side in bf16, so
+  // that each row's 16 NW columns (whole 128-byte lines) are stored together
+  // (double-buffered by round; row stride 16 NW + 8 halfwords keeps 16-byte pieces
+  // aligned).  Per-wave 32-byte row pieces left the lines to be merged in L2 between the
+  // weight reads: 68.9 -> 64.9 us at c5 T = 2048 (96-row units), 47.1 -> 46.8 at T = 128.
+  __shared__ __attribute__((aligned(16))) uint16_t wstage[2][ROWS][16 * WAVES + 8];
   int wbuf = 0;
   __shared__ int32_t sh_pre[kStreamGroupedMaxExperts + 1];  // units before expert e
   __shared__ int32_t sh_off[kStreamGroupedMaxExperts + 1];  // expert_offsets
@@ -655,58 +653,37 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
         }
       }
     };
-    // store the round's NW n-tiles: one super-tile per wave stores its own product (no
-    // workgroup barrier); else the WK partials of each n-tile are summed in LDS in K order
+    // store the round's NW n-tiles: with one super-tile per wave the waves' products meet
+    // in LDS and are stored as whole row lines; else the WK partials of each n-tile are
+    // summed in LDS in K order
     auto finish = [&](const v4f (&acc)[MT], int64_t round) {
       if (WK == 1) {
-        const int64_t nt = nl + rnd(round) * NW;
-        if constexpr (MT > 1) {
-          if (p.N % 8 == 0 && p.ldc % 8 == 0 && ((uintptr_t)p.out & 15) == 0 && NW == WAVES) {
-            // every wave puts its 16 MT x 16 tile beside the others', then the workgroup
-            // stores whole 16 NW-column pieces of each row
-            if (nt < ntiles) {
-#pragma unroll
-              for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int x = 0; x < 4; ++x) wstage[wbuf][16 * i + 4 * q + x][16 * nl + r] = f32_to_bf16(acc[i][x]);
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            constexpr int SEG = 2 * WAVES;  // 16-byte pieces per row
-            const int64_t col0 = rnd(round) * NW * 16;
-            const int nrows = (int)(hi - lo);
-            for (int k = 0; k < (ROWS * SEG + 64 * WAVES - 1) / (64 * WAVES); ++k) {
-              const int piece = t + 64 * WAVES * k, row = piece / SEG, seg = piece % SEG;
-              const int64_t col = col0 + 8 * seg;
-              if (row < nrows && col < p.N) {
-                const uint4 v = *reinterpret_cast<const uint4*>(&wstage[wbuf][row][8 * seg]);
-                *reinterpret_cast<uint4*>(p.out + (lo + row) * p.ldc + col) = v;
-              }
-            }
-            wbuf ^= 1;
-            return;
-          }
-        }
-        if (nt >= ntiles) return;
+        const int64_t nt = nl + rnd(round) * NW;  // NW == WAVES: every wave has its own n-tile
         if (p.N % 8 == 0 && p.ldc % 8 == 0 && ((uintptr_t)p.out & 15) == 0) {
-          // lane (q, r) holds column r of rows 16 i + 4 q + x: through the wave's LDS block,
-          // then each lane stores 16-byte pieces (row, half) of it
+          // every wave puts its 16 MT x 16 tile beside the others' (lane (q, r) holds column
+          // r of rows 16 i + 4 q + x), then the workgroup stores 16-byte pieces of each row
+          if (nt < ntiles) {
 #pragma unroll
-          for (int i = 0; i < MT; ++i)
+            for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int x = 0; x < 4; ++x) stage[wv][16 * i + 4 * q + x][r] = f32_to_bf16(acc[i][x]);
-          __builtin_amdgcn_wave_barrier();
-#pragma unroll
-          for (int k = 0; k < (2 * ROWS + 63) / 64; ++k) {
-            const int piece = lane + 64 * k, row = piece >> 1, half = piece & 1;
-            const int64_t col = nt * 16 + 8 * half;
-            if (row < ROWS && lo + row < hi && col < p.N) {
-              const uint4 v = *reinterpret_cast<const uint4*>(&stage[wv][row][8 * half]);
+              for (int x = 0; x < 4; ++x) wstage[wbuf][16 * i + 4 * q + x][16 * nl + r] = f32_to_bf16(acc[i][x]);
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+          constexpr int SEG = 2 * WAVES;  // 16-byte pieces per row
+          const int64_t col0 = rnd(round) * NW * 16;
+          const int nrows = (int)(hi - lo);
+          for (int k = 0; k < (ROWS * SEG + 64 * WAVES - 1) / (64 * WAVES); ++k) {
+            const int piece = t + 64 * WAVES * k, row = piece / SEG, seg = piece % SEG;
+            const int64_t col = col0 + 8 * seg;
+            if (row < nrows && col < p.N) {
+              const uint4 v = *reinterpret_cast<const uint4*>(&wstage[wbuf][row][8 * seg]);
               *reinterpret_cast<uint4*>(p.out + (lo + row) * p.ldc + col) = v;
             }
           }
-          __builtin_amdgcn_wave_barrier();
+          wbuf ^= 1;
           return;
         }
+        if (nt >= ntiles) return;
         const int64_t col = nt * 16 + r;
 #pragma unroll
         for (int i = 0; i < MT; ++i)
