@@ -512,7 +512,7 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
   // that each row's 16 NW columns (whole 128-byte lines) are stored together
   // (double-buffered by round; row stride 16 NW + 8 halfwords keeps 16-byte pieces
   // aligned).  Per-wave 32-byte row pieces left the lines to be merged in L2 between the
-  // weight reads: 68.9 -> 64.9 us at c5 T = 2048 (96-row units), 47.1 -> 46.8 at T = 128.
+  // weight reads: 68.9 -> 64.9 us at c5 T = 2048 (96-row units), 47.1 -> 46.5 at T = 128.
   __shared__ __attribute__((aligned(16))) uint16_t wstage[2][ROWS][16 * WAVES + 8];
   int wbuf = 0;
   __shared__ int32_t sh_pre[kStreamGroupedMaxExperts + 1];  // units before expert e
