@@ -26,6 +26,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -49,18 +50,24 @@ def copies_for(nbytes: int) -> int:
     return min(128, max(2, -(-ROTATION_BYTES // max(nbytes, 1))))
 
 
-def measured_traffic(config: str, m: int, kernel: str):
-    """HBM bytes per launch of the op `kernel` at (config, M) from the committed rocprofv3
-    counter summary (FETCH_SIZE and WRITE_SIZE runs, calibrated), or None."""
+def measured_traffic(config: str, m: int, kernel: str, plan: str):
+    """(HBM bytes per launch, note) of the op `kernel` at (config, M) from the committed
+    rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE runs, calibrated).  The row's
+    kernels (the backquoted names, joined by " + ") must be exactly `plan`, the kernels
+    the library launches for this op now (``mxl_gemm_plan_name``); a row measured on other
+    kernels is stale and gives (None, why)."""
     try:
         for line in TRAFFIC_TABLE.read_text().splitlines():
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
             if (len(cells) >= 4 and cells[0] == config and cells[1] == str(m)
                     and kernel.startswith(cells[2] + " ")):
-                return int(cells[-1].replace(",", ""))
-    except (OSError, ValueError):
-        return None
-    return None
+                measured = " + ".join(re.findall(r"`([^`]+)`", cells[3]))
+                if measured != plan:
+                    return None, f"stale row: measured on {measured!r}, the op now runs {plan!r}"
+                return int(cells[-1].replace(",", "")), "matches the kernels the op runs"
+    except (OSError, ValueError) as e:
+        return None, f"unreadable table: {e}"
+    return None, "no row for this op"
 
 
 def graph_time_us(fn_list, stream, replays=20, trials=9):
@@ -136,6 +143,15 @@ class Workload:
     def flops(self, x) -> float:
         raise NotImplementedError
 
+    def plan(self, kname: str, x) -> str:
+        """The kernels the library launches for op `kname` of kernels(x) (its traffic row key)."""
+        raise NotImplementedError
+
+
+def _dense_plan(M, N, K, fmt, block=False) -> str:
+    from vllm_mach_amd import _lib
+    return _lib.plan_name("mxl_gemm_plan_name", M, N, K, fmt, int(block))
+
 
 class SwigluDown(Workload):
     """c2: SwiGLU -> MXFP8 producer + MXFP8 down projection."""
@@ -161,6 +177,9 @@ class SwigluDown(Workload):
 
     def flops(self, M):
         return 2.0 * M * self.N * self.K
+
+    def plan(self, kname, M):
+        return _dense_plan(M, self.N, self.K, self.ops.E4M3)
 
     def kernels(self, M):
         ops, N, K = self.ops, self.N, self.K
@@ -218,6 +237,9 @@ class MxLinear(Workload):
     def flops(self, M):
         return 2.0 * M * self.N * self.K
 
+    def plan(self, kname, M):
+        return _dense_plan(M, self.N, self.K, self.fmt)
+
     def kernels(self, M):
         ops, N, K, fmt = self.ops, self.N, self.K, self.fmt
         a, sa = self.quant[M]
@@ -274,6 +296,9 @@ class BlockFp8Linear(Workload):
 
     def flops(self, M):
         return 2.0 * M * self.N * self.K
+
+    def plan(self, kname, M):
+        return _dense_plan(M, self.N, self.K, self.ops.E4M3, block=True)
 
     def kernels(self, M):
         N, K = self.N, self.K
@@ -343,6 +368,17 @@ class MoeLayer(Workload):
 
     def flops(self, T):
         return 2.0 * T * self.TOPK * (2 * self.I * self.H + self.H * self.I)
+
+    def plan(self, kname, T):
+        from vllm_mach_amd import _lib
+        ops, routes = self.ops, T * self.TOPK
+        w13 = kname.startswith("grouped w13")
+        K = self.H if w13 else self.I
+        prod = 0
+        if ops.grouped_fused_supported(routes, self.E, K, ops.E2M3):
+            prod = 1 if w13 else 2
+        rule = ops.FLOOR_CARRY175 if w13 else ops.CEIL_DIV448
+        return _lib.plan_name("mxl_grouped_plan_name", routes, self.E, K, ops.E2M3, prod, rule)
 
     def kernels(self, T):
         ops, H, I, k = self.ops, self.H, self.I, self.TOPK
@@ -693,9 +729,12 @@ def main():
         "config": {"workload": wl.describe, "M": list(wl.sweep), "parallelism": "single GPU"},
         "per_m": per_m, "roofline": roofline_of(dom[0], dom[1]),
     }
-    out["roofline"]["traffic"] = measured_traffic(args.config, dom[2], dom[0])
+    plan = wl.plan(dom[0], dom[2])
+    traffic, note = measured_traffic(args.config, dom[2], dom[0], plan)
+    out["roofline"]["traffic"] = traffic
+    out["roofline"]["kernels"] = plan
     out["roofline"]["traffic_source"] = ("profiles/hbm_traffic.md (rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, "
-                                         "calibrated on a 256 MiB device copy)")
+                                         f"calibrated on a 256 MiB device copy): {note}")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.config, wl.sweep)
     print(json.dumps(out))

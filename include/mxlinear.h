@@ -142,10 +142,14 @@ int mxl_pack_weight(const void* codes, const void* scales, int64_t N, int64_t K,
 int mxl_pack_weight_ex(const void* codes, const void* scales, int scale_layout, int64_t N, int64_t K, int fmt,
                        void* tiled_codes, void* tiled_scales, void* stream);
 
-/* Per-call GEMM options: the activation-scale layout and the tuning overrides
+/* Per-call GEMM options: the activation-scale layout, the tuning overrides
  * of the reference's native GEMM (tactic, splits: _DEFAULT_CONFIG,
- * src/vllm_mach/mxfp8/native_backend.py:29).  A NULL options pointer means
- * {0, -1, 0, 0, 0, 0, 0}: logical scales, everything chosen by the cost model. */
+ * src/vllm_mach/mxfp8/native_backend.py:29) and the output format and scale of
+ * mxfp6::gemm_from_float / gemm_from_swiglu / gemm_w6a8_pdl (`alpha`, `dtype`,
+ * src/vllm_mach/mxfp6/dense.py:122-129, src/vllm_mach/mxfp6/fused_mlp.py:16-19).
+ * A NULL options pointer means {0, -1, 0, 0, 0, 0, 0, 0, 1.0f}: logical scales,
+ * everything chosen by the cost model, bf16 output, no scaling.  alpha must be
+ * finite and non-zero (a zero-filled struct is rejected with MXL_EINVAL). */
 typedef struct mxl_gemm_options {
   int sa_layout; /* MX activation scales: 0 logical [M, K/32], 1 swizzled */
   int kernel;    /* -1 automatic; 0 weight-streaming (M <= 16), 1 wide (M >= 64,
@@ -158,6 +162,11 @@ typedef struct mxl_gemm_options {
   int hybrid;    /* wide, splits == 1: whole-K full rounds, the remainder split */
   int waves;     /* wide MX dense with 128-row tiles: 4 waves per workgroup (each all
                     128 rows) or 8 (two per SIMD, each 64 rows); 0 automatic */
+  int out_dtype; /* output elements: 0 bf16, 1 fp16 (dense GEMMs; the grouped and
+                    two-limb GEMMs write bf16 only) */
+  float alpha;   /* output scale: out = round(alpha * sum) with the fp32 sum scaled
+                    in fp32 and rounded once to out_dtype (a bias is added after
+                    that rounding and the sum rounded again) */
 } mxl_gemm_options;
 
 /* Scratch bytes the GEMMs may use for split-K partials at (M, N, K) (the
@@ -229,6 +238,13 @@ int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, cons
                        const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
                        void* stream);
 
+/* mxl_swiglu_mx_gemm with the output format and scale of `options` (out_dtype,
+ * alpha; NULL: bf16, 1).  Replaces mxfp6::gemm_from_swiglu(gate_up, w, ws, N,
+ * alpha, dtype) (src/vllm_mach/mxfp6/fused_mlp.py:16-19). */
+int mxl_swiglu_mx_gemm_ex(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
+                          const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
+                          const mxl_gemm_options* options, void* stream);
+
 /* MXFP8 quantization -> MX GEMM for one bf16 activation row, in one launch: the weight-
  * streaming GEMM computes the row's codes and scales from x bf16 [1, K] itself, with the
  * activation quantizer's arithmetic (mxl_quantize_mxfp8, rule 0, 1 or 2), so y is
@@ -238,6 +254,13 @@ int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, cons
  * (src/vllm_mach/mxfp6/dense_mxfp8.py:89-96, src/vllm_mach/mxfp6/dense.py:122-129). */
 int mxl_quant_mx_gemm(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled, const void* sw_tiled,
                       int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc, void* stream);
+
+/* mxl_quant_mx_gemm with the output format and scale of `options` (out_dtype,
+ * alpha; NULL: bf16, 1).  Replaces mxfp6::gemm_from_float(x, w, ws, N, alpha,
+ * dtype) (src/vllm_mach/mxfp6/dense.py:122-129). */
+int mxl_quant_mx_gemm_ex(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled, const void* sw_tiled,
+                         int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
+                         const mxl_gemm_options* options, void* stream);
 
 /* Block-FP8 GEMM: y[m, n] = sum_g sa[g*M + m] * sb[(n/128) * (K/128) + g] *
  * (A_g . W_g) with fp32 FMA per K128 block, bf16 out.  A E4M3 [M, K]; W tiled
@@ -311,6 +334,18 @@ int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, int64_t E, i
  * (src/vllm_mach/mxfp6/moe.py:697-702, src/vllm_mach/mxfp6/moe_utils.py:445-488). */
 int mxl_moe_reduce(const void* routed_output, const float* topk_weights, const int32_t* inverse, int64_t T,
                    int64_t topk, int64_t H, void* out, void* stream);
+
+/* The kernels a dense GEMM call (mxl_mx_gemm_ex, block = 0; mxl_block_fp8_gemm_ex,
+ * block = 1) or a grouped GEMM call (mxl_grouped_gemm_ex, prod = 0;
+ * mxl_grouped_gemm_quant, prod = 1; mxl_grouped_gemm_swiglu, prod = 2) launches
+ * for a shape and options, named as the profiler prints them (template arguments
+ * without spaces) and joined by " + ", written NUL-terminated into buf[len].  No
+ * counterpart in the reference: a diagnostic for matching profiles to the kernels
+ * that run (the plan assumes a workspace large enough for the K split). */
+int mxl_gemm_plan_name(int64_t M, int64_t N, int64_t K, int w_fmt, int block, const mxl_gemm_options* options,
+                       char* buf, int64_t len);
+int mxl_grouped_plan_name(int64_t routed_rows, int64_t num_experts, int64_t K, int w_fmt, int prod, int rule,
+                          const mxl_gemm_options* options, char* buf, int64_t len);
 
 #ifdef __cplusplus
 }

@@ -74,6 +74,46 @@ def test_invalid_arguments_fail_before_any_launch(pkg):
     with pytest.raises(_lib.MxlError, match="invalid options"):
         _lib.call("mxl_mx_gemm_dual_ex", 16, 16, 16, 16, 1, 16, 16, 16, 128, 0, None, 16, 16, 16, 1 << 20,
                   _lib.options_ptr(_lib.GemmOptions(waves=5)), None)
+    # the output scale and format: a zero-filled struct (alpha 0) is refused, as are unknown
+    # formats and non-finite scales; the grouped and two-limb GEMMs write bf16 unscaled only
+    for bad in ({"alpha": 0.0}, {"alpha": float("inf")}, {"alpha": float("nan")}, {"out_dtype": 2}):
+        opts = _lib.GemmOptions(**bad)
+        with pytest.raises(_lib.MxlError, match="alpha must be finite"):
+            _lib.call("mxl_mx_gemm_ex", 16, 16, 1, 16, 16, 16, 128, 0, None, 16, 16, None, 0,
+                      _lib.options_ptr(opts), None)
+        with pytest.raises(_lib.MxlError, match="invalid"):
+            _lib.call("mxl_quant_mx_gemm_ex", 16, 1, 128, 0, 16, 16, 16, 0, None, 16, 16,
+                      _lib.options_ptr(opts), None)
+    with pytest.raises(_lib.MxlError, match="bf16 output without scaling only"):
+        _lib.call("mxl_grouped_gemm_ex", 16, 16, 16, None, 1, 16, 1, 16, 16, 16, 16, 128, 0, 16,
+                  _lib.options_ptr(_lib.GemmOptions(out_dtype=1)), None)
+    with pytest.raises(_lib.MxlError, match="bf16 output without scaling only"):
+        _lib.call("mxl_mx_gemm_dual_ex", 16, 16, 16, 16, 1, 16, 16, 16, 128, 0, None, 16, 16, 16, 1 << 20,
+                  _lib.options_ptr(_lib.GemmOptions(alpha=0.5)), None)
+
+
+def test_plan_names_without_gpu(pkg):
+    """The kernels a call launches, as the profiler names them: what the committed traffic
+    rows and traces are matched against.  (No GPU here: the plan assumes 256 CUs.)"""
+    from vllm_mach_amd import _lib
+    if not LIB.exists():
+        pytest.skip("libmxlinear.so not built")
+    if torch.cuda.is_available():
+        pytest.skip("the expected plans are those of a 256-CU device")
+    name = lambda *a, **k: _lib.plan_name("mxl_gemm_plan_name", *a, **k)  # noqa: E731
+    assert name(16, 2560, 9216, 0, 0) == "gemm_stream_kernel<0,2,false,false,-1>"
+    assert name(16, 2048, 2048, 0, 0) == "gemm_stream_kernel<0,1,true,false,-1>"
+    assert name(512, 2560, 9216, 0, 0).startswith("gemm_wide_kernel<0,8,")
+    wide8 = name(512, 2560, 9216, 0, 0, options=_lib.GemmOptions(waves=8))
+    assert wide8.startswith("gemm_wide_kernel<0,8,") and wide8.split(" + ")[0].endswith(",2>")
+    assert name(40, 1024, 1024, 3, 0).startswith("gemm_kernel<3,")
+    assert name(512, 2560, 9216, 0, 0, options=_lib.GemmOptions(tile_n=2, splits=3)) == \
+        "gemm_wide_kernel<0,8,2,false,false,1> + splitk_reduce8_kernel"
+    grouped = lambda *a: _lib.plan_name("mxl_grouped_plan_name", *a)  # noqa: E731
+    assert grouped(1024, 256, 2048, 2, 1, 0) == "gemm_stream_grouped_kernel<2,1,4>"
+    assert grouped(1024, 256, 512, 2, 2, 1) == "gemm_stream_grouped_kernel<2,1,9>"
+    assert grouped(16384, 256, 512, 2, 0, 0) == "gemm_stream_grouped_kernel<2,6,0>"
+    assert grouped(16384, 256, 2048, 2, 0, 0) == "gemm_wide_kernel<2,8,2,false,true,1>"
 
 
 def test_missing_library_fails_loudly(tmp_path, monkeypatch, pkg):

@@ -159,7 +159,71 @@ def test_mxfp6_gemm_from_float_e3m2(api, oracle_mod, dev, M):
     assert torch.equal(y2, y)
     y3 = torch.ops.mxfp6.gemm_from_float(x.to(dev), w, wsw, N, 0.5, torch.float16)
     assert y3.dtype == torch.float16
-    torch.testing.assert_close(y3.float(), (y.float() * 0.5).half().float(), rtol=1e-2, atol=1e-2)
+    ref16 = (oracle_mod.mx_gemm_ref(rc, rs, wc, ws, 3) * np.float32(0.5)).astype(np.float16)
+    _check(y3.float().cpu().numpy(), ref16.astype(np.float32))
+
+
+def _integer_operands(oracle_mod, M, N, K, seed):
+    """Integer-valued bf16 operands in [-7, 7]: every value is exact in MXFP8 (floor_carry175)
+    and in E3M2 (OCP floor rule), and every fp32 partial sum of their products is an integer
+    below 2^24, so any summation order gives the exact product."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randint(-7, 8, (N, K), generator=g).float().bfloat16()
+    x = torch.randint(-7, 8, (M, K), generator=g).float().bfloat16()
+    wc, ws = oracle_mod.quant_mxfp6(w, 3)
+    assert np.array_equal(oracle_mod.dequant_mx(wc, ws, 3), w.float().numpy())
+    xc, xs = oracle_mod.quant_mxfp8(x, 0)
+    assert np.array_equal(oracle_mod.dequant_mx(xc, xs, 0), x.float().numpy())
+    exact = x.double().numpy() @ w.double().numpy().T
+    assert np.abs(exact).max() < 2 ** 24
+    return x, oracle_mod.pack_fp6(wc), ws, exact
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 256])
+@pytest.mark.parametrize("dtype,alpha", [(torch.float16, 0.375), (torch.float16, 1.0), (torch.bfloat16, 0.5),
+                                         (torch.bfloat16, 1.0)])
+def test_mxfp6_output_rounds_once(api, oracle_mod, dev, M, dtype, alpha):
+    """mxfp6::gemm_from_float / gemm_w6a8_pdl / gemm_from_swiglu with (alpha, dtype): the fp32
+    sum is scaled in fp32 and rounded once to the requested dtype (src/vllm_mach/mxfp6/
+    dense.py:122-129).  With exact operands the output must equal round_dtype(alpha * exact)
+    bit for bit; a bf16 rounding on the way to fp16 would not (it keeps 8 of fp16's 11
+    significand bits).  Covers the one-row fused launch (M = 1), the weight-streaming kernel,
+    the two-call fused path (M = 4) and the wide kernel with its K split (M = 256)."""
+    N, K = 1024, 5120
+    x, wp, ws, exact = _integer_operands(oracle_mod, M, N, K, 40 + M)
+    w = torch.from_numpy(wp).to(dev)
+    wsw = api.pack_scales(torch.from_numpy(ws).to(dev))
+    expected = torch.from_numpy((exact.astype(np.float32) * np.float32(alpha))).to(dtype)
+    y = torch.ops.mxfp6.gemm_from_float(x.to(dev), w, wsw, N, alpha, dtype)
+    assert y.dtype == dtype and torch.equal(y.cpu(), expected)
+    codes, sa = torch.ops.mxfp6.quantize_mxfp8(x.to(dev))
+    y2 = torch.ops.mxfp6.gemm_w6a8_pdl(codes, w, sa, wsw, M, N, K, alpha, dtype)
+    assert torch.equal(y2, y)
+    if dtype == torch.float16 and alpha != 1.0:  # the double rounding this replaces differs
+        assert not torch.equal(y.cpu(), expected.bfloat16().to(dtype))
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_mxfp6_gemm_from_swiglu_rounds_once(api, oracle_mod, dev, M):
+    """gemm_from_swiglu with (alpha, fp16): one rounding of alpha times the GEMM of the
+    producer's codes, for the one-row launch and the two-call path."""
+    N, K = 1024, 2048
+    g = torch.Generator().manual_seed(7 + M)
+    wb = torch.randint(-7, 8, (N, K), generator=g).float().bfloat16()
+    wc, ws = oracle_mod.quant_mxfp6(wb, 3)
+    w = torch.from_numpy(oracle_mod.pack_fp6(wc)).to(dev)
+    wsw = api.pack_scales(torch.from_numpy(ws).to(dev))
+    gu = torch.randn(M, 2 * K, generator=g).bfloat16()
+    rc, rs = oracle_mod.swiglu_mxfp8(gu, oracle_mod.RULE_CEIL_DIV448)
+    y16 = torch.ops.mxfp6.gemm_from_swiglu(gu.to(dev), w, wsw, N, 0.375, torch.float16)
+    ref = oracle_mod.mx_gemm_ref(rc, rs, wc, ws, 3) * np.float32(0.375)
+    _check(y16.float().cpu().numpy(), ref.astype(np.float16).astype(np.float32))
+    # the same launch in bf16 without scaling: the fp16 output is the fp32 sum scaled and
+    # rounded once, so it carries more of the sum than the bf16 output does
+    y = torch.ops.mxfp6.gemm_from_swiglu(gu.to(dev), w, wsw, N, 1.0, torch.bfloat16)
+    e16 = np.linalg.norm(y16.double().cpu().numpy() - ref) / np.linalg.norm(ref)
+    e_bf = np.linalg.norm(y.double().cpu().numpy() * 0.375 - ref) / np.linalg.norm(ref)
+    assert e16 < 0.25 * e_bf, (e16, e_bf)
 
 
 @pytest.mark.parametrize("M", [1, 4])

@@ -78,6 +78,8 @@ def _check_gemm(got, ref):
     (32, 2048, 512, 128, 8, 2),
     (16, 2048, 512, 512, 8, 3),
     (256, 2048, 512, 128, 8, 2),   # c5 at T = 128: every expert checked
+    (256, 2048, 512, 2048, 8, 2),  # c5 at T = 2048: the default schedules (grouped wide w13,
+                                   # 96-row w2 units), every expert checked
 ])
 def test_moe_layer_matches_oracle(pkg, oracle_mod, dev, E, H, I, T, topk, fmt):
     """Each stage against the oracle on the GPU's own inputs to that stage (quantizers and

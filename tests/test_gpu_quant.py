@@ -42,7 +42,7 @@ def test_quantize_mxfp8_strided_rows(pkg, oracle_mod, dev):
     assert np.array_equal(_u8(codes), rc) and np.array_equal(_u8(scales), rs)
 
 
-@pytest.mark.parametrize("M", [1, 4, 16, 24, 32, 64])
+@pytest.mark.parametrize("M", [1, 4, 16, 24, 32, 64, 128, 512])  # 128 and 512: the c2 prefill producers
 @pytest.mark.parametrize("K", [6144, 9216])
 def test_swiglu_mxfp8_bit_exact(pkg, oracle_mod, dev, M, K):
     for magnitude in [1.0, 0.0, 1e-15, 50.0]:

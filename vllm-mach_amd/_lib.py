@@ -54,6 +54,8 @@ SIGNATURES = {
     "mxl_grouped_gemm_ex": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P, _P]),
     "mxl_swiglu_mx_gemm": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P]),
     "mxl_quant_mx_gemm": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P]),
+    "mxl_swiglu_mx_gemm_ex": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P, _P]),
+    "mxl_quant_mx_gemm_ex": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P, _P]),
     "mxl_block_fp8_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
     "mxl_grouped_gemm": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P]),
     "mxl_grouped_fused_supported": (_I, [_I64, _I64, _I64, _I]),
@@ -62,15 +64,19 @@ SIGNATURES = {
     "mxl_moe_route_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "mxl_moe_route": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "mxl_moe_reduce": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    "mxl_gemm_plan_name": (_I, [_I64, _I64, _I64, _I, _I, _P, ctypes.c_char_p, _I64]),
+    "mxl_grouped_plan_name": (_I, [_I64, _I64, _I64, _I, _I, _I, _P, ctypes.c_char_p, _I64]),
 }
 
 class GemmOptions(ctypes.Structure):
-    """``mxl_gemm_options``: activation-scale layout and tuning overrides of one GEMM call."""
+    """``mxl_gemm_options``: activation-scale layout, tuning overrides and output format of one
+    GEMM call (out_dtype 0 bf16, 1 fp16; alpha the output scale)."""
     _fields_ = [("sa_layout", _I), ("kernel", _I), ("splits", _I), ("tile_n", _I), ("tile_m", _I),
-                ("hybrid", _I), ("waves", _I)]
+                ("hybrid", _I), ("waves", _I), ("out_dtype", _I), ("alpha", _F)]
 
-    def __init__(self, sa_layout=0, kernel=-1, splits=0, tile_n=0, tile_m=0, hybrid=0, waves=0):
-        super().__init__(sa_layout, kernel, splits, tile_n, tile_m, hybrid, waves)
+    def __init__(self, sa_layout=0, kernel=-1, splits=0, tile_n=0, tile_m=0, hybrid=0, waves=0, out_dtype=0,
+                 alpha=1.0):
+        super().__init__(sa_layout, kernel, splits, tile_n, tile_m, hybrid, waves, out_dtype, alpha)
 
 
 def options_ptr(opts: "GemmOptions | None"):
@@ -117,6 +123,13 @@ def query(name: str, *args):
 
 def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def plan_name(fn: str, *args, options: "GemmOptions | None" = None) -> str:
+    """The kernels ``mxl_gemm_plan_name`` / ``mxl_grouped_plan_name`` report for a call."""
+    buf = ctypes.create_string_buffer(512)
+    call(fn, *args, options_ptr(options), buf, len(buf))
+    return buf.value.decode()
 
 
 def stream_handle(device: torch.device) -> int:

@@ -40,6 +40,9 @@
 // that a second kernel sums in split order: both orders are fixed, so every
 // result is deterministic.
 #include <mutex>
+#include <string>
+#include <string.h>
+#include <stdio.h>
 
 #include "gemm_common.h"
 
@@ -148,11 +151,11 @@ __device__ __forceinline__ void compute_tile(const GemmParams& p, const ATile<MT
   }
 }
 
-// Write one 16x16 fp32 tile (lane holds rows 4q+i, col r) to bf16 output or fp32 partials.
+// Write one 16x16 fp32 tile (lane holds rows 4q+i, col r) to the output or fp32 partials.
 __device__ __forceinline__ void store_tile(const GemmParams& p, v4f v, int64_t row0, int64_t row_hi,
                                            int64_t col, int64_t split) {
   if (col >= p.N) return;
-  float bias = p.bias ? bf16_to_f32(p.bias[col]) : 0.0f;
+  const uint16_t bias = p.bias ? p.bias[col] : (uint16_t)0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t row = row0 + i;
@@ -160,9 +163,7 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, v4f v, int64_t r
     if (p.S > 1) {
       p.partial[(split * p.a_rows + row) * p.N + col] = v[i];
     } else {
-      float y = bf16_round(v[i]);
-      if (p.bias) y = y + bias;
-      p.out[row * p.ldc + col] = f32_to_bf16(y);
+      p.out[row * p.ldc + col] = out_bits(v[i], p.alpha, p.out_f16, p.bias != nullptr, bias);
     }
   }
 }
@@ -255,9 +256,7 @@ __global__ __launch_bounds__(MT == 1 && NT == 1 ? 1024 : 512) void gemm_kernel(G
           if (p.S > 1) {
             p.partial[(split * p.a_rows + row) * p.N + col] = s;
           } else {
-            float y = bf16_round(s);
-            if (p.bias) y = y + bf16_to_f32(p.bias[col]);
-            p.out[row * p.ldc + col] = f32_to_bf16(y);
+            p.out[row * p.ldc + col] = out_bits(p, s, col);
           }
         }
       }
@@ -273,17 +272,17 @@ __global__ __launch_bounds__(MT == 1 && NT == 1 ? 1024 : 512) void gemm_kernel(G
   }
 }
 
-// Sum split-K partials in split order, round to bf16, add bias in bf16.
+// Sum split-K partials in split order, then the output rounding (out_bits: alpha, the
+// output format, the bias added after the rounding).
 __global__ void splitk_reduce_kernel(const float* __restrict__ partial, const uint16_t* __restrict__ bias,
-                                     uint16_t* __restrict__ out, int64_t M, int64_t N, int64_t ldc, int S) {
+                                     uint16_t* __restrict__ out, int64_t M, int64_t N, int64_t ldc, int S,
+                                     float alpha, int f16) {
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= M * N) return;
   const int64_t m = id / N, n = id - m * N;
   float s = partial[id];
   for (int k = 1; k < S; ++k) s += partial[(int64_t)k * M * N + id];
-  float y = bf16_round(s);
-  if (bias) y = y + bf16_to_f32(bias[n]);
-  out[m * ldc + n] = f32_to_bf16(y);
+  out[m * ldc + n] = out_bits(s, alpha, f16, bias != nullptr, bias ? bias[n] : (uint16_t)0);
 }
 
 // The same sum, eight columns per thread (N, ldc multiples of 8, 16-byte aligned
@@ -292,7 +291,7 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ partial, const ui
 __global__ __launch_bounds__(256) void splitk_reduce8_kernel(const float* __restrict__ partial,
                                                              const uint16_t* __restrict__ bias,
                                                              uint16_t* __restrict__ out, int64_t M, int64_t N,
-                                                             int64_t ldc, int S) {
+                                                             int64_t ldc, int S, float alpha, int f16) {
   const int64_t n8 = N / 8;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= M * n8) return;
@@ -303,26 +302,26 @@ __global__ __launch_bounds__(256) void splitk_reduce8_kernel(const float* __rest
   uint32_t h[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    float y0 = bf16_round(f[2 * k]), y1 = bf16_round(f[2 * k + 1]);
-    if (bias) {
-      y0 = y0 + bf16_to_f32(bias[n + 2 * k]);
-      y1 = y1 + bf16_to_f32(bias[n + 2 * k + 1]);
-    }
-    h[k] = (uint32_t)f32_to_bf16(y0) | ((uint32_t)f32_to_bf16(y1) << 16);
+    const bool b = bias != nullptr;
+    const uint16_t h0 = out_bits(f[2 * k], alpha, f16, b, b ? bias[n + 2 * k] : (uint16_t)0);
+    const uint16_t h1 = out_bits(f[2 * k + 1], alpha, f16, b, b ? bias[n + 2 * k + 1] : (uint16_t)0);
+    h[k] = (uint32_t)h0 | ((uint32_t)h1 << 16);
   }
   *reinterpret_cast<uint4*>(out + m * ldc + n) = uint4{h[0], h[1], h[2], h[3]};
 }
 
 // Launch the split-K sum: vectorized when the shapes and buffers allow it.
 hipError_t launch_splitk_reduce(const float* partial, const uint16_t* bias, uint16_t* out, int64_t M, int64_t N,
-                                int64_t ldc, int S, hipStream_t s) {
+                                int64_t ldc, int S, hipStream_t s, float alpha, int f16) {
   const bool vec = N % 8 == 0 && ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(partial) & 15) == 0;
   if (vec) {
     const int64_t items = M * (N / 8);
-    splitk_reduce8_kernel<<<dim3((unsigned)((items + 255) / 256)), 256, 0, s>>>(partial, bias, out, M, N, ldc, S);
+    splitk_reduce8_kernel<<<dim3((unsigned)((items + 255) / 256)), 256, 0, s>>>(partial, bias, out, M, N, ldc, S,
+                                                                               alpha, f16);
   } else {
-    splitk_reduce_kernel<<<dim3((unsigned)((M * N + 255) / 256)), 256, 0, s>>>(partial, bias, out, M, N, ldc, S);
+    splitk_reduce_kernel<<<dim3((unsigned)((M * N + 255) / 256)), 256, 0, s>>>(partial, bias, out, M, N, ldc, S,
+                                                                              alpha, f16);
   }
   return hipGetLastError();
 }
@@ -444,26 +443,44 @@ static int pack_common(const void* codes, const void* scales, int scale_layout, 
 }
 
 // The option fields a call may set: anything else is an argument error, not a default.
+// An output scale must be finite and non-zero: a zero-filled options struct (alpha 0) is
+// a caller's mistake, not a request for zeros.
+static bool epilogue_valid(const GemmOptions& o) {
+  return (o.out_dtype == kOutBf16 || o.out_dtype == kOutF16) && o.alpha == o.alpha && o.alpha != 0.0f &&
+         o.alpha - o.alpha == 0.0f;
+}
+
 static bool options_valid(const GemmOptions& o, const char* who) {
   const bool ok = (o.sa_layout == 0 || o.sa_layout == 1) && o.kernel >= kAuto && o.kernel <= kStreamWide &&
                   o.splits >= 0 && o.splits <= 64 && (o.tile_n == 0 || o.tile_n == 1 || o.tile_n == 2 ||
                   o.tile_n == 4) && (o.tile_m == 0 || o.tile_m == 4 || o.tile_m == 8) &&
-                  (o.hybrid == 0 || o.hybrid == 1) && (o.waves == 0 || o.waves == 4 || o.waves == 8);
+                  (o.hybrid == 0 || o.hybrid == 1) && (o.waves == 0 || o.waves == 4 || o.waves == 8) &&
+                  epilogue_valid(o);
   if (!ok)
-    set_error("%s: invalid options {sa_layout %d, kernel %d, splits %d, tile_n %d, tile_m %d, hybrid %d, waves %d}",
-              who, o.sa_layout, o.kernel, o.splits, o.tile_n, o.tile_m, o.hybrid, o.waves);
+    set_error("%s: invalid options {sa_layout %d, kernel %d, splits %d, tile_n %d, tile_m %d, hybrid %d, waves %d, "
+              "out_dtype %d, alpha %g} (alpha must be finite and non-zero: 1 for no scaling)",
+              who, o.sa_layout, o.kernel, o.splits, o.tile_n, o.tile_m, o.hybrid, o.waves, o.out_dtype,
+              (double)o.alpha);
   return ok;
 }
+
+// The C ABI's mxl_gemm_options (include/mxlinear.h), field for field.
+struct AbiGemmOptions {
+  int sa_layout, kernel, splits, tile_n, tile_m, hybrid, waves, out_dtype;
+  float alpha;
+};
 
 static GemmOptions options_of(const void* opts) {
   GemmOptions o;
   if (opts) {
-    const int* v = static_cast<const int*>(opts);  // mxl_gemm_options: seven ints in declaration order
-    o.sa_layout = v[0]; o.kernel = v[1]; o.splits = v[2]; o.tile_n = v[3]; o.tile_m = v[4]; o.hybrid = v[5];
-    o.waves = v[6];
+    const AbiGemmOptions& v = *static_cast<const AbiGemmOptions*>(opts);
+    o.sa_layout = v.sa_layout; o.kernel = v.kernel; o.splits = v.splits; o.tile_n = v.tile_n; o.tile_m = v.tile_m;
+    o.hybrid = v.hybrid; o.waves = v.waves; o.out_dtype = v.out_dtype; o.alpha = v.alpha;
   }
   return o;
 }
+
+static bool default_epilogue(const GemmOptions& o) { return o.out_dtype == kOutBf16 && o.alpha == 1.0f; }
 
 // The dense kernel and split a call runs with (shared by the launch and the workspace
 // query, so that the bytes the query reports are the bytes the launch uses).
@@ -515,6 +532,8 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
   p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out; p.partial = (float*)workspace;
   p.lda = K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
   p.row_div = 1;
+  p.alpha = o.alpha;
+  p.out_f16 = o.out_dtype == kOutF16;
   set_sa_layout(p, o.sa_layout);
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
@@ -545,7 +564,8 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
     return MXL_EHIP;
   }
   if (p.S > 1) {
-    e = launch_splitk_reduce((const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, p.S, s);
+    e = launch_splitk_reduce((const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, p.S, s,
+                             p.alpha, p.out_f16);
     if (e != hipSuccess) {
       set_error("%s: split-K reduce launch failed: %s", who, hipGetErrorString(e));
       return MXL_EHIP;
@@ -663,10 +683,12 @@ extern "C" int mxl_mx_gemm_noalloc(const void* a, const void* sa, int64_t M, con
                      GemmOptions(), stream, who);
 }
 
-extern "C" int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
-                                  const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out,
-                                  int64_t ldc, void* stream) {
+static int swiglu_row_common(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
+                             const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
+                             const GemmOptions& o, void* stream) {
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_swiglu_mx_gemm: unknown weight format %d", w_fmt);
+  MXL_CHECK_ARG(epilogue_valid(o), "mxl_swiglu_mx_gemm: output format %d / alpha %g invalid", o.out_dtype,
+                (double)o.alpha);
   MXL_CHECK_ARG(N > 0 && ldc >= N, "mxl_swiglu_mx_gemm: need N > 0 and ldc >= N");
   MXL_CHECK_ARG(((uintptr_t)gate_up & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
                 "mxl_swiglu_mx_gemm: gate_up and w must be 16-byte aligned");
@@ -680,6 +702,7 @@ extern "C" int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int
   p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled; p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out;
   p.lda = 2 * K; p.ldc = ldc; p.M = 1; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = 1;
   p.row_div = 1; p.S = 1;
+  p.alpha = o.alpha; p.out_f16 = o.out_dtype == kOutF16;
   const hipError_t e = launch_gemm_stream_swiglu(w_fmt, rule, p, (hipStream_t)stream);
   if (e != hipSuccess) {
     set_error("mxl_swiglu_mx_gemm: launch failed: %s", hipGetErrorString(e));
@@ -688,10 +711,25 @@ extern "C" int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int
   return MXL_OK;
 }
 
-extern "C" int mxl_quant_mx_gemm(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled,
-                                 const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
-                                 void* stream) {
+extern "C" int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
+                                  const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out,
+                                  int64_t ldc, void* stream) {
+  return swiglu_row_common(gate_up, M, K, rule, w_tiled, sw_tiled, N, w_fmt, bias, out, ldc, GemmOptions(), stream);
+}
+
+extern "C" int mxl_swiglu_mx_gemm_ex(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
+                                     const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out,
+                                     int64_t ldc, const void* options, void* stream) {
+  return swiglu_row_common(gate_up, M, K, rule, w_tiled, sw_tiled, N, w_fmt, bias, out, ldc, options_of(options),
+                           stream);
+}
+
+static int quant_row_common(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled, const void* sw_tiled,
+                            int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc, const GemmOptions& o,
+                            void* stream) {
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_quant_mx_gemm: unknown weight format %d", w_fmt);
+  MXL_CHECK_ARG(epilogue_valid(o), "mxl_quant_mx_gemm: output format %d / alpha %g invalid", o.out_dtype,
+                (double)o.alpha);
   MXL_CHECK_ARG(N > 0 && ldc >= N, "mxl_quant_mx_gemm: need N > 0 and ldc >= N");
   MXL_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
                 "mxl_quant_mx_gemm: x and w must be 16-byte aligned");
@@ -705,12 +743,25 @@ extern "C" int mxl_quant_mx_gemm(const void* x, int64_t M, int64_t K, int rule, 
   p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled; p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out;
   p.lda = K; p.ldc = ldc; p.M = 1; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = 1;
   p.row_div = 1; p.S = 1;
+  p.alpha = o.alpha; p.out_f16 = o.out_dtype == kOutF16;
   const hipError_t e = launch_gemm_stream_quant_row(w_fmt, rule, p, (hipStream_t)stream);
   if (e != hipSuccess) {
     set_error("mxl_quant_mx_gemm: launch failed: %s", hipGetErrorString(e));
     return MXL_EHIP;
   }
   return MXL_OK;
+}
+
+extern "C" int mxl_quant_mx_gemm(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled,
+                                 const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
+                                 void* stream) {
+  return quant_row_common(x, M, K, rule, w_tiled, sw_tiled, N, w_fmt, bias, out, ldc, GemmOptions(), stream);
+}
+
+extern "C" int mxl_quant_mx_gemm_ex(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled,
+                                    const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out,
+                                    int64_t ldc, const void* options, void* stream) {
+  return quant_row_common(x, M, K, rule, w_tiled, sw_tiled, N, w_fmt, bias, out, ldc, options_of(options), stream);
 }
 
 static int gemm_dual_common(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,
@@ -720,6 +771,7 @@ static int gemm_dual_common(const void* hi, const void* s_hi, const void* res, c
   MXL_CHECK_ARG(valid_wfmt(w_fmt), "mxl_mx_gemm_dual: unknown weight format %d", w_fmt);
   MXL_CHECK_ARG(o.sa_layout == 0 || o.sa_layout == 1, "mxl_mx_gemm_dual: sa_layout must be 0 or 1");
   if (!options_valid(o, "mxl_mx_gemm_dual")) return MXL_EINVAL;
+  MXL_CHECK_ARG(default_epilogue(o), "mxl_mx_gemm_dual: bf16 output without scaling only");
   MXL_CHECK_ARG(M >= 0 && M <= 64 && N > 0 && K > 0 && K % 128 == 0,
                 "mxl_mx_gemm_dual: need M <= 64, N > 0, K %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
                 (long long)N, (long long)K);
@@ -748,7 +800,8 @@ static int gemm_dual_common(const void* hi, const void* s_hi, const void* res, c
     set_error("mxl_mx_gemm_dual: launch failed: %s", hipGetErrorString(e));
     return MXL_EHIP;
   }
-  e = launch_splitk_reduce((const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, 2, s);
+  e = launch_splitk_reduce((const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, 2, s, 1.0f,
+                           kOutBf16);
   if (e != hipSuccess) {
     set_error("mxl_mx_gemm_dual: split-K reduce launch failed: %s", hipGetErrorString(e));
     return MXL_EHIP;
@@ -856,6 +909,31 @@ static int grouped_common(const void* a, const void* sa, int64_t a_rows, const i
                           const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, void* out,
                           const GemmOptions& o, void* stream);
 
+// The grouped schedule a call runs (shared by the launch and the plan query).
+struct GroupedPlan {
+  int kernel;     // kStream (weight-streaming units of 16 stream_mt rows), kWide or kGeneric
+  int stream_mt;  // 1 or kGroupedStreamWideMT with kStream
+  int MT;         // kWide: 16-row tiles per block
+};
+
+static GroupedPlan plan_grouped(int64_t a_rows, int64_t num_experts, int64_t routed_rows, int64_t K, int w_fmt,
+                                const GemmOptions& o) {
+  const int force = o.kernel;
+  int stream_mt = 0;
+  if (force == kStream || force == kStreamWide) {
+    stream_mt = force == kStream ? 1 : kGroupedStreamWideMT;
+  } else if (force == kAuto) {
+    if (routed_rows < 32 * num_experts) stream_mt = 1;
+    else if (routed_rows <= 96 * num_experts && K <= kTileK) stream_mt = kGroupedStreamWideMT;
+  }
+  if (stream_mt && !stream_grouped_eligible(K, num_experts, w_fmt, stream_mt)) stream_mt = 0;
+  const bool wide_ok = K % 256 == 0 && a_rows * K < (int64_t(1) << 32) && num_experts <= kWideGroupedMaxExperts;
+  if (!stream_mt && force != kGeneric && wide_ok && (force == kWide || routed_rows >= 32 * num_experts))
+    return GroupedPlan{kWide, 0, o.tile_m == 4 ? 4 : 8};
+  if (stream_mt) return GroupedPlan{kStream, stream_mt, 0};
+  return GroupedPlan{kGeneric, 0, 0};
+}
+
 extern "C" int mxl_grouped_gemm(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index, int row_div,
                                 const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
                                 const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
@@ -891,17 +969,10 @@ static int grouped_common(const void* a, const void* sa, int64_t a_rows, const i
   MXL_CHECK_ARG(o.kernel >= kAuto && o.kernel <= kStreamWide, "mxl_grouped_gemm: unknown kernel %d", o.kernel);
   MXL_CHECK_ARG(o.sa_layout == 0, "mxl_grouped_gemm: grouped activations take logical scales");
   if (!options_valid(o, "mxl_grouped_gemm")) return MXL_EINVAL;
-  const int force = o.kernel;
-  int stream_mt = 0;
-  if (force == kStream || force == kStreamWide) {
-    stream_mt = force == kStream ? 1 : kGroupedStreamWideMT;
-  } else if (force == kAuto) {
-    if (routed_rows < 32 * num_experts) stream_mt = 1;
-    else if (routed_rows <= 96 * num_experts && K <= kTileK) stream_mt = kGroupedStreamWideMT;
-  }
-  if (stream_mt && !stream_grouped_eligible(K, num_experts, w_fmt, stream_mt)) stream_mt = 0;
-  const bool wide_ok = K % 256 == 0 && a_rows * K < (int64_t(1) << 32) && num_experts <= kWideGroupedMaxExperts;
-  if (!stream_mt && force != kGeneric && wide_ok && (force == kWide || routed_rows >= 32 * num_experts)) {
+  MXL_CHECK_ARG(default_epilogue(o), "mxl_grouped_gemm: bf16 output without scaling only");
+  const GroupedPlan gp = plan_grouped(a_rows, num_experts, routed_rows, K, w_fmt, o);
+  const int stream_mt = gp.stream_mt;
+  if (gp.kernel == kWide) {
     // enough rows per expert on average for 128-row blocks: the wide kernel
     GemmParams p{};
     p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;
@@ -913,7 +984,7 @@ static int grouped_common(const void* a, const void* sa, int64_t a_rows, const i
     WideConfig wc{2, 1, (K + kTileK - 1) / kTileK};
     // 128-row blocks: with 64 rows per expert on average (c5, T = 2048) 64-row blocks
     // measured 8-10 % slower, since experts past 64 rows then copy their weights twice
-    wc.MT = o.tile_m == 4 ? 4 : 8;
+    wc.MT = gp.MT;
     hipError_t e = launch_gemm_wide(w_fmt, false, wc, p, num_experts, (hipStream_t)stream);
     if (e != hipSuccess) {
       set_error("mxl_grouped_gemm: launch failed: %s", hipGetErrorString(e));
@@ -955,4 +1026,71 @@ static int grouped_common(const void* a, const void* sa, int64_t a_rows, const i
     return MXL_EHIP;
   }
   return MXL_OK;
+}
+
+// ------------------------------------------------------------------ plan names
+
+// The kernels a call launches, named as the profiler prints them (template arguments
+// without spaces), joined by " + ".  For matching profiles to the code that runs.
+static int plan_name_out(const std::string& name, char* buf, int64_t len) {
+  MXL_CHECK_ARG(buf && len > (int64_t)name.size(), "plan name needs %lld bytes", (long long)name.size() + 1);
+  memcpy(buf, name.c_str(), name.size() + 1);
+  return MXL_OK;
+}
+
+static const char* tf(bool b) { return b ? "true" : "false"; }
+
+extern "C" int mxl_gemm_plan_name(int64_t M, int64_t N, int64_t K, int w_fmt, int block, const void* options,
+                                  char* buf, int64_t len) {
+  MXL_CHECK_ARG(M > 0 && N > 0 && K > 0 && K % 128 == 0 && valid_wfmt(w_fmt), "mxl_gemm_plan_name: bad shape");
+  const GemmOptions o = options_of(options);
+  if (!options_valid(o, "mxl_gemm_plan_name")) return MXL_EINVAL;
+  DensePlan d;
+  if (!plan_dense(M, N, K, w_fmt, block != 0, o, d)) {
+    set_error("mxl_gemm_plan_name: kernel %d does not run this shape", o.kernel);
+    return MXL_EUNSUPPORTED;
+  }
+  char k[160];
+  std::string name;
+  const int64_t KT = (K + kTileK - 1) / kTileK;
+  int S = 1;
+  if (d.kernel == kStream) {
+    const bool db = KT <= stream_max_waves(block != 0);
+    snprintf(k, sizeof k, "gemm_stream_kernel<%d,%d,%s,%s,-1>", w_fmt, db ? 1 : 2, tf(db), tf(block != 0));
+    name = k;
+  } else if (d.kernel == kWide) {
+    snprintf(k, sizeof k, "gemm_wide_kernel<%d,%d,%d,%s,false,%d>", w_fmt, d.wide.MT, d.wide.NT, tf(block != 0),
+             d.wide.WM);
+    name = k;
+    if (d.wide.dp_tiles > 0) name += " + wide_tile_reduce_kernel";
+    S = d.wide.S;
+  } else {
+    snprintf(k, sizeof k, "gemm_kernel<%d,%d,%d,%s,false>", w_fmt, d.gen.MT, d.gen.NT, tf(block != 0));
+    name = k;
+    S = d.gen.S;
+  }
+  if (S > 1) name += N % 8 == 0 ? " + splitk_reduce8_kernel" : " + splitk_reduce_kernel";
+  return plan_name_out(name, buf, len);
+}
+
+extern "C" int mxl_grouped_plan_name(int64_t routed_rows, int64_t num_experts, int64_t K, int w_fmt, int prod,
+                                     int rule, const void* options, char* buf, int64_t len) {
+  MXL_CHECK_ARG(routed_rows > 0 && num_experts > 0 && K > 0 && K % 128 == 0 && valid_wfmt(w_fmt) && prod >= 0 &&
+                    prod <= 2,
+                "mxl_grouped_plan_name: bad shape");
+  const GemmOptions o = options_of(options);
+  if (!options_valid(o, "mxl_grouped_plan_name")) return MXL_EINVAL;
+  char k[160];
+  if (prod) {  // the fused producers run the 16-row units
+    snprintf(k, sizeof k, "gemm_stream_grouped_kernel<%d,1,%d>", w_fmt, 4 * prod + rule);
+    return plan_name_out(k, buf, len);
+  }
+  const GroupedPlan gp = plan_grouped(routed_rows, num_experts, routed_rows, K, w_fmt, o);
+  if (gp.kernel == kWide)
+    snprintf(k, sizeof k, "gemm_wide_kernel<%d,%d,2,false,true,1>", w_fmt, gp.MT);
+  else if (gp.kernel == kStream)
+    snprintf(k, sizeof k, "gemm_stream_grouped_kernel<%d,%d,0>", w_fmt, gp.stream_mt);
+  else
+    snprintf(k, sizeof k, "gemm_kernel<%d,1,1,false,true>", w_fmt);
+  return plan_name_out(k, buf, len);
 }

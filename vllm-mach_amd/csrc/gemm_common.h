@@ -35,7 +35,36 @@ struct GemmParams {
   int row_div, S;
   int sa_swz = 0;     // MX activation scales: 0 logical [rows, K/32], 1 swizzled 128 x 4 tiles
   int64_t sa_ss = 4;  // bytes between the scale dwords of consecutive K128 slices of a row (4 or 512)
+  float alpha = 1.0f;  // output scale, applied to the fp32 sum before its one rounding
+  int out_f16 = 0;     // output element format: 0 bf16, 1 fp16
 };
+
+// Output element formats (mxl_gemm_options.out_dtype).
+enum OutFmt : int { kOutBf16 = 0, kOutF16 = 1 };
+
+// round-to-nearest-even binary32 -> binary16 (v_cvt_f16_f32: overflow to infinity,
+// subnormal results kept), NaN -> 0x7E00
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return f != f ? (uint16_t)0x7E00 : __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// The bits of one output element from its fp32 sum v: alpha v rounded once to the output
+// format; with a bias (bf16 bits, `has_bias`) the rounded value plus the bias in binary32,
+// rounded again (y + bias in the output format).  alpha = 1 leaves v unchanged, so a bf16
+// output without scaling is f32_to_bf16(v).
+__device__ __forceinline__ uint16_t out_bits(float v, float alpha, int f16, bool has_bias, uint16_t bias) {
+  const float y = v * alpha;
+  if (!f16) {
+    const uint16_t h = f32_to_bf16(y);
+    return has_bias ? f32_to_bf16(bf16_to_f32(h) + bf16_to_f32(bias)) : h;
+  }
+  const uint16_t h = f32_to_f16(y);
+  return has_bias ? f32_to_f16(f16_to_f32(h) + bf16_to_f32(bias)) : h;
+}
+__device__ __forceinline__ uint16_t out_bits(const GemmParams& p, float v, int64_t col) {
+  return out_bits(v, p.alpha, p.out_f16, p.bias != nullptr, p.bias ? p.bias[col] : (uint16_t)0);
+}
 
 // Byte offset of row `row`'s scale dword of K128 slice 0; slice s is sa_ss bytes further.
 // Logical: row * K/32.  Swizzled (the reference's activation layout, 128-row x 4-group
@@ -99,6 +128,8 @@ struct GemmOptions {
   int tile_m = 0;     // wide: MT in {4, 8}; 0 auto
   int hybrid = 0;     // wide, splits == 1: full rounds whole-K, the remainder split
   int waves = 0;      // wide MX dense, 128-row tiles: 4 or 8 waves per workgroup; 0 auto
+  int out_dtype = kOutBf16;  // output element format
+  float alpha = 1.0f;        // output scale
 };
 
 template <int MT>
@@ -240,6 +271,8 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
 
 // Weight-streaming kernel for decode-sized M (gemm_stream.hip), MX or block-FP8.
 bool stream_gemm_eligible(int64_t M, int64_t K, bool block);
+// Most K super-tiles the one-super-tile-per-wave variant takes (more: two per wave).
+int stream_max_waves(bool block);
 hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s);
 // One activation row computed from its bf16 gate/up row inside the weight-streaming
 // GEMM (p.a = gate_up, M = 1, SwiGLU rule 1 or 2)

@@ -338,7 +338,7 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
       if (!in) a[u][j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
     }
 
-  // reduce the W wave partials of n-tile nt (buffer `buf`) and store bf16
+  // reduce the W wave partials of n-tile nt (buffer `buf`) and store the output elements
   auto finish = [&](const v4f& acc, uint32_t bias_bits, int64_t nt, int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[buf][wv][i][lane] = acc[i];
@@ -350,11 +350,8 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
       float sum = red[buf][0][i][l];
       for (int v = 1; v < W; ++v) sum += red[buf][v][i][l];
       const int64_t row = 4 * (l >> 4) + i, col = nt * 16 + (l & 15);
-      if (row < p.M && col < p.N) {
-        float y = bf16_round(sum);
-        if (p.bias) y = y + bf16_to_f32((uint16_t)bias_bits);
-        p.out[row * p.ldc + col] = f32_to_bf16(y);
-      }
+      if (row < p.M && col < p.N)
+        p.out[row * p.ldc + col] = out_bits(sum, p.alpha, p.out_f16, p.bias != nullptr, (uint16_t)bias_bits);
     }
   };
 
@@ -900,6 +897,8 @@ hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_
   if (mt == kGroupedStreamWideMT) return launch_grouped_mt<kGroupedStreamWideMT>(fmt, p, num_experts, prod, rule, s);
   return hipErrorInvalidValue;
 }
+
+int stream_max_waves(bool block) { return block ? kStreamBlockMaxWaves : kStreamMaxWaves; }
 
 hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s) {
   const int64_t ntiles = (p.N + 15) / 16;

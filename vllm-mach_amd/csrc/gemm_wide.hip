@@ -554,8 +554,10 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
         for (int k = 0; k < 4 && col + k < p.N; ++k) dst[k] = f[k];
       }
     }
-  } else {  // bf16 out (bias added in bf16), 8 columns per piece
+  } else {  // output elements (out_bits: alpha, format, bias), 8 columns per piece
     const bool vec = p.ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+    // bf16 without scale or bias: paired conversions
+    const bool plain = !p.out_f16 && p.alpha == 1.0f && !p.bias;
     if (vec && col0 + TW <= p.N) {
       constexpr int P = BM * (TW / 8) / kThreads;
 #pragma unroll
@@ -574,16 +576,14 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
           const int rr = c / (TW / 8), cc = (c % (TW / 8)) * 8;
           float f[8] = {v[k][0].x, v[k][0].y, v[k][0].z, v[k][0].w, v[k][1].x, v[k][1].y, v[k][1].z, v[k][1].w};
           uint32_t h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
-          if (p.bias) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float y = u2f(e & 1 ? h[e >> 1] & 0xFFFF0000u : h[e >> 1] << 16);
-              f[e] = y + bf16_to_f32(p.bias[col0 + cc + e]);
-            }
+          if (plain) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) h[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              h[e] = (uint32_t)out_bits(p, f[2 * e], col0 + cc + 2 * e) |
+                     ((uint32_t)out_bits(p, f[2 * e + 1], col0 + cc + 2 * e + 1) << 16);
           }
           if (row_base + rr < hi)
             *reinterpret_cast<uint4*>(p.out + (row_base + rr) * p.ldc + col0 + cc) = uint4{h[0], h[1], h[2], h[3]};
@@ -599,16 +599,16 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
       const float4 v1 = *reinterpret_cast<const float4*>(tile + rr * ST + cc + 4);
       float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
       uint32_t h[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) h[k] = pack_bf16x2(f[2 * k], f[2 * k + 1]);
-      if (p.bias) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float y = u2f(k & 1 ? h[k >> 1] & 0xFFFF0000u : h[k >> 1] << 16);
-          f[k] = y + bf16_to_f32(p.bias[col + k < p.N ? col + k : p.N - 1]);
-        }
+      if (plain) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) h[k] = pack_bf16x2(f[2 * k], f[2 * k + 1]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int64_t c0 = col + 2 * k < p.N ? col + 2 * k : p.N - 1;
+          const int64_t c1 = col + 2 * k + 1 < p.N ? col + 2 * k + 1 : p.N - 1;
+          h[k] = (uint32_t)out_bits(p, f[2 * k], c0) | ((uint32_t)out_bits(p, f[2 * k + 1], c1) << 16);
+        }
       }
       uint16_t* dst = p.out + row * p.ldc + col;
       if (vec && col + 8 <= p.N) {
@@ -747,13 +747,14 @@ __global__ __launch_bounds__(256 * WM, GROUPED ? 2 : 1) void gemm_wide_kernel(Ge
 }
 
 // Sum the compact split partials of output tiles [tile0, tile0 + tiles) in split
-// order, round to bf16, add the bias in bf16 (the split-K reduce's arithmetic).
-// One thread per 8 columns of one tile row.
+// order, then the output rounding (out_bits: alpha, format, bias; the split-K reduce's
+// arithmetic).  One thread per 8 columns of one tile row.
 __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __restrict__ partial,
                                                                const uint16_t* __restrict__ bias,
                                                                uint16_t* __restrict__ out, int64_t M, int64_t N,
                                                                int64_t ldc, int64_t mblocks, int64_t tile0,
-                                                               int64_t tiles, int S, int BM, int TW) {
+                                                               int64_t tiles, int S, int BM, int TW, float alpha,
+                                                               int f16) {
   const int64_t per_tile = (int64_t)BM * (TW / 8);
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= tiles * per_tile) return;
@@ -767,11 +768,8 @@ __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __re
   const float f[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   uint16_t h[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    float y = bf16_round(f[k]);
-    if (bias) y = y + bf16_to_f32(bias[col + k < N ? col + k : N - 1]);
-    h[k] = f32_to_bf16(y);
-  }
+  for (int k = 0; k < 8; ++k)
+    h[k] = out_bits(f[k], alpha, f16, bias != nullptr, bias ? bias[col + k < N ? col + k : N - 1] : (uint16_t)0);
   uint16_t* dst = out + row * ldc + col;
   if (col + 8 <= N && ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
     *reinterpret_cast<uint4*>(dst) = uint4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
@@ -976,7 +974,8 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
   if (e != hipSuccess) return e;
   const int64_t items = gd.rem_tiles * bm * (64 * c.NT / 8);
   wide_tile_reduce_kernel<<<dim3((unsigned)((items + 255) / 256)), 256, 0, s>>>(
-      p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, gd.rem_tile0, gd.rem_tiles, c.S2, (int)bm, 64 * c.NT);
+      p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, gd.rem_tile0, gd.rem_tiles, c.S2, (int)bm, 64 * c.NT,
+      p.alpha, p.out_f16);
   return hipGetLastError();
 }
 

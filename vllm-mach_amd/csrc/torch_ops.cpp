@@ -18,14 +18,18 @@
 // scales, swizzled E8M0 weight scales); the GEMMs read an MFMA-tiled copy made
 // once per weight (the repack the reference does at load time) and cached,
 // keyed by the weight's and scale's storage, invalidated when either tensor's
-// version changes.  A cache miss or a workspace that must grow during HIP graph
-// capture raises: warm every shape first, as the reference requires
-// (native_backend.py:159-169).
+// version changes; an entry whose weight or scale storage has been freed is
+// dropped by the next calls (each call checks a few entries, a cache miss all of
+// them), so a freed weight's copy does not outlive it.  A cache miss or a
+// workspace that must grow during HIP graph capture raises: warm every shape on
+// the capture stream first, as the reference requires (native_backend.py:159-170).
 #include <ATen/ATen.h>
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 #include <torch/library.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <map>
 #include <mutex>
@@ -74,6 +78,7 @@ struct TensorStamp {
     if (!storage || storage->expired() || ptr != t.data_ptr() || version != t._version()) return false;
     return storage->lock().get() == t.storage().unsafeGetStorageImpl();
   }
+  bool expired() const { return !storage || storage->expired(); }
 };
 
 struct Tiled {
@@ -85,10 +90,30 @@ std::mutex g_mu;
 // (device, weight ptr, scale ptr, fmt, N, K, kind) -> tiled copy
 using TileKey = std::tuple<int, const void*, const void*, int, int64_t, int64_t, int>;
 std::map<TileKey, Tiled> g_tiles;
+TileKey g_sweep_at{};  // where the bounded sweep resumes
+
+// Drop cached copies whose weight or scale storage has been freed: `budget` entries
+// from where the last sweep stopped (all of them for budget < 0).  Caller holds g_mu.
+void sweep_tiles(int budget) {
+  if (g_tiles.empty()) return;
+  const size_t n = budget < 0 ? g_tiles.size() : std::min<size_t>((size_t)budget, g_tiles.size());
+  auto it = g_tiles.lower_bound(g_sweep_at);
+  for (size_t i = 0; i < n; ++i) {
+    if (it == g_tiles.end()) it = g_tiles.begin();
+    if (it->second.w.expired() || it->second.s.expired()) it = g_tiles.erase(it);
+    else ++it;
+    if (g_tiles.empty()) return;
+  }
+  g_sweep_at = it == g_tiles.end() ? TileKey{} : it->first;
+}
+
+constexpr int kSweepPerCall = 4;
 
 // MX weight: codes (E4M3 [N, K] or packed FP6 [N, 3K/4]) + E8M0 scales in `scale_layout`.
-const Tiled& tiled_mx(const at::Tensor& w, const at::Tensor& ws, int fmt, int64_t N, int64_t K, int scale_layout,
-                      hipStream_t s) {
+// Returned by value (the tensors are reference-counted), so a concurrent re-tile of the
+// same key cannot change them under the caller.
+Tiled tiled_mx(const at::Tensor& w, const at::Tensor& ws, int fmt, int64_t N, int64_t K, int scale_layout,
+               hipStream_t s) {
   TORCH_CHECK(w.is_cuda() && ws.is_cuda() && w.device() == ws.device(), "weights must be on one HIP device");
   TORCH_CHECK(w.is_contiguous() && ws.is_contiguous(), "weight codes and scales must be contiguous");
   const int64_t need_s = scale_layout ? mxl_swizzled_scale_bytes(N, K) : N * (K / 32);
@@ -97,9 +122,14 @@ const Tiled& tiled_mx(const at::Tensor& w, const at::Tensor& ws, int fmt, int64_
   std::lock_guard<std::mutex> lock(g_mu);
   const TileKey key{(int)w.device().index(), w.data_ptr(), ws.data_ptr(), fmt, N, K, scale_layout};
   auto it = g_tiles.find(key);
-  if (it != g_tiles.end() && it->second.w.same(w) && it->second.s.same(ws)) return it->second;
+  if (it != g_tiles.end() && it->second.w.same(w) && it->second.s.same(ws)) {
+    Tiled hit = it->second;
+    sweep_tiles(kSweepPerCall);
+    return hit;
+  }
   TORCH_CHECK(!capturing(s), "mach_amd: weight [", N, ", ", K, "] was not prepared before graph capture; "
               "run the shape once outside capture (warmup)");
+  sweep_tiles(-1);
   Tiled t;
   auto opts = w.options().dtype(at::kByte);
   t.tiled = at::empty({mxl_tiled_weight_bytes(N, K, fmt)}, opts);
@@ -115,13 +145,18 @@ const Tiled& tiled_mx(const at::Tensor& w, const at::Tensor& ws, int fmt, int64_
 // Block-FP8 weight: E4M3 [N, K] + the reference's 64-row duplicated scales
 // sb64 [N/64, K/128] (scale.repeat_interleave(2, dim=0), fp8/linear.py:137-154),
 // reduced to the 128-row block scales [ceil(N/128), K/128] this library reads.
-const Tiled& tiled_block(const at::Tensor& w, const at::Tensor& sb64, int64_t N, int64_t K, hipStream_t s) {
+Tiled tiled_block(const at::Tensor& w, const at::Tensor& sb64, int64_t N, int64_t K, hipStream_t s) {
   std::lock_guard<std::mutex> lock(g_mu);
   const TileKey key{(int)w.device().index(), w.data_ptr(), sb64.data_ptr(), kE4M3, N, K, 2};
   auto it = g_tiles.find(key);
-  if (it != g_tiles.end() && it->second.w.same(w) && it->second.s.same(sb64)) return it->second;
+  if (it != g_tiles.end() && it->second.w.same(w) && it->second.s.same(sb64)) {
+    Tiled hit = it->second;
+    sweep_tiles(kSweepPerCall);
+    return hit;
+  }
   TORCH_CHECK(!capturing(s), "mach_amd: block-FP8 weight [", N, ", ", K, "] was not prepared before graph "
               "capture; run the shape once outside capture (warmup)");
+  sweep_tiles(-1);
   Tiled t;
   t.tiled = at::empty({mxl_tiled_weight_bytes(N, K, kE4M3)}, w.options().dtype(at::kByte));
   check(mxl_pack_weight(w.data_ptr(), nullptr, N, K, kE4M3, t.tiled.data_ptr(), nullptr, s), "mxl_pack_weight");
@@ -134,7 +169,10 @@ const Tiled& tiled_block(const at::Tensor& w, const at::Tensor& sb64, int64_t N,
 // --------------------------------------------------------------- workspaces
 
 // Split-K scratch per (device, stream), grown outside capture; a superseded buffer is
-// kept (a captured graph may hold its address), so none is ever freed.
+// kept (a captured graph may hold its address), so none is ever freed.  A capture that
+// would need a bigger buffer than its stream holds raises, as the reference's
+// capture_cache_miss does (native_backend.py:163-170): running it with less scratch
+// would change the K split and so the summation order of the captured result.
 std::map<std::pair<int, hipStream_t>, std::vector<at::Tensor>> g_ws;
 
 std::pair<void*, int64_t> workspace(const at::Tensor& like, int64_t nbytes, hipStream_t s) {
@@ -142,11 +180,9 @@ std::pair<void*, int64_t> workspace(const at::Tensor& like, int64_t nbytes, hipS
   std::lock_guard<std::mutex> lock(g_mu);
   auto& v = g_ws[{(int)like.device().index(), s}];
   if (v.empty() || v.back().numel() < nbytes) {
-    if (capturing(s)) {
-      // run unsplit rather than allocate during capture (the GEMMs accept a smaller workspace)
-      return v.empty() ? std::pair<void*, int64_t>{nullptr, 0}
-                       : std::pair<void*, int64_t>{v.back().data_ptr(), v.back().numel()};
-    }
+    TORCH_CHECK(!capturing(s), "mach_amd: this shape needs a ", nbytes, "-byte split-K workspace but the capture "
+                "stream holds ", v.empty() ? 0 : v.back().numel(), " bytes; warm this shape before capture "
+                "(run it once on the capture stream outside capture)");
     const int64_t size = std::max<int64_t>(nbytes, v.empty() ? 0 : 2 * v.back().numel());
     v.push_back(at::empty({size}, like.options().dtype(at::kByte)));
   }
@@ -154,7 +190,7 @@ std::pair<void*, int64_t> workspace(const at::Tensor& like, int64_t nbytes, hipS
 }
 
 mxl_gemm_options options(int sa_layout, int64_t tactic, int64_t splits) {
-  mxl_gemm_options o{sa_layout, -1, 0, 0, 0, 0};
+  mxl_gemm_options o{sa_layout, -1, 0, 0, 0, 0, 0, 0, 1.0f};
   if (tactic >= 0) {  // an explicit kernel, with the caller's split count
     o.kernel = (int)tactic;
     o.splits = splits > 0 ? (int)splits : 0;
@@ -162,10 +198,18 @@ mxl_gemm_options options(int sa_layout, int64_t tactic, int64_t splits) {
   return o;
 }
 
-at::Tensor finish(at::Tensor y, double alpha, at::ScalarType dtype) {
-  if (alpha != 1.0) y.mul_(alpha);
-  return dtype == at::kBFloat16 ? y : y.to(dtype);
+// The output format and scale of the mxfp6 ops (`alpha`, `dtype`): the GEMMs scale the
+// fp32 sum and round it once to bf16 or fp16.
+mxl_gemm_options with_output(mxl_gemm_options o, double alpha, at::ScalarType dtype, const char* who) {
+  TORCH_CHECK(dtype == at::kBFloat16 || dtype == at::kHalf, who, ": output dtype must be bfloat16 or float16, got ",
+              dtype);
+  TORCH_CHECK(std::isfinite(alpha) && alpha != 0.0, who, ": alpha must be finite and non-zero");
+  o.out_dtype = dtype == at::kHalf ? 1 : 0;
+  o.alpha = (float)alpha;
+  return o;
 }
+
+at::ScalarType out_dtype_of(const mxl_gemm_options& o) { return o.out_dtype == 1 ? at::kHalf : at::kBFloat16; }
 
 void check_act(const at::Tensor& a, int64_t K, const char* who) {
   TORCH_CHECK(a.is_cuda() && a.dim() == 2 && a.is_contiguous() && a.size(1) == K, who,
@@ -177,10 +221,10 @@ at::Tensor mx_gemm(const at::Tensor& a, const at::Tensor& sa, int sa_layout, con
                    int64_t K, const mxl_gemm_options& o, const at::Tensor& out_opt, const at::Tensor& ws_opt,
                    hipStream_t s) {
   const int64_t M = a.size(0);
-  at::Tensor out = out_opt.defined() ? out_opt : at::empty({M, N}, a.options().dtype(at::kBFloat16));
-  TORCH_CHECK(out.scalar_type() == at::kBFloat16 && out.dim() == 2 && out.size(0) == M && out.size(1) == N &&
+  at::Tensor out = out_opt.defined() ? out_opt : at::empty({M, N}, a.options().dtype(out_dtype_of(o)));
+  TORCH_CHECK(out.scalar_type() == out_dtype_of(o) && out.dim() == 2 && out.size(0) == M && out.size(1) == N &&
                   out.stride(1) == 1 && out.stride(0) >= N,
-              "out must be bf16 [M, N] with unit column stride");
+              "out must be ", out_dtype_of(o), " [M, N] with unit column stride");
   const int64_t need_s = sa_layout ? mxl_swizzled_scale_bytes(M, K) : M * (K / 32);
   TORCH_CHECK(sa.is_cuda() && sa.is_contiguous() && sa.numel() * sa.element_size() >= need_s,
               "activation scales hold ", sa.numel() * sa.element_size(), " bytes, need ", need_s);
@@ -210,13 +254,13 @@ std::tuple<at::Tensor, at::Tensor> quantize_logical(const at::Tensor& x, int rul
 // One bf16 row quantized inside the weight-streaming GEMM (one launch, the same bits as
 // quantize + GEMM); nullopt for shapes that take the two calls.
 std::optional<at::Tensor> quant_row(const at::Tensor& x, const Tiled& t, int fmt, int64_t N, int64_t K,
-                                    hipStream_t s) {
+                                    const mxl_gemm_options& o, hipStream_t s) {
   if (x.size(0) != 1 || K % 128 != 0 || K > 12288 || x.scalar_type() != at::kBFloat16 || !x.is_cuda()) return {};
   at::Tensor xc = x.contiguous();
-  at::Tensor out = at::empty({1, N}, xc.options().dtype(at::kBFloat16));
-  check(mxl_quant_mx_gemm(xc.data_ptr(), 1, K, kFloorCarry175, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N, fmt,
-                          nullptr, out.data_ptr(), N, s),
-        "mxl_quant_mx_gemm");
+  at::Tensor out = at::empty({1, N}, xc.options().dtype(out_dtype_of(o)));
+  check(mxl_quant_mx_gemm_ex(xc.data_ptr(), 1, K, kFloorCarry175, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N, fmt,
+                             nullptr, out.data_ptr(), N, &o, s),
+        "mxl_quant_mx_gemm_ex");
   return out;
 }
 
@@ -242,10 +286,10 @@ at::Tensor block_fp8_mm(const at::Tensor& a, const at::Tensor& b, const at::Tens
   TORCH_CHECK(b.device() == a.device() && sa.device() == a.device() && sb.device() == a.device(),
               "vllm_mach_block_fp8::mm: operands on different devices");
   hipStream_t s = stream_of(a);
-  const Tiled& t = tiled_block(b.t(), sb.t(), N, K, s);
+  const Tiled t = tiled_block(b.t(), sb.t(), N, K, s);
   at::Tensor out = at::empty({M, N}, a.options().dtype(at::kBFloat16));
   if (M == 0) return out;
-  const mxl_gemm_options o{0, -1, 0, 0, 0, 0};
+  const mxl_gemm_options o = options(0, -1, 0);
   auto w = workspace(a, mxl_gemm_workspace_bytes_ex(M, N, K, kE4M3, 1, &o), s);
   check(mxl_block_fp8_gemm_ex(a.data_ptr(), sa.data_ptr(), M, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N, K, nullptr,
                               out.data_ptr(), N, w.first, w.second, &o, s),
@@ -298,7 +342,7 @@ at::Tensor mxfp8_gemm(const at::Tensor& a, const at::Tensor& b, const at::Tensor
   check_act(a, K, "mxfp8_sm120::gemm");
   TORCH_CHECK(N % 16 == 0 && K % 128 == 0, "mxfp8_sm120::gemm: need N % 16 == 0 and K % 128 == 0");
   hipStream_t s = stream_of(a);
-  const Tiled& t = tiled_mx(b, sb, kE4M3, N, K, 1, s);
+  const Tiled t = tiled_mx(b, sb, kE4M3, N, K, 1, s);
   return mx_gemm(a, sa, 1, t, kE4M3, N, K, options(1, tactic, splits), out.value_or(at::Tensor()),
                  ws.value_or(at::Tensor()), s);
 }
@@ -325,8 +369,8 @@ at::Tensor mxfp8_gemm_from_float(const at::Tensor& x, const at::Tensor& w, const
   const int64_t N = w.size(0), K = w.size(1);
   TORCH_CHECK(x.dim() == 2 && x.size(1) == K, "mxfp8_sm120::gemm_from_float: x must be [M, K]");
   hipStream_t s = stream_of(x);
-  const Tiled& t = tiled_mx(w, ws, kE4M3, N, K, 1, s);
-  if (auto y = quant_row(x, t, kE4M3, N, K, s)) return *y;
+  const Tiled t = tiled_mx(w, ws, kE4M3, N, K, 1, s);
+  if (auto y = quant_row(x, t, kE4M3, N, K, options(0, -1, 0), s)) return *y;
   auto q = quantize_logical(x, kFloorCarry175, s);
   return mx_gemm(std::get<0>(q), std::get<1>(q), 0, t, kE4M3, N, K, options(0, -1, 0), at::Tensor(), at::Tensor(), s);
 }
@@ -356,14 +400,12 @@ void mxfp8_dual_gemm_out(const at::Tensor& hi, const at::Tensor& weight, const a
                 "mxfp8_sm120::dual_gemm_out: activation scales hold ", t->numel() * t->element_size(),
                 " bytes, need ", need_s);
   hipStream_t s = stream_of(hi);
-  const Tiled& t = tiled_mx(weight, s_weight, kE4M3, N, K, 1, s);
+  const Tiled t = tiled_mx(weight, s_weight, kE4M3, N, K, 1, s);
   if (M == 0) return;
-  // the two limbs' partials: a workspace that must grow during capture cannot run unsplit here
+  // the two limbs' partials
   const int64_t nbytes = 2 * M * N * 4;
   auto w = workspace(hi, nbytes, s);
-  TORCH_CHECK(w.second >= nbytes, "mxfp8_sm120::dual_gemm_out: run this shape once before graph capture (its ",
-              nbytes, "-byte workspace would grow during capture)");
-  const mxl_gemm_options o{1, -1, 0, 0, 0, 0};
+  const mxl_gemm_options o = options(1, -1, 0);
   check(mxl_mx_gemm_dual_ex(hi.data_ptr(), s_hi.data_ptr(), res.data_ptr(), s_res.data_ptr(), M, t.tiled.data_ptr(),
                             t.tiled_s.data_ptr(), N, K, kE4M3, nullptr, out.data_ptr(), out.stride(0), w.first,
                             w.second, &o, s),
@@ -416,12 +458,11 @@ at::Tensor mxfp6_gemm_from_float(const at::Tensor& x, const at::Tensor& w, const
   const int64_t K = w.size(1) * 4 / 3;
   TORCH_CHECK(x.dim() == 2 && x.size(1) == K && K % 128 == 0, "mxfp6::gemm_from_float: x must be [M, K], K % 128 == 0");
   hipStream_t s = stream_of(x);
-  const Tiled& t = tiled_mx(w, ws, kE3M2, N, K, 1, s);
-  if (auto y = quant_row(x, t, kE3M2, N, K, s)) return finish(*y, alpha, dtype);
+  const Tiled t = tiled_mx(w, ws, kE3M2, N, K, 1, s);
+  const mxl_gemm_options o = with_output(options(0, -1, 0), alpha, dtype, "mxfp6::gemm_from_float");
+  if (auto y = quant_row(x, t, kE3M2, N, K, o, s)) return *y;
   auto q = quantize_logical(x, kFloorCarry175, s);
-  return finish(mx_gemm(std::get<0>(q), std::get<1>(q), 0, t, kE3M2, N, K, options(0, -1, 0), at::Tensor(),
-                        at::Tensor(), s),
-                alpha, dtype);
+  return mx_gemm(std::get<0>(q), std::get<1>(q), 0, t, kE3M2, N, K, o, at::Tensor(), at::Tensor(), s);
 }
 
 // SwiGLU (ceil_div448 with the bf16 SiLU rounding) -> MXFP8 -> W6A8 down projection;
@@ -436,20 +477,21 @@ at::Tensor mxfp6_gemm_from_swiglu(const at::Tensor& gate_up, const at::Tensor& w
   const int64_t K = w.size(1) * 4 / 3, M = gate_up.size(0);
   TORCH_CHECK(gate_up.size(1) == 2 * K && K % 128 == 0, "mxfp6::gemm_from_swiglu: gate_up width must be 2K");
   hipStream_t s = stream_of(gate_up);
-  const Tiled& t = tiled_mx(w, ws, kE3M2, N, K, 1, s);
-  at::Tensor out = at::empty({M, N}, gate_up.options().dtype(at::kBFloat16));
-  if (M == 0) return finish(out, alpha, dtype);
+  const Tiled t = tiled_mx(w, ws, kE3M2, N, K, 1, s);
+  const mxl_gemm_options o = with_output(options(0, -1, 0), alpha, dtype, "mxfp6::gemm_from_swiglu");
+  at::Tensor out = at::empty({M, N}, gate_up.options().dtype(out_dtype_of(o)));
+  if (M == 0) return out;
   if (M == 1 && K <= 12288) {
-    check(mxl_swiglu_mx_gemm(gate_up.data_ptr(), 1, K, kCeilDiv448, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N, kE3M2,
-                             nullptr, out.data_ptr(), N, s),
-          "mxl_swiglu_mx_gemm");
-    return finish(out, alpha, dtype);
+    check(mxl_swiglu_mx_gemm_ex(gate_up.data_ptr(), 1, K, kCeilDiv448, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N,
+                                kE3M2, nullptr, out.data_ptr(), N, &o, s),
+          "mxl_swiglu_mx_gemm_ex");
+    return out;
   }
   at::Tensor codes = at::empty({M, K}, gate_up.options().dtype(at::kByte));
   at::Tensor scales = at::empty({M, K / 32}, gate_up.options().dtype(at::kByte));
   check(mxl_swiglu_mxfp8(gate_up.data_ptr(), M, K, kCeilDiv448, 0, codes.data_ptr(), scales.data_ptr(), s),
         "mxl_swiglu_mxfp8");
-  return finish(mx_gemm(codes, scales, 0, t, kE3M2, N, K, options(0, -1, 0), out, at::Tensor(), s), alpha, dtype);
+  return mx_gemm(codes, scales, 0, t, kE3M2, N, K, o, out, at::Tensor(), s);
 }
 
 // Pre-quantized W6A8: codes [M, K] with swizzled activation scales.
@@ -461,9 +503,9 @@ at::Tensor mxfp6_gemm_w6a8(const at::Tensor& codes, const at::Tensor& w, const a
               "mxfp6::gemm_w6a8_pdl: w must be packed FP6 bytes [N, 3K/4]");
   check_act(codes, K, "mxfp6::gemm_w6a8_pdl");
   hipStream_t s = stream_of(codes);
-  const Tiled& t = tiled_mx(w, ws, kE3M2, N, K, 1, s);
-  return finish(mx_gemm(codes, scales, 1, t, kE3M2, N, K, options(1, -1, 0), at::Tensor(), at::Tensor(), s), alpha,
-                dtype);
+  const Tiled t = tiled_mx(w, ws, kE3M2, N, K, 1, s);
+  return mx_gemm(codes, scales, 1, t, kE3M2, N, K, with_output(options(1, -1, 0), alpha, dtype, "mxfp6::gemm_w6a8_pdl"),
+                 at::Tensor(), at::Tensor(), s);
 }
 
 }  // namespace

@@ -122,7 +122,12 @@ def quantize_mxfp8(input: torch.Tensor) -> MXFP8Tensor:
 # ----------------------------------------------------------- dense W6A8
 
 def _dtype(out_dtype) -> torch.dtype:
-    return out_dtype if out_dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+    """The GEMMs round their fp32 sums once to bf16 or fp16 (None: bf16)."""
+    if out_dtype is None:
+        return torch.bfloat16
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"W6A8 GEMM output dtype must be bfloat16 or float16, got {out_dtype}")
+    return out_dtype
 
 
 def gemm_from_float(x: torch.Tensor, weight: PackedMXFP6Tensor, out_dtype=torch.bfloat16) -> torch.Tensor:

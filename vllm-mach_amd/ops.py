@@ -423,7 +423,7 @@ def _mx_gemm_call(a8, sa8, M, w, sw, n, k, w_fmt, bias, out, ldc, opts, sa_layou
              ws, wsb, stream_handle(dev))
         return
     o = _lib.GemmOptions(sa_layout) if opts is None else _lib.GemmOptions(
-        sa_layout, opts.kernel, opts.splits, opts.tile_n, opts.tile_m, opts.hybrid)
+        sa_layout, opts.kernel, opts.splits, opts.tile_n, opts.tile_m, opts.hybrid, opts.waves)
     ws, wsb = _gemm_ws(dev, M, n, k, w_fmt, False, o)
     call("mxl_mx_gemm_ex", ptr(a8), ptr(sa8), M, ptr(w), ptr(sw), n, k, w_fmt, ptr(bias), ptr(out), ldc,
          ws, wsb, _lib.options_ptr(o), stream_handle(dev))
