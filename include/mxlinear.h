@@ -329,6 +329,24 @@ int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, int64_t E, i
                   int64_t* expert_offsets, int32_t* inverse, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/* Router: softmax -> top-k -> (renormalize) from router logits [T, E] (fp32, or bf16
+ * with logits_bf16 = 1) and the token sort of mxl_moe_route, for E <= 1024 and
+ * topk <= min(E, 64).  topk_ids int32 [T, topk] are the k largest logits of each token
+ * (softmax is increasing in the logit) in descending order, ties to the lower expert
+ * index (-0 equals +0; NaNs order by sign beyond the finite values);
+ * topk_weights fp32 [T, topk] = exp(x - max) / sum, the sum over the selected experts
+ * (renormalize = 1) or over all experts (0), with this library's binary32 exp.  Then
+ * sorted_routes / expert_offsets / inverse exactly as mxl_moe_route writes them for
+ * those ids.  One launch while T * topk <= 1024; two while topk divides 1024 and the
+ * chunk histograms fit one workgroup; otherwise the routing and mxl_moe_route's
+ * launches.  Replaces vLLM's fused top-k softmax (select_experts: softmax, topk,
+ * renormalize) and the routing of route_mxfp8_out, fused as the reference's
+ * qwen35_router_quant_out fuses them (src/vllm_mach/mxfp6/moe.py:142-152). */
+int64_t mxl_moe_router_workspace_bytes(int64_t T, int64_t topk, int64_t E);
+int mxl_moe_router(const void* logits, int logits_bf16, int64_t T, int64_t E, int64_t topk, int renormalize,
+                   float* topk_weights, int32_t* topk_ids, int32_t* sorted_routes, int64_t* expert_offsets,
+                   int32_t* inverse, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Weighted combine: out[t, h] = bf16(sum_k y[inverse[t*topk+k], h] * w[t, k])
  * in fp32, k ascending.  Replaces moe_reduce_out
  * (src/vllm_mach/mxfp6/moe.py:697-702, src/vllm_mach/mxfp6/moe_utils.py:445-488). */

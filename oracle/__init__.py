@@ -332,6 +332,37 @@ def moe_route(topk_ids: np.ndarray, num_experts: int):
     return sorted_routes, offsets, inverse
 
 
+def order_keys(logits) -> np.ndarray:
+    """Binary32 logits as unsigned keys in value order (-0 read as +0; NaNs beyond the
+    finite values by sign): the total order the router selects by."""
+    u = np.ascontiguousarray(np.asarray(logits, np.float32)).view(np.uint32).copy()
+    u[u == 0x80000000] = 0
+    neg = (u & 0x80000000) != 0
+    return np.where(neg, ~u, u | np.uint32(0x80000000)).astype(np.uint32)
+
+
+def moe_router(logits, top_k: int, renormalize: bool = True):
+    """softmax -> top-k -> (renormalize) -> token sort (vLLM's select_experts, the routing
+    half of qwen35_router_quant_out, src/vllm_mach/mxfp6/moe.py:142-152; vLLM's top-k softmax
+    kernel breaks ties to the lower expert).  ids: the k largest logits of each token,
+    descending, ties to the lower index (softmax is increasing, so these are its k
+    largest probabilities); weights: exp(x - max) / sum in float64, the sum over the
+    selected experts (renormalize) or all experts.  Returns (weights float64 [T, k],
+    ids int32 [T, k], sorted_routes, expert_offsets, inverse)."""
+    x = np.ascontiguousarray(np.asarray(logits, np.float32))
+    T, E = x.shape
+    keys = order_keys(x).astype(np.int64)
+    # descending key, ascending index: a stable sort of the negated keys
+    ids = np.argsort(-keys, axis=1, kind="stable")[:, :top_k].astype(np.int32)
+    xd = x.astype(np.float64)
+    top = np.take_along_axis(xd, ids[:, :1].astype(np.int64), axis=1)
+    e_sel = np.exp(np.take_along_axis(xd, ids.astype(np.int64), axis=1) - top)
+    denom = e_sel.sum(axis=1, keepdims=True) if renormalize else np.exp(xd - top).sum(axis=1, keepdims=True)
+    weights = e_sel / denom
+    sorted_routes, offsets, inverse = moe_route(ids, E)
+    return weights, ids, sorted_routes, offsets, inverse
+
+
 def moe_reduce(y_bits: np.ndarray, topk_weights: np.ndarray, inverse: np.ndarray) -> np.ndarray:
     """out[t] = bf16(sum_k w[t,k] * y[inverse[t*topk+k]]) (mxfp6/moe.py:697-702)."""
     y_bits = np.ascontiguousarray(y_bits, np.uint16)

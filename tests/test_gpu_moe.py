@@ -322,3 +322,68 @@ def test_moe_fused_producers_bit_identical(pkg, oracle_mod, dev, E, H, I, T, top
         gone = (emap[ids.long()] < 0).all(dim=1)
         if gone.any():
             assert (out_f[gone] == 0).all()
+
+
+@pytest.mark.parametrize("T,E,topk,bf16,renorm", [
+    (1, 256, 8, False, True),
+    (7, 4, 2, False, True),
+    (128, 256, 8, False, True),    # c5 at T = 128: routing and the sort in one launch
+    (128, 256, 8, True, True),     # bf16 logits: exact ties, to the lower expert
+    (129, 256, 8, False, False),   # two chunks; weights over every expert
+    (2048, 256, 8, False, True),   # c5 at T = 2048: routing with chunk histograms, then the scatter
+    (2048, 256, 8, True, False),
+    (3000, 64, 6, False, True),    # topk not dividing 1024: routing, then mxl_moe_route
+    (100, 1024, 16, False, True),  # the widest expert count (16 logits per lane)
+    (16, 1000, 64, True, True),    # the largest top-k; E not a multiple of 64
+    (0, 256, 8, False, True),
+])
+def test_router_matches_oracle(pkg, oracle_mod, dev, T, E, topk, bf16, renorm):
+    """softmax -> top-k -> renormalize -> token sort from router logits: ids (ties to the lower
+    expert) and the sort tables bit-exact against the oracle; weights against the float64
+    softmax within a few binary32 ulps."""
+    g = torch.Generator().manual_seed(T + E + topk)
+    logits = torch.randn(T, E, generator=g) * 2
+    if bf16:
+        logits = logits.bfloat16()
+    w, ids, s, o, inv = torch.ops.mach_amd.moe_router(logits.to(dev), topk, renorm)
+    rw, rids, rs, ro, rinv = oracle_mod.moe_router(logits.float().numpy(), topk, renorm)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    assert np.array_equal(o.cpu().numpy(), ro)
+    assert np.array_equal(s.cpu().numpy(), rs) and np.array_equal(inv.cpu().numpy(), rinv)
+    if T:
+        got = w.double().cpu().numpy()
+        assert np.abs(got - rw).max() <= 4e-6 * np.abs(rw).max(), np.abs(got - rw).max()
+        if bf16 and renorm:  # ties actually occurred among the selections
+            srt = np.sort(logits.float().numpy(), axis=1)[:, ::-1]
+            assert (srt[:, :topk + 1][:, 1:] == srt[:, :topk + 1][:, :-1]).any()
+
+
+@pytest.mark.parametrize("T", [7, 128])
+def test_moe_layer_from_router_logits(pkg, oracle_mod, dev, T):
+    """The layer from logits (one router launch feeding the grouped GEMMs) equals
+    select_experts + apply bit for bit, and the oracle's layer on the oracle's routing
+    within the whole-layer bar; at c5 T = 128 it is the router plus the three GEMM-stage
+    launches."""
+    E, H, I, topk = (256, 2048, 512, 8) if T == 128 else (4, 256, 128, 2)
+    c13, s13, c2, s2, x, _, _ = _moe_case(oracle_mod, E, H, I, T, topk, 12035, 2)
+    experts = pkg.Mxfp6Experts(fmt=2)
+    w1, w2 = experts.process_weights_after_loading(
+        torch.from_numpy(oracle_mod.pack_fp6(c13)).to(dev), torch.from_numpy(s13).to(dev),
+        torch.from_numpy(oracle_mod.pack_fp6(c2)).to(dev), torch.from_numpy(s2).to(dev))
+    logits = torch.randn(T, E, generator=torch.Generator().manual_seed(T)).to(dev)
+    xd = x.to(dev)
+    ops = pkg.ops
+    before = dict(ops._COUNTS)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    experts.apply_router(out, xd, w1, w2, logits, topk, True)
+    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items() if v != before.get(k, 0)}
+    if T == 128:
+        assert calls == {"moe_router": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu": 1, "moe_reduce": 1}, calls
+    wts, ids = pkg.select_experts(logits, topk, True)
+    out2 = torch.empty_like(out)
+    experts.apply(out2, xd, w1, w2, wts, ids, "silu", E, None, None, None, None, None, None, False)
+    assert torch.equal(out, out2)
+    rw, rids, *_ = oracle_mod.moe_router(logits.cpu().numpy(), topk, True)
+    ref = oracle_mod.bf16_to_f32(oracle_mod.moe_ref(x, c13, s13, c2, s2, rw.astype(np.float32), rids, 2))
+    got = out.float().cpu().numpy()
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2

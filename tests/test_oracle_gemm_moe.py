@@ -109,3 +109,58 @@ def test_moe_ref_matches_per_token_loop(oracle_mod):
             yk = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(oracle_mod.mx_gemm_ref(mc, ms, c2[e], s2[e], 2)))
             out[t] = out[t] + yk[0] * np.float32(wts[t, k])
     assert np.array_equal(got, oracle_mod.f32_to_bf16(out))
+
+
+def test_router_oracle_matches_torch_topk_softmax(oracle_mod):
+    """Without ties the router oracle's ids are torch.topk of the softmax (the order vLLM's
+    select_experts returns) and its weights the torch fp32 softmax / renormalization."""
+    import torch
+    g = torch.Generator().manual_seed(3)
+    for T, E, k in [(7, 4, 2), (128, 256, 8), (33, 64, 6), (5, 1024, 16)]:
+        logits = torch.randn(T, E, generator=g)
+        for renorm in (True, False):
+            w, ids, *_ = oracle_mod.moe_router(logits.numpy(), k, renorm)
+            p = torch.softmax(logits.double(), -1)
+            tw, tids = torch.topk(p, k, -1)
+            if renorm:
+                tw = tw / tw.sum(-1, keepdim=True)
+            assert np.array_equal(ids, tids.int().numpy())
+            np.testing.assert_allclose(w, tw.numpy(), rtol=1e-12, atol=0)
+
+
+def test_router_oracle_ties_and_special_values(oracle_mod):
+    """Ties go to the lower expert; -0 ties with +0; a brute-force restatement of the rule
+    (repeatedly take the largest remaining value, lowest index first) agrees."""
+    rng = np.random.default_rng(5)
+    x = rng.integers(-3, 4, size=(64, 32)).astype(np.float32)  # many exact ties
+    x[0, :4] = [0.0, -0.0, 0.0, -0.0]
+    x[1, :] = 1.0
+    for k in (1, 3, 8, 32):
+        _, ids, *_ = oracle_mod.moe_router(x, k, True)
+        for t in range(x.shape[0]):
+            left = list(range(x.shape[1]))
+            want = []
+            for _ in range(k):
+                best = max(left, key=lambda i: (x[t, i] + 0.0, -i))
+                want.append(best)
+                left.remove(best)
+            assert list(ids[t]) == want, (t, k)
+    _, ids, *_ = oracle_mod.moe_router(x[1:2], 4, True)
+    assert list(ids[0]) == [0, 1, 2, 3]  # all equal: the lowest experts
+    zeros = np.array([[-0.0, 0.0, -0.0, 0.0, -1.0]], np.float32)
+    _, ids, *_ = oracle_mod.moe_router(zeros, 4, True)
+    assert list(ids[0]) == [0, 1, 2, 3]  # -0 and +0 tie
+    # renormalized weights are the selected probabilities rescaled to sum to one
+    w, ids, *_ = oracle_mod.moe_router(x, 8, True)
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-12)
+    w2, ids2, *_ = oracle_mod.moe_router(x, 8, False)
+    assert np.array_equal(ids, ids2)
+    np.testing.assert_allclose(w2 / w2.sum(1, keepdims=True), w, rtol=1e-12)
+
+
+def test_router_oracle_sort_is_moe_route(oracle_mod):
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((300, 64)).astype(np.float32)
+    _, ids, s, o, inv = oracle_mod.moe_router(x, 4, True)
+    rs, ro, rinv = oracle_mod.moe_route(ids, 64)
+    assert np.array_equal(s, rs) and np.array_equal(o, ro) and np.array_equal(inv, rinv)

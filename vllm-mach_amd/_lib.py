@@ -64,6 +64,8 @@ SIGNATURES = {
     "mxl_moe_route_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "mxl_moe_route": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "mxl_moe_reduce": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    "mxl_moe_router_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "mxl_moe_router": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "mxl_gemm_plan_name": (_I, [_I64, _I64, _I64, _I, _I, _P, ctypes.c_char_p, _I64]),
     "mxl_grouped_plan_name": (_I, [_I64, _I64, _I64, _I, _I, _I, _P, ctypes.c_char_p, _I64]),
 }

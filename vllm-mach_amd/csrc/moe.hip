@@ -180,16 +180,16 @@ constexpr int kSingleMaxExperts = 1024;
 constexpr int kRouteMaxExperts = 160 * 1024 / ((kChunk / 64) * (int)sizeof(int32_t));
 static_assert(kRouteMaxExperts == 2560, "the documented expert limit");
 
-__global__ __launch_bounds__(kChunk) void route_single_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
-                                                             int64_t* __restrict__ expert_offsets,
-                                                             int32_t* __restrict__ sorted_routes,
-                                                             int32_t* __restrict__ inverse) {
+// The single-chunk sort for route t (expert e, -1 if none): per-wavefront expert counts in
+// LDS, per-expert totals scanned into the offsets, then the rank and scatter.  Called by
+// every thread of a 1024-thread workgroup (t = threadIdx.x).
+__device__ __forceinline__ void single_chunk_sort(int32_t e, int64_t R, int E, int64_t* __restrict__ expert_offsets,
+                                                  int32_t* __restrict__ sorted_routes,
+                                                  int32_t* __restrict__ inverse, int32_t* whist,
+                                                  int32_t (*tot)[kSingleMaxExperts]) {
   constexpr int W = kChunk / 64;
-  __shared__ int32_t whist[W * kSingleMaxExperts];
-  __shared__ int32_t tot[2][kSingleMaxExperts];
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   for (int i = t; i < W * E; i += kChunk) whist[i] = 0;
-  const int32_t e = t < R ? ids[t] : -1;
   const bool valid = e >= 0 && e < E;
   const int rank = same_expert_rank(valid ? e : E, E, lane);
   __syncthreads();
@@ -225,6 +225,233 @@ __global__ __launch_bounds__(kChunk) void route_single_kernel(const int32_t* __r
   const int32_t pos = (e > 0 ? tot[src][e - 1] : 0) + whist[w * E + e] + rank;
   sorted_routes[pos] = t;
   inverse[t] = pos;
+}
+
+__global__ __launch_bounds__(kChunk) void route_single_kernel(const int32_t* __restrict__ ids, int64_t R, int E,
+                                                             int64_t* __restrict__ expert_offsets,
+                                                             int32_t* __restrict__ sorted_routes,
+                                                             int32_t* __restrict__ inverse) {
+  __shared__ int32_t whist[(kChunk / 64) * kSingleMaxExperts];
+  __shared__ int32_t tot[2][kSingleMaxExperts];
+  const int t = threadIdx.x;
+  single_chunk_sort(t < R ? ids[t] : -1, R, E, expert_offsets, sorted_routes, inverse, whist, tot);
+}
+
+// ------------------------------------------------------------------ router
+//
+// softmax -> top-k -> (renormalize) from router logits, the selection of vLLM's fused
+// top-k softmax that the reference's MoE layer runs before its experts (select_experts;
+// src/vllm_mach/mxfp6/moe.py:142-152 fuses it into qwen35_router_quant_out): the k largest
+// logits of a token (softmax is increasing, so they are its k largest probabilities), ties
+// to the lower expert index, weights exp(x - max) / sum, the sum over the k selected
+// (renormalize) or over every expert.  One wavefront per token, the token's logits spread
+// over its lanes (expert i at lane i % 64, slot i / 64); each of the k rounds takes the
+// wavefront maximum of (order key, lower index) over the logits not yet taken.
+
+constexpr int kRouterSlots = kSingleMaxExperts / 64;  // logits per lane: E <= 1024
+constexpr int kRouterMaxTopk = 64;
+
+// Binary32 as an unsigned key in value order (-0 read as +0, so equal values tie; NaNs
+// order outside the finite values by sign).
+__device__ __forceinline__ uint32_t order_key(float x) {
+  uint32_t u = f2u(x);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) { return u2f((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k); }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Route token t with the calling wavefront: ids / weights [t * topk + r] for r < topk;
+// returns the lane's id (lane r < topk holds selection r, other lanes -1).
+template <bool BF16>
+__device__ __forceinline__ int32_t route_token(const void* __restrict__ logits, int64_t t, int E, int topk,
+                                               bool renorm, int lane, int32_t* __restrict__ ids,
+                                               float* __restrict__ weights) {
+  uint32_t key[kRouterSlots];
+#pragma unroll
+  for (int j = 0; j < kRouterSlots; ++j) {
+    const int i = lane + 64 * j;
+    float x = 0.0f;
+    if (i < E) x = BF16 ? bf16_to_f32(static_cast<const uint16_t*>(logits)[t * E + i])
+                        : static_cast<const float*>(logits)[t * E + i];
+    key[j] = i < E ? order_key(x) : 0u;
+  }
+  uint32_t taken = 0u;
+  float my_x = 0.0f;
+  int32_t my_id = -1;
+  float top = 0.0f;
+  for (int r = 0; r < topk; ++r) {
+    uint64_t best = 0;  // (key, ~index): the larger key, then the lower index
+#pragma unroll
+    for (int j = 0; j < kRouterSlots; ++j) {
+      const int i = lane + 64 * j;
+      if (i < E && !((taken >> j) & 1u)) {
+        const uint64_t c = ((uint64_t)key[j] << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+        best = c > best ? c : best;
+      }
+    }
+    best = wave_max_u64(best);
+    const int idx = (int)(0xFFFFFFFFu - (uint32_t)best);
+    const float x = key_value((uint32_t)(best >> 32));
+    if ((idx & 63) == lane) taken |= 1u << (idx >> 6);
+    if (r == 0) top = x;
+    if (lane == r) {
+      my_x = x;
+      my_id = idx;
+    }
+  }
+  const float e = lane < topk ? mx_exp(my_x - top) : 0.0f;
+  float denom;
+  if (renorm) {
+    denom = wave_sum(e);
+  } else {
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRouterSlots; ++j)
+      if (lane + 64 * j < E) part = part + mx_exp(key_value(key[j]) - top);
+    denom = wave_sum(part);
+  }
+  if (lane < topk) {
+    ids[t * topk + lane] = my_id;
+    weights[t * topk + lane] = e / denom;
+  }
+  return my_id;
+}
+
+// T * topk <= 1024 routes and E <= 1024: routing and the token sort in one workgroup.
+template <bool BF16>
+__global__ __launch_bounds__(kChunk) void router_single_kernel(const void* __restrict__ logits, int64_t T, int E,
+                                                              int topk, int renorm, int32_t* __restrict__ ids,
+                                                              float* __restrict__ weights,
+                                                              int64_t* __restrict__ expert_offsets,
+                                                              int32_t* __restrict__ sorted_routes,
+                                                              int32_t* __restrict__ inverse) {
+  __shared__ int32_t whist[(kChunk / 64) * kSingleMaxExperts];
+  __shared__ int32_t tot[2][kSingleMaxExperts];
+  __shared__ int32_t sids[kChunk];
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  for (int64_t tok = w; tok < T; tok += kChunk / 64) {
+    const int32_t id = route_token<BF16>(logits, tok, E, topk, renorm != 0, lane, ids, weights);
+    if (lane < topk) sids[tok * topk + lane] = id;
+  }
+  __syncthreads();
+  const int64_t R = T * topk;
+  single_chunk_sort(t < R ? sids[t] : -1, R, E, expert_offsets, sorted_routes, inverse, whist, tot);
+}
+
+// Chunk c of 1024 routes = 1024 / topk whole tokens (topk divides 1024): route them and
+// count the chunk's routes per expert (the histogram the scatter's chunk bases come from).
+template <bool BF16>
+__global__ __launch_bounds__(kChunk) void router_hist_kernel(const void* __restrict__ logits, int64_t T, int E,
+                                                            int topk, int renorm, int32_t* __restrict__ ids,
+                                                            float* __restrict__ weights,
+                                                            int32_t* __restrict__ chunk_counts) {
+  __shared__ int32_t hist[kSingleMaxExperts];
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int64_t c = blockIdx.x, per = kChunk / topk;
+  for (int e = t; e < E; e += kChunk) hist[e] = 0;
+  __syncthreads();
+  for (int64_t k = w; k < per; k += kChunk / 64) {
+    const int64_t tok = c * per + k;
+    if (tok >= T) break;
+    const int32_t id = route_token<BF16>(logits, tok, E, topk, renorm != 0, lane, ids, weights);
+    if (lane < topk) atomicAdd(&hist[id], 1);
+  }
+  __syncthreads();
+  for (int e = t; e < E; e += kChunk) chunk_counts[c * E + e] = hist[e];
+}
+
+// Every chunk's scatter from the chunk histograms (C x E <= kCountScanMaxEntries,
+// E <= 1024): the workgroup sums the histograms of the chunks before its own (its chunk
+// bases) and of all chunks (the expert totals, scanned into the offsets, which workgroup 0
+// writes), then ranks and scatters its routes as route_scatter_kernel does.
+__global__ __launch_bounds__(kChunk) void route_scan_scatter_kernel(const int32_t* __restrict__ ids, int64_t R,
+                                                                   int64_t C, int E,
+                                                                   const int32_t* __restrict__ chunk_counts,
+                                                                   int64_t* __restrict__ expert_offsets,
+                                                                   int32_t* __restrict__ sorted_routes,
+                                                                   int32_t* __restrict__ inverse) {
+  constexpr int W = kChunk / 64;
+  __shared__ int32_t whist[W * kSingleMaxExperts];
+  __shared__ int32_t base[kSingleMaxExperts];
+  __shared__ int32_t tot[2][kSingleMaxExperts];
+  const int64_t c = blockIdx.x;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  for (int x = t; x < E; x += kChunk) {
+    int32_t before = 0, all = 0;
+    for (int64_t cc = 0; cc < C; ++cc) {
+      const int32_t n = chunk_counts[cc * E + x];
+      if (cc < c) before += n;
+      all += n;
+    }
+    base[x] = before;
+    tot[0][x] = all;
+  }
+  for (int i = t; i < W * E; i += kChunk) whist[i] = 0;
+  const int64_t r = c * kChunk + t;
+  const int32_t e = r < R ? ids[r] : -1;
+  const bool valid = e >= 0 && e < E;
+  const int rank = same_expert_rank(valid ? e : E, E, lane);
+  __syncthreads();
+  if (valid) atomicAdd(&whist[w * E + e], 1);
+  int src = 0;  // inclusive scan of the totals (ping-pong)
+  for (int d = 1; d < E; d <<= 1) {
+    __syncthreads();
+    for (int x = t; x < E; x += kChunk) {
+      int32_t v = tot[src][x];
+      if (x >= d) v += tot[src][x - d];
+      tot[1 - src][x] = v;
+    }
+    src = 1 - src;
+  }
+  __syncthreads();
+  if (c == 0) {
+    for (int x = t; x < E; x += kChunk) expert_offsets[x + 1] = tot[src][x];
+    if (t == 0) expert_offsets[0] = 0;
+  }
+  for (int x = t; x < E; x += kChunk) {
+    int32_t run = 0;
+    for (int v = 0; v < W; ++v) {
+      const int32_t n = whist[v * E + x];
+      whist[v * E + x] = run;
+      run += n;
+    }
+  }
+  __syncthreads();
+  if (r >= R) return;
+  if (!valid) {
+    inverse[r] = -1;
+    return;
+  }
+  const int64_t pos = (e > 0 ? tot[src][e - 1] : 0) + base[e] + whist[w * E + e] + rank;
+  sorted_routes[pos] = (int32_t)r;
+  inverse[r] = (int32_t)pos;
+}
+
+// Routing only (shapes the fused schedules above do not take): ids and weights, sorted by
+// mxl_moe_route afterwards.
+template <bool BF16>
+__global__ __launch_bounds__(256) void router_kernel(const void* __restrict__ logits, int64_t T, int E, int topk,
+                                                     int renorm, int32_t* __restrict__ ids,
+                                                     float* __restrict__ weights) {
+  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok < T) route_token<BF16>(logits, tok, E, topk, renorm != 0, threadIdx.x & 63, ids, weights);
 }
 
 // One thread: 8 consecutive hidden columns of one token.
@@ -304,6 +531,62 @@ extern "C" int mxl_moe_route(const int32_t* topk_ids, int64_t T, int64_t topk, i
     MXL_CHECK_LAUNCH("mxl_moe_route(scatter)");
   }
   return MXL_OK;
+}
+
+// Router workspace: the chunk histograms of the two-launch schedule, or, for shapes the
+// fused schedules do not take, mxl_moe_route's.
+extern "C" int64_t mxl_moe_router_workspace_bytes(int64_t T, int64_t topk, int64_t E) {
+  return mxl_moe_route_workspace_bytes(T, topk, E);
+}
+
+extern "C" int mxl_moe_router(const void* logits, int logits_bf16, int64_t T, int64_t E, int64_t topk,
+                              int renormalize, float* topk_weights, int32_t* topk_ids, int32_t* sorted_routes,
+                              int64_t* expert_offsets, int32_t* inverse, void* workspace, int64_t workspace_bytes,
+                              void* stream) {
+  MXL_CHECK_ARG(T >= 0 && E > 0 && E <= kSingleMaxExperts && topk > 0 && topk <= kRouterMaxTopk && topk <= E,
+                "mxl_moe_router: need 0 < topk <= min(E, %d) and 0 < E <= %d (E=%lld topk=%lld)", kRouterMaxTopk,
+                kSingleMaxExperts, (long long)E, (long long)topk);
+  MXL_CHECK_ARG(logits_bf16 == 0 || logits_bf16 == 1, "mxl_moe_router: logits are fp32 (0) or bf16 (1)");
+  const int64_t R = T * topk;
+  const int64_t C = (R + kChunk - 1) / kChunk;
+  MXL_CHECK_ARG(workspace_bytes >= mxl_moe_router_workspace_bytes(T, topk, E) && (C == 0 || workspace),
+                "mxl_moe_router: workspace too small (%lld < %lld bytes)", (long long)workspace_bytes,
+                (long long)mxl_moe_router_workspace_bytes(T, topk, E));
+  hipStream_t s = (hipStream_t)stream;
+  const int renorm = renormalize ? 1 : 0;
+  if (R <= kChunk) {  // routing and the sort in one workgroup (also T = 0: the offsets)
+    if (logits_bf16)
+      router_single_kernel<true><<<1, kChunk, 0, s>>>(logits, T, (int)E, (int)topk, renorm, topk_ids, topk_weights,
+                                                      expert_offsets, sorted_routes, inverse);
+    else
+      router_single_kernel<false><<<1, kChunk, 0, s>>>(logits, T, (int)E, (int)topk, renorm, topk_ids, topk_weights,
+                                                       expert_offsets, sorted_routes, inverse);
+    MXL_CHECK_LAUNCH("mxl_moe_router(single)");
+    return MXL_OK;
+  }
+  int32_t* counts = (int32_t*)workspace;
+  if (kChunk % topk == 0 && C * E <= kCountScanMaxEntries) {
+    // chunks of whole tokens: routing with the chunk histograms, then the scan and scatter
+    if (logits_bf16)
+      router_hist_kernel<true><<<dim3((unsigned)C), kChunk, 0, s>>>(logits, T, (int)E, (int)topk, renorm, topk_ids,
+                                                                    topk_weights, counts);
+    else
+      router_hist_kernel<false><<<dim3((unsigned)C), kChunk, 0, s>>>(logits, T, (int)E, (int)topk, renorm, topk_ids,
+                                                                     topk_weights, counts);
+    MXL_CHECK_LAUNCH("mxl_moe_router(hist)");
+    route_scan_scatter_kernel<<<dim3((unsigned)C), kChunk, 0, s>>>(topk_ids, R, C, (int)E, counts, expert_offsets,
+                                                                   sorted_routes, inverse);
+    MXL_CHECK_LAUNCH("mxl_moe_router(scatter)");
+    return MXL_OK;
+  }
+  const unsigned blocks = (unsigned)((T + 3) / 4);
+  if (logits_bf16)
+    router_kernel<true><<<blocks, 256, 0, s>>>(logits, T, (int)E, (int)topk, renorm, topk_ids, topk_weights);
+  else
+    router_kernel<false><<<blocks, 256, 0, s>>>(logits, T, (int)E, (int)topk, renorm, topk_ids, topk_weights);
+  MXL_CHECK_LAUNCH("mxl_moe_router(route)");
+  return mxl_moe_route(topk_ids, T, topk, E, sorted_routes, expert_offsets, inverse, workspace, workspace_bytes,
+                       stream);
 }
 
 extern "C" int mxl_moe_reduce(const void* routed_output, const float* topk_weights, const int32_t* inverse, int64_t T,

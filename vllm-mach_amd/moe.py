@@ -23,12 +23,11 @@ SILU = "silu"
 
 
 def select_experts(router_logits: torch.Tensor, top_k: int, renormalize: bool = True):
-    """softmax -> top-k -> optional renormalization (fp32 weights, int32 ids)."""
-    probs = torch.softmax(router_logits.float(), dim=-1)
-    weights, ids = torch.topk(probs, top_k, dim=-1)
-    if renormalize:
-        weights = weights / weights.sum(dim=-1, keepdim=True)
-    return weights.float(), ids.to(torch.int32)
+    """softmax -> top-k -> optional renormalization (fp32 weights [T, k], int32 ids [T, k]),
+    vLLM's ``select_experts`` with softmax scoring, in one router launch (``ops.moe_router``;
+    ties go to the lower expert, as vLLM's top-k softmax kernel breaks them)."""
+    weights, ids, _, _, _ = torch.ops.mach_amd.moe_router(router_logits, top_k, renormalize)
+    return weights, ids
 
 
 class Mxfp6Experts:
@@ -95,6 +94,30 @@ class Mxfp6Experts:
         if T == 0:
             return
         sorted_routes, offsets, inverse = torch.ops.mach_amd.moe_route(ids, E)
+        self._experts(output, hidden_states, w1, w2, topk_weights, topk, sorted_routes, offsets, inverse)
+
+    def apply_router(self, output: torch.Tensor, hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                     router_logits: torch.Tensor, top_k: int, renormalize: bool = True) -> None:
+        """The layer from router logits [T, E]: one router launch (softmax, top-k,
+        renormalization and the token sort, ``ops.moe_router``) feeds the grouped GEMMs
+        directly, the reference's router-fused schedules (src/vllm_mach/mxfp6/moe.py:126-190,
+        219-300: qwen35_router_quant_out routes before the expert GEMMs).  Writes ``output``;
+        the same bits as ``select_experts`` then ``apply``."""
+        if self.shapes is None:
+            raise RuntimeError("process_weights_after_loading must run before apply")
+        E, H, _ = self.shapes
+        T, hidden = hidden_states.shape
+        if hidden != H or router_logits.shape != (T, E):
+            raise ValueError("hidden states [T, H] and router logits [T, E] must match the experts")
+        if T == 0:
+            return
+        weights, _, sorted_routes, offsets, inverse = torch.ops.mach_amd.moe_router(router_logits, top_k,
+                                                                                    renormalize)
+        self._experts(output, hidden_states, w1, w2, weights, top_k, sorted_routes, offsets, inverse)
+
+    def _experts(self, output, hidden_states, w1, w2, topk_weights, topk, sorted_routes, offsets, inverse):
+        E, H, I = self.shapes
+        T = hidden_states.shape[0]
         routes = T * topk
         # Below ~96 routed rows per expert the grouped GEMMs stream each expert's weights
         # past its rows and produce their own MXFP8 operands (the activation quantization in
@@ -195,6 +218,15 @@ class Mxfp6MoEMethod:
         for name, value in zip(_MOE_PARAMS, (w1, self.experts.w1_scale, w2, self.experts.w2_scale)):
             setattr(layer, name, torch.nn.Parameter(value, requires_grad=False))
         layer.mxl_experts = self.experts  # found by warmup()
+
+    def apply_router(self, layer: torch.nn.Module, x: torch.Tensor, router_logits: torch.Tensor,
+                     top_k: int, renormalize: bool = True) -> torch.Tensor:
+        """The layer from router logits (``Mxfp6Experts.apply_router``): routing fused
+        ahead of the expert GEMMs, as the reference's MoE runner does
+        (src/vllm_mach/mxfp6/moe.py:219-240)."""
+        out = torch.empty_like(x)
+        self.experts.apply_router(out, x, layer.w13_weight, layer.w2_weight, router_logits, top_k, renormalize)
+        return out
 
     def apply(self, layer: torch.nn.Module, x: torch.Tensor, topk_weights: torch.Tensor,
               topk_ids: torch.Tensor, expert_map: Optional[torch.Tensor] = None,

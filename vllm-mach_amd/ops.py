@@ -701,6 +701,47 @@ def _(topk_ids, num_experts):
             topk_ids.new_empty((R,), dtype=torch.int32))
 
 
+@torch.library.custom_op("mach_amd::moe_router", mutates_args=())
+def moe_router(router_logits: torch.Tensor, top_k: int, renormalize: bool = True
+               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Router logits [T, E] (fp32 or bf16) -> (topk_weights f32 [T, k], topk_ids i32 [T, k],
+    sorted_routes i32 [T k], expert_offsets i64 [E+1], inverse i32 [T k]): softmax, top-k
+    (ties to the lower expert), renormalization and the stable token sort of ``moe_route``,
+    in one launch up to 1024 routes (vLLM's fused top-k softmax + the routing of
+    ``route_mxfp8_out``, as qwen35_router_quant_out fuses them, src/vllm_mach/mxfp6/moe.py:142-152).
+    """
+    _check_cuda(router_logits)
+    if router_logits.ndim != 2 or router_logits.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("moe_router needs fp32 or bf16 logits [T, E]")
+    logits = router_logits.contiguous()
+    T, E = logits.shape
+    dev = logits.device
+    weights = torch.empty((T, top_k), dtype=torch.float32, device=dev)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    R = T * top_k
+    sorted_routes = torch.empty(R, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int64, device=dev)
+    inverse = torch.empty(R, dtype=torch.int32, device=dev)
+    nbytes = query("mxl_moe_router_workspace_bytes", T, top_k, E)
+    buf = workspace(dev, nbytes, "route")
+    call("mxl_moe_router", ptr(logits), int(logits.dtype == torch.bfloat16), T, E, top_k, int(renormalize),
+         ptr(weights), ptr(ids), ptr(sorted_routes), ptr(offsets), ptr(inverse), ptr(buf), nbytes,
+         stream_handle(dev))
+    _count("moe_router")
+    return weights, ids, sorted_routes, offsets, inverse
+
+
+@moe_router.register_fake
+def _(router_logits, top_k, renormalize=True):
+    T, E = router_logits.shape
+    R = T * top_k
+    return (router_logits.new_empty((T, top_k), dtype=torch.float32),
+            router_logits.new_empty((T, top_k), dtype=torch.int32),
+            router_logits.new_empty((R,), dtype=torch.int32),
+            router_logits.new_empty((E + 1,), dtype=torch.int64),
+            router_logits.new_empty((R,), dtype=torch.int32))
+
+
 @torch.library.custom_op("mach_amd::grouped_gemm", mutates_args=())
 def grouped_gemm(a: torch.Tensor, sa: torch.Tensor, row_index: Optional[torch.Tensor], row_div: int,
                  expert_offsets: torch.Tensor, routed_rows: int, w: torch.Tensor, sw: torch.Tensor,
