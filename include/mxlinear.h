@@ -320,6 +320,46 @@ int mxl_grouped_gemm_swiglu(const void* gate_up, const int64_t* expert_offsets, 
                             int64_t routed_rows, const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K,
                             int w_fmt, int rule, void* out, void* stream);
 
+/* Down projection with the weighted combine in the same launch.  The routed
+ * rows are computed as mxl_grouped_gemm (row_index NULL: row p of A is routed
+ * row p; else A[row_index[p] / row_div]) or mxl_grouped_gemm_swiglu compute them and stored into routed_out
+ * (bf16 [routed_rows, N]); each token's row out[t] = bf16(sum over k ascending
+ * of topk_weights[t, k] * routed_out[inverse[t * topk + k]]) in fp32 -- the
+ * arithmetic of mxl_moe_reduce, so out is bit-identical to the GEMM followed by
+ * mxl_moe_reduce -- is written by the workgroup that stores the token's last
+ * routed row (a per-token device-scope atomic counter; the routed rows are
+ * stored and read device-coherently, the count taken after the stores complete).
+ * Tokens whose routes are all dropped get a zero row.  counters: int32 [T], zero
+ * before the first call; every call leaves them zero, so calls that share
+ * counters must not overlap (one set per stream).  They run the
+ * small-batch schedule (16-row weight-streaming units: fewer than 32 routed rows
+ * per expert) at K <= 512, topk <= 16 and routed_rows * N * 2 below 2 GiB;
+ * mxl_grouped_combine_supported says whether a shape has one (prod 0: plain
+ * MXFP8 operands, 2: the SwiGLU producer) and the entry points return
+ * MXL_EUNSUPPORTED otherwise.  Replace grouped_gemm_w6a8_out + moe_reduce_out
+ * (src/vllm_mach/mxfp6/moe.py:671-702) in one launch, as the reference's
+ * qwen35_w2_splitk_reduce_out / array_gemm_w6a8_reduce_out fold the combine
+ * into w2 (src/vllm_mach/mxfp6/moe.py:163-186). */
+typedef struct mxl_moe_combine {
+  const int32_t* sorted_routes; /* [routed_rows]: route t * topk + k of routed row p */
+  const int32_t* inverse;       /* [T * topk]: routed row of route (t, k), -1 if dropped */
+  const float* topk_weights;    /* fp32 [T, topk] */
+  int64_t T;
+  int64_t topk;                 /* 1 .. 16 */
+  void* out;                    /* bf16 [T, N] */
+  int32_t* counters;            /* int32 [T], zero; left zero */
+} mxl_moe_combine;
+int mxl_grouped_combine_supported(int64_t routed_rows, int64_t num_experts, int64_t N, int64_t K, int w_fmt,
+                                  int prod);
+int mxl_grouped_gemm_combine(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index, int row_div,
+                             const int64_t* expert_offsets, int64_t num_experts, int64_t routed_rows,
+                             const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt,
+                             void* routed_out, const mxl_moe_combine* combine, void* stream);
+int mxl_grouped_gemm_swiglu_combine(const void* gate_up, const int64_t* expert_offsets, int64_t num_experts,
+                                    int64_t routed_rows, const void* w_tiled, const void* sw_tiled, int64_t N,
+                                    int64_t K, int w_fmt, int rule, void* routed_out,
+                                    const mxl_moe_combine* combine, void* stream);
+
 /* Token sort by expert (stable): topk_ids int32 [T, topk] -> sorted_routes
  * int32 [T*topk], expert_offsets int64 [E+1], inverse int32 [T*topk] (-1 for
  * ids outside [0, E)).  1 <= E <= 2560.  Replaces route_mxfp8_out's routing outputs
@@ -352,6 +392,13 @@ int mxl_moe_router(const void* logits, int logits_bf16, int64_t T, int64_t E, in
  * (src/vllm_mach/mxfp6/moe.py:697-702, src/vllm_mach/mxfp6/moe_utils.py:445-488). */
 int mxl_moe_reduce(const void* routed_output, const float* topk_weights, const int32_t* inverse, int64_t T,
                    int64_t topk, int64_t H, void* out, void* stream);
+
+/* The same combine with a bf16 addend [T, H] (a shared expert's output) added to
+ * the fp32 sum after the routes, before the one rounding: out[t, h] =
+ * bf16(sum_k y[...] * w[t, k] + addend[t, h]).  Replaces the shared-output form of
+ * qwen35_grouped_reduce_out (src/vllm_mach/mxfp6/moe.py:301-302). */
+int mxl_moe_reduce_add(const void* routed_output, const float* topk_weights, const int32_t* inverse, int64_t T,
+                       int64_t topk, int64_t H, const void* addend, void* out, void* stream);
 
 /* The kernels a dense GEMM call (mxl_mx_gemm_ex, block = 0; mxl_block_fp8_gemm_ex,
  * block = 1) or a grouped GEMM call (mxl_grouped_gemm_ex, prod = 0;

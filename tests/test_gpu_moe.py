@@ -281,9 +281,10 @@ def test_grouped_stream_96_row_units(pkg, oracle_mod, dev, monkeypatch, E, N, K,
     (64, 1024, 384, 100, 8, 3, False),     # ragged: 12.5 rows per expert, K = 1024 / 384 (three K waves)
 ])
 def test_moe_fused_producers_bit_identical(pkg, oracle_mod, dev, E, H, I, T, topk, fmt, mapped):
-    """The grouped GEMMs with fused producers (quantization in w13, SwiGLU in w2) give the
-    same bits as the separate quantize / SwiGLU launches; at T = 128 the layer is four
-    launches (route, w13, w2, combine); an expert_map's dropped routes contribute nothing."""
+    """The grouped GEMMs with fused producers (quantization in w13, SwiGLU in w2), with and
+    without the combine inside w2, give the same bits as the separate quantize / SwiGLU /
+    combine launches; at T = 128 the layer is four launches (route, w13, w2, combine), three
+    with the combine in w2; an expert_map's dropped routes contribute nothing."""
     ops = pkg.ops
     g = torch.Generator().manual_seed(E + T + H)
     Eg = 2 * E if mapped else E
@@ -314,10 +315,22 @@ def test_moe_fused_producers_bit_identical(pkg, oracle_mod, dev, E, H, I, T, top
     if (E, T) == (256, 128):
         assert fused[0] and calls == {"moe_route": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu": 1,
                                       "moe_reduce": 1}, calls
+    experts.fuse_combine = True  # the combine inside w2: three launches, the same bits
+    out_c = torch.empty_like(out_f)
+    before = dict(ops._COUNTS)
+    experts.apply(out_c, x, e1, e2, wts, ids, "silu", Eg, emap, None, None, None, None, None, False)
+    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items() if v != before.get(k, 0)}
+    assert torch.equal(out_f, out_c)
+    if (E, T) == (256, 128):
+        assert calls == {"moe_route": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu_combine": 1}, calls
     experts.fuse = False
     out_u = torch.empty_like(out_f)
     experts.apply(out_u, x, e1, e2, wts, ids, "silu", Eg, emap, None, None, None, None, None, False)
     assert torch.equal(out_f, out_u)
+    experts.fuse_combine = False  # every stage its own launch
+    out_s = torch.empty_like(out_f)
+    experts.apply(out_s, x, e1, e2, wts, ids, "silu", Eg, emap, None, None, None, None, None, False)
+    assert torch.equal(out_f, out_s)
     if mapped:  # tokens whose routes all left the node get exactly zero
         gone = (emap[ids.long()] < 0).all(dim=1)
         if gone.any():
@@ -362,8 +375,8 @@ def test_router_matches_oracle(pkg, oracle_mod, dev, T, E, topk, bf16, renorm):
 def test_moe_layer_from_router_logits(pkg, oracle_mod, dev, T):
     """The layer from logits (one router launch feeding the grouped GEMMs) equals
     select_experts + apply bit for bit, and the oracle's layer on the oracle's routing
-    within the whole-layer bar; at c5 T = 128 it is the router plus the three GEMM-stage
-    launches."""
+    within the whole-layer bar; at c5 T = 128 it is three launches with the combine in w2
+    (four by default, the same bits)."""
     E, H, I, topk = (256, 2048, 512, 8) if T == 128 else (4, 256, 128, 2)
     c13, s13, c2, s2, x, _, _ = _moe_case(oracle_mod, E, H, I, T, topk, 12035, 2)
     experts = pkg.Mxfp6Experts(fmt=2)
@@ -373,12 +386,17 @@ def test_moe_layer_from_router_logits(pkg, oracle_mod, dev, T):
     logits = torch.randn(T, E, generator=torch.Generator().manual_seed(T)).to(dev)
     xd = x.to(dev)
     ops = pkg.ops
+    experts.fuse_combine = True
     before = dict(ops._COUNTS)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     experts.apply_router(out, xd, w1, w2, logits, topk, True)
     calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items() if v != before.get(k, 0)}
-    if T == 128:
-        assert calls == {"moe_router": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu": 1, "moe_reduce": 1}, calls
+    if T == 128:  # three launches: router + sort, w13 + quantization, w2 + SwiGLU + combine
+        assert calls == {"moe_router": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu_combine": 1}, calls
+    experts.fuse_combine = False
+    out_d = torch.empty_like(out)
+    experts.apply_router(out_d, xd, w1, w2, logits, topk, True)  # the default: four launches
+    assert torch.equal(out, out_d)
     wts, ids = pkg.select_experts(logits, topk, True)
     out2 = torch.empty_like(out)
     experts.apply(out2, xd, w1, w2, wts, ids, "silu", E, None, None, None, None, None, None, False)
@@ -387,3 +405,86 @@ def test_moe_layer_from_router_logits(pkg, oracle_mod, dev, T):
     ref = oracle_mod.bf16_to_f32(oracle_mod.moe_ref(x, c13, s13, c2, s2, rw.astype(np.float32), rids, 2))
     got = out.float().cpu().numpy()
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
+
+
+@pytest.mark.parametrize("E,N,K,T,topk,swiglu,fmt,drop", [
+    (256, 2048, 512, 128, 8, True, 2, False),    # c5 T = 128 down projection: 16-row units + SwiGLU
+    (256, 2048, 512, 128, 8, False, 2, False),   # the same on MXFP8 operands
+    (8, 256, 384, 40, 4, True, 3, True),         # E3M2, dropped routes and fully dropped tokens
+    (16, 264, 512, 60, 6, False, 0, True),       # E4M3, ragged N, dropped routes
+    (32, 512, 256, 20, 16, True, 2, False),      # the largest top-k
+])
+def test_grouped_combine_matches_reduce(pkg, oracle_mod, dev, E, N, K, T, topk, swiglu, fmt, drop):
+    """The down projection with the weighted combine in its launch writes the bits of the
+    grouped GEMM followed by moe_reduce: twice in a row (the second call with fewer tokens,
+    so the per-token counters must have been left zero) and under graph replay."""
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(E + N + K + T)
+    ids = torch.randint(0, E, (T, topk), generator=g, dtype=torch.int32)
+    if drop:  # ids outside [0, E) are dropped by the sort; tokens 0-2 lose every route
+        ids[::3, 1] = E + 3
+        ids[:3] = -1
+    wts = torch.rand(T, topk, generator=g).float()
+    wts = wts / wts.sum(-1, keepdim=True)
+    w = torch.randint(0, 256, (E, N, K if fmt == 0 else K * 3 // 4), generator=g, dtype=torch.uint8)
+    if fmt == 0:  # E4M3 codes without the NaN pattern (every FP6 pattern is a number)
+        w[(w & 0x7F) == 0x7F] = 0x3F
+    w = w.to(dev)
+    s = torch.randint(118, 124, (E, N, K // 32), generator=g, dtype=torch.uint8).to(dev)
+    w_t, s_t = ops.pack_weight(w, s, fmt)
+    R = T * topk
+    assert ops.grouped_combine_supported(R, E, N, K, fmt, swiglu, topk)
+    # 96-row units (tens of rows per expert) keep the combine in its own launch
+    assert not ops.grouped_combine_supported(64 * E, E, N, K, fmt, swiglu, topk)
+
+    def case(Tc):
+        idc = ids[:Tc].to(dev)
+        routes, offsets, inverse = torch.ops.mach_amd.moe_route(idc, E)
+        Rc = Tc * topk
+        if swiglu:
+            gu = (torch.randn(Rc, 2 * K, generator=g) * 2).bfloat16().to(dev)
+            y = torch.ops.mach_amd.grouped_gemm_swiglu(gu, offsets, Rc, w_t, s_t, N, K, fmt, ops.CEIL_DIV448)
+        else:
+            a, sa = torch.ops.mach_amd.quantize_mxfp8((torch.randn(Rc, K, generator=g)).bfloat16().to(dev), 0)
+            y = torch.ops.mach_amd.grouped_gemm(a, sa, None, 1, offsets, Rc, w_t, s_t, N, K, fmt)
+        ref = torch.empty(Tc, N, dtype=torch.bfloat16, device=dev)
+        wd = wts[:Tc].to(dev)
+        torch.ops.mach_amd.moe_reduce(ref, y, wd, inverse)
+
+        def run(out):
+            if swiglu:
+                torch.ops.mach_amd.grouped_gemm_swiglu_combine(out, gu, offsets, Rc, w_t, s_t, N, K, fmt,
+                                                               ops.CEIL_DIV448, routes, inverse, wd)
+            else:
+                torch.ops.mach_amd.grouped_gemm_combine(out, a, sa, None, 1, offsets, Rc, w_t, s_t, N, K, fmt,
+                                                        routes, inverse, wd)
+        return ref, run
+
+    ref, run = case(T)
+    out = torch.full((T, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    run(out)
+    assert torch.equal(out, ref)
+    if drop:
+        assert (out[:3] == 0).all()
+    ref2, run2 = case(T // 2 + 1)
+    out2 = torch.empty_like(ref2)
+    run2(out2)
+    assert torch.equal(out2, ref2)
+    # graph replays with eager calls between them: the counters stay consistent
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        run(out)
+        graph = torch.cuda.CUDAGraph()
+        out_g = torch.empty_like(ref)
+        with torch.cuda.graph(graph, stream=stream):
+            run(out_g)
+        for _ in range(3):
+            out_g.zero_()
+            graph.replay()
+            stream.synchronize()
+            assert torch.equal(out_g, ref)
+            run(out)
+            stream.synchronize()
+            assert torch.equal(out, ref)
+    torch.cuda.current_stream().wait_stream(stream)

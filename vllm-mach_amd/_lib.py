@@ -61,9 +61,13 @@ SIGNATURES = {
     "mxl_grouped_fused_supported": (_I, [_I64, _I64, _I64, _I]),
     "mxl_grouped_gemm_quant": (_I, [_P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _P, _P]),
     "mxl_grouped_gemm_swiglu": (_I, [_P, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _P, _P]),
+    "mxl_grouped_combine_supported": (_I, [_I64, _I64, _I64, _I64, _I, _I]),
+    "mxl_grouped_gemm_combine": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P, _P]),
+    "mxl_grouped_gemm_swiglu_combine": (_I, [_P, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _P, _P, _P]),
     "mxl_moe_route_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "mxl_moe_route": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "mxl_moe_reduce": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    "mxl_moe_reduce_add": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P]),
     "mxl_moe_router_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "mxl_moe_router": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "mxl_gemm_plan_name": (_I, [_I64, _I64, _I64, _I, _I, _P, ctypes.c_char_p, _I64]),
@@ -79,6 +83,13 @@ class GemmOptions(ctypes.Structure):
     def __init__(self, sa_layout=0, kernel=-1, splits=0, tile_n=0, tile_m=0, hybrid=0, waves=0, out_dtype=0,
                  alpha=1.0):
         super().__init__(sa_layout, kernel, splits, tile_n, tile_m, hybrid, waves, out_dtype, alpha)
+
+
+class MoeCombine(ctypes.Structure):
+    """``mxl_moe_combine``: the weighted combine a down projection runs in its own launch
+    (routes, inverse, fp32 weights [T, topk], the bf16 [T, N] output, zeroed counters [T])."""
+    _fields_ = [("sorted_routes", _P), ("inverse", _P), ("topk_weights", _P), ("T", _I64), ("topk", _I64),
+                ("out", _P), ("counters", _P)]
 
 
 def options_ptr(opts: "GemmOptions | None"):

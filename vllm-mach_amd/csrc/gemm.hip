@@ -909,6 +909,97 @@ static int grouped_common(const void* a, const void* sa, int64_t a_rows, const i
                           const void* w_tiled, const void* sw_tiled, int64_t N, int64_t K, int w_fmt, void* out,
                           const GemmOptions& o, void* stream);
 
+// ------------------------------------------------ down projection + weighted combine
+
+// Same layout as mxl_moe_combine in include/mxlinear.h.
+struct MoeCombine {
+  const int32_t* sorted_routes;
+  const int32_t* inverse;
+  const float* topk_weights;
+  int64_t T, topk;
+  void* out;
+  int32_t* counters;
+};
+
+// The 16-row or 96-row weight-streaming schedule of a down projection whose combine runs
+// in the kernel (prod 0: MXFP8 operands; prod 2: the SwiGLU producer, 16-row units
+// only); 0 when the shape takes another schedule.
+static int combine_grouped_mt(int64_t routed_rows, int64_t num_experts, int64_t K, int fmt, int prod) {
+  if (K > kTileK) return 0;  // one super-tile per wave: the whole-line (coherent) store path
+  if (prod == 2) return fused_grouped_mt(routed_rows, num_experts, K, fmt);
+  if (prod != 0) return 0;
+  // the 16-row units (below 32 routed rows per expert): the small-batch schedule
+  return routed_rows < 32 * num_experts && stream_grouped_eligible(K, num_experts, fmt, 1) ? 1 : 0;
+}
+
+extern "C" int mxl_grouped_combine_supported(int64_t routed_rows, int64_t num_experts, int64_t N, int64_t K,
+                                             int w_fmt, int prod) {
+  return routed_rows > 0 && num_experts > 0 && N > 0 && N % 8 == 0 && K > 0 && K % 128 == 0 && valid_wfmt(w_fmt) &&
+         (prod == 0 || prod == 2) && combine_grouped_mt(routed_rows, num_experts, K, w_fmt, prod) != 0;
+}
+
+static int grouped_combine_common(const char* who, const void* a, const void* sa, int64_t a_rows,
+                                  const int32_t* row_index, int row_div, const int64_t* expert_offsets,
+                                  int64_t num_experts, int64_t routed_rows, const void* w_tiled, const void* sw_tiled,
+                                  int64_t N, int64_t K, int w_fmt, int prod, int rule, void* routed_out,
+                                  const void* combine, void* stream) {
+  MXL_CHECK_ARG(valid_wfmt(w_fmt), "%s: unknown weight format %d", who, w_fmt);
+  MXL_CHECK_ARG(prod == 0 || rule == kCeilDiv448 || rule == kRpUe8m0, "%s: unknown SwiGLU rule %d", who, rule);
+  MXL_CHECK_ARG(N > 0 && N % 8 == 0 && K > 0 && K % 128 == 0 && num_experts > 0 && routed_rows >= 0 && row_div >= 1,
+                "%s: need N %% 8 == 0, K %% 128 == 0, experts > 0", who);
+  MXL_CHECK_ARG(combine != nullptr, "%s: no combine descriptor", who);
+  const MoeCombine c = *static_cast<const MoeCombine*>(combine);
+  MXL_CHECK_ARG(c.T >= 0 && c.topk >= 1 && c.topk <= 16 && routed_rows <= c.T * c.topk,
+                "%s: need 1 <= topk <= 16 and routed rows <= T * topk", who);
+  MXL_CHECK_ARG(routed_rows * N * 2 < (int64_t(1) << 31), "%s: the routed output must stay below 2 GiB", who);
+  MXL_CHECK_ARG(c.out && c.counters && c.inverse && c.topk_weights && (routed_rows == 0 || c.sorted_routes),
+                "%s: combine descriptor has a null pointer", who);
+  MXL_CHECK_ARG(((uintptr_t)a & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0 && ((uintptr_t)routed_out & 15) == 0 &&
+                    ((uintptr_t)c.out & 15) == 0,
+                "%s: operands and outputs must be 16-byte aligned", who);
+  if (c.T == 0) return MXL_OK;
+  const int mt = combine_grouped_mt(routed_rows > 0 ? routed_rows : 1, num_experts, K, w_fmt, prod);
+  if (!mt) {
+    set_error("%s: no weight-streaming schedule for %lld routed rows over %lld experts at K=%lld", who,
+              (long long)routed_rows, (long long)num_experts, (long long)K);
+    return MXL_EUNSUPPORTED;
+  }
+  GemmParams p{};
+  p.a = (const uint8_t*)a; p.sa = sa; p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled;
+  p.out = (uint16_t*)routed_out; p.row_index = row_index; p.expert_offsets = expert_offsets;
+  p.lda = prod ? 2 * K : K; p.ldc = N; p.M = routed_rows; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK;
+  p.a_rows = a_rows;
+  p.w_expert_stride = mxl_tiled_weight_bytes(N, K, w_fmt);
+  p.sw_expert_stride = mxl_tiled_scale_bytes(N, K);
+  p.row_div = row_div; p.S = 1;
+  p.comb_out = (uint16_t*)c.out; p.comb_w = c.topk_weights; p.comb_inv = c.inverse;
+  p.comb_routes = c.sorted_routes; p.comb_cnt = c.counters; p.comb_T = c.T; p.comb_topk = (int)c.topk;
+  const hipError_t e = launch_gemm_stream_grouped(w_fmt, p, num_experts, mt, (hipStream_t)stream, prod, rule, true);
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", who, hipGetErrorString(e));
+    return MXL_EHIP;
+  }
+  return MXL_OK;
+}
+
+extern "C" int mxl_grouped_gemm_combine(const void* a, const void* sa, int64_t a_rows, const int32_t* row_index,
+                                        int row_div, const int64_t* expert_offsets, int64_t num_experts,
+                                        int64_t routed_rows, const void* w_tiled, const void* sw_tiled, int64_t N,
+                                        int64_t K, int w_fmt, void* routed_out, const void* combine, void* stream) {
+  return grouped_combine_common("mxl_grouped_gemm_combine", a, sa, a_rows, row_index, row_div, expert_offsets,
+                                num_experts, routed_rows, w_tiled, sw_tiled, N, K, w_fmt, 0, 0, routed_out, combine,
+                                stream);
+}
+
+extern "C" int mxl_grouped_gemm_swiglu_combine(const void* gate_up, const int64_t* expert_offsets,
+                                               int64_t num_experts, int64_t routed_rows, const void* w_tiled,
+                                               const void* sw_tiled, int64_t N, int64_t K, int w_fmt, int rule,
+                                               void* routed_out, const void* combine, void* stream) {
+  return grouped_combine_common("mxl_grouped_gemm_swiglu_combine", gate_up, nullptr, routed_rows, nullptr, 1,
+                                expert_offsets, num_experts, routed_rows, w_tiled, sw_tiled, N, K, w_fmt, 2, rule,
+                                routed_out, combine, stream);
+}
+
 // The grouped schedule a call runs (shared by the launch and the plan query).
 struct GroupedPlan {
   int kernel;     // kStream (weight-streaming units of 16 stream_mt rows), kWide or kGeneric

@@ -37,6 +37,17 @@ struct GemmParams {
   int64_t sa_ss = 4;  // bytes between the scale dwords of consecutive K128 slices of a row (4 or 512)
   float alpha = 1.0f;  // output scale, applied to the fp32 sum before its one rounding
   int out_f16 = 0;     // output element format: 0 bf16, 1 fp16
+  // Grouped down projection with the weighted combine (gemm_stream_grouped_kernel,
+  // COMB): routed output row p belongs to route comb_routes[p] = t * comb_topk + k; the
+  // token rows are summed into comb_out [comb_T, N] bf16 by the unit that stores a
+  // token's last row (comb_cnt: one zeroed int32 counter per token, left zero).
+  uint16_t* comb_out = nullptr;
+  const float* comb_w = nullptr;         // fp32 [comb_T, comb_topk] route weights
+  const int32_t* comb_inv = nullptr;     // [comb_T * comb_topk] routed row of route (t, k), -1 dropped
+  const int32_t* comb_routes = nullptr;  // [routed rows] route of each routed row
+  int32_t* comb_cnt = nullptr;
+  int64_t comb_T = 0;
+  int comb_topk = 0;
 };
 
 // Output element formats (mxl_gemm_options.out_dtype).
@@ -292,6 +303,6 @@ bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt, int mt);
 constexpr int64_t kGroupedStageMaxBytes = 64 * 1024;
 bool stream_grouped_fused_eligible(int64_t K, int64_t num_experts, int fmt, int mt);
 hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, int mt, hipStream_t s,
-                                      int prod = 0, int rule = 0);
+                                      int prod = 0, int rule = 0, bool combine = false);
 
 }  // namespace mxl

@@ -494,7 +494,86 @@ __device__ __forceinline__ void grouped_produce(const GemmParams& p, int64_t lo,
   }
 }
 
-template <int FMT, int MT, int PROD>
+// Device-coherent access to the routed output of a combine-fused launch (COMB): buffer
+// loads and stores with the sc1 cache policy, the bits the compiler gives agent-scope
+// atomic loads and stores, so a row stored by a workgroup on one XCD and read by one on
+// another needs no L2 write-back or invalidation (device-scope fences around every unit
+// cost 141.7 -> 225.2 us at c5 T = 128, 233 -> 650 us at T = 2048).  Byte offsets are
+// 32-bit: the host bounds the routed output below 2 GiB.
+constexpr int kCpolSc1 = 16;  // the sc1 bit of a buffer access's cache-policy operand
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t routed_rsrc(const GemmParams& p) {
+  return __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void store16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
+  typedef int v4i_ __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(v4i_{(int)v.x, (int)v.y, (int)v.z, (int)v.w}, r, off, 0, kCpolSc1);
+}
+__device__ __forceinline__ uint4 load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1);
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+
+// Most routes per token of a combine-fused launch (the route table of each token a
+// unit completes is kept in LDS).
+constexpr int kCombineMaxTopk = 16;
+
+// Weighted combine of the ntok tokens a unit completed (COMB): out[tok] = bf16(sum over k
+// ascending of w[tok, k] * y[pos[tok, k]]) in fp32 (the moe_reduce_kernel arithmetic).
+// Items (token, eight columns) are spread over every thread of the workgroup, and an
+// item's row loads are all issued before its sums, so each thread has up to topk
+// loads in flight.
+__device__ __forceinline__ void grouped_combine(const GemmParams& p, int ntok, const int32_t* tok,
+                                                const int32_t (*pos)[kCombineMaxTopk],
+                                                const float (*wt)[kCombineMaxTopk], int t, int nthreads) {
+  const __amdgpu_buffer_rsrc_t ry = routed_rsrc(p);
+  const int topk = p.comb_topk;
+  const int per = (int)(p.N / 8);
+  for (int it = t; it < ntok * per; it += nthreads) {
+    const int i = it / per, c = it - i * per;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    for (int k0 = 0; k0 < topk; k0 += 8) {
+      uint4 raw[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int32_t q = k0 + u < topk ? pos[i][k0 + u] : -1;
+        raw[u] = q >= 0 ? load16_coherent(ry, (uint32_t)(((int64_t)q * p.ldc + 8 * c) * 2)) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (k0 + u >= topk || pos[i][k0 + u] < 0) continue;
+        const float wk = wt[i][k0 + u];
+        float v[8];
+        bf16x8_to_f32(raw[u], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float term = v[e] * wk;
+          acc[e] = acc[e] + term;
+        }
+      }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = (uint32_t)f32_to_bf16(acc[2 * e]) | ((uint32_t)f32_to_bf16(acc[2 * e + 1]) << 16);
+    *reinterpret_cast<uint4*>(p.comb_out + (int64_t)tok[i] * p.N + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// COMB: the weighted combine runs inside the kernel.  A unit stores its routed rows
+// device-coherently (sc1), waits for those stores to complete, and each row adds one to
+// its token's counter (a device-scope atomic); the unit whose row completes a token's
+// count (its routes with inv >= 0) reads the token's rows device-coherently, writes the
+// combined row and resets the counter to zero for the next launch.  Tokens with no routed
+// row are written as zeros at the start.  Every token's last row is stored by some unit,
+// so every combined row is written once, by whichever unit finishes it; no wave waits on
+// another.  K must be one super-tile per wave (WK = 1: the whole-line store path).  Used
+// with the 16-row units (the small-batch schedule): at c5 T = 128 the layer took 141.0 us
+// with the combine as its own launch; at T = 2048 (96-row units, ~96 tokens completed per
+// unit, 64 MB of routed rows re-read at the units' ends) the in-kernel combine measured
+// 573 against 231 us and is not used.
+template <int FMT, int MT, int PROD, bool COMB = false>
 __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_stream_grouped_kernel(GemmParams p, int E,
                                                                                                 int WK, int NW) {
   // PROD = 4 producer + rule: producer 0 (none), 1 (quantization) or 2 (SwiGLU), rule the
@@ -544,6 +623,22 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
   if (t == nthreads - 1) sh_pre[E] = sh_scan[t];
   __syncthreads();
   const int units = __builtin_amdgcn_readfirstlane(sh_pre[E]);
+  // COMB: the tokens this unit completes, with their routes' rows and weights
+  __shared__ int32_t sh_tok[COMB ? ROWS : 1];
+  __shared__ int32_t sh_pos[COMB ? ROWS : 1][kCombineMaxTopk];
+  __shared__ float sh_wt[COMB ? ROWS : 1][kCombineMaxTopk];
+  __shared__ int32_t sh_ntok;
+  if constexpr (COMB) {
+    // tokens without a routed row (every route dropped) get a zero row
+    const int topk = p.comb_topk;
+    for (int64_t tk = (int64_t)blockIdx.x * nthreads + t; tk < p.comb_T; tk += (int64_t)gridDim.x * nthreads) {
+      bool any = false;
+      for (int k = 0; k < topk; ++k) any = any || p.comb_inv[tk * topk + k] >= 0;
+      if (!any)
+        for (int64_t c = 0; c < p.N / 8; ++c)
+          *reinterpret_cast<uint4*>(p.comb_out + tk * p.N + 8 * c) = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
 
   int buf = 0;
   for (int u = (int)blockIdx.x; u < units; u += (int)gridDim.x) {
@@ -562,6 +657,12 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
     const uint8_t* sw = static_cast<const uint8_t*>(p.sw) + e * p.sw_expert_stride;
     const int64_t kt1[1] = {kw < p.KT ? kw : p.KT - 1};
     const bool valid[1] = {kw < p.KT};
+    // COMB: the token of this thread's unit row, requested now so that the count at the
+    // unit's end does not wait for it
+    int64_t ctok = 0;
+    if constexpr (COMB) {
+      if (t < hi - lo) ctok = p.comb_routes[lo + t] / p.comb_topk;
+    }
 
     // the first round's weights first, then the unit's gathered activation fragments
     StreamB<FMT, 1> b0;
@@ -674,7 +775,10 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
             const int64_t col = col0 + 8 * seg;
             if (row < nrows && col < p.N) {
               const uint4 v = *reinterpret_cast<const uint4*>(&wstage[wbuf][row][8 * seg]);
-              *reinterpret_cast<uint4*>(p.out + (lo + row) * p.ldc + col) = v;
+              if constexpr (COMB)
+                store16_coherent(routed_rsrc(p), (uint32_t)(((lo + row) * p.ldc + col) * 2), v);
+              else
+                *reinterpret_cast<uint4*>(p.out + (lo + row) * p.ldc + col) = v;
             }
           }
           wbuf ^= 1;
@@ -742,6 +846,39 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
           }
         }
       }
+    }
+    if constexpr (COMB) {
+      // this unit's rows are stored (coherently) before they are counted
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (t == 0) sh_ntok = 0;
+      __syncthreads();
+      const int nrows = (int)(hi - lo), topk = p.comb_topk;
+      if (t < nrows) {
+        const int64_t tok = ctok;
+        int32_t pos[kCombineMaxTopk];
+        int expect = 0;
+#pragma unroll
+        for (int k = 0; k < kCombineMaxTopk; ++k) {
+          pos[k] = k < topk ? p.comb_inv[tok * topk + k] : -1;
+          expect += pos[k] >= 0 ? 1 : 0;
+        }
+        const int old = __hip_atomic_fetch_add(p.comb_cnt + tok, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1 == expect) {
+          const int slot = atomicAdd(&sh_ntok, 1);
+          sh_tok[slot] = (int32_t)tok;
+#pragma unroll
+          for (int k = 0; k < kCombineMaxTopk; ++k) {
+            sh_pos[slot][k] = pos[k];
+            sh_wt[slot][k] = k < topk ? p.comb_w[tok * topk + k] : 0.0f;
+          }
+          // every route of the token is counted: zero for the next launch (a device-scope store)
+          __hip_atomic_store(p.comb_cnt + tok, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      __syncthreads();
+      const int ntok = sh_ntok;
+      if (ntok > 0) grouped_combine(p, ntok, sh_tok, sh_pos, sh_wt, t, nthreads);
+      __syncthreads();  // sh_tok / sh_ntok are reused by the next unit
     }
   }
 }
@@ -837,7 +974,8 @@ int grouped_waves(int fmt) {
 int64_t grouped_stage_bytes(int mt, int64_t K) { return ((16 * mt * K * 33 / 32) + 15) / 16 * 16; }
 
 template <int MT>
-hipError_t launch_grouped_mt(int fmt, const GemmParams& p, int64_t num_experts, int prod, int rule, hipStream_t s) {
+hipError_t launch_grouped_mt(int fmt, const GemmParams& p, int64_t num_experts, int prod, int rule, hipStream_t s,
+                             bool combine) {
   const int waves = grouped_waves<MT>(fmt);
   const int WK = (int)p.KT;
   if (WK < 1 || WK > waves) return hipErrorInvalidValue;
@@ -848,22 +986,30 @@ hipError_t launch_grouped_mt(int fmt, const GemmParams& p, int64_t num_experts, 
   const dim3 grid((unsigned)G), blk((unsigned)(64 * WK * NW));
   const int E = (int)num_experts;
   const size_t shmem = prod ? (size_t)grouped_stage_bytes(MT, p.K) : 0;
-  // the fused producers are instantiated for the 16-row units only (the schedule that uses them)
-  if (prod && MT != 1) return hipErrorInvalidValue;
-#define MXL_GROUPED_LAUNCH(F_, P_) \
-  hipLaunchKernelGGL((gemm_stream_grouped_kernel<F_, MT, (MT == 1 ? P_ : 0)>), grid, blk, shmem, s, p, E, WK, NW)
+  // the fused producers and the combine are instantiated for the 16-row units only (the
+  // schedule that uses them)
+  if ((prod || combine) && MT != 1) return hipErrorInvalidValue;
+  if (combine && (p.comb_topk < 1 || p.comb_topk > kCombineMaxTopk)) return hipErrorInvalidValue;
+#define MXL_GROUPED_LAUNCH(F_, P_, C_)                                                                         \
+  hipLaunchKernelGGL((gemm_stream_grouped_kernel<F_, MT, (MT == 1 ? P_ : 0), (MT == 1 && C_)>), grid, blk, shmem, \
+                     s, p, E, WK, NW)
   if (prod && (rule < kFloorCarry175 || rule > kRpUe8m0)) return hipErrorInvalidValue;
-  const int code = prod ? 4 * prod + rule : 0;
-#define MXL_GROUPED_PROD(F_)                       \
-  switch (code) {                                  \
-    case 0: MXL_GROUPED_LAUNCH(F_, 0); break;      \
-    case 4: MXL_GROUPED_LAUNCH(F_, 4); break;      \
-    case 5: MXL_GROUPED_LAUNCH(F_, 5); break;      \
-    case 6: MXL_GROUPED_LAUNCH(F_, 6); break;      \
-    case 8: MXL_GROUPED_LAUNCH(F_, 8); break;      \
-    case 9: MXL_GROUPED_LAUNCH(F_, 9); break;      \
-    case 10: MXL_GROUPED_LAUNCH(F_, 10); break;    \
-    default: return hipErrorInvalidValue;          \
+  const int code = (prod ? 4 * prod + rule : 0) + (combine ? 16 : 0);
+  // the combine runs in the down projection: plain operands, or the SwiGLU producer
+  // under the two rules the MoE's intermediate activations use
+#define MXL_GROUPED_PROD(F_)                            \
+  switch (code) {                                       \
+    case 0: MXL_GROUPED_LAUNCH(F_, 0, false); break;    \
+    case 4: MXL_GROUPED_LAUNCH(F_, 4, false); break;    \
+    case 5: MXL_GROUPED_LAUNCH(F_, 5, false); break;    \
+    case 6: MXL_GROUPED_LAUNCH(F_, 6, false); break;    \
+    case 8: MXL_GROUPED_LAUNCH(F_, 8, false); break;    \
+    case 9: MXL_GROUPED_LAUNCH(F_, 9, false); break;    \
+    case 10: MXL_GROUPED_LAUNCH(F_, 10, false); break;  \
+    case 16: MXL_GROUPED_LAUNCH(F_, 0, true); break;    \
+    case 25: MXL_GROUPED_LAUNCH(F_, 9, true); break;    \
+    case 26: MXL_GROUPED_LAUNCH(F_, 10, true); break;   \
+    default: return hipErrorInvalidValue;               \
   }
   if (fmt == kE4M3) {
     MXL_GROUPED_PROD(kE4M3)
@@ -891,10 +1037,11 @@ bool stream_grouped_fused_eligible(int64_t K, int64_t num_experts, int fmt, int 
 }
 
 hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_experts, int mt, hipStream_t s,
-                                      int prod, int rule) {
+                                      int prod, int rule, bool combine) {
   if (prod && grouped_stage_bytes(mt, p.K) > kGroupedStageMaxBytes) return hipErrorInvalidValue;
-  if (mt == 1) return launch_grouped_mt<1>(fmt, p, num_experts, prod, rule, s);
-  if (mt == kGroupedStreamWideMT) return launch_grouped_mt<kGroupedStreamWideMT>(fmt, p, num_experts, prod, rule, s);
+  if (mt == 1) return launch_grouped_mt<1>(fmt, p, num_experts, prod, rule, s, combine);
+  if (mt == kGroupedStreamWideMT)
+    return launch_grouped_mt<kGroupedStreamWideMT>(fmt, p, num_experts, prod, rule, s, combine);
   return hipErrorInvalidValue;
 }
 

@@ -455,10 +455,12 @@ __global__ __launch_bounds__(256) void router_kernel(const void* __restrict__ lo
 }
 
 // One thread: 8 consecutive hidden columns of one token.
+// addend (bf16 [T, H] or null): added to the fp32 sum after the routes, before the one rounding
 __global__ __launch_bounds__(256) void moe_reduce_kernel(const uint16_t* __restrict__ y,
                                                          const float* __restrict__ topk_weights,
                                                          const int32_t* __restrict__ inverse, int64_t T, int topk,
-                                                         int64_t H, uint16_t* __restrict__ out) {
+                                                         int64_t H, const uint16_t* __restrict__ addend,
+                                                         uint16_t* __restrict__ out) {
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t per_row = H / 8;
   if (id >= T * per_row) return;
@@ -477,6 +479,12 @@ __global__ __launch_bounds__(256) void moe_reduce_kernel(const uint16_t* __restr
       const float term = v[i] * wk;
       acc[i] = acc[i] + term;
     }
+  }
+  if (addend) {
+    float v[8];
+    bf16x8_to_f32(*reinterpret_cast<const uint4*>(addend + t * H + h0), v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
   }
   uint32_t o[4];
 #pragma unroll
@@ -589,14 +597,29 @@ extern "C" int mxl_moe_router(const void* logits, int logits_bf16, int64_t T, in
                        stream);
 }
 
-extern "C" int mxl_moe_reduce(const void* routed_output, const float* topk_weights, const int32_t* inverse, int64_t T,
-                              int64_t topk, int64_t H, void* out, void* stream) {
-  MXL_CHECK_ARG(T >= 0 && topk > 0 && H > 0 && H % 8 == 0, "mxl_moe_reduce: need H %% 8 == 0 (H=%lld)", (long long)H);
-  MXL_CHECK_ARG(((uintptr_t)routed_output & 15) == 0 && ((uintptr_t)out & 15) == 0, "mxl_moe_reduce: misaligned");
+static int moe_reduce_common(const char* who, const void* routed_output, const float* topk_weights,
+                             const int32_t* inverse, int64_t T, int64_t topk, int64_t H, const void* addend, void* out,
+                             void* stream) {
+  MXL_CHECK_ARG(T >= 0 && topk > 0 && H > 0 && H % 8 == 0, "%s: need H %% 8 == 0 (H=%lld)", who, (long long)H);
+  MXL_CHECK_ARG(((uintptr_t)routed_output & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)addend & 15) == 0,
+                "%s: misaligned", who);
   if (T == 0) return MXL_OK;
   const int64_t n = T * (H / 8);
   moe_reduce_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)routed_output, topk_weights, inverse, T, (int)topk, H, (uint16_t*)out);
-  MXL_CHECK_LAUNCH("mxl_moe_reduce");
+      (const uint16_t*)routed_output, topk_weights, inverse, T, (int)topk, H, (const uint16_t*)addend,
+      (uint16_t*)out);
+  MXL_CHECK_LAUNCH(who);
   return MXL_OK;
+}
+
+extern "C" int mxl_moe_reduce(const void* routed_output, const float* topk_weights, const int32_t* inverse, int64_t T,
+                              int64_t topk, int64_t H, void* out, void* stream) {
+  return moe_reduce_common("mxl_moe_reduce", routed_output, topk_weights, inverse, T, topk, H, nullptr, out, stream);
+}
+
+extern "C" int mxl_moe_reduce_add(const void* routed_output, const float* topk_weights, const int32_t* inverse,
+                                  int64_t T, int64_t topk, int64_t H, const void* addend, void* out, void* stream) {
+  MXL_CHECK_ARG(addend != nullptr, "mxl_moe_reduce_add: no addend");
+  return moe_reduce_common("mxl_moe_reduce_add", routed_output, topk_weights, inverse, T, topk, H, addend, out,
+                           stream);
 }

@@ -9,7 +9,10 @@ rows through the sorted route list, so no permuted copy of the activations is
 written, and experts that receive no rows read no weights.  Where the grouped
 weight-streaming schedules run (below ~96 routed rows per expert), they produce
 their own MXFP8 operands -- the quantization inside w13, the SwiGLU inside w2 --
-so a small-batch layer is four launches (route, w13, w2, combine).
+so a small-batch layer from router logits is four launches (router + sort, w13, w2,
+combine).  The down projection can also run the weighted combine itself (each token's
+row summed by the workgroup that stores its last routed row; ``fuse_combine``), which
+makes it three launches with the same bits but measured slower on MI355X.
 """
 from __future__ import annotations
 
@@ -46,6 +49,12 @@ class Mxfp6Experts:
         self.act_rule = act_rule
         self.mid_rule = mid_rule
         self.fuse = True  # fused producers where the grouped schedule admits them (False: separate launches)
+        # the weighted combine inside the down projection's launch (three launches from router
+        # logits at small batch; the same bits).  Off by default: measured at c5 T = 128 the
+        # layer takes 146.7 us with it against 141.4 us with the combine as its own launch --
+        # each unit's end waits on its device-coherent stores, the token counter and the
+        # routed rows' reads from beyond its XCD (w2 46.7 -> 58.4 us), more than a launch costs.
+        self.fuse_combine = False
         self.w1_scale: Optional[torch.Tensor] = None
         self.w2_scale: Optional[torch.Tensor] = None
         self.shapes: Optional[tuple[int, int, int]] = None  # (E, H, I)
@@ -130,7 +139,20 @@ class Mxfp6Experts:
             a, sa = torch.ops.mach_amd.quantize_mxfp8(hidden_states, self.act_rule)
             gate_up = torch.ops.mach_amd.grouped_gemm(a, sa, sorted_routes, topk, offsets, routes, w1,
                                                       self.w1_scale, 2 * I, H, self.fmt)
-        if self.fuse and ops.grouped_fused_supported(routes, E, I, self.fmt):
+        swiglu_fused = self.fuse and ops.grouped_fused_supported(routes, E, I, self.fmt)
+        if self.fuse_combine and ops.grouped_combine_supported(routes, E, H, I, self.fmt, swiglu_fused, topk) \
+                and output.is_contiguous():
+            # the weighted combine inside the down projection's launch (the same bits)
+            if swiglu_fused:
+                torch.ops.mach_amd.grouped_gemm_swiglu_combine(output, gate_up, offsets, routes, w2, self.w2_scale,
+                                                               H, I, self.fmt, self.mid_rule, sorted_routes, inverse,
+                                                               topk_weights)
+            else:
+                a2, sa2 = torch.ops.mach_amd.swiglu_mxfp8(gate_up, self.mid_rule, False)
+                torch.ops.mach_amd.grouped_gemm_combine(output, a2, sa2, None, 1, offsets, routes, w2, self.w2_scale,
+                                                        H, I, self.fmt, sorted_routes, inverse, topk_weights)
+            return
+        if swiglu_fused:
             y = torch.ops.mach_amd.grouped_gemm_swiglu(gate_up, offsets, routes, w2, self.w2_scale, H, I, self.fmt,
                                                        self.mid_rule)
         else:

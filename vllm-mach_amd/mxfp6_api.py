@@ -20,9 +20,11 @@ The reference binds its MX kernels through two kinds of native entry points:
   ``mxfp6.mxfp8`` (dense MXFP8, dense_mxfp8.py:45-220) and ``mxfp6.mxfp8_dual``
   (two-limb MXFP8, mxfp8/dual.py:40-50, 109-111) as the attributes ``mxfp8`` and
   ``mxfp8_dual``.  This module provides them with the same names, argument order and
-  mutation contracts.  The Qwen3.5 TP2 schedules (``qwen35_*``,
-  ``array_gemm_w6a8_reduce_out``, ``Qwen35GroupedWorkspace``) are multi-GPU and are
-  not provided.
+  mutation contracts.  The rest of the MoE API the reference checks for
+  (``_MOE_REQUIRED_API``, moe_utils.py:28-44: ``qwen35_*``, ``array_gemm_w6a8_reduce_out``,
+  ``Qwen35GroupedWorkspace``) are single-GPU schedules over one rank's experts; they are
+  provided over the same kernels for any shape those take (the router, the grouped GEMMs
+  with fused producers, the down projection with the combine in its launch).
 
 Layouts at this boundary are the reference's: weights stay in their checkpoint form
 (E4M3 [N, K], packed FP6 [E, N, 3K/4]); weight scales are ``pack_scales`` output,
@@ -37,11 +39,11 @@ buffer has the reference's size, rows + 127 per expert), and ``scale_offsets`` e
 from __future__ import annotations
 
 import threading
-import weakref
 from pathlib import Path
 from typing import NamedTuple, Optional
 
 import torch
+from torch.utils.weak import WeakTensorKeyDictionary
 
 from . import _lib, ops
 from ._lib import call, ptr, query, stream_handle
@@ -173,7 +175,9 @@ def to_mma_k64_weight(weight: torch.Tensor) -> torch.Tensor:
 
 # ---------------------------------------------------------- tiled experts
 
-_tiles: "weakref.WeakKeyDictionary[torch.Tensor, tuple]" = weakref.WeakKeyDictionary()
+# keyed by tensor identity (a WeakKeyDictionary would compare colliding keys with the
+# tensors' elementwise ==); an entry goes when its weight tensor does
+_tiles = WeakTensorKeyDictionary()
 
 
 def _tiled_experts(weight: torch.Tensor, weight_scales: torch.Tensor, fmt: int):
@@ -260,6 +264,234 @@ def moe_reduce_out(output: torch.Tensor, routed_output: torch.Tensor, topk_weigh
                    inverse_permutation: torch.Tensor) -> None:
     """output[t] = bf16(sum_k w[t, k] y[inverse[t*topk + k]]) in fp32 (moe.py:697-702)."""
     torch.ops.mach_amd.moe_reduce(output, routed_output, topk_weights, inverse_permutation)
+
+
+# ------------------------------------------- fused and grouped MoE schedules
+#
+# The reference's native schedules (src/vllm_mach/mxfp6/moe.py:126-313; names in
+# moe_utils.py:28-44) are written for one TP2 shard of a Qwen3.5 layer with a shared
+# expert appended to the routed ones (moe.py:398-426: w13/w2/scales gain expert E,
+# combined_gate = [router gate; shared expert gate]).  Their kernels are in the absent
+# wheel, so the arithmetic below is this library's definition, for any shape the grouped
+# kernels take (the unsharded c5 layer included):
+#   * logits = bf16(hidden . combined_gate^T) (fp32 accumulation); routed_logits are its
+#     first E columns, shared_gate the last;
+#   * top-k of softmax(routed_logits) renormalized (the router kernel, ties to the lower
+#     expert), MXFP8 input codes under floor_carry175;
+#   * with a shared expert, each token has a (topk + 1)-th route to expert E weighted
+#     sigmoid(shared_gate) (binary32), combined last;
+#   * routed activations SwiGLU -> MXFP8 under ceil_div448 (bf16 SiLU), as the layer's;
+#   * the combine sums a token's routes in route order in fp32 and rounds once.
+
+
+# The combine inside the down projection's launch (the reference's reduce-fused w2
+# schedules); off by default: on MI355X the separate combine launch measured faster
+# (c5 T = 128 layer 141.4 against 146.7 us).
+FUSE_COMBINE = False
+
+
+def _route_ext(topk_ids: torch.Tensor, topk_weights: Optional[torch.Tensor], routes: int, experts: int,
+               shared_gate: Optional[torch.Tensor]):
+    """Route table [T, k] with the shared expert's route appended when ``routes`` holds
+    T * (topk + 1) rows; its weight sigmoid(shared_gate)."""
+    T, topk = topk_ids.shape
+    ids = topk_ids.to(torch.int32)
+    wts = None if topk_weights is None else topk_weights.to(torch.float32)
+    if routes == T * (topk + 1):
+        ids = torch.cat([ids, torch.full((T, 1), experts - 1, dtype=torch.int32, device=ids.device)], 1)
+        if wts is not None:
+            if shared_gate is None:
+                raise ValueError("a shared-expert route needs shared_gate")
+            wts = torch.cat([wts, torch.sigmoid(shared_gate.float().reshape(T, 1))], 1)
+    elif routes != T * topk:
+        raise ValueError(f"{routes} routed rows for {T} tokens x {topk} routes")
+    return ids.contiguous(), None if wts is None else wts.contiguous()
+
+
+def qwen35_router_quant_out(quantized: torch.Tensor, input_scales: torch.Tensor, routed_logits: torch.Tensor,
+                            topk_weights: torch.Tensor, topk_ids: torch.Tensor, shared_gate: torch.Tensor,
+                            hidden_states: torch.Tensor, combined_gate: torch.Tensor, renormalize: bool = True) -> None:
+    """Router GEMM, softmax top-k and MXFP8 input quantization (moe.py:142-152): writes
+    every output argument.  ``combined_gate`` [E + 1, H] bf16 (the routed gate rows, then
+    the shared expert's gate row)."""
+    T, H = hidden_states.shape
+    E = routed_logits.shape[1]
+    if combined_gate.shape != (E + 1, H) or shared_gate.numel() != T:
+        raise ValueError("combined_gate must be [E + 1, H] with shared_gate [T]")
+    logits = torch.matmul(hidden_states, combined_gate.t())
+    routed_logits.copy_(logits[:, :E])
+    shared_gate.copy_(logits[:, E].reshape(shared_gate.shape))
+    w, ids, _, _, _ = torch.ops.mach_amd.moe_router(routed_logits, topk_ids.shape[1], renormalize)
+    topk_weights.copy_(w)
+    topk_ids.copy_(ids)
+    call("mxl_quantize_mxfp8", ptr(hidden_states), T, H, hidden_states.stride(0), ops.FLOOR_CARRY175,
+         ptr(quantized), ptr(input_scales), stream_handle(hidden_states.device))
+
+
+def qwen35_w1_splitk_silu_mxfp8_out(activation: torch.Tensor, activation_scales: torch.Tensor,
+                                    w1_partial: torch.Tensor, quantized: torch.Tensor, input_scales: torch.Tensor,
+                                    w1: torch.Tensor, w1_scales: torch.Tensor, topk_ids: torch.Tensor) -> None:
+    """Grouped gate_up GEMM of every route, SwiGLU -> MXFP8 (moe.py:153-162): activation
+    [routes, I] E4M3 and activation_scales [routes, I/32] in route order (token-major,
+    the shared expert's route last).  ``w1_partial`` is the reference's split-K scratch,
+    unused here."""
+    tiled, tiled_s, N, K = _tiled_experts(w1, w1_scales, WEIGHT_FORMAT)
+    experts = w1.shape[0]
+    routes = activation.shape[0]
+    ids, _ = _route_ext(topk_ids, None, routes, experts, None)
+    sorted_routes, offsets, inverse = torch.ops.mach_amd.moe_route(ids, experts)
+    gate_up = torch.ops.mach_amd.grouped_gemm(quantized, input_scales, sorted_routes, ids.shape[1], offsets, routes,
+                                              tiled, tiled_s, N, K, WEIGHT_FORMAT)
+    codes, scales = torch.ops.mach_amd.swiglu_mxfp8(gate_up, ops.CEIL_DIV448, False)
+    # route r's row is sorted row inverse[r] (no route is dropped: every id is an expert)
+    torch.index_select(codes.view(torch.uint8), 0, inverse.long(), out=activation.view(torch.uint8))
+    torch.index_select(scales.view(torch.uint8), 0, inverse.long(), out=activation_scales.view(torch.uint8))
+
+
+def _w2_reduce(output, activation, activation_scales, w2, w2_scales, topk_ids, topk_weights, shared_gate):
+    tiled, tiled_s, N, K = _tiled_experts(w2, w2_scales, WEIGHT_FORMAT)
+    experts = w2.shape[0]
+    routes = activation.shape[0]
+    ids, wts = _route_ext(topk_ids, topk_weights, routes, experts, shared_gate)
+    sorted_routes, offsets, inverse = torch.ops.mach_amd.moe_route(ids, experts)
+    a, sa = activation.view(torch.uint8), activation_scales.view(torch.uint8)
+    if FUSE_COMBINE and ops.grouped_combine_supported(routes, experts, N, K, WEIGHT_FORMAT, False, ids.shape[1]) \
+            and output.is_contiguous():
+        # routed row p gathers activation row sorted_routes[p]; the combine runs in the launch
+        torch.ops.mach_amd.grouped_gemm_combine(output, a, sa, sorted_routes, 1, offsets, routes, tiled, tiled_s, N, K,
+                                                WEIGHT_FORMAT, sorted_routes, inverse, wts)
+    else:
+        y = torch.ops.mach_amd.grouped_gemm(a, sa, sorted_routes, 1, offsets, routes, tiled, tiled_s, N, K,
+                                            WEIGHT_FORMAT)
+        torch.ops.mach_amd.moe_reduce(output, y, wts, inverse)
+
+
+def qwen35_w2_splitk_reduce_out(output: torch.Tensor, w2_partial: torch.Tensor, activation: torch.Tensor,
+                                activation_scales: torch.Tensor, w2: torch.Tensor, w2_scales: torch.Tensor,
+                                topk_ids: torch.Tensor, topk_weights: torch.Tensor, shared_gate: torch.Tensor) -> None:
+    """Grouped down projection of the routed activations with the weighted combine
+    (moe.py:163-175): output [T, H] bf16.  ``w2_partial`` (split-K scratch) is unused."""
+    _w2_reduce(output, activation, activation_scales, w2, w2_scales, topk_ids, topk_weights, shared_gate)
+
+
+def array_gemm_w6a8_reduce_out(output: torch.Tensor, activation: torch.Tensor, activation_scales: torch.Tensor,
+                               w2: torch.Tensor, w2_scales: torch.Tensor, topk_ids: torch.Tensor,
+                               topk_weights: torch.Tensor, shared_gate: torch.Tensor,
+                               use_packed_vector_loads: bool = False) -> None:
+    """The multi-token form of ``qwen35_w2_splitk_reduce_out`` (moe.py:176-186); the load
+    width option is the reference kernel's and has no counterpart here."""
+    _w2_reduce(output, activation, activation_scales, w2, w2_scales, topk_ids, topk_weights, shared_gate)
+
+
+def qwen35_grouped_workspace_shapes(tokens: int, hidden: int = 2048, intermediate: int = 512, top_k: int = 8):
+    """(workspace13, workspace2) shapes of the grouped schedule (moe.py:193-214): the
+    routed gate/up rows [T k, 2I] and the routed down-projection rows [T k, H], bf16."""
+    return (tokens * top_k, 2 * intermediate), (tokens * top_k, hidden)
+
+
+class Qwen35GroupedWorkspace:
+    """Buffers of the grouped schedule (moe.py:193-214): the layer output, the routed gate/up
+    rows (workspace13) and routed output rows (workspace2), plus the routing of the last
+    ``qwen35_grouped_gemm_out`` for ``qwen35_grouped_reduce_out``."""
+
+    def __init__(self, output: torch.Tensor, workspace13: torch.Tensor, workspace2: torch.Tensor):
+        self.output = output
+        self.workspace13 = workspace13
+        self.workspace2 = workspace2
+        self.topk_weights: Optional[torch.Tensor] = None
+        self.inverse: Optional[torch.Tensor] = None
+
+    @classmethod
+    def from_storage(cls, output: torch.Tensor, workspace13: torch.Tensor, workspace2: torch.Tensor):
+        return cls(output, workspace13, workspace2)
+
+
+def _grouped_gemms(workspace: Qwen35GroupedWorkspace, hidden_states, w1, w1_scales, w2, w2_scales,
+                   weights, ids, sorted_routes, offsets, inverse, output: Optional[torch.Tensor]):
+    """w13 (input quantization fused where the schedule takes it) into workspace13, then
+    SwiGLU -> MXFP8 and w2 into workspace2, or with ``output`` the combine in w2's launch."""
+    t1, s1, N1, K1 = _tiled_experts(w1, w1_scales, WEIGHT_FORMAT)
+    t2, s2, N2, K2 = _tiled_experts(w2, w2_scales, WEIGHT_FORMAT)
+    E = w1.shape[0]
+    T, topk = ids.shape
+    routes = T * topk
+    gate_up = workspace.workspace13.reshape(-1)[: routes * N1].view(routes, N1)
+    dev = hidden_states.device
+    st = stream_handle(dev)
+    if ops.grouped_fused_supported(routes, E, K1, WEIGHT_FORMAT) and hidden_states.stride(1) == 1:
+        call("mxl_grouped_gemm_quant", ptr(hidden_states), hidden_states.stride(0), ptr(sorted_routes), topk,
+             ptr(offsets), E, routes, ptr(t1), ptr(s1), N1, K1, WEIGHT_FORMAT, ops.FLOOR_CARRY175, ptr(gate_up), st)
+    else:
+        a, sa = torch.ops.mach_amd.quantize_mxfp8(hidden_states, ops.FLOOR_CARRY175)
+        call("mxl_grouped_gemm", ptr(a), ptr(sa), T, ptr(sorted_routes), topk, ptr(offsets), E, routes, ptr(t1),
+             ptr(s1), N1, K1, WEIGHT_FORMAT, ptr(gate_up), st)
+    I = N1 // 2
+    fused = ops.grouped_fused_supported(routes, E, I, WEIGHT_FORMAT)
+    if output is not None and FUSE_COMBINE and ops.grouped_combine_supported(routes, E, N2, K2, WEIGHT_FORMAT,
+                                                                              fused, topk):
+        if fused:
+            torch.ops.mach_amd.grouped_gemm_swiglu_combine(output, gate_up, offsets, routes, t2, s2, N2, K2,
+                                                           WEIGHT_FORMAT, ops.CEIL_DIV448, sorted_routes, inverse,
+                                                           weights)
+        else:
+            a2, sa2 = torch.ops.mach_amd.swiglu_mxfp8(gate_up, ops.CEIL_DIV448, False)
+            torch.ops.mach_amd.grouped_gemm_combine(output, a2, sa2, None, 1, offsets, routes, t2, s2, N2, K2,
+                                                    WEIGHT_FORMAT, sorted_routes, inverse, weights)
+        return
+    y = workspace.workspace2.reshape(-1)[: routes * N2].view(routes, N2)
+    if fused:
+        call("mxl_grouped_gemm_swiglu", ptr(gate_up), ptr(offsets), E, routes, ptr(t2), ptr(s2), N2, K2,
+             WEIGHT_FORMAT, ops.CEIL_DIV448, ptr(y), st)
+    else:
+        a2, sa2 = torch.ops.mach_amd.swiglu_mxfp8(gate_up, ops.CEIL_DIV448, False)
+        call("mxl_grouped_gemm", ptr(a2), ptr(sa2), routes, None, 1, ptr(offsets), E, routes, ptr(t2), ptr(s2), N2,
+             K2, WEIGHT_FORMAT, ptr(y), st)
+    if output is not None:
+        torch.ops.mach_amd.moe_reduce(output, y, weights, inverse)
+
+
+def qwen35_grouped_gemm_out(workspace: Qwen35GroupedWorkspace, hidden_states: torch.Tensor,
+                            router_logits: torch.Tensor, w1: torch.Tensor, w1_scales: torch.Tensor, w2: torch.Tensor,
+                            w2_scales: torch.Tensor, renormalize: bool = True) -> None:
+    """The grouped schedule from router logits (moe.py:282-291): the router kernel (softmax,
+    top-k, sort), w13 and w2 into the workspace; ``qwen35_grouped_reduce_out`` combines.
+    The top-k is the workspace's routed rows per token."""
+    T = hidden_states.shape[0]
+    topk = workspace.workspace13.shape[0] // T if T else 1
+    weights, ids, sorted_routes, offsets, inverse = torch.ops.mach_amd.moe_router(router_logits, topk, renormalize)
+    _grouped_gemms(workspace, hidden_states, w1, w1_scales, w2, w2_scales, weights, ids, sorted_routes, offsets,
+                   inverse, None)
+    workspace.topk_weights, workspace.inverse = weights, inverse
+
+
+def qwen35_grouped_reduce_out(workspace: Qwen35GroupedWorkspace, output: torch.Tensor,
+                              shared_output: Optional[torch.Tensor] = None) -> None:
+    """Weighted combine of the workspace's routed rows into ``output`` (moe.py:296-302),
+    with ``shared_output`` added to the fp32 sum before the one rounding."""
+    if workspace.inverse is None:
+        raise RuntimeError("qwen35_grouped_gemm_out must run before qwen35_grouped_reduce_out")
+    T, H = output.shape
+    topk = workspace.topk_weights.shape[1]
+    y = workspace.workspace2.reshape(-1)[: T * topk * H].view(T * topk, H)
+    if shared_output is None:
+        torch.ops.mach_amd.moe_reduce(output, y, workspace.topk_weights, workspace.inverse)
+        return
+    if not output.is_contiguous() or shared_output.shape != output.shape:
+        raise ValueError("output must be contiguous and shared_output of its shape")
+    add = shared_output.to(torch.bfloat16).contiguous()
+    call("mxl_moe_reduce_add", ptr(y), ptr(workspace.topk_weights), ptr(workspace.inverse), T, topk, H, ptr(add),
+         ptr(output), stream_handle(output.device))
+
+
+def qwen35_grouped_moe_out(workspace: Qwen35GroupedWorkspace, output: torch.Tensor, hidden_states: torch.Tensor,
+                           w1: torch.Tensor, w1_scale: torch.Tensor, w2: torch.Tensor, w2_scale: torch.Tensor,
+                           topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> None:
+    """The routed layer from a given routing (moe_utils.py:47-74): sort, w13, w2 and the
+    combine into ``output`` (the combine inside w2's launch where the schedule takes it)."""
+    ids = topk_ids.to(torch.int32).contiguous()
+    sorted_routes, offsets, inverse = torch.ops.mach_amd.moe_route(ids, w1.shape[0])
+    _grouped_gemms(workspace, hidden_states, w1, w1_scale, w2, w2_scale, topk_weights.to(torch.float32).contiguous(),
+                   ids, sorted_routes, offsets, inverse, output)
 
 
 # ---------------------------------------------------- workspace planning

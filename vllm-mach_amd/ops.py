@@ -17,6 +17,7 @@ mxfp6/warmup.py:75-147).
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import threading
 from typing import Optional
 
@@ -59,9 +60,10 @@ def inspect() -> dict:
     captured graphs."""
     with _ws_lock:
         return {"counts": dict(_COUNTS),
-                "workspaces": {f"{d}:{s:#x}:{kind}": w.buf.numel() for (d, s, kind), w in _workspaces.items()},
+                "workspaces": {**{f"{d}:{s:#x}:{kind}": w.buf.numel() for (d, s, kind), w in _workspaces.items()},
+                               **{f"{d}:{s:#x}:combine": 4 * w.buf.numel() for (d, s), w in _counters.items()}},
                 "planned": {f"{d}:{kind}": n for (d, kind), n in _planned.items()},
-                "retired_bytes": sum(t.numel() for t in _retired)}
+                "retired_bytes": sum(t.numel() * t.element_size() for t in _retired)}
 
 
 def _device_index(device: torch.device) -> int:
@@ -109,7 +111,10 @@ def reserve_workspaces(device: torch.device) -> None:
     with _ws_lock:
         for (d, kind), n in list(_planned.items()):
             if d == di:
-                workspace(device, n, kind)
+                if kind == "combine":
+                    combine_counters(device, n // 4)
+                else:
+                    workspace(device, n, kind)
 
 
 # Kernel-selection override for tuning runs and tests (None: the library's cost model).
@@ -846,4 +851,114 @@ def moe_reduce(output: torch.Tensor, routed_output: torch.Tensor, topk_weights: 
 
 @moe_reduce.register_fake
 def _(output, routed_output, topk_weights, inverse):
+    return None
+
+
+# (device index, stream handle) -> zeroed int32 token counters of the combine-fused down
+# projections (each launch leaves them zero); superseded buffers a graph may hold are kept
+_counters: dict[tuple[int, int], _Workspace] = {}
+
+
+def combine_counters(device: torch.device, tokens: int) -> torch.Tensor:
+    """Per-(device, stream) int32 counters, zero, for ``tokens`` tokens: grown outside
+    capture (zero-filled on the stream), never reallocated during capture (a miss raises,
+    as a workspace miss does)."""
+    di = _device_index(device)
+    key = (di, stream_handle(device))
+    capturing = torch.cuda.is_current_stream_capturing()
+    with _ws_lock:
+        _planned[(di, "combine")] = max(_planned.get((di, "combine"), 0), 4 * tokens)
+        ws = _counters.get(key)
+        if ws is None or ws.buf.numel() < tokens:
+            if capturing:
+                _count("capture_cache_miss")
+                raise RuntimeError(f"mach_amd combine counters for stream {key[1]:#x} hold "
+                                   f"{0 if ws is None else ws.buf.numel()} tokens but this call needs {tokens}; "
+                                   "run the shape once (warmup) before graph capture")
+            size = max(tokens, _planned[(di, "combine")] // 4, 0 if ws is None else 2 * ws.buf.numel())
+            if ws is not None and ws.captured:
+                _retired.append(ws.buf)
+            ws = _Workspace(torch.zeros(size, dtype=torch.int32, device=device))
+            _counters[key] = ws
+            _count("workspace_miss")
+        if capturing:
+            ws.captured = True
+        return ws.buf
+
+
+def grouped_combine_supported(routed_rows: int, num_experts: int, n: int, k: int, w_fmt: int,
+                              swiglu: bool, topk: int = 8) -> bool:
+    """Whether a down projection with the weighted combine in its launch runs this shape
+    (``swiglu``: with the SwiGLU producer fused as well): the small-batch schedule, at most
+    16 routes per token."""
+    return 1 <= topk <= 16 and bool(query("mxl_grouped_combine_supported", routed_rows, num_experts, n, k, w_fmt,
+                                          2 if swiglu else 0))
+
+
+def _combine_call(fn: str, output: torch.Tensor, routed_rows: int, n: int, sorted_routes: torch.Tensor,
+                  inverse: torch.Tensor, topk_weights: torch.Tensor, *lead):
+    T = output.shape[0]
+    topk = topk_weights.shape[1]
+    if output.dtype != torch.bfloat16 or tuple(output.shape) != (T, n) or not output.is_contiguous():
+        raise ValueError(f"combine output must be contiguous bf16 [T, {n}]")
+    if tuple(topk_weights.shape) != (T, topk) or inverse.numel() != T * topk:
+        raise ValueError("topk_weights [T, topk] and inverse [T * topk] must match the output")
+    dev = output.device
+    y = torch.empty((routed_rows, n), dtype=torch.bfloat16, device=dev)
+    w = topk_weights.to(torch.float32).contiguous()
+    inv = inverse.contiguous()
+    routes = sorted_routes.contiguous()
+    cnt = combine_counters(dev, T)
+    desc = _lib.MoeCombine(ptr(routes), ptr(inv), ptr(w), T, topk, ptr(output), ptr(cnt))
+    call(fn, *lead, ptr(y), ctypes.byref(desc), stream_handle(dev))
+
+
+@torch.library.custom_op("mach_amd::grouped_gemm_combine", mutates_args=("output",))
+def grouped_gemm_combine(output: torch.Tensor, a: torch.Tensor, sa: torch.Tensor, row_index: Optional[torch.Tensor],
+                         row_div: int, expert_offsets: torch.Tensor, routed_rows: int, w: torch.Tensor,
+                         sw: torch.Tensor, n: int, k: int, w_fmt: int, sorted_routes: torch.Tensor,
+                         inverse: torch.Tensor, topk_weights: torch.Tensor) -> None:
+    """Grouped down projection (routed row p = A[row_index[p] // row_div] . W[e]^T, or A[p]
+    without row_index) with the weighted combine in the same launch: ``output`` [T, n] =
+    the bits of ``grouped_gemm`` then ``moe_reduce`` (grouped_gemm_w6a8_out + moe_reduce_out
+    as one kernel, the role of the reference's array_gemm_w6a8_reduce_out,
+    src/vllm_mach/mxfp6/moe.py:163-186)."""
+    _check_cuda(output, a, sa, row_index, expert_offsets, w, sw, sorted_routes, inverse, topk_weights)
+    a8 = _u8(a).contiguous()
+    sa8 = _u8(sa).contiguous()
+    E = expert_offsets.shape[0] - 1
+    _combine_call("mxl_grouped_gemm_combine", output, routed_rows, n, sorted_routes, inverse, topk_weights,
+                  ptr(a8), ptr(sa8), a8.shape[0], ptr(row_index), row_div, ptr(expert_offsets), E, routed_rows,
+                  ptr(w), ptr(sw), n, k, w_fmt)
+    _count("grouped_gemm_combine")
+
+
+@grouped_gemm_combine.register_fake
+def _(output, a, sa, row_index, row_div, expert_offsets, routed_rows, w, sw, n, k, w_fmt, sorted_routes, inverse,
+      topk_weights):
+    return None
+
+
+@torch.library.custom_op("mach_amd::grouped_gemm_swiglu_combine", mutates_args=("output",))
+def grouped_gemm_swiglu_combine(output: torch.Tensor, gate_up: torch.Tensor, expert_offsets: torch.Tensor,
+                                routed_rows: int, w: torch.Tensor, sw: torch.Tensor, n: int, k: int, w_fmt: int,
+                                rule: int, sorted_routes: torch.Tensor, inverse: torch.Tensor,
+                                topk_weights: torch.Tensor) -> None:
+    """SwiGLU -> MXFP8 of the routed gate/up rows, the grouped down projection and the
+    weighted combine in one launch: ``output`` [T, n] = the bits of ``grouped_gemm_swiglu``
+    then ``moe_reduce`` (the reference's qwen35_w2_splitk_reduce_out role,
+    src/vllm_mach/mxfp6/moe.py:163-175)."""
+    _check_cuda(output, gate_up, expert_offsets, w, sw, sorted_routes, inverse, topk_weights)
+    if gate_up.dtype != torch.bfloat16 or gate_up.ndim != 2 or gate_up.shape[1] != 2 * k:
+        raise ValueError("grouped_gemm_swiglu_combine needs bf16 gate/up rows [R, 2K]")
+    gate_up = gate_up.contiguous()
+    E = expert_offsets.shape[0] - 1
+    _combine_call("mxl_grouped_gemm_swiglu_combine", output, routed_rows, n, sorted_routes, inverse, topk_weights,
+                  ptr(gate_up), ptr(expert_offsets), E, routed_rows, ptr(w), ptr(sw), n, k, w_fmt, rule)
+    _count("grouped_gemm_swiglu_combine")
+
+
+@grouped_gemm_swiglu_combine.register_fake
+def _(output, gate_up, expert_offsets, routed_rows, w, sw, n, k, w_fmt, rule, sorted_routes, inverse,
+      topk_weights):
     return None
