@@ -311,7 +311,8 @@ def test_moe_fused_producers_bit_identical(pkg, oracle_mod, dev, E, H, I, T, top
     out_f = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     before = dict(ops._COUNTS)
     experts.apply(out_f, x, e1, e2, wts, ids, "silu", Eg, emap, None, None, None, None, None, False)
-    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items() if v != before.get(k, 0)}
+    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items()
+             if v != before.get(k, 0) and k != "workspace_miss"}  # launches, not allocations
     if (E, T) == (256, 128):
         assert fused[0] and calls == {"moe_route": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu": 1,
                                       "moe_reduce": 1}, calls
@@ -319,7 +320,8 @@ def test_moe_fused_producers_bit_identical(pkg, oracle_mod, dev, E, H, I, T, top
     out_c = torch.empty_like(out_f)
     before = dict(ops._COUNTS)
     experts.apply(out_c, x, e1, e2, wts, ids, "silu", Eg, emap, None, None, None, None, None, False)
-    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items() if v != before.get(k, 0)}
+    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items()
+             if v != before.get(k, 0) and k != "workspace_miss"}  # launches, not allocations
     assert torch.equal(out_f, out_c)
     if (E, T) == (256, 128):
         assert calls == {"moe_route": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu_combine": 1}, calls
@@ -390,7 +392,8 @@ def test_moe_layer_from_router_logits(pkg, oracle_mod, dev, T):
     before = dict(ops._COUNTS)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     experts.apply_router(out, xd, w1, w2, logits, topk, True)
-    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items() if v != before.get(k, 0)}
+    calls = {k: v - before.get(k, 0) for k, v in ops._COUNTS.items()
+             if v != before.get(k, 0) and k != "workspace_miss"}  # launches, not allocations
     if T == 128:  # three launches: router + sort, w13 + quantization, w2 + SwiGLU + combine
         assert calls == {"moe_router": 1, "grouped_gemm_quant": 1, "grouped_gemm_swiglu_combine": 1}, calls
     experts.fuse_combine = False
