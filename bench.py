@@ -192,8 +192,8 @@ class SwigluDown(Workload):
                                               mx_weight_bytes(N, K, 0) + M * K * (1 + 1 / 32) + M * N * 2),
             f"swiglu_mxfp8 M={M} K={K}": (prod, 0.0, M * K * 4 + M * K * (1 + 1 / 32)),
         }
-        if ops.swiglu_row_fusable(M, K, ops.CEIL_DIV448):
-            # the step's path at one row: producer and GEMM in one launch
+        if ops.swiglu_row_fusable(M, K, ops.CEIL_DIV448, ops.E4M3):
+            # the step's path at decode sizes: producer and GEMM in one launch
             fused = [lambda wt=wt, st=st: torch.ops.mach_amd.swiglu_mx_gemm(self.inputs[M], wt, st, N, ops.E4M3,
                                                                               ops.CEIL_DIV448)
                      for wt, st in self.copies]
@@ -252,8 +252,8 @@ class MxLinear(Workload):
                                               mx_weight_bytes(N, K, fmt) + M * K * (1 + 1 / 32) + M * N * 2),
             f"quantize_mxfp8 M={M} K={K}": (quant, 0.0, M * K * 2 + M * K * (1 + 1 / 32)),
         }
-        if ops.quant_row_fusable(M, K, ops.FLOOR_CARRY175):
-            # the step's path for one row: the quantizer inside the weight-streaming GEMM
+        if ops.quant_row_fusable(M, K, ops.FLOOR_CARRY175, fmt):
+            # the step's path at decode sizes: the quantizer inside the weight-streaming GEMM
             fused = [lambda wt=wt, st=st: torch.ops.mach_amd.quant_mx_gemm(self.inputs[M], wt, st, N, fmt,
                                                                            ops.FLOOR_CARRY175, None)
                      for wt, st in self.copies]
@@ -287,8 +287,7 @@ class BlockFp8Linear(Workload):
         self.quant = {M: torch.ops.mach_amd.quantize_block_fp8(self.inputs[M]) for M in self.sweep}
 
     def _linear(self, x, wt, sb):
-        q, s = torch.ops.mach_amd.quantize_block_fp8(x)
-        return torch.ops.mach_amd.block_fp8_gemm(q, s, wt, sb, self.N, self.K, None)
+        return self.ops.block_fp8_from_float(x, wt, sb, self.N)
 
     def step_fns(self, ci):
         wt, sb = self.copies[ci % len(self.copies)]
@@ -307,10 +306,17 @@ class BlockFp8Linear(Workload):
                 for wt, sb in self.copies]
         quant = [lambda: torch.ops.mach_amd.quantize_block_fp8(self.inputs[M])] * 8
         w_bytes = N * K + (N // 128) * (K // 128) * 4
-        return {
+        out = {
             f"block_fp8 gemm M={M} N={N} K={K}": (gemm, self.flops(M), w_bytes + M * K * (1 + 4 / 128) + M * N * 2),
             f"quantize_block_fp8 M={M} K={K}": (quant, 0.0, M * K * 2 + M * K * (1 + 4 / 128)),
         }
+        if self.ops.block_row_fusable(M, K):
+            # the step's path at decode sizes: the quantizer inside the weight-streaming GEMM
+            fused = [lambda wt=wt, sb=sb: torch.ops.mach_amd.block_fp8_quant_gemm(self.inputs[M], wt, sb, N, None)
+                     for wt, sb in self.copies]
+            out[f"quantize->block_fp8 gemm, one launch, M={M} N={N} K={K}"] = (
+                fused, self.flops(M), w_bytes + M * K * 2 + M * N * 2)
+        return out
 
 
 class MoeLayer(Workload):

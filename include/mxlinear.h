@@ -228,39 +228,70 @@ int64_t mxl_noalloc_scratch_bytes(void);
 int mxl_mx_gemm_noalloc(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,
                         int64_t N, int64_t K, int w_fmt, const void* bias, void* out, int64_t ldc, void* stream);
 
-/* SwiGLU -> MXFP8 -> MX GEMM for one activation row, in one launch: the weight-
- * streaming GEMM computes the row's codes and scales from gate_up bf16 [1, 2K]
- * itself, with the producer's arithmetic (mxl_swiglu_mxfp8, rule 1 or 2), so y is
- * bit-identical to mxl_swiglu_mxfp8 followed by mxl_mx_gemm.  K % 128 == 0,
- * K <= 12288; other shapes return MXL_EUNSUPPORTED (use the two calls).  Replaces
- * mach_swiglu_mxfp8_down at M = 1 (src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22,71-76). */
+/* SwiGLU -> MXFP8 -> MX GEMM for M <= 16 activation rows in one launch, bit-identical
+ * to mxl_swiglu_mxfp8 (logical scales) followed by mxl_mx_gemm; rule 1 or 2, gate_up bf16
+ * [M, 2K], K % 128 == 0.  M > 1: the last wavefront of every workgroup of the weight-
+ * streaming GEMM is a producer wave that computes its share of the [M, K] codes with the
+ * producer's arithmetic into a per-(device, stream) slot of the library's static scratch
+ * (64 slots of 200 KiB per GPU, held until the process ends; a 65th stream on one device
+ * returns MXL_EUNSUPPORTED), then a grid-wide handoff through device-scope counters in the
+ * slot (left zero) lets the weight waves, whose weights were requested at launch, read the
+ * codes.  All workgroups are resident at once (at most one per CU).  The handoff shapes:
+ * K <= 7680 or 8192 < K <= 11264 (E4M3) and K <= 7680 (FP6).  M = 1: any K <= 12288, by
+ * the handoff or with every wavefront recomputing the row's codes from gate_up.  Other
+ * shapes return MXL_EUNSUPPORTED (use the two calls; mxl_producer_gemm_supported says which
+ * run).  Calls on one stream are ordered; calls on different streams use different slots.
+ * Replaces mach_swiglu_mxfp8_down at M <= 16 and mxfp6::gemm_from_swiglu's fused rows
+ * (src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22,71-76, src/vllm_mach/mxfp6/fused_mlp.py:13-19). */
 int mxl_swiglu_mx_gemm(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
                        const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
                        void* stream);
 
-/* mxl_swiglu_mx_gemm with the output format and scale of `options` (out_dtype,
- * alpha; NULL: bf16, 1).  Replaces mxfp6::gemm_from_swiglu(gate_up, w, ws, N,
- * alpha, dtype) (src/vllm_mach/mxfp6/fused_mlp.py:16-19). */
+/* mxl_swiglu_mx_gemm with the output format and scale of `options` (out_dtype, alpha;
+ * NULL: bf16, 1) and the scheme in options->kernel: -1 automatic (the handoff where it
+ * runs), 0 the producer waves and handoff, 3 every wavefront recomputes the row (M = 1).
+ * Replaces mxfp6::gemm_from_swiglu(gate_up, w, ws, N, alpha, dtype)
+ * (src/vllm_mach/mxfp6/fused_mlp.py:16-19). */
 int mxl_swiglu_mx_gemm_ex(const void* gate_up, int64_t M, int64_t K, int rule, const void* w_tiled,
                           const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
                           const mxl_gemm_options* options, void* stream);
 
-/* MXFP8 quantization -> MX GEMM for one bf16 activation row, in one launch: the weight-
- * streaming GEMM computes the row's codes and scales from x bf16 [1, K] itself, with the
- * activation quantizer's arithmetic (mxl_quantize_mxfp8, rule 0, 1 or 2), so y is
- * bit-identical to mxl_quantize_mxfp8 followed by mxl_mx_gemm.  K % 128 == 0,
- * K <= 12288; other shapes return MXL_EUNSUPPORTED (use the two calls).  Replaces
- * mxfp8_sm120::gemm_from_float and mxfp6::gemm_from_float at M = 1
+/* MXFP8 quantization -> MX GEMM for M <= 16 bf16 activation rows x [M, K] in one launch,
+ * bit-identical to mxl_quantize_mxfp8 (rule 0, 1 or 2) followed by mxl_mx_gemm; the
+ * producer waves, scratch slots, handoff and shapes of mxl_swiglu_mx_gemm.  Replaces
+ * mxfp8_sm120::gemm_from_float and mxfp6::gemm_from_float at M <= 16
  * (src/vllm_mach/mxfp6/dense_mxfp8.py:89-96, src/vllm_mach/mxfp6/dense.py:122-129). */
 int mxl_quant_mx_gemm(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled, const void* sw_tiled,
                       int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc, void* stream);
 
-/* mxl_quant_mx_gemm with the output format and scale of `options` (out_dtype,
- * alpha; NULL: bf16, 1).  Replaces mxfp6::gemm_from_float(x, w, ws, N, alpha,
- * dtype) (src/vllm_mach/mxfp6/dense.py:122-129). */
+/* mxl_quant_mx_gemm with the output format, scale and scheme of `options` (as for
+ * mxl_swiglu_mx_gemm_ex).  Replaces mxfp6::gemm_from_float(x, w, ws, N, alpha, dtype)
+ * (src/vllm_mach/mxfp6/dense.py:122-129). */
 int mxl_quant_mx_gemm_ex(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled, const void* sw_tiled,
                          int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
                          const mxl_gemm_options* options, void* stream);
+
+/* Block-FP8 activation quantization -> block-FP8 GEMM for M <= 16 bf16 rows x [M, K] in
+ * one launch, bit-identical to mxl_quantize_block_fp8 followed by mxl_block_fp8_gemm (the
+ * producer waves, scratch slots and handoff of mxl_swiglu_mx_gemm); K % 128 == 0, K <= 3584
+ * or 4096 < K <= 7168.  Replaces the per-token-group quantization + block-FP8 GEMM pair
+ * of the patched CutlassFp8BlockScaledMMKernel at decode sizes
+ * (src/vllm_mach/fp8/linear.py:65-81,157-216). */
+int mxl_block_fp8_quant_gemm(const void* x, int64_t M, int64_t K, const void* w_tiled, const void* sb, int64_t N,
+                             const void* bias, void* out, int64_t ldc, void* stream);
+
+/* mxl_block_fp8_quant_gemm with the output format and scale of `options`
+ * (options->kernel -1 or 0). */
+int mxl_block_fp8_quant_gemm_ex(const void* x, int64_t M, int64_t K, const void* w_tiled, const void* sb, int64_t N,
+                                const void* bias, void* out, int64_t ldc, const mxl_gemm_options* options,
+                                void* stream);
+
+/* 1 when the one-launch producer + GEMM runs (kind 0 mxl_swiglu_mx_gemm, 1
+ * mxl_quant_mx_gemm, 2 mxl_block_fp8_quant_gemm) for M rows, K, scale rule and weight
+ * format, else 0.  No counterpart in the reference (its fused rows are fixed,
+ * src/vllm_mach/mxfp6/fused_mlp.py:13-19); for callers choosing between one launch and
+ * two. */
+int mxl_producer_gemm_supported(int kind, int64_t M, int64_t K, int rule, int w_fmt);
 
 /* Block-FP8 GEMM: y[m, n] = sum_g sa[g*M + m] * sb[(n/128) * (K/128) + g] *
  * (A_g . W_g) with fp32 FMA per K128 block, bf16 out.  A E4M3 [M, K]; W tiled

@@ -302,9 +302,9 @@ def test_quant_row_fused_graph_replay_and_limits(pkg, oracle_mod, dev):
             stream.synchronize()
             assert torch.equal(replayed.view(torch.int16), eager.view(torch.int16))
     torch.cuda.current_stream().wait_stream(stream)
-    assert not ops.quant_row_fusable(2, K, 0) and not ops.quant_row_fusable(1, 12416, 0)
+    assert not ops.quant_row_fusable(17, K, 0) and not ops.quant_row_fusable(1, 12416, 0)
     with pytest.raises(ValueError):
-        torch.ops.mach_amd.quant_mx_gemm(torch.zeros(2, K, dtype=torch.bfloat16, device=dev), tiled, tiled_s, N, 2)
+        torch.ops.mach_amd.quant_mx_gemm(torch.zeros(17, K, dtype=torch.bfloat16, device=dev), tiled, tiled_s, N, 2)
 
 
 @pytest.mark.parametrize("fmt", [0, 2])
@@ -346,7 +346,7 @@ def test_swiglu_row_fused_rejects_other_shapes(pkg, dev):
     ops = pkg.ops
     w = torch.zeros(16 * 512, dtype=torch.uint8, device=dev)
     with pytest.raises(ValueError):
-        torch.ops.mach_amd.swiglu_mx_gemm(torch.zeros(2, 1024, dtype=torch.bfloat16, device=dev), w, w, 16, 0, 1)
+        torch.ops.mach_amd.swiglu_mx_gemm(torch.zeros(17, 1024, dtype=torch.bfloat16, device=dev), w, w, 16, 0, 1)
     with pytest.raises(ValueError):
         torch.ops.mach_amd.swiglu_mx_gemm(torch.zeros(1, 1024, dtype=torch.bfloat16, device=dev), w, w, 16, 0, 0)
     assert not ops.swiglu_row_fusable(1, 12800, 1) and ops.swiglu_row_fusable(1, 9216, 2)

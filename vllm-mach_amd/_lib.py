@@ -57,6 +57,9 @@ SIGNATURES = {
     "mxl_swiglu_mx_gemm_ex": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P, _P]),
     "mxl_quant_mx_gemm_ex": (_I, [_P, _I64, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _P, _P]),
     "mxl_block_fp8_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P, _I64, _P]),
+    "mxl_block_fp8_quant_gemm": (_I, [_P, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _P]),
+    "mxl_block_fp8_quant_gemm_ex": (_I, [_P, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _P, _P]),
+    "mxl_producer_gemm_supported": (_I, [_I, _I64, _I64, _I, _I]),
     "mxl_grouped_gemm": (_I, [_P, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P]),
     "mxl_grouped_fused_supported": (_I, [_I64, _I64, _I64, _I]),
     "mxl_grouped_gemm_quant": (_I, [_P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I64, _I64, _I, _I, _P, _P]),

@@ -692,17 +692,30 @@ static int swiglu_row_common(const void* gate_up, int64_t M, int64_t K, int rule
   MXL_CHECK_ARG(N > 0 && ldc >= N, "mxl_swiglu_mx_gemm: need N > 0 and ldc >= N");
   MXL_CHECK_ARG(((uintptr_t)gate_up & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
                 "mxl_swiglu_mx_gemm: gate_up and w must be 16-byte aligned");
-  if (!stream_swiglu_eligible(M, K, rule)) {
-    set_error("mxl_swiglu_mx_gemm: unsupported (one row, K %% 128 == 0, K <= 12288, rule 1 or 2; "
-              "M=%lld K=%lld rule=%d)", (long long)M, (long long)K, rule);
+  const bool rule_ok = rule == kCeilDiv448 || rule == kRpUe8m0;
+  const bool handoff = rule_ok && stream_fused_eligible(M, K, false, w_fmt);
+  const bool rowwise = stream_swiglu_eligible(M, K, rule);
+  // automatic: the row recomputed by every wavefront where it runs (M = 1: measured faster
+  // than the handoff, whose grid-wide synchronisation costs more than the launch it saves)
+  const bool use_rowwise = o.kernel == kStreamWide || (o.kernel == kAuto && rowwise);
+  if (use_rowwise ? !rowwise : (!handoff || (o.kernel != kAuto && o.kernel != kStream))) {
+    set_error("mxl_swiglu_mx_gemm: unsupported (M <= 16, K %% 128 == 0, K <= 12288 except 7680 < K <= 8192 and "
+              "K > 11264 for M > 1, rule 1 or 2; options.kernel -1, 0 or 3 (3: M = 1); M=%lld K=%lld rule=%d "
+              "kernel=%d)", (long long)M, (long long)K, rule, o.kernel);
     return MXL_EUNSUPPORTED;
   }
+  if (M == 0) return MXL_OK;
   GemmParams p{};
   p.a = (const uint8_t*)gate_up;
   p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled; p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out;
-  p.lda = 2 * K; p.ldc = ldc; p.M = 1; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = 1;
+  p.lda = 2 * K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
   p.row_div = 1; p.S = 1;
   p.alpha = o.alpha; p.out_f16 = o.out_dtype == kOutF16;
+  if (!use_rowwise) {
+    p.fsrc = (const uint16_t*)gate_up;
+    p.fsrc_ld = 2 * K;
+    return launch_gemm_stream_fused(w_fmt, rule, p, (hipStream_t)stream, "mxl_swiglu_mx_gemm");
+  }
   const hipError_t e = launch_gemm_stream_swiglu(w_fmt, rule, p, (hipStream_t)stream);
   if (e != hipSuccess) {
     set_error("mxl_swiglu_mx_gemm: launch failed: %s", hipGetErrorString(e));
@@ -733,17 +746,30 @@ static int quant_row_common(const void* x, int64_t M, int64_t K, int rule, const
   MXL_CHECK_ARG(N > 0 && ldc >= N, "mxl_quant_mx_gemm: need N > 0 and ldc >= N");
   MXL_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
                 "mxl_quant_mx_gemm: x and w must be 16-byte aligned");
-  if (!stream_quant_row_eligible(M, K, rule)) {
-    set_error("mxl_quant_mx_gemm: unsupported (one row, K %% 128 == 0, K <= 12288, rule 0, 1 or 2; "
-              "M=%lld K=%lld rule=%d)", (long long)M, (long long)K, rule);
+  const bool rule_ok = rule >= kFloorCarry175 && rule <= kRpUe8m0;
+  const bool handoff = rule_ok && stream_fused_eligible(M, K, false, w_fmt);
+  const bool rowwise = stream_quant_row_eligible(M, K, rule);
+  // automatic: the row recomputed by every wavefront where it runs (M = 1: measured faster
+  // than the handoff, whose grid-wide synchronisation costs more than the launch it saves)
+  const bool use_rowwise = o.kernel == kStreamWide || (o.kernel == kAuto && rowwise);
+  if (use_rowwise ? !rowwise : (!handoff || (o.kernel != kAuto && o.kernel != kStream))) {
+    set_error("mxl_quant_mx_gemm: unsupported (M <= 16, K %% 128 == 0, K <= 12288 except 7680 < K <= 8192 and "
+              "K > 11264 for M > 1, rule 0, 1 or 2; options.kernel -1, 0 or 3 (3: M = 1); M=%lld K=%lld "
+              "rule=%d kernel=%d)", (long long)M, (long long)K, rule, o.kernel);
     return MXL_EUNSUPPORTED;
   }
+  if (M == 0) return MXL_OK;
   GemmParams p{};
   p.a = (const uint8_t*)x;
   p.w = (const uint8_t*)w_tiled; p.sw = sw_tiled; p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out;
-  p.lda = K; p.ldc = ldc; p.M = 1; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = 1;
+  p.lda = K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
   p.row_div = 1; p.S = 1;
   p.alpha = o.alpha; p.out_f16 = o.out_dtype == kOutF16;
+  if (!use_rowwise) {
+    p.fsrc = (const uint16_t*)x;
+    p.fsrc_ld = K;
+    return launch_gemm_stream_fused(w_fmt, 4 + rule, p, (hipStream_t)stream, "mxl_quant_mx_gemm");
+  }
   const hipError_t e = launch_gemm_stream_quant_row(w_fmt, rule, p, (hipStream_t)stream);
   if (e != hipSuccess) {
     set_error("mxl_quant_mx_gemm: launch failed: %s", hipGetErrorString(e));
@@ -762,6 +788,59 @@ extern "C" int mxl_quant_mx_gemm_ex(const void* x, int64_t M, int64_t K, int rul
                                     const void* sw_tiled, int64_t N, int w_fmt, const void* bias, void* out,
                                     int64_t ldc, const void* options, void* stream) {
   return quant_row_common(x, M, K, rule, w_tiled, sw_tiled, N, w_fmt, bias, out, ldc, options_of(options), stream);
+}
+
+extern "C" int mxl_producer_gemm_supported(int kind, int64_t M, int64_t K, int rule, int w_fmt) {
+  if (M < 0 || K <= 0) return 0;
+  const int64_t m = M > 0 ? M : 1;
+  switch (kind) {
+    case 0:  // SwiGLU -> MXFP8 -> MX GEMM
+      return valid_wfmt(w_fmt) && (rule == kCeilDiv448 || rule == kRpUe8m0) &&
+             (stream_fused_eligible(m, K, false, w_fmt) || stream_swiglu_eligible(m, K, rule));
+    case 1:  // MXFP8 quantization -> MX GEMM
+      return valid_wfmt(w_fmt) && rule >= kFloorCarry175 && rule <= kRpUe8m0 &&
+             (stream_fused_eligible(m, K, false, w_fmt) || stream_quant_row_eligible(m, K, rule));
+    case 2:  // block-FP8 quantization -> block-FP8 GEMM
+      return stream_fused_eligible(m, K, true, kE4M3);
+    default:
+      return 0;
+  }
+}
+
+// Block-FP8 activation quantization + block-FP8 GEMM in one launch (M <= 16).
+static int block_quant_common(const void* x, int64_t M, int64_t K, const void* w_tiled, const void* sb, int64_t N,
+                              const void* bias, void* out, int64_t ldc, const GemmOptions& o, void* stream) {
+  MXL_CHECK_ARG(N > 0 && ldc >= N && K > 0 && K % 128 == 0 && M >= 0,
+                "mxl_block_fp8_quant_gemm: need M >= 0, N > 0, ldc >= N, K %% 128 == 0");
+  MXL_CHECK_ARG(epilogue_valid(o), "mxl_block_fp8_quant_gemm: output format %d / alpha %g invalid", o.out_dtype,
+                (double)o.alpha);
+  MXL_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
+                "mxl_block_fp8_quant_gemm: x and w must be 16-byte aligned");
+  if (!stream_fused_eligible(M > 0 ? M : 1, K, true, kE4M3) || (o.kernel != kAuto && o.kernel != kStream)) {
+    set_error("mxl_block_fp8_quant_gemm: unsupported (M <= 16, K %% 128 == 0, K <= 3584 or 4096 < K <= 7168; "
+              "options.kernel -1 or 0; M=%lld K=%lld)", (long long)M, (long long)K);
+    return MXL_EUNSUPPORTED;
+  }
+  if (M == 0) return MXL_OK;
+  GemmParams p{};
+  p.w = (const uint8_t*)w_tiled; p.sw = sb; p.bias = (const uint16_t*)bias; p.out = (uint16_t*)out;
+  p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
+  p.row_div = 1; p.S = 1;
+  p.alpha = o.alpha; p.out_f16 = o.out_dtype == kOutF16;
+  p.fsrc = (const uint16_t*)x;
+  p.fsrc_ld = K;
+  return launch_gemm_stream_fused(kE4M3, kFusedBlockFp8, p, (hipStream_t)stream, "mxl_block_fp8_quant_gemm");
+}
+
+extern "C" int mxl_block_fp8_quant_gemm(const void* x, int64_t M, int64_t K, const void* w_tiled, const void* sb,
+                                        int64_t N, const void* bias, void* out, int64_t ldc, void* stream) {
+  return block_quant_common(x, M, K, w_tiled, sb, N, bias, out, ldc, GemmOptions(), stream);
+}
+
+extern "C" int mxl_block_fp8_quant_gemm_ex(const void* x, int64_t M, int64_t K, const void* w_tiled, const void* sb,
+                                           int64_t N, const void* bias, void* out, int64_t ldc, const void* options,
+                                           void* stream) {
+  return block_quant_common(x, M, K, w_tiled, sb, N, bias, out, ldc, options_of(options), stream);
 }
 
 static int gemm_dual_common(const void* hi, const void* s_hi, const void* res, const void* s_res, int64_t M,

@@ -48,6 +48,13 @@ struct GemmParams {
   int32_t* comb_cnt = nullptr;
   int64_t comb_T = 0;
   int comb_topk = 0;
+  // Weight-streaming GEMM with its activation producer in the same launch (M <= 16,
+  // gemm_stream_kernel FPROD): the bf16 input (gate/up [M, 2K] or x [M, K], row stride
+  // fsrc_ld) is produced into p.a / p.sa, a per-stream slot of the library's scratch;
+  // fsync: the slot's grid handoff counters (arrive, depart), zero between launches.
+  const uint16_t* fsrc = nullptr;
+  int64_t fsrc_ld = 0;
+  uint32_t* fsync = nullptr;
 };
 
 // Output element formats (mxl_gemm_options.out_dtype).
@@ -293,6 +300,14 @@ hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hip
 // (the activation quantizer's arithmetic, rule 0, 1 or 2)
 bool stream_quant_row_eligible(int64_t M, int64_t K, int rule);
 hipError_t launch_gemm_stream_quant_row(int fmt, int rule, const GemmParams& p, hipStream_t s);
+// Producer + weight-streaming GEMM in one launch (M <= 16): prod 1 / 2 = SwiGLU ->
+// MXFP8 under that rule (p.fsrc = gate/up [M, 2K]), 4 + rule = the MXFP8 activation
+// quantizer, kFusedBlockFp8 = the block-FP8 quantizer (p.fsrc = x [M, K]); p.fsrc_ld is
+// the input's row stride.  Sets p.a / p.sa to the stream's scratch slot and launches;
+// returns an MXL status (MXL_EUNSUPPORTED when the shape does not fit one launch).
+constexpr int kFusedBlockFp8 = 8;
+bool stream_fused_eligible(int64_t M, int64_t K, bool block, int fmt);
+int launch_gemm_stream_fused(int fmt, int prod, GemmParams& p, hipStream_t s, const char* who);
 // Grouped (MoE) variant: persistent workgroups over (expert, up to 16 mt rows) units,
 // each streaming the expert's weights; mt = 1 (few rows per expert) or 8.
 bool stream_grouped_eligible(int64_t K, int64_t num_experts, int fmt, int mt);

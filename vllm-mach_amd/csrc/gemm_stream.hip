@@ -27,6 +27,10 @@
 //     ride with each n-tile's weights.  At most eight waves (K <= 8192).
 #include "gemm_common.h"
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 
 namespace mxl {
 
@@ -39,6 +43,21 @@ constexpr int64_t kStreamMaxK = 12288;  // two super-tiles per wave, at most twe
 constexpr int kStreamBlockMaxWaves = 8;
 constexpr int64_t kStreamBlockMaxK = 8192;
 constexpr int kStreamGroupedMaxExperts = 1024;
+// one-launch producer + GEMM: a scratch slot holds [16, K] codes then the scales
+constexpr int kFusedSlots = 64;
+constexpr int64_t kFusedCodeBytes = 16 * kStreamMaxK;
+constexpr int64_t kFusedSlotBytes = kFusedCodeBytes + 16 * (kStreamMaxK / 32);
+static_assert(kFusedSlotBytes % 256 == 0, "slots stay 256-byte aligned");
+static_assert(16 * (kStreamBlockMaxK / 128) * 4 <= 16 * (kStreamMaxK / 32), "block-FP8 scales fit the slot");
+
+// Buffer descriptors over a scratch slot's codes and scales: loads and stores through them
+// carry the sc1 policy (coherent at device scope: no L2 writeback or invalidate is needed
+// to hand data between workgroups on different XCDs), and offsets past the slot read 0.
+typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
+constexpr int kCpolSc1 = 16;  // the sc1 bit of a buffer access's cache-policy operand
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
 
 template <int FMT>
 struct StreamFmt {
@@ -182,6 +201,112 @@ __device__ __forceinline__ v4f stream_mfma_packed(const v8i (&a)[4], uint32_t sa
   return acc;
 }
 
+// Spin bound of the grid handoff below (polls about 128 cycles apart: about a second).
+// Every workgroup of a launch is resident at once (at most one per CU), so the bound is
+// only reached if that fails; the launch then completes with unspecified outputs.
+constexpr uint32_t kHandoffSpinLimit = 1u << 23;
+
+// Producer wave of a weight-streaming GEMM with its activation producer in the same
+// launch (FPROD: 1, 2 = SwiGLU -> MXFP8 under that rule; 4 + rule = the MXFP8 activation
+// quantizer; 8 = the block-FP8 quantizer).  The producer waves of the G workgroups split
+// the [M, K] producer work in the standalone kernels' lane mapping (lane task i: 8
+// values, row i / (K/8), elements 8 (i % (K/8)) .. + 7; four lanes per 32-block, sixteen
+// per 128-group) and the standalone kernels' arithmetic, so codes and scales are bit-
+// identical to theirs; they store them into p.a / p.sa with device-coherent stores, the
+// codes (and the MX scales) in MFMA fragment order, the block-FP8 scales column-major
+// [K/128, M]; rows M..15 of the fragments are left unwritten (their outputs are not
+// stored, and an MFMA output row depends on its own activation row only).  Then
+// the grid handoff: each producer wave waits for its stores to complete, counts itself in
+// at fsync[0] and waits until all G have; the last to leave resets fsync[0] and fsync[32]
+// (the departures) to zero for the next launch on the slot.  A final barrier releases its
+// workgroup's weight waves, whose weights were requested at launch and which read the
+// codes with device-coherent loads.
+template <int FPROD>
+__device__ __forceinline__ void stream_produce(const GemmParams& p, int lane, int64_t g, int64_t G) {
+  constexpr bool SWI = FPROD < 4, BLK = FPROD == 8;
+  constexpr int RULE = FPROD & 3;
+  constexpr int U = 2;  // lane tasks per pass, their loads issued together
+  const int64_t per_row = p.K >> 3;
+  const int64_t tasks = p.M * per_row;  // a multiple of 16: K % 128 == 0
+  uint8_t* codes = const_cast<uint8_t*>(p.a);
+  const __amdgpu_buffer_rsrc_t srs_ = slot_rsrc(p.sa, kFusedSlotBytes - kFusedCodeBytes);
+  for (int64_t base = g * 64; base < tasks; base += G * 64 * U) {
+    uint4 raw[U][SWI ? 2 : 1];
+    int64_t row[U], off[U];
+    bool live[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t task = base + (int64_t)u * G * 64 + lane;
+      live[u] = task < tasks;  // whole 4- (16-) lane groups: base is a multiple of 64
+      const int64_t tc = live[u] ? task : tasks - 1;
+      row[u] = tc / per_row;
+      off[u] = (tc - row[u] * per_row) * 8;
+      const uint16_t* src = p.fsrc + row[u] * p.fsrc_ld + off[u];
+      raw[u][0] = *reinterpret_cast<const uint4*>(src);
+      if constexpr (SWI) raw[u][SWI ? 1 : 0] = *reinterpret_cast<const uint4*>(src + p.K);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float v[8];
+      uint32_t pk[2];
+      if constexpr (BLK) {
+        bf16x8_to_f32(raw[u][0], v);
+        quiet8(v);
+        const float scale = block_fp8_quant8(v, pk);
+        if (live[u] && (lane & 15) == 0)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, scale), srs_,
+                                                (int)(((off[u] >> 7) * p.M + row[u]) * 4), 0, kCpolSc1);
+      } else {
+        uint32_t s;
+        if constexpr (SWI) {
+          float gt[8], up[8];
+          bf16x8_to_f32(raw[u][0], gt);
+          bf16x8_to_f32(raw[u][SWI ? 1 : 0], up);
+          swiglu8<RULE>(gt, up, v);
+          s = quant8x4<RULE, true>(v, pk);
+        } else {
+          bf16x8_to_f32(raw[u][0], v);
+          quiet8(v);
+          s = quant8x4<RULE>(v, pk);
+        }
+        if (live[u] && (lane & 3) == 0) {
+          // block b of the row: super-tile b / 16, slice (b % 16) / 4, lane group b % 4
+          const int64_t b = off[u] >> 5;
+          const int64_t at = (b >> 4) * 256 + (16 * (b & 3) + row[u]) * 4 + ((b & 15) >> 2);
+          __builtin_amdgcn_raw_buffer_store_b8((uint8_t)s, srs_, (int)at, 0, kCpolSc1);
+        }
+      }
+      if (live[u]) {
+        // fragment order: K index k of slice s sits in lane 16 ((k % 64) / 16) + row, byte
+        // 16 (k / 64) + k % 16 of the lane's 32
+        const int64_t k = off[u] & 127;
+        const int64_t at = (off[u] >> 7) * 2048 + (16 * ((k & 63) >> 4) + row[u]) * 32 + 16 * (k >> 6) + (k & 15);
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(codes + at), (uint64_t)pk[0] | (uint64_t)pk[1] << 32,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  // Every store above is device-coherent (sc1); once they are complete the workgroup
+  // counts itself in.  The codes are read back with device-coherent loads as well, so no
+  // L2 writeback or invalidate is involved (measured: a release/acquire fence pair per
+  // workgroup multiplied the launch time).
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  uint32_t* arrive = p.fsync;
+  uint32_t* depart = p.fsync + 32;
+  if (lane == 0) {
+    __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t spins = 0;
+    while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)G &&
+           ++spins < kHandoffSpinLimit)
+      __builtin_amdgcn_s_sleep(2);
+    if (__hip_atomic_fetch_add(depart, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)G - 1) {
+      __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(depart, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  asm volatile("s_barrier" ::: "memory");
+}
+
 }  // namespace
 
 // ROWP >= 0 (one activation row): each wave computes its own super-tiles' MXFP8 codes
@@ -190,19 +315,35 @@ __device__ __forceinline__ v4f stream_mfma_packed(const v8i (&a)[4], uint32_t sa
 //   ROWP = rule (0..2): p.a is the gate/up row [2K], swiglu8 + quant8x4 under the rule;
 //   ROWP = 4 + rule:    p.a is the row [K], quiet8 + quant8x4 under the rule (the
 //                       activation quantizer's).
-template <int FMT, int RUN, bool DB, bool BLOCK, int ROWP = -1>
+//
+// FPROD >= 0 (M <= 16, the activation producer in the same launch): the last wave of
+// each workgroup is a producer wave (stream_produce) that writes its share of the
+// [M, K] codes and scales into p.a / p.sa and takes part in a grid handoff; the other
+// waves request their first weights, wait at a workgroup barrier for that handoff and
+// then read the codes (device-coherent loads, sc1) as the two-launch path's GEMM does,
+// with the same MFMA chain and sums.
+template <int FMT, int RUN, bool DB, bool BLOCK, int ROWP = -1, int FPROD = -1>
 __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_stream_kernel(GemmParams p) {
   static_assert(!BLOCK || FMT == kE4M3, "block-FP8 weights are E4M3");
   static_assert(ROWP < 0 || !BLOCK, "the fused producer row feeds MX GEMMs");
+  static_assert(ROWP < 0 || FPROD < 0, "one producer scheme per launch");
+  static_assert(FPROD < 0 || (FPROD == 8) == BLOCK, "block-FP8 GEMMs take the block-FP8 quantizer");
   constexpr bool ROW = ROWP >= 0, SWI = ROWP >= 0 && ROWP < 4;
+  constexpr bool FUSED = FPROD >= 0;
   constexpr int RRULE = ROWP & 3;
   __shared__ float red[2][kStreamMaxWaves][4][64];
   const int t = threadIdx.x, lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int W = (int)(blockDim.x >> 6);
+  const int W = (int)(blockDim.x >> 6) - (FUSED ? 1 : 0);  // weight waves
   const int r = lane & 15, q = lane >> 4;
   const int64_t ntiles = (p.N + 15) / 16;
   const int64_t G = gridDim.x, g = blockIdx.x;
+  if constexpr (FUSED) {
+    if (wv == W) {
+      stream_produce<FPROD>(p, lane, g, G);
+      return;
+    }
+  }
   const uint8_t* w = p.w;
   const uint8_t* sw = static_cast<const uint8_t*>(p.sw);
 
@@ -235,8 +376,34 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
     }
     __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
   }
+  if constexpr (FUSED) {
+    // the producer wave has seen every workgroup's codes complete: this barrier hands
+    // them over.  The weights are requested only after it: requested at launch they fill
+    // the memory queues, and every round trip of the handoff (the producer's inputs, its
+    // stores, the counter) then waits behind them -- measured 6-11 us per launch more than
+    // the producer and the GEMM as two launches.
+    asm volatile("s_barrier" ::: "memory");
+  }
   StreamB<FMT, RUN, BLOCK> b0;
   stream_load_b<FMT, RUN, BLOCK>(p, w, sw, g < ntiles ? g : ntiles - 1, kt, lane, b0);
+  // the activation side: plain loads, or device-coherent ones from the scratch slot
+  const __amdgpu_buffer_rsrc_t a_rs = slot_rsrc(p.a, FUSED ? kFusedCodeBytes : 0);
+  const __amdgpu_buffer_rsrc_t s_rs = slot_rsrc(p.sa, FUSED ? kFusedSlotBytes - kFusedCodeBytes : 0);
+  auto load_a16 = [&](const uint8_t* ptr) -> uint4 {
+    if constexpr (FUSED) {
+      const v4u32 v = __builtin_amdgcn_raw_buffer_load_b128(a_rs, (int)(ptr - p.a), 0, kCpolSc1);
+      return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+      return *reinterpret_cast<const uint4*>(ptr);
+    }
+  };
+  auto load_s32 = [&](const void* ptr) -> uint32_t {
+    if constexpr (FUSED)
+      return __builtin_amdgcn_raw_buffer_load_b32(
+          s_rs, (int)(static_cast<const uint8_t*>(ptr) - static_cast<const uint8_t*>(p.sa)), 0, kCpolSc1);
+    else
+      return *static_cast<const uint32_t*>(ptr);
+  };
   // The loads are row-major -- lane l reads piece l % 4 of row l / 4, so four
   // neighbouring lanes move one row's 64 bytes in one access (lanes on sixteen
   // rows, the fragment order, would cost an access each) -- and a lane-permute
@@ -255,8 +422,10 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int64_t gi = kt[u] * 4 + j < G ? kt[u] * 4 + j : G - 1;
-        s4[u][j] = float4{sa[gi * p.M + rows[0]], sa[gi * p.M + rows[1]], sa[gi * p.M + rows[2]],
-                          sa[gi * p.M + rows[3]]};
+        s4[u][j] = float4{__builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[0])),
+                          __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[1])),
+                          __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[2])),
+                          __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[3]))};
       }
   }
   if constexpr (ROW) {
@@ -293,6 +462,27 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
         sraw[u][j] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * 4 * (4 * j + q), (int)sc) << (8 * q);
       }
     }
+  } else if constexpr (FUSED) {
+    // the scratch holds the codes in fragment order (stream_produce): slice s's 32 bytes
+    // of fragment lane l at 2048 s + 32 l, so each lane loads its own fragments; the MX
+    // scale dword of lane l for super-tile kt at 256 kt + 4 l holds slice j's code in byte
+    // j, placed in byte q where the two-launch path's scale dword has it
+    const int64_t nsl = p.K >> 7;
+#pragma unroll
+    for (int u = 0; u < RUN; ++u) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t sl = kt[u] * 4 + j < nsl ? kt[u] * 4 + j : nsl - 1;  // clamped inside K
+        const uint4 lo = load_a16(p.a + sl * 2048 + lane * 32);
+        const uint4 hi = load_a16(p.a + sl * 2048 + lane * 32 + 16);
+        a[u][j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+      if constexpr (!BLOCK) {
+        const uint32_t sd = load_s32(static_cast<const uint8_t*>(p.sa) + kt[u] * 256 + lane * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sraw[u][j] = ((sd >> (8 * j)) & 0xFFu) << (8 * q);
+      }
+    }
   } else {
     const int cr = lane >> 2, cp = lane & 3;
     const int64_t row = cr < p.M ? cr : p.M - 1;
@@ -309,13 +499,12 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
       for (int j = 0; j < 4; ++j) {
         const int64_t k0 = kt[u] * kTileK + 128 * j;
         const int64_t kc = k0 < p.K ? k0 : p.K - 128;
-        lo[j] = *reinterpret_cast<const uint4*>(arow + kc + 16 * cp);
-        hi[j] = *reinterpret_cast<const uint4*>(arow + kc + 64 + 16 * cp);
+        lo[j] = load_a16(arow + kc + 16 * cp);
+        hi[j] = load_a16(arow + kc + 64 + 16 * cp);
       }
       // scale dword of slice cp (E8M0 of blocks 4 cp .. 4 cp + 3 of the super-tile)
       const int64_t ks = kt[u] * kTileK + 128 * cp;
-      const uint32_t sd =
-          BLOCK ? 0u : *reinterpret_cast<const uint32_t*>(srow + scale_slice_offset(p, ks));
+      const uint32_t sd = BLOCK ? 0u : load_s32(srow + scale_slice_offset(p, ks));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t x[8] = {lo[j].x, lo[j].y, lo[j].z, lo[j].w, hi[j].x, hi[j].y, hi[j].z, hi[j].w};
@@ -500,7 +689,6 @@ __device__ __forceinline__ void grouped_produce(const GemmParams& p, int64_t lo,
 // another needs no L2 write-back or invalidation (device-scope fences around every unit
 // cost 141.7 -> 225.2 us at c5 T = 128, 233 -> 650 us at T = 2048).  Byte offsets are
 // 32-bit: the host bounds the routed output below 2 GiB.
-constexpr int kCpolSc1 = 16;  // the sc1 bit of a buffer access's cache-policy operand
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t routed_rsrc(const GemmParams& p) {
   return __builtin_amdgcn_make_buffer_rsrc(p.out, (short)0, 0x7fffffff, 0x00020000);
 }
@@ -1046,6 +1234,140 @@ hipError_t launch_gemm_stream_grouped(int fmt, const GemmParams& p, int64_t num_
 }
 
 int stream_max_waves(bool block) { return block ? kStreamBlockMaxWaves : kStreamMaxWaves; }
+
+// ------------------------------------------- producer + GEMM in one launch (M <= 16)
+
+// Scratch of the one-launch producer + GEMM: per slot the [16, K] codes (K <= 12288)
+// followed by the scales (E8M0 [16, K/32], or block-FP8 fp32 [K/128, 16]), and the grid
+// handoff counters, each slot's on its own 256 bytes.  Static device memory: every GPU
+// holds its own copy (zero at load) until the process ends; one slot per (device,
+// stream), so launches on one stream reuse their slot in order.
+__device__ __align__(256) uint8_t g_fused_scratch[kFusedSlots][kFusedSlotBytes];
+__device__ __align__(256) uint32_t g_fused_sync[kFusedSlots][64];
+
+// Weight waves of the one-launch variant: RUN = 1 needs KT + 1 waves, RUN = 2
+// ceil(KT / 2) + 1, within the kernel's launch bound; the RUN must be the one the
+// two-launch GEMM takes for this K (its MFMA chain and wave sums), so KT = 16 (MX) and
+// KT = 8 (block-FP8) do not fit.  FP6 weights with RUN = 2 do not fit the registers of
+// three waves per SIMD beside the handoff (the compiler spills), so they take two launches.
+static int fused_run(int64_t K, bool block, int fmt) {
+  const int64_t KT = (K + kTileK - 1) / kTileK;
+  const int maxw = block ? kStreamBlockMaxWaves : kStreamMaxWaves;  // RUN = 1 bound, in waves
+  const int max2 = block ? kStreamBlockMaxWaves : 12;               // RUN = 2 bound
+  if (KT <= maxw) return KT + 1 <= maxw ? 1 : 0;
+  return fmt == kE4M3 && (KT + 1) / 2 + 1 <= max2 ? 2 : 0;
+}
+
+bool stream_fused_eligible(int64_t M, int64_t K, bool block, int fmt) {
+  return stream_gemm_eligible(M, K, block) && fused_run(K, block, fmt) > 0;
+}
+
+namespace {
+struct FusedSlotTable {
+  std::mutex mu;
+  std::map<std::pair<int, uintptr_t>, int> slot;
+  int used[64] = {};
+  uint8_t* scratch[64] = {};
+  uint32_t* sync[64] = {};
+};
+FusedSlotTable& fused_slots() {
+  static FusedSlotTable t;
+  return t;
+}
+
+template <int FMT, bool BLOCK, int FPROD>
+hipError_t launch_fused_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (fused_run(p.K, BLOCK, FMT) == 1)
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, BLOCK, -1, FPROD>), grid, dim3((unsigned)((p.KT + 1) * 64)),
+                       0, s, p);
+  else if constexpr (FMT == kE4M3)
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 2, false, BLOCK, -1, FPROD>), grid,
+                       dim3((unsigned)(((p.KT + 1) / 2 + 1) * 64)), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+template <int FPROD>
+hipError_t launch_fused_prod(int fmt, const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (fmt == kE4M3) return launch_fused_fmt<kE4M3, false, FPROD>(p, grid, s);
+  if (fmt == kE2M3) return launch_fused_fmt<kE2M3, false, FPROD>(p, grid, s);
+  if (fmt == kE3M2) return launch_fused_fmt<kE3M2, false, FPROD>(p, grid, s);
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+int launch_gemm_stream_fused(int fmt, int prod, GemmParams& p, hipStream_t s, const char* who) {
+  const bool block = prod == kFusedBlockFp8;
+  if (!stream_fused_eligible(p.M, p.K, block, fmt)) {
+    set_error("%s: M=%lld K=%lld does not run as one launch", who, (long long)p.M, (long long)p.K);
+    return MXL_EUNSUPPORTED;
+  }
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("%s: no current device", who);
+    return MXL_EHIP;
+  }
+  if (s) {  // the scratch is the current device's: the stream must belong to it
+    int sdev = -1;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess || sdev != dev) {
+      set_error("%s: the stream's device (%d) is not the current device (%d)", who, sdev, dev);
+      return MXL_EINVAL;
+    }
+  }
+  FusedSlotTable& T = fused_slots();
+  int slot;
+  {
+    std::lock_guard<std::mutex> lk(T.mu);
+    if (!T.scratch[dev]) {
+      void* a = nullptr;
+      void* b = nullptr;
+      if (hipGetSymbolAddress(&a, HIP_SYMBOL(g_fused_scratch)) != hipSuccess ||
+          hipGetSymbolAddress(&b, HIP_SYMBOL(g_fused_sync)) != hipSuccess || !a || !b) {
+        set_error("%s: scratch address: %s", who, hipGetErrorString(hipGetLastError()));
+        return MXL_EHIP;
+      }
+      T.scratch[dev] = static_cast<uint8_t*>(a);
+      T.sync[dev] = static_cast<uint32_t*>(b);
+    }
+    const auto key = std::make_pair(dev, (uintptr_t)s);
+    auto it = T.slot.find(key);
+    if (it == T.slot.end()) {
+      if (T.used[dev] >= kFusedSlots) {
+        set_error("%s: more than %d streams on device %d use the one-launch producer; use the two calls", who,
+                  kFusedSlots, dev);
+        return MXL_EUNSUPPORTED;
+      }
+      it = T.slot.emplace(key, T.used[dev]++).first;
+    }
+    slot = it->second;
+  }
+  uint8_t* base = T.scratch[dev] + (int64_t)slot * kFusedSlotBytes;
+  p.a = base;
+  p.sa = base + kFusedCodeBytes;
+  p.fsync = T.sync[dev] + (int64_t)slot * 64;
+  p.lda = p.K;
+  set_sa_layout(p, 0);
+  p.a_rows = p.M;
+  const int64_t ntiles = (p.N + 15) / 16;
+  const dim3 grid((unsigned)(ntiles < cu_count() ? ntiles : cu_count()));
+  hipError_t e = hipErrorInvalidValue;
+  switch (prod) {
+    case 1: e = launch_fused_prod<1>(fmt, p, grid, s); break;
+    case 2: e = launch_fused_prod<2>(fmt, p, grid, s); break;
+    case 4: e = launch_fused_prod<4>(fmt, p, grid, s); break;
+    case 5: e = launch_fused_prod<5>(fmt, p, grid, s); break;
+    case 6: e = launch_fused_prod<6>(fmt, p, grid, s); break;
+    case kFusedBlockFp8:
+      if (fmt == kE4M3) e = launch_fused_fmt<kE4M3, true, kFusedBlockFp8>(p, grid, s);
+      break;
+    default: break;
+  }
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", who, hipGetErrorString(e));
+    return MXL_EHIP;
+  }
+  return MXL_OK;
+}
 
 hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStream_t s) {
   const int64_t ntiles = (p.N + 15) / 16;

@@ -260,6 +260,27 @@ __device__ __forceinline__ void quiet8(float* f) {
   for (int i = 0; i < 8; ++i) f[i] = __builtin_canonicalizef(f[i]);
 }
 
+// Block-FP8 activation quantization of one 128-element group held by 16 consecutive
+// lanes (8 quieted values each; fp8/_quantize_kernel.py:7-18): the group amax by an
+// xor-shuffle max (order-free), floored at 1e-10, scale = amax / 448, codes =
+// E4M3(clamp(v / scale, +-448)).  Returns the scale; the lane's codes in w[0], w[1].
+__device__ __forceinline__ float block_fp8_quant8(const float* v, uint32_t* w) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+#pragma unroll
+  for (int d = 8; d >= 1; d >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, d, 16));
+  m = __builtin_fmaxf(m, 1e-10f);
+  const float scale = m / 448.0f;
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = __builtin_fminf(__builtin_fmaxf(v[i] / scale, -448.0f), 448.0f);
+  // the clamp leaves no NaN: the hardware conversion equals f32_to_e4m3 here
+  w[0] = e4m3x4_raw(y[0], y[1], y[2], y[3]);
+  w[1] = e4m3x4_raw(y[4], y[5], y[6], y[7]);
+  return scale;
+}
+
 }  // namespace mxl
 
 // ---------------------------------------------------------------- host side

@@ -222,19 +222,10 @@ __global__ __launch_bounds__(256) void quant_block_fp8_kernel(const uint16_t* __
   float v[8];
   bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * K + col * 128 + sub * 8), v);
   quiet8(v);
-  float m = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
-  m = group16_amax(m);
-  m = __builtin_fmaxf(m, 1e-10f);
-  const float scale = m / 448.0f;
-  float y[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) y[i] = __builtin_fminf(__builtin_fmaxf(v[i] / scale, -448.0f), 448.0f);
-  // the clamp leaves no NaN: the hardware conversion equals f32_to_e4m3 here
-  const uint32_t w0 = e4m3x4_raw(y[0], y[1], y[2], y[3]), w1 = e4m3x4_raw(y[4], y[5], y[6], y[7]);
+  uint32_t w[2];
+  const float scale = block_fp8_quant8(v, w);
   if (!live) return;
-  *reinterpret_cast<uint2*>(q + row * K + col * 128 + sub * 8) = make_uint2(w0, w1);
+  *reinterpret_cast<uint2*>(q + row * K + col * 128 + sub * 8) = make_uint2(w[0], w[1]);
   if (sub == 0) s_colmajor[col * M + row] = scale;
 }
 

@@ -252,13 +252,17 @@ std::tuple<at::Tensor, at::Tensor> quantize_logical(const at::Tensor& x, int rul
 }
 
 // One bf16 row quantized inside the weight-streaming GEMM (one launch, the same bits as
-// quantize + GEMM); nullopt for shapes that take the two calls.
+// quantize + GEMM); nullopt for shapes that take the two calls (more rows: the one-launch
+// handoff measured slower than the two launches).
 std::optional<at::Tensor> quant_row(const at::Tensor& x, const Tiled& t, int fmt, int64_t N, int64_t K,
                                     const mxl_gemm_options& o, hipStream_t s) {
-  if (x.size(0) != 1 || K % 128 != 0 || K > 12288 || x.scalar_type() != at::kBFloat16 || !x.is_cuda()) return {};
+  const int64_t M = x.size(0);
+  if (M != 1 || !mxl_producer_gemm_supported(1, M, K, kFloorCarry175, fmt) ||
+      x.scalar_type() != at::kBFloat16 || !x.is_cuda())
+    return {};
   at::Tensor xc = x.contiguous();
-  at::Tensor out = at::empty({1, N}, xc.options().dtype(out_dtype_of(o)));
-  check(mxl_quant_mx_gemm_ex(xc.data_ptr(), 1, K, kFloorCarry175, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N, fmt,
+  at::Tensor out = at::empty({M, N}, xc.options().dtype(out_dtype_of(o)));
+  check(mxl_quant_mx_gemm_ex(xc.data_ptr(), M, K, kFloorCarry175, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N, fmt,
                              nullptr, out.data_ptr(), N, &o, s),
         "mxl_quant_mx_gemm_ex");
   return out;
@@ -481,8 +485,8 @@ at::Tensor mxfp6_gemm_from_swiglu(const at::Tensor& gate_up, const at::Tensor& w
   const mxl_gemm_options o = with_output(options(0, -1, 0), alpha, dtype, "mxfp6::gemm_from_swiglu");
   at::Tensor out = at::empty({M, N}, gate_up.options().dtype(out_dtype_of(o)));
   if (M == 0) return out;
-  if (M == 1 && K <= 12288) {
-    check(mxl_swiglu_mx_gemm_ex(gate_up.data_ptr(), 1, K, kCeilDiv448, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N,
+  if (M == 1 && mxl_producer_gemm_supported(0, M, K, kCeilDiv448, kE3M2)) {
+    check(mxl_swiglu_mx_gemm_ex(gate_up.data_ptr(), M, K, kCeilDiv448, t.tiled.data_ptr(), t.tiled_s.data_ptr(), N,
                                 kE3M2, nullptr, out.data_ptr(), N, &o, s),
           "mxl_swiglu_mx_gemm_ex");
     return out;

@@ -253,8 +253,7 @@ class BlockFp8LinearKernel(_Kernel):
             raise ValueError("block-FP8 requires BF16 activations with matching K")
         if x.numel() == 0:
             return x.new_empty((*x.shape[:-1], n))
-        q, s = torch.ops.mach_amd.quantize_block_fp8(_flatten(x, k).contiguous())
-        y = torch.ops.mach_amd.block_fp8_gemm(q, s, layer.weight, layer.mxl_block_scale, n, k, None)
+        y = ops.block_fp8_from_float(_flatten(x, k).contiguous(), layer.weight, layer.mxl_block_scale, n)
         y = y.reshape(*x.shape[:-1], n)
         return y if bias is None else y + bias
 

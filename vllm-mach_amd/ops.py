@@ -465,33 +465,39 @@ def _(a, sa, w, sw, n, k, w_fmt, bias=None):
     return a.new_empty((a.shape[0], n), dtype=torch.bfloat16)
 
 
-def swiglu_row_fusable(m: int, k: int, rule: int) -> bool:
-    """Shapes ``mxl_swiglu_mx_gemm`` runs in one launch (one row, the weight-streaming
-    GEMM's K range, rules ceil_div448 and rp_ue8m0)."""
-    return m == 1 and k % 128 == 0 and 128 <= k <= 12288 and rule in (CEIL_DIV448, RP_UE8M0)
+def swiglu_row_fusable(m: int, k: int, rule: int, w_fmt: int = E4M3) -> bool:
+    """Shapes ``mxl_swiglu_mx_gemm`` runs in one launch (M <= 16 rows; rules ceil_div448 and
+    rp_ue8m0; the weight-streaming GEMM's K range, see ``mxl_producer_gemm_supported``)."""
+    return 1 <= m <= 16 and bool(query("mxl_producer_gemm_supported", 0, m, k, rule, w_fmt))
 
 
-def quant_row_fusable(m: int, k: int, rule: int) -> bool:
-    """Shapes ``mxl_quant_mx_gemm`` runs in one launch (one row, the weight-streaming GEMM's
-    K range, every MXFP8 scale rule)."""
-    return m == 1 and k % 128 == 0 and 128 <= k <= 12288 and rule in (FLOOR_CARRY175, CEIL_DIV448, RP_UE8M0)
+def quant_row_fusable(m: int, k: int, rule: int, w_fmt: int = E4M3) -> bool:
+    """Shapes ``mxl_quant_mx_gemm`` runs in one launch (M <= 16 rows, every MXFP8 scale rule;
+    the weight-streaming GEMM's K range, see ``mxl_producer_gemm_supported``)."""
+    return 1 <= m <= 16 and bool(query("mxl_producer_gemm_supported", 1, m, k, rule, w_fmt))
+
+
+def block_row_fusable(m: int, k: int) -> bool:
+    """Shapes ``mxl_block_fp8_quant_gemm`` runs in one launch (M <= 16 rows)."""
+    return 1 <= m <= 16 and bool(query("mxl_producer_gemm_supported", 2, m, k, 0, E4M3))
 
 
 @torch.library.custom_op("mach_amd::quant_mx_gemm", mutates_args=())
 def quant_mx_gemm(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
                   rule: int = FLOOR_CARRY175, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """MXFP8 quantization -> MX GEMM of one bf16 row in one launch, bit-identical to
+    """MXFP8 quantization -> MX GEMM of M <= 16 bf16 rows in one launch, bit-identical to
     ``quantize_mxfp8`` then ``mx_gemm`` (``mxfp8_sm120::gemm_from_float`` /
-    ``mxfp6::gemm_from_float`` at M = 1, src/vllm_mach/mxfp6/dense_mxfp8.py:89-96)."""
+    ``mxfp6::gemm_from_float`` at decode sizes, src/vllm_mach/mxfp6/dense_mxfp8.py:89-96)."""
     _check_cuda(x, w, sw, bias)
     if x.dtype != torch.bfloat16 or x.dim() != 2:
-        raise ValueError("quant_mx_gemm needs bf16 [1, K]")
+        raise ValueError("quant_mx_gemm needs bf16 [M, K]")
     x = x.contiguous()
     M, K = x.shape
-    if not quant_row_fusable(M, K, rule):
-        raise ValueError(f"quant_mx_gemm runs one row with K % 128 == 0, K <= 12288 (M={M}, K={K}, rule={rule})")
-    out = torch.empty((1, n), dtype=torch.bfloat16, device=x.device)
-    call("mxl_quant_mx_gemm", ptr(x), 1, K, rule, ptr(w), ptr(sw), n, w_fmt, ptr(bias), ptr(out), n,
+    if not quant_row_fusable(M, K, rule, w_fmt):
+        raise ValueError(f"quant_mx_gemm runs M <= 16 rows of the one-launch shapes "
+                         f"(M={M}, K={K}, rule={rule}, w_fmt={w_fmt})")
+    out = torch.empty((M, n), dtype=torch.bfloat16, device=x.device)
+    call("mxl_quant_mx_gemm", ptr(x), M, K, rule, ptr(w), ptr(sw), n, w_fmt, ptr(bias), ptr(out), n,
          stream_handle(x.device))
     _count("quant_mx_gemm")
     return out
@@ -505,19 +511,19 @@ def _(x, w, sw, n, w_fmt, rule=FLOOR_CARRY175, bias=None):
 @torch.library.custom_op("mach_amd::swiglu_mx_gemm", mutates_args=())
 def swiglu_mx_gemm(gate_up: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
                    rule: int = CEIL_DIV448, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """SwiGLU -> MXFP8 -> MX GEMM of one row in one launch, bit-identical to
-    ``swiglu_mxfp8`` then ``mx_gemm`` (``mach_swiglu_mxfp8_down`` at M = 1,
-    src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22)."""
+    """SwiGLU -> MXFP8 -> MX GEMM of M <= 16 rows in one launch, bit-identical to
+    ``swiglu_mxfp8`` then ``mx_gemm`` (``mach_swiglu_mxfp8_down`` / ``mxfp6::gemm_from_swiglu``
+    at decode sizes, src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22, src/vllm_mach/mxfp6/fused_mlp.py:13-19)."""
     _check_cuda(gate_up, w, sw, bias)
     if gate_up.dtype != torch.bfloat16 or gate_up.ndim != 2 or gate_up.shape[1] % 64:
-        raise ValueError("swiglu_mx_gemm needs bf16 [1, 2K]")
+        raise ValueError("swiglu_mx_gemm needs bf16 [M, 2K]")
     gate_up = gate_up.contiguous()
     M, K = gate_up.shape[0], gate_up.shape[1] // 2
-    if not swiglu_row_fusable(M, K, rule):
-        raise ValueError(f"swiglu_mx_gemm runs one row with K % 128 == 0, K <= 12288, rule 1 or 2 "
-                         f"(M={M}, K={K}, rule={rule})")
-    out = torch.empty((1, n), dtype=torch.bfloat16, device=gate_up.device)
-    call("mxl_swiglu_mx_gemm", ptr(gate_up), 1, K, rule, ptr(w), ptr(sw), n, w_fmt, ptr(bias), ptr(out), n,
+    if not swiglu_row_fusable(M, K, rule, w_fmt):
+        raise ValueError(f"swiglu_mx_gemm runs M <= 16 rows of the one-launch shapes, rule 1 or 2 "
+                         f"(M={M}, K={K}, rule={rule}, w_fmt={w_fmt})")
+    out = torch.empty((M, n), dtype=torch.bfloat16, device=gate_up.device)
+    call("mxl_swiglu_mx_gemm", ptr(gate_up), M, K, rule, ptr(w), ptr(sw), n, w_fmt, ptr(bias), ptr(out), n,
          stream_handle(gate_up.device))
     _count("swiglu_mx_gemm")
     return out
@@ -526,6 +532,31 @@ def swiglu_mx_gemm(gate_up: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: 
 @swiglu_mx_gemm.register_fake
 def _(gate_up, w, sw, n, w_fmt, rule=CEIL_DIV448, bias=None):
     return gate_up.new_empty((gate_up.shape[0], n), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("mach_amd::block_fp8_quant_gemm", mutates_args=())
+def block_fp8_quant_gemm(x: torch.Tensor, w: torch.Tensor, sb: torch.Tensor, n: int,
+                         bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block-FP8 activation quantization -> block-FP8 GEMM of M <= 16 bf16 rows in one launch,
+    bit-identical to ``quantize_block_fp8`` then ``block_fp8_gemm`` (the per-token-group
+    quantization + scaled GEMM pair, src/vllm_mach/fp8/linear.py:65-81,157-216)."""
+    _check_cuda(x, w, sb, bias)
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise ValueError("block_fp8_quant_gemm needs bf16 [M, K]")
+    x = x.contiguous()
+    M, K = x.shape
+    if not block_row_fusable(M, K):
+        raise ValueError(f"block_fp8_quant_gemm runs M <= 16 rows of the one-launch shapes (M={M}, K={K})")
+    out = torch.empty((M, n), dtype=torch.bfloat16, device=x.device)
+    call("mxl_block_fp8_quant_gemm", ptr(x), M, K, ptr(w), ptr(sb), n, ptr(bias), ptr(out), n,
+         stream_handle(x.device))
+    _count("block_fp8_quant_gemm")
+    return out
+
+
+@block_fp8_quant_gemm.register_fake
+def _(x, w, sb, n, bias=None):
+    return x.new_empty((x.shape[0], n), dtype=torch.bfloat16)
 
 
 @torch.library.custom_op("mach_amd::quantize_mxfp8_dual", mutates_args=())
@@ -600,9 +631,11 @@ def mx_gemm_from_float(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: in
 
     Replaces ``mxfp8_sm120::gemm_from_float`` / ``mxfp6::gemm_from_float``
     (src/vllm_mach/mxfp6/dense_mxfp8.py:96, src/vllm_mach/mxfp6/dense.py:122-129).  One
-    row runs as one launch (``quant_mx_gemm``, the same bits).
+    One row runs as one launch (``quant_mx_gemm``, the same bits: every wavefront
+    recomputes the row's codes); more rows take the quantizer and the GEMM, which measured
+    faster than the one-launch handoff that ``quant_mx_gemm`` offers up to 16 rows.
     """
-    if quant_row_fusable(x.shape[0], x.shape[1], rule):
+    if x.shape[0] == 1 and quant_row_fusable(1, x.shape[1], rule, w_fmt):
         return torch.ops.mach_amd.quant_mx_gemm(x, w, sw, n, w_fmt, rule, bias)
     a, sa = torch.ops.mach_amd.quantize_mxfp8(x, rule)
     return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, x.shape[1], w_fmt, bias)
@@ -614,7 +647,7 @@ def swiglu_mx_down(gate_up: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: 
     src/vllm_mach/mxfp6/mxfp8_mlp.py:15-22)."""
     if gate_up.shape[0] == 0:
         return gate_up.new_empty((0, n))
-    if swiglu_row_fusable(gate_up.shape[0], gate_up.shape[1] // 2, rule):
+    if gate_up.shape[0] == 1 and swiglu_row_fusable(1, gate_up.shape[1] // 2, rule, w_fmt):
         return torch.ops.mach_amd.swiglu_mx_gemm(gate_up, w, sw, n, w_fmt, rule)
     a, sa = torch.ops.mach_amd.swiglu_mxfp8(gate_up, rule, False)
     return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, gate_up.shape[1] // 2, w_fmt, None)
@@ -671,6 +704,16 @@ def block_fp8_gemm(a: torch.Tensor, sa: torch.Tensor, w: torch.Tensor, sb: torch
 @block_fp8_gemm.register_fake
 def _(a, sa, w, sb, n, k, bias=None):
     return a.new_empty((a.shape[0], n), dtype=torch.bfloat16)
+
+
+def block_fp8_from_float(x: torch.Tensor, w: torch.Tensor, sb: torch.Tensor, n: int,
+                         bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Quantize bf16 activations to block-FP8 (fp32 scale per row per 128) and run the
+    block-FP8 GEMM (the patched ``CutlassFp8BlockScaledMMKernel.apply_weights`` pair,
+    src/vllm_mach/fp8/linear.py:157-216), as two launches: they measured faster than the
+    one-launch handoff ``block_fp8_quant_gemm`` offers up to 16 rows."""
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x)
+    return torch.ops.mach_amd.block_fp8_gemm(q, s, w, sb, n, x.shape[1], bias)
 
 
 # ---------------------------------------------------------------------- MoE
