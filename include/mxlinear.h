@@ -153,7 +153,9 @@ int mxl_pack_weight_ex(const void* codes, const void* scales, int scale_layout, 
 typedef struct mxl_gemm_options {
   int sa_layout; /* MX activation scales: 0 logical [M, K/32], 1 swizzled */
   int kernel;    /* -1 automatic; 0 weight-streaming (M <= 16), 1 wide (M >= 64,
-                    K % 256 == 0), 2 generic; grouped GEMMs also 3 (96-row
+                    K % 256 == 0), 2 generic, 4 K-chunked weight streaming (MX,
+                    M <= 128: activations stationary in registers, weights through an
+                    LDS ring, fp32 partials per chunk); grouped GEMMs also 3 (96-row
                     weight-streaming units).  A kernel the shape does not admit
                     returns MXL_EUNSUPPORTED. */
   int splits;    /* 0 automatic, else the K split (wide with tile_n, generic) */

@@ -118,6 +118,66 @@ def test_wide_block_fp8_gemm(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
     _check(y.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("M,N,K,cfg", [
+    (200, 1024, 1280, "2,2"),
+    (512, 18432, 2560, "2,1"),
+    (128, 18432, 2560, "1,3"),
+    (300, 640, 768, "2,1,h"),
+])
+def test_wide_block_fp8_eight_waves(pkg, oracle_mod, dev, monkeypatch, M, N, K, cfg):
+    """Block-FP8 with eight waves (two per SIMD, one's per-K128 folds under the other's
+    MFMAs): bit-identical to the four-wave kernel (each 16 x 16 output tile sees the same
+    MFMA chain and folds) and within the bar of the oracle."""
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(191 + M + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    wb = w.reshape(N // 128, 128, K // 128, 128)
+    sb = (wb.abs().amax(dim=(1, 3)) / 448.0).float()
+    wq = (wb / sb[:, None, :, None]).reshape(N, K).to(torch.float8_e4m3fn)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    tiled, _ = ops.pack_weight(wq.to(dev), None, 0)
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x.to(dev))
+    force(monkeypatch, ops, cfg, waves=4)
+    y4 = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, None)
+    force(monkeypatch, ops, cfg, waves=8)
+    y8 = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, None)
+    assert torch.equal(y8, y4)
+    if N * K <= 4_000_000:
+        rq, rs = oracle_mod.quant_block_fp8(x)
+        ref = oracle_mod.bf16_to_f32(oracle_mod.block_fp8_gemm_ref(rq, rs, wq.view(torch.uint8).numpy(), sb.numpy()))
+        _check(y8.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,same_as", [
+    (64, 1024, 1280, None),            # half the 128-row tile past the last row
+    (200, 2048, 1536, None),           # ragged M
+    (256, 18432, 2560, "2,1,h"),       # c3: 288 tiles, whole-K round plus split remainder
+    (512, 18432, 2560, "2,1"),         # c3: three whole-K rounds
+])
+def test_wide_block_fp8_auto_plan(pkg, oracle_mod, dev, monkeypatch, M, N, K, same_as):
+    """The planner's own block-FP8 choice (eight waves on 128 x 128 tiles): within the bar of
+    the oracle, and at the c3 shapes bit-identical to the four-wave kernel on the same tiles."""
+    ops = pkg.ops
+    g = torch.Generator().manual_seed(401 + M + N)
+    w = torch.randn(N, K, generator=g) * 0.02
+    wb = w.reshape(N // 128, 128, K // 128, 128)
+    sb = (wb.abs().amax(dim=(1, 3)) / 448.0).float()
+    wq = (wb / sb[:, None, :, None]).reshape(N, K).to(torch.float8_e4m3fn)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    tiled, _ = ops.pack_weight(wq.to(dev), None, 0)
+    q, s = torch.ops.mach_amd.quantize_block_fp8(x.to(dev))
+    monkeypatch.setattr(ops, "_tuning", None)
+    y = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, None)
+    if same_as:
+        force(monkeypatch, ops, same_as, waves=4)
+        y4 = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sb.to(dev), N, K, None)
+        assert torch.equal(y, y4)
+    else:
+        rq, rs = oracle_mod.quant_block_fp8(x)
+        ref = oracle_mod.bf16_to_f32(oracle_mod.block_fp8_gemm_ref(rq, rs, wq.view(torch.uint8).numpy(), sb.numpy()))
+        _check(y.float().cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("M,N,K,fmt,cfg,bias", [
     (512, 8320, 1024, 0, "2,1,h", True),     # 260 tiles: 256 whole-K, 4 split two ways
     (300, 11000, 1536, 2, "2,1,h", False),   # ragged M and N: 258 tiles, remainder split three ways

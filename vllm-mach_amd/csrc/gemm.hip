@@ -451,7 +451,7 @@ static bool epilogue_valid(const GemmOptions& o) {
 }
 
 static bool options_valid(const GemmOptions& o, const char* who) {
-  const bool ok = (o.sa_layout == 0 || o.sa_layout == 1) && o.kernel >= kAuto && o.kernel <= kStreamWide &&
+  const bool ok = (o.sa_layout == 0 || o.sa_layout == 1) && o.kernel >= kAuto && o.kernel <= kChunk &&
                   o.splits >= 0 && o.splits <= 64 && (o.tile_n == 0 || o.tile_n == 1 || o.tile_n == 2 ||
                   o.tile_n == 4) && (o.tile_m == 0 || o.tile_m == 4 || o.tile_m == 8) &&
                   (o.hybrid == 0 || o.hybrid == 1) && (o.waves == 0 || o.waves == 4 || o.waves == 8) &&
@@ -485,7 +485,7 @@ static bool default_epilogue(const GemmOptions& o) { return o.out_dtype == kOutB
 // The dense kernel and split a call runs with (shared by the launch and the workspace
 // query, so that the bytes the query reports are the bytes the launch uses).
 struct DensePlan {
-  int kernel;  // kStream, kWide or kGeneric
+  int kernel;  // kStream, kWide, kGeneric or kChunk
   WideConfig wide{2, 1, 1};
   GemmConfig gen{};
   int64_t need = 0;  // split-K workspace bytes of the plan
@@ -494,13 +494,34 @@ struct DensePlan {
 static bool plan_dense(int64_t M, int64_t N, int64_t K, int fmt, bool block, const GemmOptions& o, DensePlan& d) {
   const bool stream_ok = stream_gemm_eligible(M, K, block);
   const bool wide_ok = wide_gemm_eligible(M, K) && (!block || K <= int64_t(128) * kWideBlockStages);
-  d.kernel = o.kernel == kAuto ? (stream_ok ? kStream : wide_ok ? kWide : kGeneric) : o.kernel;
-  if ((d.kernel == kStream && !stream_ok) || (d.kernel == kWide && !wide_ok) ||
-      (d.kernel != kStream && d.kernel != kWide && d.kernel != kGeneric))
+  const bool chunk_ok = !block && chunk_gemm_eligible(M, K, fmt);
+  d.kernel = o.kernel == kAuto
+                 ? (stream_ok ? kStream : chunk_ok && chunk_gemm_preferred(M, N, K) ? kChunk : wide_ok ? kWide : kGeneric)
+                 : o.kernel;
+  if ((d.kernel == kStream && !stream_ok) || (d.kernel == kWide && !wide_ok) || (d.kernel == kChunk && !chunk_ok) ||
+      (d.kernel != kStream && d.kernel != kWide && d.kernel != kGeneric && d.kernel != kChunk))
     return false;
+  if (d.kernel == kChunk) {
+    const int64_t nch = chunk_count(K, kChunkSuperTiles);
+    d.need = nch > 1 ? nch * M * N * 4 : 0;
+    return true;
+  }
   if (d.kernel == kWide) {
-    d.wide = wide_config(M, N, K, fmt, o);
-    if (block) d.wide.WM = 1;  // eight-wave tiles are MX only
+    if (block && o.tile_n == 0 && o.waves == 0 && o.splits == 0 && !o.hybrid && o.tile_m == 0) {
+      // Block-FP8: eight waves (two per SIMD, so one wave's per-K128 folds run under the
+      // other's MFMAs) on 128 x 128 tiles, which fit their registers.  Measured at c3 (N =
+      // 18432, K = 2560; µs, four-wave pick -> this): M = 128 23.4 -> 20.3, M = 256 37.2 ->
+      // 33.7 (one full round plus split remainder), M = 512 58.6 -> 55.5 (three rounds: the
+      // split remainder after two full rounds measured 63.7).
+      GemmOptions o2 = o;
+      o2.tile_n = 2;
+      d.wide = wide_config(M, N, K, fmt, o2);
+      if (d.wide.dp_tiles >= 2 * (int64_t)cu_count()) d.wide = WideConfig{2, 1, (K + kTileK - 1) / kTileK};
+      d.wide.WM = 2;
+    } else {
+      d.wide = wide_config(M, N, K, fmt, o);
+      if (block && d.wide.NT == 4) d.wide.WM = 1;  // no eight-wave block-FP8 tile of four n-tiles per wave
+    }
     d.need = wide_workspace_bytes(d.wide, M, N);
   } else if (d.kernel == kGeneric) {
     d.gen = choose_config(M, N, K);
@@ -541,6 +562,14 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
   if (d.kernel == kStream) {
     p.S = 1;
     e = launch_gemm_stream(fmt, block, p, s);
+  } else if (d.kernel == kChunk) {
+    if (!room) {
+      set_error("%s: the K-chunked kernel needs %lld bytes of workspace (have %lld)", who, (long long)d.need,
+                (long long)workspace_bytes);
+      return MXL_EINVAL;
+    }
+    p.S = (int)chunk_count(K, kChunkSuperTiles);
+    e = launch_gemm_chunk(fmt, p, s);
   } else if (d.kernel == kWide) {
     WideConfig wc = d.wide;
     if (!room) {
@@ -1226,8 +1255,12 @@ extern "C" int mxl_gemm_plan_name(int64_t M, int64_t N, int64_t K, int w_fmt, in
   int S = 1;
   if (d.kernel == kStream) {
     const bool db = KT <= stream_max_waves(block != 0);
-    snprintf(k, sizeof k, "gemm_stream_kernel<%d,%d,%s,%s,-1>", w_fmt, db ? 1 : 2, tf(db), tf(block != 0));
+    snprintf(k, sizeof k, "gemm_stream_kernel<%d,%d,%s,%s,-1,-1>", w_fmt, db ? 1 : 2, tf(db), tf(block != 0));
     name = k;
+  } else if (d.kernel == kChunk) {
+    snprintf(k, sizeof k, "gemm_chunk_kernel<%d,%d,1>", w_fmt, kChunkSuperTiles);
+    name = k;
+    S = (int)chunk_count(K, kChunkSuperTiles);
   } else if (d.kernel == kWide) {
     snprintf(k, sizeof k, "gemm_wide_kernel<%d,%d,%d,%s,false,%d>", w_fmt, d.wide.MT, d.wide.NT, tf(block != 0),
              d.wide.WM);

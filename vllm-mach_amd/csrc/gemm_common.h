@@ -137,7 +137,7 @@ __device__ __forceinline__ void sum_splits8(const float* src, int64_t stride, in
 // Per-call selection: the scale layout of A and the tuning overrides (the reference's
 // tactic / splits overrides, src/vllm_mach/mxfp8/native_backend.py:29).  Same layout
 // as mxl_gemm_options in include/mxlinear.h.
-enum KernelChoice : int { kAuto = -1, kStream = 0, kWide = 1, kGeneric = 2, kStreamWide = 3 };
+enum KernelChoice : int { kAuto = -1, kStream = 0, kWide = 1, kGeneric = 2, kStreamWide = 3, kChunk = 4 };
 struct GemmOptions {
   int sa_layout = 0;  // 0 logical, 1 swizzled
   int kernel = kAuto;
@@ -286,6 +286,15 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
                             hipStream_t s);
 
 
+
+// K-chunked weight-streaming kernel for up to 128 rows (gemm_chunk.hip), MX weights:
+// chunks of kChunkSuperTiles super-tiles, fp32 partials [chunks][M][N] when K has more
+// than one chunk; preferred by the planner only where it measured faster.
+constexpr int kChunkSuperTiles = 4;
+bool chunk_gemm_eligible(int64_t M, int64_t K, int fmt);
+bool chunk_gemm_preferred(int64_t M, int64_t N, int64_t K);
+int64_t chunk_count(int64_t K, int kc);
+hipError_t launch_gemm_chunk(int fmt, const GemmParams& p, hipStream_t s);
 
 // Weight-streaming kernel for decode-sized M (gemm_stream.hip), MX or block-FP8.
 bool stream_gemm_eligible(int64_t M, int64_t K, bool block);

@@ -55,7 +55,7 @@ namespace {
 template <int MT, int NT, bool BLOCK, int WM = 1>
 struct WideSlot {
   static_assert(MT == 4 || MT == 8, "64- or 128-row workgroup tiles");
-  static_assert(WM == 1 || (WM == 2 && !BLOCK && MT == 8), "two m-groups of waves: MX 128-row tiles only");
+  static_assert(WM == 1 || (WM == 2 && MT == 8), "two m-groups of waves: 128-row tiles only");
   // MX with NT <= 2: the activation scales live in a separate ring of three
   // super-tile entries (16 MT rows x 16 bytes), filled a super-tile ahead, so a
   // copy moves 16 bytes per row instead of one dword from each row.
@@ -647,7 +647,8 @@ __global__ __launch_bounds__(256 * WM, GROUPED ? 2 : 1) void gemm_wide_kernel(Ge
     const int64_t xcd = Lid & 7, per = G >> 3, extra = G & 7;
     const int64_t logical = xcd * per + (xcd < extra ? xcd : extra) + (Lid >> 3);
     constexpr int TW = 64 * NT;
-    float* const sbw = sb_lds + (BLOCK ? wv * kWideBlockStages : 0);
+    // (the two waves of an n-group share its row: they copy the same scales to it)
+    float* const sbw = sb_lds + (BLOCK ? (wv & 3) * kWideBlockStages : 0);
     const uint8_t* const sw = static_cast<const uint8_t*>(p.sw);
     if (g.rem_tiles == 0) {
       const int64_t local = logical % g.tiles, split = logical / g.tiles;
@@ -893,15 +894,22 @@ template <int FMT, int MT, bool BLOCK, bool GROUPED>
 static hipError_t launch_wide_mt(const WideConfig& c, const GemmParams& p, const WideGrid& g, int64_t grid,
                                  hipStream_t s) {
   const dim3 gr((unsigned)grid), blk(256);
-  if (c.WM == 2) {  // eight waves: MX dense 128-row tiles
-    if constexpr (BLOCK || GROUPED || MT != 8) {
+  if (c.WM == 2) {  // eight waves: dense 128-row tiles
+    if constexpr (GROUPED || MT != 8) {
       return hipErrorInvalidValue;
     } else {
       const dim3 blk8(512);
-      if (c.NT == 4) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 4, false, false, 2>), gr, blk8, 0, s, p, g);
-      else if (c.NT == 2) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 2, false, false, 2>), gr, blk8, 0, s, p, g);
-      else if (c.NT == 1) hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 1, false, false, 2>), gr, blk8, 0, s, p, g);
-      else return hipErrorInvalidValue;
+      if (c.NT == 4) {
+        // block-FP8 with four n-tiles per wave does not fit two waves' registers per SIMD
+        if constexpr (BLOCK) return hipErrorInvalidValue;
+        else hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 4, false, false, 2>), gr, blk8, 0, s, p, g);
+      } else if (c.NT == 2) {
+        hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 2, BLOCK, false, 2>), gr, blk8, 0, s, p, g);
+      } else if (c.NT == 1) {
+        hipLaunchKernelGGL((gemm_wide_kernel<FMT, 8, 1, BLOCK, false, 2>), gr, blk8, 0, s, p, g);
+      } else {
+        return hipErrorInvalidValue;
+      }
       return hipGetLastError();
     }
   }

@@ -121,7 +121,7 @@ def reserve_workspaces(device: torch.device) -> None:
 # Set through ``tuning()``; read once per GEMM call, never from the environment.
 _tuning: Optional[_lib.GemmOptions] = None
 
-KERNEL_AUTO, KERNEL_STREAM, KERNEL_WIDE, KERNEL_GENERIC, KERNEL_STREAM_WIDE = -1, 0, 1, 2, 3
+KERNEL_AUTO, KERNEL_STREAM, KERNEL_WIDE, KERNEL_GENERIC, KERNEL_STREAM_WIDE, KERNEL_CHUNK = -1, 0, 1, 2, 3, 4
 
 
 @contextlib.contextmanager
