@@ -103,7 +103,10 @@ def test_plan_names_without_gpu(pkg):
     name = lambda *a, **k: _lib.plan_name("mxl_gemm_plan_name", *a, **k)  # noqa: E731
     assert name(16, 2560, 9216, 0, 0) == "gemm_stream_kernel<0,2,false,false,-1,-1>"
     assert name(16, 2048, 2048, 0, 0) == "gemm_stream_kernel<0,1,true,false,-1,-1>"
-    assert name(512, 2560, 9216, 0, 0).startswith("gemm_wide_kernel<0,8,")
+    # c2 M = 512: 128 x 128 tiles, three K splits, eight waves
+    assert name(512, 2560, 9216, 0, 0) == "gemm_wide_kernel<0,8,2,false,false,2> + splitk_reduce8_kernel"
+    assert name(512, 2560, 9216, 0, 0, options=_lib.GemmOptions(waves=4)) == \
+        "gemm_wide_kernel<0,8,2,false,false,1> + splitk_reduce8_kernel"
     wide8 = name(512, 2560, 9216, 0, 0, options=_lib.GemmOptions(waves=8))
     assert wide8.startswith("gemm_wide_kernel<0,8,") and wide8.split(" + ")[0].endswith(",2>")
     assert name(40, 1024, 1024, 3, 0).startswith("gemm_kernel<3,")

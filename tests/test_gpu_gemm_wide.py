@@ -92,6 +92,26 @@ def test_wide_eight_waves(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, cfg, 
     _check(y8.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("M,N,K,fmt,same_as", [
+    (512, 2560, 9216, 0, "2,3"),       # c2 M = 512
+    (128, 17408, 5120, 2, "2,1"),      # c4 M = 128
+    (256, 17408, 5120, 2, "2,1,h"),    # c4 M = 256: whole-K round plus split remainder
+])
+def test_wide_mx_auto_plan(pkg, oracle_mod, dev, monkeypatch, M, N, K, fmt, same_as):
+    """The planner's own MX choice on 128 x 128 tiles (eight waves): bit-identical to the
+    four-wave kernel on the same tiles and splits."""
+    ops = pkg.ops
+    wc, ws, stored = _weights(oracle_mod, N, K, fmt, 0.02, 29 + N + K)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(stored).to(dev), torch.from_numpy(ws).to(dev), fmt)
+    x = _act(M, K, 17 + M)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    monkeypatch.setattr(ops, "_tuning", None)
+    y = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, None)
+    force(monkeypatch, ops, same_as, waves=4)
+    y4 = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, None)
+    assert torch.equal(y, y4)
+
+
 @pytest.mark.parametrize("M,N,K,cfg", [
     (64, 256, 512, None),
     (200, 384, 1280, "2,2"),
