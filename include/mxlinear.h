@@ -181,6 +181,24 @@ int64_t mxl_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int64_t mxl_gemm_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, int w_fmt, int block,
                                     const mxl_gemm_options* options);
 
+/* Per-shape plan overrides: a measured table's entry for exactly (M, N, K, w_fmt, block)
+ * on the current device.  Replaces the reference's registration of its measured
+ * projection table (set_w6a8_config per row, w6a8_config_abi for the table's ABI check:
+ * src/vllm_mach/mxfp6/moe_projection.py:35-105, table
+ * src/vllm_mach/mxfp6/profile/qwen35_moe_projection.json).  The entry keeps the tuning
+ * fields of `options` (kernel, splits, tile_n, tile_m, hybrid, waves); every dense GEMM
+ * call at that shape whose own tuning fields are automatic (NULL options included) runs
+ * with them, keeping its own scale layout and epilogue, and the workspace and plan-name
+ * queries report that plan.  An entry whose options do not run the shape is refused
+ * (MXL_EINVAL); registering a shape again replaces its entry; at most 4096 shapes.
+ * Register before warmup and graph capture (a captured graph keeps the plan it was
+ * captured with).  mxl_gemm_config_abi() is the version of the fields and kernel ids an
+ * entry may name (a table records the value it was measured with). */
+int64_t mxl_gemm_config_abi(void);
+int mxl_set_gemm_config(int64_t M, int64_t N, int64_t K, int w_fmt, int block, const mxl_gemm_options* options);
+int mxl_clear_gemm_configs(void);
+int64_t mxl_gemm_config_count(void);
+
 /* Two-limb MX GEMM for M <= 64: y = bf16(hi . W^T + res . W^T) with the limbs
  * accumulated separately in fp32 (each limb's partial goes to the workspace,
  * >= 2 M N 4 bytes) and summed before the one bf16 rounding; bias as in

@@ -32,3 +32,13 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _no_registered_gemm_configs():
+    """Every test starts and ends with the cost model's plans: a per-shape entry that one
+    test registers (tactics.prepare, mxl_set_gemm_config) is process-wide state."""
+    yield
+    mod = sys.modules.get("vllm_mach_amd._lib")
+    if mod is not None and getattr(mod, "_lib", None) is not None:
+        mod.call("mxl_clear_gemm_configs")

@@ -40,8 +40,10 @@ def test_chunk_gemm_plan_and_limits(pkg, dev):
     assert _lib.plan_name("mxl_gemm_plan_name", 128, 2560, 9216, 0, 0, options=opts) == \
         "gemm_chunk_kernel<0,4,1> + splitk_reduce8_kernel"
     assert _lib.plan_name("mxl_gemm_plan_name", 128, 2560, 2048, 2, 0, options=opts) == "gemm_chunk_kernel<2,4,1>"
-    # chosen automatically where it measured faster: K in one chunk, an item per CU
-    assert _lib.plan_name("mxl_gemm_plan_name", 128, 2048, 2048, 0, 0) == "gemm_chunk_kernel<0,4,1>"
+    # chosen automatically where it measured fastest: K in one chunk, more n-tiles than CUs;
+    # with fewer n-tiles the generic kernel measured faster
+    assert _lib.plan_name("mxl_gemm_plan_name", 128, 4608, 2048, 2, 0) == "gemm_chunk_kernel<2,4,1>"
+    assert _lib.plan_name("mxl_gemm_plan_name", 128, 2048, 2048, 0, 0) == "gemm_kernel<0,4,1,false,false>"
     assert _lib.plan_name("mxl_gemm_plan_name", 128, 2560, 9216, 0, 0).startswith("gemm_wide_kernel")
     with pytest.raises(_lib.MxlError):  # more than 128 rows
         _lib.plan_name("mxl_gemm_plan_name", 129, 2560, 9216, 0, 0, options=opts)

@@ -22,6 +22,7 @@ from .linear import (  # noqa: F401
     swiglu_mxfp8_down,
 )
 from .moe import Mxfp6Experts, Mxfp6MoEMethod, select_experts  # noqa: F401
+from . import tactics  # noqa: F401  (the measured per-shape GEMM table: tactics.prepare)
 from . import warmup  # noqa: F401  (the module: warmup.warmup, warmup.collect_problems)
 from .warmup import warmup_mxfp6_sm120, warmup_mxfp6_sm120_stream, warmup_mxfp8  # noqa: F401
 from .checkpoint import (  # noqa: F401

@@ -46,6 +46,10 @@ SIGNATURES = {
     "mxl_pack_weight_ex": (_I, [_P, _P, _I, _I64, _I64, _I, _P, _P, _P]),
     "mxl_gemm_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "mxl_gemm_workspace_bytes_ex": (_I64, [_I64, _I64, _I64, _I, _I, _P]),
+    "mxl_gemm_config_abi": (_I64, []),
+    "mxl_set_gemm_config": (_I, [_I64, _I64, _I64, _I, _I, _P]),
+    "mxl_clear_gemm_configs": (_I, []),
+    "mxl_gemm_config_count": (_I64, []),
     "mxl_mx_gemm": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P, _I64, _P]),
     "mxl_noalloc_scratch_bytes": (_I64, []),
     "mxl_mx_gemm_noalloc": (_I, [_P, _P, _I64, _P, _P, _I64, _I64, _I, _P, _P, _I64, _P]),

@@ -39,8 +39,10 @@
 // cannot fill 256 CUs, S workgroups split K further and write fp32 partials
 // that a second kernel sums in split order: both orders are fixed, so every
 // result is deterministic.
+#include <atomic>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <string.h>
 #include <stdio.h>
 
@@ -491,12 +493,90 @@ struct DensePlan {
   int64_t need = 0;  // split-K workspace bytes of the plan
 };
 
+// ------------------------------------------------------------ per-shape plan overrides
+//
+// A measured per-shape table replaces the cost model's choice for exact (M, N, K, weight
+// format, block) shapes on one device: the role of the reference's registered projection
+// configs (src/vllm_mach/mxfp6/moe_projection.py:35-105, set_w6a8_config per table row).
+// An entry holds the tuning fields (kernel, splits, tile_n, tile_m, hybrid, waves); a call
+// whose own tuning fields are all automatic takes them, its scale layout and epilogue
+// unchanged.  Lookups cost one relaxed atomic load while the table is empty.
+namespace {
+constexpr int64_t kGemmConfigAbi = 1;  // the fields and kernel ids an entry may name
+constexpr int64_t kGemmConfigMax = 4096;
+
+struct ShapeKey {
+  int dev;
+  int64_t M, N, K;
+  int fmt, block;
+  bool operator==(const ShapeKey& b) const {
+    return dev == b.dev && M == b.M && N == b.N && K == b.K && fmt == b.fmt && block == b.block;
+  }
+};
+struct ShapeKeyHash {
+  size_t operator()(const ShapeKey& k) const {
+    uint64_t h = 1469598103934665603ull;
+    const int64_t v[6] = {k.dev, k.M, k.N, k.K, k.fmt, k.block};
+    for (int64_t x : v) h = (h ^ (uint64_t)x) * 1099511628211ull;
+    return (size_t)h;
+  }
+};
+std::mutex g_cfg_mu;
+std::unordered_map<ShapeKey, GemmOptions, ShapeKeyHash> g_cfg;
+std::atomic<int64_t> g_cfg_count{0};
+
+int config_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;  // no device (host-side planning): device 0
+  return dev;
+}
+
+bool tuning_auto(const GemmOptions& o) {
+  return o.kernel == kAuto && o.splits == 0 && o.tile_n == 0 && o.tile_m == 0 && o.hybrid == 0 && o.waves == 0;
+}
+
+// o with the registered tuning fields of this shape, when o leaves them automatic
+GemmOptions with_override(int64_t M, int64_t N, int64_t K, int fmt, bool block, const GemmOptions& o) {
+  if (g_cfg_count.load(std::memory_order_relaxed) == 0 || !tuning_auto(o)) return o;
+  const ShapeKey key{config_device(), M, N, K, fmt, block ? 1 : 0};
+  std::lock_guard<std::mutex> lock(g_cfg_mu);
+  const auto it = g_cfg.find(key);
+  if (it == g_cfg.end()) return o;
+  GemmOptions r = o;
+  r.kernel = it->second.kernel;
+  r.splits = it->second.splits;
+  r.tile_n = it->second.tile_n;
+  r.tile_m = it->second.tile_m;
+  r.hybrid = it->second.hybrid;
+  r.waves = it->second.waves;
+  return r;
+}
+}  // namespace
+
+static bool plan_dense_as(int64_t M, int64_t N, int64_t K, int fmt, bool block, const GemmOptions& o,
+                          DensePlan& d);
+
 static bool plan_dense(int64_t M, int64_t N, int64_t K, int fmt, bool block, const GemmOptions& o, DensePlan& d) {
+  return plan_dense_as(M, N, K, fmt, block, with_override(M, N, K, fmt, block, o), d);
+}
+
+static bool plan_dense_as(int64_t M, int64_t N, int64_t K, int fmt, bool block, const GemmOptions& o,
+                          DensePlan& d) {
   const bool stream_ok = stream_gemm_eligible(M, K, block);
   const bool wide_ok = wide_gemm_eligible(M, K) && (!block || K <= int64_t(128) * kWideBlockStages);
   const bool chunk_ok = !block && chunk_gemm_eligible(M, K, fmt);
+  // Short K over few n-tiles: the generic kernel splits K over the waves of one workgroup
+  // and writes bf16 directly, where the wide kernel needs a K split and its reduce to fill
+  // the CUs.  Measured by a per-shape sweep over every kernel, tile and split (µs, generic
+  // against the wide or K-chunked pick): MXFP8 2048 x 2048 at M = 64 / 128 / 256 6.5 /
+  // 7.5 / 8.5 against 8.6 / 8.7 / 13.0, W6A8 N = 512 and 2048, K = 2048 at M = 64..128
+  // 5.9-7.2 against 8.1-8.4.
+  const bool generic_pref = !block && M > 32 && M <= 256 && K >= 1024 && K <= 2048 && (N + 15) / 16 <= 128;
   d.kernel = o.kernel == kAuto
-                 ? (stream_ok ? kStream : chunk_ok && chunk_gemm_preferred(M, N, K) ? kChunk : wide_ok ? kWide : kGeneric)
+                 ? (stream_ok                                        ? kStream
+                    : chunk_ok && chunk_gemm_preferred(M, N, K)      ? kChunk
+                    : generic_pref || !wide_ok                       ? kGeneric
+                                                                     : kWide)
                  : o.kernel;
   if ((d.kernel == kStream && !stream_ok) || (d.kernel == kWide && !wide_ok) || (d.kernel == kChunk && !chunk_ok) ||
       (d.kernel != kStream && d.kernel != kWide && d.kernel != kGeneric && d.kernel != kChunk))
@@ -513,11 +593,18 @@ static bool plan_dense(int64_t M, int64_t N, int64_t K, int fmt, bool block, con
       // 18432, K = 2560; µs, four-wave pick -> this): M = 128 23.4 -> 20.3, M = 256 37.2 ->
       // 33.7 (one full round plus split remainder), M = 512 58.6 -> 55.5 (three rounds: the
       // split remainder after two full rounds measured 63.7).
+      // At most 64 rows: 64-row tiles on four waves (c3 M = 64: 16.2 against 19.7 µs for
+      // half-empty 128-row tiles on eight).
       GemmOptions o2 = o;
       o2.tile_n = 2;
+      if (M <= 64) o2.tile_m = 4;
       d.wide = wide_config(M, N, K, fmt, o2);
-      if (d.wide.dp_tiles >= 2 * (int64_t)cu_count()) d.wide = WideConfig{2, 1, (K + kTileK - 1) / kTileK};
-      d.wide.WM = 2;
+      if (d.wide.dp_tiles >= 2 * (int64_t)cu_count()) {
+        const int mt = d.wide.MT;
+        d.wide = WideConfig{2, 1, (K + kTileK - 1) / kTileK};
+        d.wide.MT = mt;
+      }
+      d.wide.WM = d.wide.MT == 8 ? 2 : 1;
     } else {
       d.wide = wide_config(M, N, K, fmt, o);
       if (block && d.wide.NT == 4) d.wide.WM = 1;  // no eight-wave block-FP8 tile of four n-tiles per wave
@@ -626,6 +713,42 @@ extern "C" int64_t mxl_gemm_workspace_bytes_ex(int64_t M, int64_t N, int64_t K, 
   if (M <= 0 || N <= 0 || K <= 0 || K % 128 || !valid_wfmt(w_fmt)) return 0;
   DensePlan d;
   return plan_dense(M, N, K, w_fmt, block != 0, options_of(options), d) ? d.need : 0;
+}
+
+extern "C" int64_t mxl_gemm_config_abi(void) { return kGemmConfigAbi; }
+
+extern "C" int64_t mxl_gemm_config_count(void) { return g_cfg_count.load(std::memory_order_relaxed); }
+
+extern "C" int mxl_set_gemm_config(int64_t M, int64_t N, int64_t K, int w_fmt, int block, const void* options) {
+  const char* who = "mxl_set_gemm_config";
+  MXL_CHECK_ARG(valid_wfmt(w_fmt), "%s: unknown weight format %d", who, w_fmt);
+  MXL_CHECK_ARG(M > 0 && N > 0 && K > 0 && K % 128 == 0, "%s: need M, N, K > 0 and K %% 128 == 0 (M=%lld N=%lld K=%lld)",
+                who, (long long)M, (long long)N, (long long)K);
+  MXL_CHECK_ARG(options != nullptr, "%s: options must not be NULL", who);
+  const GemmOptions o = options_of(options);
+  if (!options_valid(o, who)) return MXL_EINVAL;
+  DensePlan d;
+  MXL_CHECK_ARG(plan_dense_as(M, N, K, w_fmt, block != 0, o, d),
+                "%s: the options {kernel %d, splits %d, tile_n %d, tile_m %d, hybrid %d, waves %d} do not run "
+                "M=%lld N=%lld K=%lld (format %d, block %d)",
+                who, o.kernel, o.splits, o.tile_n, o.tile_m, o.hybrid, o.waves, (long long)M, (long long)N,
+                (long long)K, w_fmt, block);
+  const ShapeKey key{config_device(), M, N, K, w_fmt, block ? 1 : 0};
+  std::lock_guard<std::mutex> lock(g_cfg_mu);
+  if (g_cfg.find(key) == g_cfg.end() && (int64_t)g_cfg.size() >= kGemmConfigMax) {
+    set_error("%s: the table holds at most %lld shapes", who, (long long)kGemmConfigMax);
+    return MXL_EINVAL;
+  }
+  g_cfg[key] = o;
+  g_cfg_count.store((int64_t)g_cfg.size(), std::memory_order_relaxed);
+  return MXL_OK;
+}
+
+extern "C" int mxl_clear_gemm_configs(void) {
+  std::lock_guard<std::mutex> lock(g_cfg_mu);
+  g_cfg.clear();
+  g_cfg_count.store(0, std::memory_order_relaxed);
+  return MXL_OK;
 }
 
 extern "C" int mxl_mx_gemm(const void* a, const void* sa, int64_t M, const void* w_tiled, const void* sw_tiled,

@@ -288,11 +288,14 @@ hipError_t launch_gemm_chunk(int fmt, const GemmParams& p, hipStream_t s) {
 }
 
 bool chunk_gemm_preferred(int64_t M, int64_t N, int64_t K) {
-  // measured faster than the wide and generic kernels only where the whole K is one chunk
-  // and every item has a CU of its own (c1's 2048 x 2048 at M = 64..128: 8.9-9.1 against
-  // 10.2-11.6 us); with more items per CU the activation fragments are re-read from L2
-  // for too few weight bytes (c2 M = 128: 22.2 against 17.0 us)
-  return M >= 64 && M <= 128 && chunk_count(K, kChunkSuperTiles) == 1 && (N + 15) / 16 <= cu_count();
+  // measured fastest (a per-shape sweep over every kernel, tile and split) only where the
+  // whole K is one chunk and there are more n-tiles than CUs, so that a workgroup's
+  // activation fragments serve more than one weight tile: W6A8 N = 4608 / 6144, K = 2048
+  // at M = 72..128, 11.8-12.2 against 12.7-14.0 us for the wide kernel.  With at most one
+  // n-tile per CU the generic or the wide kernel won (N = 512 / 2048, K = 256 / 2048:
+  // 5.0-7.5 against 8.1-8.7 us), and with several chunks the partials cost more (c2
+  // M = 128: 22.2 against 17.0 us).
+  return M >= 64 && M <= 128 && chunk_count(K, kChunkSuperTiles) == 1 && (N + 15) / 16 > cu_count();
 }
 
 }  // namespace mxl

@@ -21,6 +21,7 @@ from typing import Iterable, Union
 import torch
 
 from . import ops
+from . import tactics as _tactics
 
 # extra prefill sizes whose split-K layouts the graph sizes alone would miss
 # (the reference's set, src/vllm_mach/mxfp6/dense_mxfp8.py:206-209)
@@ -71,11 +72,14 @@ def _device_of(layer) -> torch.device:
 
 
 @torch.inference_mode()
-def warmup(model, token_sizes: Iterable[int], *, stream: bool = False) -> dict:
+def warmup(model, token_sizes: Iterable[int], *, stream: bool = False, tactics: str = "auto") -> dict:
     """Plan and reserve the workspaces of every prepared layer in ``model`` (a module or
     an iterable of modules) for the token counts ``token_sizes``.
 
-    ``stream=False`` (before capture): run each distinct dense problem at every size and
+    ``stream=False`` (before capture): register the packaged per-shape GEMM table's
+    entries for the model's dense problems (``tactics.prepare``, mode ``tactics``: "auto",
+    "on" or "off"; the reference's warmup registers its projection table first,
+    src/vllm_mach/mxfp6/warmup.py:110-112), run each distinct dense problem at every size and
     each MoE problem at every token count, then give the current stream workspaces of
     the planned maxima.  ``stream=True`` (on the capture stream, after a planning pass):
     give the current stream the planned workspaces without running anything.  Returns
@@ -83,7 +87,10 @@ def warmup(model, token_sizes: Iterable[int], *, stream: bool = False) -> dict:
     dense, moe = collect_problems(model)
     sizes = _sizes(token_sizes)
     devices = {_device_of(layer) for layer in list(dense.values()) + list(moe.values())}
+    registered = 0
     if not stream:
+        if dense and _tactics.TABLE.is_file():
+            registered = _tactics.prepare(dense.keys(), mode=tactics, device=_device_of(next(iter(dense.values()))))
         for (cls, n, k, fmt, dual), layer in dense.items():
             for m in sizes:
                 x = torch.zeros((m, k), device=_device_of(layer), dtype=torch.bfloat16)
@@ -103,7 +110,8 @@ def warmup(model, token_sizes: Iterable[int], *, stream: bool = False) -> dict:
     for dev in devices:
         ops.reserve_workspaces(dev)
         torch.cuda.synchronize(dev)
-    return {"dense": sorted(dense), "moe": sorted(moe), "sizes": sizes, "workspaces": ops.inspect()}
+    return {"dense": sorted(dense), "moe": sorted(moe), "sizes": sizes, "workspaces": ops.inspect(),
+            "tactics": registered}
 
 
 def warmup_mxfp8(model, token_sizes, *, stream: bool = False) -> dict:
