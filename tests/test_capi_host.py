@@ -104,14 +104,14 @@ def test_plan_names_without_gpu(pkg):
     assert name(16, 2560, 9216, 0, 0) == "gemm_stream_kernel<0,2,false,false,-1,-1>"
     assert name(16, 2048, 2048, 0, 0) == "gemm_stream_kernel<0,1,true,false,-1,-1>"
     # c2 M = 512: 128 x 128 tiles, three K splits, eight waves
-    assert name(512, 2560, 9216, 0, 0) == "gemm_wide_kernel<0,8,2,false,false,2> + splitk_reduce8_kernel"
+    assert name(512, 2560, 9216, 0, 0) == "gemm_wide_kernel<0,8,2,false,false,2> + wide_tile_reduce_kernel"
     assert name(512, 2560, 9216, 0, 0, options=_lib.GemmOptions(waves=4)) == \
-        "gemm_wide_kernel<0,8,2,false,false,1> + splitk_reduce8_kernel"
+        "gemm_wide_kernel<0,8,2,false,false,1> + wide_tile_reduce_kernel"
     wide8 = name(512, 2560, 9216, 0, 0, options=_lib.GemmOptions(waves=8))
     assert wide8.startswith("gemm_wide_kernel<0,8,") and wide8.split(" + ")[0].endswith(",2>")
     assert name(40, 1024, 1024, 3, 0).startswith("gemm_kernel<3,")
     assert name(512, 2560, 9216, 0, 0, options=_lib.GemmOptions(tile_n=2, splits=3)) == \
-        "gemm_wide_kernel<0,8,2,false,false,1> + splitk_reduce8_kernel"
+        "gemm_wide_kernel<0,8,2,false,false,1> + wide_tile_reduce_kernel"
     # block-FP8 prefill at c3 (N = 18432, K = 2560): eight waves on 128 x 128 tiles, the
     # remainder split only when one full round precedes it
     assert name(128, 18432, 2560, 0, 1) == "gemm_wide_kernel<0,8,2,true,false,2>"

@@ -684,7 +684,7 @@ static int gemm_common(const void* a, const void* sa, int64_t M, const void* w_t
     set_error("%s: launch failed: %s", who, hipGetErrorString(e));
     return MXL_EHIP;
   }
-  if (p.S > 1) {
+  if (p.S > 1 && d.kernel != kWide) {  // (the wide kernel's launch runs its own tile reduce)
     e = launch_splitk_reduce((const float*)workspace, (const uint16_t*)bias, (uint16_t*)out, M, N, ldc, p.S, s,
                              p.alpha, p.out_f16);
     if (e != hipSuccess) {
@@ -1393,8 +1393,8 @@ extern "C" int mxl_gemm_plan_name(int64_t M, int64_t N, int64_t K, int w_fmt, in
     snprintf(k, sizeof k, "gemm_wide_kernel<%d,%d,%d,%s,false,%d>", w_fmt, d.wide.MT, d.wide.NT, tf(block != 0),
              d.wide.WM);
     name = k;
-    if (d.wide.dp_tiles > 0) name += " + wide_tile_reduce_kernel";
-    S = d.wide.S;
+    if (d.wide.dp_tiles > 0 || d.wide.S > 1) name += " + wide_tile_reduce_kernel";
+    S = 1;  // (its split reduce is the tile reduce)
   } else {
     snprintf(k, sizeof k, "gemm_kernel<%d,%d,%d,%s,false>", w_fmt, d.gen.MT, d.gen.NT, tf(block != 0));
     name = k;

@@ -36,8 +36,9 @@
 //
 // Grid: one workgroup per (m-block, n-block, K split), remapped so that the
 // m-blocks sharing a weight slice are consecutive on one XCD (workgroup L runs
-// on XCD L % 8) and hit its L2.  K splits (whole 512-wide super-tiles) write
-// fp32 partials that a second kernel sums in split order.  When the whole-K tiles
+// on XCD L % 8) and hit its L2.  K splits (whole 512-wide super-tiles) store their
+// fp32 partials straight from the accumulators in MFMA fragment order, one block per
+// tile, and a second kernel sums them in split order and writes the rows.  When the whole-K tiles
 // leave a partial last round (more tiles than CUs), the same launch runs the
 // leftover tiles split in K: workgroup L computes whole-K tile L and then unit L
 // of the split leftovers, so no CU waits for a second launch.  The grouped variant
@@ -314,7 +315,6 @@ struct WideGrid {
   int64_t kt_per_split;  // 512-wide super-tiles per split
   int64_t num_experts;   // grouped only
   int64_t tile0, tiles;  // dense: this launch covers output tiles [tile0, tile0 + tiles) (tile = nb * mblocks + mb)
-  int compact;           // dense, split: partials as [split][tile - tile0][16 MT][64 NT] instead of [split][M][N]
   // dense, one-launch hybrid: after its whole-K tile (tiles [0, tiles), bf16 out) workgroup
   // L also runs unit L < rem_tiles * S2 of the remainder: tile rem_tile0 + L % rem_tiles,
   // K split L / rem_tiles of kt2 super-tiles, into compact partials
@@ -328,7 +328,7 @@ struct WideGrid {
 template <int FMT, int MT, int NT, bool BLOCK, bool GROUPED, int WM>
 __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int64_t row_base, int64_t hi,
                                           const uint8_t* w, const uint8_t* sw, int64_t nb, int64_t split,
-                                          float* pdst, int64_t pld, uint8_t* ring, uint8_t* sa_ring, float* sb_stage,
+                                          float* pdst, uint8_t* ring, uint8_t* sa_ring, float* sb_stage,
                                           int t, int lane, int wv, int r, int q) {
   using S = WideSlot<MT, NT, BLOCK, WM>;
   constexpr int C = S::COPIES;
@@ -504,6 +504,22 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
   // per 64 values with 64-bit address arithmetic for each.
   constexpr int TW = 64 * NT, ST = TW + 4;
   static_assert(BM * ST * 4 <= (GROUPED ? kWideGroupedSlots : S::SLOTS) * S::BYTES, "epilogue tile exceeds the ring");
+  if (pdst) {
+    // fp32 split partials go straight from the accumulators, in MFMA fragment order: the
+    // tile's block at pdst holds fragment f = m-tile * 4 NT + n-tile as 64 lanes x 4
+    // floats (lane (q, r): rows 4 q .. 4 q + 3, column r), so every store instruction
+    // writes 1 KiB contiguously; the split reduce puts them in row order.  No LDS round
+    // trip or barrier (rows past M hold the padding rows' sums; the reduce skips them).
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int i = 0; i < MTW; ++i) {
+        const int f = (wm * MTW + i) * (4 * NT) + wn * NT + n;
+        *reinterpret_cast<float4*>(pdst + (f * 64 + lane) * 4) =
+            float4{acc[i][n][0], acc[i][n][1], acc[i][n][2], acc[i][n][3]};
+      }
+    return;
+  }
   float* const tile = reinterpret_cast<float*>(ring);
   wide_barrier();  // every wave is past its last fragment reads
 #pragma unroll
@@ -520,41 +536,7 @@ __device__ __forceinline__ void wide_tile(const GemmParams& p, int64_t kps, int6
   // waits on LDS once per batch instead of once per piece.
   constexpr int kThreads = 64 * S::WAVES;
   static_assert((BM * TW / 4) % kThreads == 0 && (BM * TW / 8) % kThreads == 0, "epilogue pieces per thread");
-  if (pdst) {  // fp32 partials, 4 columns per piece, row rr of the tile at pdst + rr * pld
-    const bool vec = pld % 4 == 0 && (reinterpret_cast<uintptr_t>(pdst) & 15) == 0;
-    if (vec && col0 + TW <= p.N) {
-      constexpr int P = BM * (TW / 4) / kThreads;
-#pragma unroll
-      for (int k0 = 0; k0 < P; k0 += 8) {
-        float4 v[8];
-#pragma unroll
-        for (int k = 0; k < 8 && k0 + k < P; ++k) {
-          const int c = t + (k0 + k) * kThreads;
-          v[k] = *reinterpret_cast<const float4*>(tile + (c / (TW / 4)) * ST + (c % (TW / 4)) * 4);
-        }
-#pragma unroll
-        for (int k = 0; k < 8 && k0 + k < P; ++k) {
-          const int c = t + (k0 + k) * kThreads;
-          const int rr = c / (TW / 4);
-          if (row_base + rr < hi) *reinterpret_cast<float4*>(pdst + rr * pld + (c % (TW / 4)) * 4) = v[k];
-        }
-      }
-      return;
-    }
-    for (int c = t; c < BM * (TW / 4); c += 64 * S::WAVES) {
-      const int rr = c / (TW / 4), cc = (c % (TW / 4)) * 4;
-      const int64_t row = row_base + rr, col = col0 + cc;
-      if (row >= hi || col >= p.N) continue;
-      const float4 v = *reinterpret_cast<const float4*>(tile + rr * ST + cc);
-      float* dst = pdst + rr * pld + cc;
-      if (vec) {
-        *reinterpret_cast<float4*>(dst) = v;
-      } else {
-        const float f[4] = {v.x, v.y, v.z, v.w};
-        for (int k = 0; k < 4 && col + k < p.N; ++k) dst[k] = f[k];
-      }
-    }
-  } else {  // output elements (out_bits: alpha, format, bias), 8 columns per piece
+  {  // output elements (out_bits: alpha, format, bias), 8 columns per piece
     const bool vec = p.ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
     // bf16 without scale or bias: paired conversions
     const bool plain = !p.out_f16 && p.alpha == 1.0f && !p.bias;
@@ -654,18 +636,16 @@ __global__ __launch_bounds__(256 * WM, GROUPED ? 2 : 1) void gemm_wide_kernel(Ge
       const int64_t local = logical % g.tiles, split = logical / g.tiles;
       const int64_t tile = g.tile0 + local;
       const int64_t mb = tile % g.mblocks, nb = tile / g.mblocks;
-      float* const pdst = p.S == 1 ? nullptr
-                          : g.compact ? p.partial + (split * g.tiles + local) * BM * TW
-                                      : p.partial + (split * p.M + mb * BM) * p.N + nb * TW;
-      const int64_t pld = g.compact ? TW : p.N;
-      wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g.kt_per_split, mb * BM, p.M, p.w, sw, nb, split, pdst, pld, ring,
+      // split partials: the tile's fragment-ordered block, [split][tile][BM x TW]
+      float* const pdst = p.S == 1 ? nullptr : p.partial + (split * g.tiles + local) * BM * TW;
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g.kt_per_split, mb * BM, p.M, p.w, sw, nb, split, pdst, ring,
                                                  sa_ring, sbw, t, lane, wv, r, q);
       return;
     }
     // one-launch hybrid: the whole-K tile, then the remainder unit (if any)
     if (logical < g.tiles) {
       const int64_t mb = logical % g.mblocks, nb = logical / g.mblocks;
-      wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g.kt_per_split, mb * BM, p.M, p.w, sw, nb, 0, nullptr, 0, ring,
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g.kt_per_split, mb * BM, p.M, p.w, sw, nb, 0, nullptr, ring,
                                                  sa_ring, sbw, t, lane, wv, r, q);
     }
     if (logical < g.rem_tiles * g.S2) {
@@ -674,7 +654,7 @@ __global__ __launch_bounds__(256 * WM, GROUPED ? 2 : 1) void gemm_wide_kernel(Ge
       const int64_t mb = tile % g.mblocks, nb = tile / g.mblocks;
       __syncthreads();  // the first tile's epilogue reads of the ring are done
       wide_tile<FMT, MT, NT, BLOCK, GROUPED, WM>(p, g.kt2, mb * BM, p.M, p.w, sw, nb, split,
-                                                 p.partial + (split * g.rem_tiles + local) * BM * TW, TW, ring, sa_ring,
+                                                 p.partial + (split * g.rem_tiles + local) * BM * TW, ring, sa_ring,
                                                  sbw, t, lane, wv, r, q);
     }
     return;
@@ -739,45 +719,56 @@ __global__ __launch_bounds__(256 * WM, GROUPED ? 2 : 1) void gemm_wide_kernel(Ge
     // 64-row tile path in the same ring: half the activation copies and MFMAs
     if (MT == 8 && __builtin_amdgcn_readfirstlane((int)(rhi - rb)) <= 64)
       wide_tile<FMT, (MT == 8 ? 4 : MT), NT, BLOCK, GROUPED, 1>(p, g.kt_per_split, rb, rhi, we, swe, nb, 0, nullptr,
-                                                             0, ring, sa_ring, sb_lds, t, lane, wv, r, q);
+                                                             ring, sa_ring, sb_lds, t, lane, wv, r, q);
     else
-      wide_tile<FMT, MT, NT, BLOCK, GROUPED, 1>(p, g.kt_per_split, rb, rhi, we, swe, nb, 0, nullptr, 0, ring, sa_ring,
+      wide_tile<FMT, MT, NT, BLOCK, GROUPED, 1>(p, g.kt_per_split, rb, rhi, we, swe, nb, 0, nullptr, ring, sa_ring,
                                              sb_lds, t, lane, wv, r, q);
     __syncthreads();  // the epilogue's LDS reads are done before the next tile's copies
   }
 }
 
-// Sum the compact split partials of output tiles [tile0, tile0 + tiles) in split
-// order, then the output rounding (out_bits: alpha, format, bias; the split-K reduce's
-// arithmetic).  One thread per 8 columns of one tile row.
+// Sum the split partials of output tiles [tile0, tile0 + tiles) in split order, then the
+// output rounding (out_bits: alpha, format, bias; the split-K reduce's arithmetic).  The
+// partials are fragment-ordered tile blocks, [split][tile - tile0][BM x TW]: fragment f =
+// m-tile * (TW / 16) + n-tile of a block is 64 lanes x 4 floats, lane (q, r) holding rows
+// 4 q .. 4 q + 3 of column r.  One thread per (tile, fragment, lane): its S float4 loads
+// are contiguous across the wave, and each of its four rows gets one 2-byte store (sixteen
+// lanes cover 32 contiguous bytes of a row).
 __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __restrict__ partial,
                                                                const uint16_t* __restrict__ bias,
                                                                uint16_t* __restrict__ out, int64_t M, int64_t N,
                                                                int64_t ldc, int64_t mblocks, int64_t tile0,
                                                                int64_t tiles, int S, int BM, int TW, float alpha,
                                                                int f16) {
-  const int64_t per_tile = (int64_t)BM * (TW / 8);
+  const int64_t per_tile = (int64_t)BM * TW / 4;  // float4 items of a tile block
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= tiles * per_tile) return;
-  const int64_t local = id / per_tile, rem = id - local * per_tile;
-  const int rr = (int)(rem / (TW / 8)), cc = (int)(rem % (TW / 8)) * 8;
+  const int64_t local = id / per_tile;
+  const int item = (int)(id - local * per_tile), f = item >> 6, lane = item & 63;
+  const int nts = TW / 16;
   const int64_t tile = tile0 + local, mb = tile % mblocks, nb = tile / mblocks;
-  const int64_t row = mb * BM + rr, col = nb * TW + cc;
-  if (row >= M || col >= N) return;
-  float4 lo, hi;
-  sum_splits8(partial + (local * BM + rr) * TW + cc, tiles * BM * TW, S, lo, hi);
-  const float f[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-  uint16_t h[8];
+  const int64_t row0 = mb * BM + 16 * (f / nts) + 4 * (lane >> 4), col = nb * TW + 16 * (f % nts) + (lane & 15);
+  if (row0 >= M || col >= N) return;
+  const float4* src = reinterpret_cast<const float4*>(partial) + local * per_tile + item;
+  const int64_t stride = tiles * per_tile;  // float4s per split
+  float4 acc = src[0];
+  for (int k0 = 1; k0 < S; k0 += 8) {
+    float4 v[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k)
-    h[k] = out_bits(f[k], alpha, f16, bias != nullptr, bias ? bias[col + k < N ? col + k : N - 1] : (uint16_t)0);
-  uint16_t* dst = out + row * ldc + col;
-  if (col + 8 <= N && ldc % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
-    *reinterpret_cast<uint4*>(dst) = uint4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
-                                           h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
-  } else {
-    for (int k = 0; k < 8 && col + k < N; ++k) dst[k] = h[k];
+    for (int u = 0; u < 8; ++u)
+      if (k0 + u < S) v[u] = src[(int64_t)(k0 + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (k0 + u < S) {
+        acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+      }
   }
+  const float a4[4] = {acc.x, acc.y, acc.z, acc.w};
+  const bool b = bias != nullptr;
+  const uint16_t bv = b ? bias[col] : (uint16_t)0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (row0 + e < M) out[(row0 + e) * ldc + col] = out_bits(a4[e], alpha, f16, b, bv);
 }
 
 // ------------------------------------------------------------ configuration
@@ -880,12 +871,11 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptio
 }
 
 int64_t wide_workspace_bytes(const WideConfig& c, int64_t M, int64_t N) {
-  if (c.dp_tiles > 0) {
-    const int64_t bm = 16 * c.MT;
-    const int64_t tiles = ((M + bm - 1) / bm) * ((N + 64 * c.NT - 1) / (64 * c.NT));
-    return (int64_t)c.S2 * (tiles - c.dp_tiles) * bm * 64 * c.NT * 4;
-  }
-  return c.S > 1 ? (int64_t)c.S * M * N * 4 : 0;
+  // fragment-ordered partial blocks of whole tiles (padding rows and columns included)
+  const int64_t bm = 16 * c.MT;
+  const int64_t tiles = ((M + bm - 1) / bm) * ((N + 64 * c.NT - 1) / (64 * c.NT));
+  if (c.dp_tiles > 0) return (int64_t)c.S2 * (tiles - c.dp_tiles) * bm * 64 * c.NT * 4;
+  return c.S > 1 ? (int64_t)c.S * tiles * bm * 64 * c.NT * 4 : 0;
 }
 
 bool wide_gemm_eligible(int64_t M, int64_t K) { return M >= 64 && K % 256 == 0 && M * K < (int64_t(1) << 32); }
@@ -956,7 +946,6 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
   g.mblocks = (p.M + bm - 1) / bm;
   g.tile0 = 0;
   g.tiles = g.mblocks * g.nblocks;
-  g.compact = 0;
   auto dense = [&](const GemmParams& q, const WideGrid& gg, int64_t n) -> hipError_t {
     if (block) return fmt == kE4M3 ? launch_wide_fmt<kE4M3, true, false>(c, q, gg, n, s) : hipErrorInvalidValue;
     if (fmt == kE4M3) return launch_wide_fmt<kE4M3, false, false>(c, q, gg, n, s);
@@ -964,7 +953,19 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
     if (fmt == kE3M2) return launch_wide_fmt<kE3M2, false, false>(c, q, gg, n, s);
     return hipErrorInvalidValue;
   };
-  if (c.dp_tiles <= 0 || c.dp_tiles >= g.tiles) return dense(p, g, g.tiles * c.S);
+  const int64_t tw = 64 * c.NT;
+  auto tile_reduce = [&](int64_t tile0, int64_t tiles, int S) -> hipError_t {
+    const int64_t items = tiles * bm * tw / 4;
+    wide_tile_reduce_kernel<<<dim3((unsigned)((items + 255) / 256)), 256, 0, s>>>(
+        p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, tile0, tiles, S, (int)bm, (int)tw, p.alpha, p.out_f16);
+    return hipGetLastError();
+  };
+  if (c.dp_tiles <= 0 || c.dp_tiles >= g.tiles) {
+    // every tile in one launch, split in K into fragment-ordered partials when S > 1
+    const hipError_t e = dense(p, g, g.tiles * c.S);
+    if (e != hipSuccess || p.S == 1) return e;
+    return tile_reduce(0, g.tiles, p.S);
+  }
   // hybrid, one launch: workgroup L runs whole-K tile L (full rounds, bf16 out) and then
   // unit L of the remainder, split in K into compact partials (p.partial); their reduce
   // follows.  (With more than one full round some units run in later rounds' workgroups;
@@ -980,11 +981,7 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
   const int64_t units = gd.rem_tiles * c.S2;
   hipError_t e = dense(q, gd, c.dp_tiles > units ? c.dp_tiles : units);
   if (e != hipSuccess) return e;
-  const int64_t items = gd.rem_tiles * bm * (64 * c.NT / 8);
-  wide_tile_reduce_kernel<<<dim3((unsigned)((items + 255) / 256)), 256, 0, s>>>(
-      p.partial, p.bias, p.out, p.M, p.N, p.ldc, g.mblocks, gd.rem_tile0, gd.rem_tiles, c.S2, (int)bm, 64 * c.NT,
-      p.alpha, p.out_f16);
-  return hipGetLastError();
+  return tile_reduce(gd.rem_tile0, gd.rem_tiles, c.S2);
 }
 
 }  // namespace mxl
