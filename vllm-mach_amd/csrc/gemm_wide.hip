@@ -797,6 +797,8 @@ bool wide_hybrid(int64_t tiles, int64_t KT, int64_t cus, WideConfig& c) {
 // 1200 + 900 NT cycles (the stage copies, not the MFMAs, set the pace); a
 // 64-row tile copies half the activations and issues half the MFMAs.
 static double wide_stage_cycles(int mt, int nt) { return mt == 8 ? 1200.0 + 900.0 * nt : 800.0 + 800.0 * nt; }
+// the split reduce's launch and ramp, in cycles of the stage model
+constexpr double kWideReduceCycles = 8000.0;
 
 // Pick the workgroup tile (MT, NT), the K split and the hybrid split from the
 // stage model; weights stream at ~5 TB/s; split partials cost a write and a
@@ -819,12 +821,15 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptio
   double best_cost = 1e300;
   const double wbytes = (double)N * K * (fmt == kE4M3 ? 1.0 : 0.75) + (double)N * K / 32;
   const double hbm = (wbytes + (double)M * K * 1.04) / (5.0e12 / 2.4e9);
-  // dense problems keep 128-row tiles unless forced: measured on the c2/c3/c4 shapes,
-  // 64-row tiles were 2-30 % slower (half the MFMAs per stage for the same weight copies)
+  // dense problems keep 128-row tiles unless forced or M <= 64: measured on the c2/c3/c4
+  // shapes at M >= 128, 64-row tiles were 2-30 % slower (half the MFMAs per stage for the
+  // same weight copies); at M = 64 the half-empty 128-row tiles lost on all three (per-shape
+  // sweep: 7 %, 18 %, 22 %)
   const int mts[2] = {8, 4};
   const int nts[3] = {4, 2, 1};
+  const int mt_auto = M <= 64 ? 4 : 8;
   for (int mt : mts) {
-    if (mt_force ? mt != mt_force : mt != 8) continue;
+    if (mt_force ? mt != mt_force : mt != mt_auto) continue;
     const int64_t MB = (M + 16 * mt - 1) / (16 * mt);
     for (int nt : nts) {
       if (mt == 4 && nt == 1) continue;  // not instantiated
@@ -839,7 +844,10 @@ WideConfig wide_config(int64_t M, int64_t N, int64_t K, int fmt, const GemmOptio
         if ((KT + per - 1) / per != s || (s_only && s != s_only)) continue;
         const double rounds = (double)((tiles * s + cus - 1) / cus);
         const double compute = rounds * per * 4 * t_stage + 3000.0;
-        const double partial = s > 1 ? ((double)M * N * 4 * s * 2 + (double)M * N * 2) / (3.0e12 / 2.4e9) : 0.0;
+        // a K split writes and re-reads its partials and adds the reduce launch (about 4 µs
+        // in a graph: MXFP8 2048 x 2048 at M = 512 ran 12.4 µs whole-K against 15.8 split)
+        const double partial =
+            s > 1 ? ((double)M * N * 4 * s * 2 + (double)M * N * 2) / (3.0e12 / 2.4e9) + kWideReduceCycles : 0.0;
         const double cost = (compute > hbm ? compute : hbm) + partial;
         if (cost < best_cost) {
           best_cost = cost;
