@@ -95,8 +95,9 @@ def prepare(problems: Optional[Iterable] = None, table=None, mode: str = "auto",
     abi = _lib.query("mxl_gemm_config_abi")
     if t["config_abi"] != abi:
         raise RuntimeError(f"GEMM tactic table config ABI {t['config_abi']!r} does not match the library's {abi!r}")
+    dev = None
     if torch.cuda.is_available():
-        dev = device or torch.device("cuda", torch.cuda.current_device())
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         cus = torch.cuda.get_device_properties(dev).multi_processor_count
         if cus != t["cu_count"]:
             if mode == "on":
@@ -104,13 +105,25 @@ def prepare(problems: Optional[Iterable] = None, table=None, mode: str = "auto",
             return 0
     keys = None if problems is None else _problem_keys(problems)
     count = 0
-    for e in t["entries"]:
-        if keys is not None and (e["n"], e["k"], e["w_fmt"], e["block"]) not in keys:
-            continue
-        _lib.call("mxl_set_gemm_config", e["m"], e["n"], e["k"], e["w_fmt"], e["block"],
-                  _lib.options_ptr(options_of(e["config"])))
-        count += 1
+    # the library keys an entry by the device current at registration
+    with torch.cuda.device(dev) if dev is not None else _no_device():
+        for e in t["entries"]:
+            if keys is not None and (e["n"], e["k"], e["w_fmt"], e["block"]) not in keys:
+                continue
+            _lib.call("mxl_set_gemm_config", e["m"], e["n"], e["k"], e["w_fmt"], e["block"],
+                      _lib.options_ptr(options_of(e["config"])))
+            count += 1
     return count
+
+
+class _no_device:
+    """Host-only planning (no HIP device): entries register under device 0."""
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
 
 
 def clear() -> None:
