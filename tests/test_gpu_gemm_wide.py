@@ -423,3 +423,43 @@ def test_stream_block_fp8_gemm(pkg, oracle_mod, dev, M, N, K, bias):
     if bias:
         ref = oracle_mod.bf16_to_f32(oracle_mod.f32_to_bf16(ref + b.float().numpy()[None, :]))
     _check(y.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,cfg,f16,alpha,bias", [
+    (200, 1000, 2560, "2,3", 1, 0.375, False),   # ragged M and N: partial tiles in both
+    (256, 1000, 2560, "1,4", 0, 0.5, True),      # 64-column tiles, bias after the scaled rounding
+    (512, 8320, 1024, "2,1,h", 1, 0.375, True),  # hybrid: 260 tiles, whole-K round plus split units
+    (130, 640, 2048, "4,2", 1, 0.5, False),      # 256-column tiles, three-slot ring
+])
+def test_wide_split_epilogue_rounds_once(pkg, oracle_mod, dev, M, N, K, cfg, f16, alpha, bias):
+    """The wide kernel's K split (fragment-ordered partials summed by the tile reduce) with
+    the output scale, format and bias, through the C ABI: integer operands make every sum
+    exact, so the output must equal round(alpha * exact) (then + bias, rounded again) bit for
+    bit in bf16 or fp16 -- rows and columns past M and N included in the tiles, not stored."""
+    from test_gpu_boundary_ops import _integer_operands
+    from vllm_mach_amd import _lib
+    ops = pkg.ops
+    x, wp, ws, exact = _integer_operands(oracle_mod, M, N, K, 900 + M + N)
+    tiled, tiled_s = ops.pack_weight(torch.from_numpy(wp).to(dev), torch.from_numpy(ws).to(dev), 3)
+    a, sa = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), 0)
+    parts = cfg.split(",")
+    opts = _lib.GemmOptions(0, 1, int(parts[1]), int(parts[0]), 0, int(len(parts) > 2), 4, f16, alpha)
+    need = _lib.query("mxl_gemm_workspace_bytes_ex", M, N, K, 3, 0, _lib.options_ptr(opts))
+    assert need > 0  # the configuration splits K
+    ws_buf = torch.empty(need, dtype=torch.uint8, device=dev)
+    dtype = torch.float16 if f16 else torch.bfloat16
+    # the bias is bf16 whatever the output format (mxl_gemm_options: added in binary32 after
+    # the scaled rounding, then rounded again)
+    b = (torch.randint(-64, 64, (N,), generator=torch.Generator().manual_seed(3)).float() / 4).bfloat16()
+    bd = b.to(dev)
+    out = torch.full((M, N + 8), 7.0, dtype=dtype, device=dev)  # ldc > N: the pad stays untouched
+    _lib.call("mxl_mx_gemm_ex", a.data_ptr(), sa.data_ptr(), M, tiled.data_ptr(), tiled_s.data_ptr(), N, K, 3,
+              bd.data_ptr() if bias else None, out.data_ptr(), N + 8, ws_buf.data_ptr(), need,
+              _lib.options_ptr(opts), torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize(dev)
+    expected = torch.from_numpy(exact.astype(np.float32) * np.float32(alpha)).to(dtype)
+    if bias:
+        expected = (expected.float() + b.float()[None, :]).to(dtype)
+    got = out.cpu()
+    assert torch.equal(got[:, :N], expected)
+    assert torch.all(got[:, N:] == 7.0)
