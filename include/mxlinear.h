@@ -277,15 +277,20 @@ int mxl_swiglu_mx_gemm_ex(const void* gate_up, int64_t M, int64_t K, int rule, c
                           const mxl_gemm_options* options, void* stream);
 
 /* MXFP8 quantization -> MX GEMM for M <= 16 bf16 activation rows x [M, K] in one launch,
- * bit-identical to mxl_quantize_mxfp8 (rule 0, 1 or 2) followed by mxl_mx_gemm; the
- * producer waves, scratch slots, handoff and shapes of mxl_swiglu_mx_gemm.  Replaces
+ * bit-identical to mxl_quantize_mxfp8 (rule 0, 1 or 2) followed by mxl_mx_gemm.  Two
+ * schemes: the GEMM's own wavefronts quantize (M = 1: each wavefront its super-tiles' row
+ * values; 2 <= M <= 16 with K <= 4096: each MFMA fragment lane the two 16-value pieces of
+ * its row it multiplies, the block amax completed with the lane holding the blocks' other
+ * halves; no scratch and no synchronisation beyond the workgroup), or the producer waves,
+ * scratch slots, handoff and shapes of mxl_swiglu_mx_gemm.  Replaces
  * mxfp8_sm120::gemm_from_float and mxfp6::gemm_from_float at M <= 16
  * (src/vllm_mach/mxfp6/dense_mxfp8.py:89-96, src/vllm_mach/mxfp6/dense.py:122-129). */
 int mxl_quant_mx_gemm(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled, const void* sw_tiled,
                       int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc, void* stream);
 
-/* mxl_quant_mx_gemm with the output format, scale and scheme of `options` (as for
- * mxl_swiglu_mx_gemm_ex).  Replaces mxfp6::gemm_from_float(x, w, ws, N, alpha, dtype)
+/* mxl_quant_mx_gemm with the output format, scale and scheme of `options`: -1 automatic
+ * (the wavefronts' own quantization where it runs, else the handoff), 0 the producer waves
+ * and handoff, 3 the wavefronts' own quantization.  Replaces mxfp6::gemm_from_float(x, w, ws, N, alpha, dtype)
  * (src/vllm_mach/mxfp6/dense.py:122-129). */
 int mxl_quant_mx_gemm_ex(const void* x, int64_t M, int64_t K, int rule, const void* w_tiled, const void* sw_tiled,
                          int64_t N, int w_fmt, const void* bias, void* out, int64_t ldc,
@@ -307,8 +312,9 @@ int mxl_block_fp8_quant_gemm_ex(const void* x, int64_t M, int64_t K, const void*
                                 void* stream);
 
 /* 1 when the one-launch producer + GEMM runs (kind 0 mxl_swiglu_mx_gemm, 1
- * mxl_quant_mx_gemm, 2 mxl_block_fp8_quant_gemm) for M rows, K, scale rule and weight
- * format, else 0.  No counterpart in the reference (its fused rows are fixed,
+ * mxl_quant_mx_gemm, 2 mxl_block_fp8_quant_gemm; 3 mxl_quant_mx_gemm with the
+ * quantization in the GEMM's own wavefronts, the scheme that measured faster than two
+ * launches) for M rows, K, scale rule and weight format, else 0.  No counterpart in the reference (its fused rows are fixed,
  * src/vllm_mach/mxfp6/fused_mlp.py:13-19); for callers choosing between one launch and
  * two. */
 int mxl_producer_gemm_supported(int kind, int64_t M, int64_t K, int rule, int w_fmt);

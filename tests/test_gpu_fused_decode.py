@@ -74,16 +74,33 @@ def test_quant_one_launch_bit_identical(pkg, oracle_mod, dev, fmt, rule, M, N, K
     special[M - 1, 40] = float("nan")
     special[0, 70] = -float("inf")
     special[M - 1, 100] = 1e-40
+    inreg = ops.quant_rows_inreg(M, K, rule, fmt)
     for rows in (x, special):
         xd = rows.to(dev)
         a, sa = torch.ops.mach_amd.quantize_mxfp8(xd, rule)
         y_ref = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, fmt, bias)
         y = torch.ops.mach_amd.quant_mx_gemm(xd, tiled, tiled_s, N, fmt, rule, bias)
         assert _eq(y, y_ref)
-    # the layer path takes one launch for one row only (more rows: the two launches, faster)
+        # each scheme by name: 0 the producer waves and handoff, 3 the GEMM's own wavefronts
+        from vllm_mach_amd import _lib
+        for kernel in (0, 3):
+            y_k = torch.empty_like(y_ref)
+            try:
+                _lib.call("mxl_quant_mx_gemm_ex", xd.data_ptr(), M, K, rule, tiled.data_ptr(), tiled_s.data_ptr(),
+                          N, fmt, bias.data_ptr() if bias is not None else None, y_k.data_ptr(), N,
+                          _lib.options_ptr(_lib.GemmOptions(kernel=kernel)),
+                          torch.cuda.current_stream(dev).cuda_stream)
+            except _lib.MxlError as e:
+                assert "unsupported" in str(e) and (kernel == 0 or not inreg), (kernel, str(e))
+                continue
+            assert kernel == 0 or inreg
+            assert _eq(y_k, y_ref), kernel
+    # the layer path takes one launch where the GEMM's wavefronts quantize (one row, or up
+    # to 16 rows at K <= 4096), else the two launches (faster than the handoff)
+    assert inreg == (M == 1 or K <= 4096)
     before = dict(ops._COUNTS)
     y_layer = ops.mx_gemm_from_float(x.to(dev), tiled, tiled_s, N, fmt, rule)
-    assert ops._COUNTS.get("quant_mx_gemm", 0) == before.get("quant_mx_gemm", 0) + (M == 1)
+    assert ops._COUNTS.get("quant_mx_gemm", 0) == before.get("quant_mx_gemm", 0) + int(inreg)
     y = torch.ops.mach_amd.quant_mx_gemm(x.to(dev), tiled, tiled_s, N, fmt, rule, None)
     assert _eq(y, y_layer)
     if M * N >= 2048 and N * K <= 2048 * 2048:

@@ -906,13 +906,18 @@ static int quant_row_common(const void* x, int64_t M, int64_t K, int rule, const
   const bool rule_ok = rule >= kFloorCarry175 && rule <= kRpUe8m0;
   const bool handoff = rule_ok && stream_fused_eligible(M, K, false, w_fmt);
   const bool rowwise = stream_quant_row_eligible(M, K, rule);
-  // automatic: the row recomputed by every wavefront where it runs (M = 1: measured faster
-  // than the handoff, whose grid-wide synchronisation costs more than the launch it saves)
-  const bool use_rowwise = o.kernel == kStreamWide || (o.kernel == kAuto && rowwise);
-  if (use_rowwise ? !rowwise : (!handoff || (o.kernel != kAuto && o.kernel != kStream))) {
+  const bool qrows = stream_quant_rows_eligible(M, K, rule);
+  // The producer inside the GEMM's own wavefronts (options.kernel 3, automatic where it
+  // runs): for one row every wavefront quantizes its super-tiles' row values; for up to 16
+  // rows (K <= 4096) every fragment lane its own pieces, once per workgroup.  Both measured
+  // faster than the producer waves' grid-wide handoff (options.kernel 0), whose
+  // synchronisation costs more than the launch it saves.
+  const bool inreg = M == 1 ? rowwise : qrows;
+  const bool use_inreg = o.kernel == kStreamWide || (o.kernel == kAuto && inreg);
+  if (use_inreg ? !inreg : (!handoff || (o.kernel != kAuto && o.kernel != kStream))) {
     set_error("mxl_quant_mx_gemm: unsupported (M <= 16, K %% 128 == 0, K <= 12288 except 7680 < K <= 8192 and "
-              "K > 11264 for M > 1, rule 0, 1 or 2; options.kernel -1, 0 or 3 (3: M = 1); M=%lld K=%lld "
-              "rule=%d kernel=%d)", (long long)M, (long long)K, rule, o.kernel);
+              "K > 11264 for M > 1, rule 0, 1 or 2; options.kernel -1, 0 or 3 (3: M = 1, or M <= 16 with "
+              "K <= 4096); M=%lld K=%lld rule=%d kernel=%d)", (long long)M, (long long)K, rule, o.kernel);
     return MXL_EUNSUPPORTED;
   }
   if (M == 0) return MXL_OK;
@@ -922,12 +927,13 @@ static int quant_row_common(const void* x, int64_t M, int64_t K, int rule, const
   p.lda = K; p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
   p.row_div = 1; p.S = 1;
   p.alpha = o.alpha; p.out_f16 = o.out_dtype == kOutF16;
-  if (!use_rowwise) {
+  if (!use_inreg) {
     p.fsrc = (const uint16_t*)x;
     p.fsrc_ld = K;
     return launch_gemm_stream_fused(w_fmt, 4 + rule, p, (hipStream_t)stream, "mxl_quant_mx_gemm");
   }
-  const hipError_t e = launch_gemm_stream_quant_row(w_fmt, rule, p, (hipStream_t)stream);
+  const hipError_t e = M == 1 ? launch_gemm_stream_quant_row(w_fmt, rule, p, (hipStream_t)stream)
+                              : launch_gemm_stream_quant_rows(w_fmt, rule, p, (hipStream_t)stream);
   if (e != hipSuccess) {
     set_error("mxl_quant_mx_gemm: launch failed: %s", hipGetErrorString(e));
     return MXL_EHIP;
@@ -956,9 +962,12 @@ extern "C" int mxl_producer_gemm_supported(int kind, int64_t M, int64_t K, int r
              (stream_fused_eligible(m, K, false, w_fmt) || stream_swiglu_eligible(m, K, rule));
     case 1:  // MXFP8 quantization -> MX GEMM
       return valid_wfmt(w_fmt) && rule >= kFloorCarry175 && rule <= kRpUe8m0 &&
-             (stream_fused_eligible(m, K, false, w_fmt) || stream_quant_row_eligible(m, K, rule));
+             (stream_fused_eligible(m, K, false, w_fmt) || stream_quant_row_eligible(m, K, rule) ||
+              stream_quant_rows_eligible(m, K, rule));
     case 2:  // block-FP8 quantization -> block-FP8 GEMM
       return stream_fused_eligible(m, K, true, kE4M3);
+    case 3:  // MXFP8 quantization inside the GEMM's own wavefronts (no handoff)
+      return valid_wfmt(w_fmt) && (m == 1 ? stream_quant_row_eligible(1, K, rule) : stream_quant_rows_eligible(m, K, rule));
     default:
       return 0;
   }

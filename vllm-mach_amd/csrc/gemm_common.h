@@ -309,6 +309,10 @@ hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hip
 // (the activation quantizer's arithmetic, rule 0, 1 or 2)
 bool stream_quant_row_eligible(int64_t M, int64_t K, int rule);
 hipError_t launch_gemm_stream_quant_row(int fmt, int rule, const GemmParams& p, hipStream_t s);
+// MXFP8 quantization of up to 16 bf16 rows inside the weight-streaming GEMM, each fragment
+// lane quantizing its own pieces (K <= 4096)
+bool stream_quant_rows_eligible(int64_t M, int64_t K, int rule);
+hipError_t launch_gemm_stream_quant_rows(int fmt, int rule, const GemmParams& p, hipStream_t s);
 // Producer + weight-streaming GEMM in one launch (M <= 16): prod 1 / 2 = SwiGLU ->
 // MXFP8 under that rule (p.fsrc = gate/up [M, 2K]), 4 + rule = the MXFP8 activation
 // quantizer, kFusedBlockFp8 = the block-FP8 quantizer (p.fsrc = x [M, K]); p.fsrc_ld is

@@ -37,6 +37,10 @@ namespace mxl {
 namespace {
 
 constexpr int kStreamMaxWaves = 16;
+// the in-register MXFP8 quantizer for up to 16 rows: at most this many super-tiles (one
+// per wave, two waves per SIMD), so the raw rows' registers fit beside the weights
+// (K <= 4096; at ten waves the 168-register budget spilled)
+constexpr int kStreamQuantRowsMaxKT = 8;
 constexpr int64_t kStreamMaxK = 12288;  // two super-tiles per wave, at most twelve waves
 // block-FP8 keeps four fp32 activation scales per slice in registers: at most eight
 // waves (two per SIMD, 256 registers each), one super-tile each up to K = 4096, two up to 8192
@@ -323,12 +327,15 @@ __device__ __forceinline__ void stream_produce(const GemmParams& p, int lane, in
 // then read the codes (device-coherent loads, sc1) as the two-launch path's GEMM does,
 // with the same MFMA chain and sums.
 template <int FMT, int RUN, bool DB, bool BLOCK, int ROWP = -1, int FPROD = -1>
-__global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_stream_kernel(GemmParams p) {
+__global__ __launch_bounds__(BLOCK ? 512 : (ROWP >= 8 ? 64 * kStreamQuantRowsMaxKT : (RUN == 1 ? 1024 : 768)))
+void gemm_stream_kernel(GemmParams p) {
   static_assert(!BLOCK || FMT == kE4M3, "block-FP8 weights are E4M3");
   static_assert(ROWP < 0 || !BLOCK, "the fused producer row feeds MX GEMMs");
   static_assert(ROWP < 0 || FPROD < 0, "one producer scheme per launch");
   static_assert(FPROD < 0 || (FPROD == 8) == BLOCK, "block-FP8 GEMMs take the block-FP8 quantizer");
-  constexpr bool ROW = ROWP >= 0, SWI = ROWP >= 0 && ROWP < 4;
+  static_assert(ROWP < 8 || RUN == 1, "the in-register quantizer takes one super-tile per wave");
+  constexpr bool ROW = ROWP >= 0 && ROWP < 8, SWI = ROWP >= 0 && ROWP < 4;
+  constexpr bool QROWS = ROWP >= 8;
   constexpr bool FUSED = FPROD >= 0;
   constexpr int RRULE = ROWP & 3;
   __shared__ float red[2][kStreamMaxWaves][4][64];
@@ -373,6 +380,24 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
       const int64_t kc = k0 < p.K ? k0 : p.K - 8;  // blocks past K: any valid data, zeroed below
       gu_raw[u][0] = *reinterpret_cast<const uint4*>(gu + kc);
       if constexpr (SWI) gu_raw[u][SWI ? 1 : 0] = *reinterpret_cast<const uint4*>(gu + p.K + kc);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
+  }
+  // QROWS: fragment lane (q, r)'s bf16 pieces of row r (rows past M read row M - 1 and are
+  // never stored), K values 16 q .. 16 q + 15 and 64 + 16 q .. + 15 of each slice, also
+  // requested ahead of the weights
+  uint4 qr_raw[QROWS ? 4 : 1][QROWS ? 4 : 1];
+  if constexpr (QROWS) {
+    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(p.a) + (r < p.M ? r : p.M - 1) * p.lda;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t k0 = kt[0] * kTileK + 128 * j;
+      const int64_t kc = k0 < p.K ? k0 : p.K - 128;  // slices past K: any valid data, zeroed below
+      const uint16_t* b0 = xrow + kc + 16 * q;
+      qr_raw[j][0] = *reinterpret_cast<const uint4*>(b0);
+      qr_raw[j][1] = *reinterpret_cast<const uint4*>(b0 + 8);
+      qr_raw[j][2] = *reinterpret_cast<const uint4*>(b0 + 64);
+      qr_raw[j][3] = *reinterpret_cast<const uint4*>(b0 + 72);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the weight loads
   }
@@ -461,6 +486,44 @@ __global__ __launch_bounds__(BLOCK ? 512 : (RUN == 1 ? 1024 : 768)) void gemm_st
         a[u][j] = v8i{y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]};
         sraw[u][j] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * 4 * (4 * j + q), (int)sc) << (8 * q);
       }
+    }
+  } else if constexpr (QROWS) {
+    // The MXFP8 quantizer of up to 16 rows in the fragment registers (the standalone
+    // kernel's quiet8 + quant8x4 arithmetic): lane (q, r)'s two 16-value pieces of slice j
+    // are halves of blocks q / 2 and 2 + q / 2 of the slice, whose other halves lane q ^ 1
+    // (lane xor 16, the same row) holds, so one shuffle completes each block amax; the
+    // MFMA takes lane (q, r)'s scale for block q, which lane q = 2 (block 1) or q = 0
+    // (block 2) computed, or the lane itself (blocks 0 and 3).
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // slice j's raw values "depend" on slice j - 1's result (an empty asm), so the
+      // compiler converts one slice at a time instead of hoisting every slice's 32 floats
+      if (j > 0) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          asm volatile("" : "+v"(qr_raw[j][h].x), "+v"(qr_raw[j][h].y), "+v"(qr_raw[j][h].z), "+v"(qr_raw[j][h].w)
+                       : "v"(sraw[0][j > 0 ? j - 1 : 0]));
+      }
+      uint32_t c[2][4], sc[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // one piece (half a block) at a time: 16 values live
+        float v[16];
+        bf16x8_to_f32(qr_raw[j][2 * h], v);
+        bf16x8_to_f32(qr_raw[j][2 * h + 1], v + 8);
+        quiet8(v);
+        quiet8(v + 8);
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+        m = __builtin_fmaxf(m, __shfl_xor(m, 16));
+        sc[h] = quant_block_codes<RRULE, false, 16>(v, m, c[h]);
+      }
+      a[0][j] = v8i{(int)c[0][0], (int)c[0][1], (int)c[0][2], (int)c[0][3],
+                    (int)c[1][0], (int)c[1][1], (int)c[1][2], (int)c[1][3]};
+      const uint32_t b1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (r + 32), (int)sc[0]);
+      const uint32_t b2 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * r, (int)sc[1]);
+      const uint32_t sb = q == 0 ? sc[0] : q == 1 ? b1 : q == 2 ? b2 : sc[1];
+      sraw[0][j] = sb << (8 * q);
     }
   } else if constexpr (FUSED) {
     // the scratch holds the codes in fragment order (stream_produce): slice s's 32 bytes
@@ -1112,11 +1175,15 @@ namespace {
 // the quantized row)
 template <int FMT, int ROWP>
 hipError_t launch_row_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
-  if (p.KT <= kStreamMaxWaves)
+  if constexpr (ROWP >= 8) {  // the in-register quantizer: one super-tile per wave
+    if (p.KT > kStreamQuantRowsMaxKT || p.M > 16) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, false, ROWP>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
-  else
+  } else if (p.KT <= kStreamMaxWaves) {
+    hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, false, ROWP>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
+  } else {
     hipLaunchKernelGGL((gemm_stream_kernel<FMT, 2, false, false, ROWP>), grid,
                        dim3((unsigned)((p.KT + 1) / 2 * 64)), 0, s, p);
+  }
   return hipGetLastError();
 }
 template <int ROWP>
@@ -1150,6 +1217,18 @@ hipError_t launch_gemm_stream_quant_row(int fmt, int rule, const GemmParams& p, 
   if (rule == kFloorCarry175) return launch_row<4 + kFloorCarry175>(fmt, p, row_grid(p), s);
   if (rule == kCeilDiv448) return launch_row<4 + kCeilDiv448>(fmt, p, row_grid(p), s);
   if (rule == kRpUe8m0) return launch_row<4 + kRpUe8m0>(fmt, p, row_grid(p), s);
+  return hipErrorInvalidValue;
+}
+
+bool stream_quant_rows_eligible(int64_t M, int64_t K, int rule) {
+  return M >= 1 && M <= 16 && stream_gemm_eligible(M, K, false) && (K + kTileK - 1) / kTileK <= kStreamQuantRowsMaxKT &&
+         rule >= kFloorCarry175 && rule <= kRpUe8m0;
+}
+
+hipError_t launch_gemm_stream_quant_rows(int fmt, int rule, const GemmParams& p, hipStream_t s) {
+  if (rule == kFloorCarry175) return launch_row<8 + kFloorCarry175>(fmt, p, row_grid(p), s);
+  if (rule == kCeilDiv448) return launch_row<8 + kCeilDiv448>(fmt, p, row_grid(p), s);
+  if (rule == kRpUe8m0) return launch_row<8 + kRpUe8m0>(fmt, p, row_grid(p), s);
   return hipErrorInvalidValue;
 }
 

@@ -181,6 +181,60 @@ __device__ __forceinline__ void swiglu8(const float* g, const float* u, float* v
   }
 }
 
+// The E8M0 code of a block from its amax (every lane of the block passes the same
+// amax) and the lane's N codes (N % 4 == 0) packed into N / 4 dwords: quant8x4's
+// arithmetic (below) for any number of the block's values per lane.  NAN_ANY as there.
+template <int RULE, bool NAN_ANY, int N>
+__device__ __forceinline__ uint32_t quant_block_codes(const float* v, float amax, uint32_t* packed) {
+  static_assert(N % 4 == 0, "whole code dwords");
+  uint32_t s;
+  float y[N];
+  if (RULE == kRpUe8m0) {
+    // min(max(v * inverse, -448), 448): no NaN is left for the conversion
+    s = e8m0_rp(amax);
+    const float inv = e8m0_rp_inverse(s);
+#pragma unroll
+    for (int i = 0; i < N; ++i) y[i] = __builtin_fminf(__builtin_fmaxf(v[i] * inv, -448.0f), 448.0f);
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) packed[i] = e4m3x4_raw(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+    return s;
+  }
+  if (RULE == kFloorCarry175) {
+    s = scale_floor_carry175(f2u(amax) >> 16);
+    const int e2 = 127 - (int)s;
+#pragma unroll
+    for (int i = 0; i < N; ++i) y[i] = __builtin_ldexpf(v[i], e2);
+  } else {
+    const uint32_t bits = pow2_ceil_div448(amax);
+    s = bits >> 23;
+    const float mul = 1.0f / u2f(bits);
+    if (NAN_ANY && bits == 0x7F800000u) {
+      // an infinite amax: mul = 0 and inf * 0 makes a NaN of the multiply's own sign,
+      // coded by f32_to_e4m3 from the product of the canonical values
+#pragma unroll
+      for (int i = 0; i < N; ++i) y[i] = (v[i] != v[i] ? u2f(0x7FC00000u) : v[i]) * mul;
+#pragma unroll
+      for (int i = 0; i < N / 4; ++i)
+        packed[i] = f32_to_e4m3(y[4 * i]) | f32_to_e4m3(y[4 * i + 1]) << 8 | f32_to_e4m3(y[4 * i + 2]) << 16 |
+                    f32_to_e4m3(y[4 * i + 3]) << 24;
+      return s;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) y[i] = v[i] * mul;
+  }
+  if (NAN_ANY) {
+    // every NaN (and every value from 480 up) -> 480 -> 0x7F
+#pragma unroll
+    for (int i = 0; i < N; ++i) y[i] = __builtin_fminf(y[i], 480.0f);
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) packed[i] = e4m3x4_raw(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) packed[i] = e4m3x4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+  }
+  return s;
+}
+
 // Quantize one 32-element block held by 4 consecutive lanes (8 values each,
 // lane (tid & 3) owns elements [8 (tid & 3), +8)).  The block amax is an
 // xor-shuffle max over the 4 lanes (order-free, so identical to a serial max).
@@ -196,50 +250,7 @@ __device__ __forceinline__ uint32_t quant8x4(const float* v, uint32_t* packed) {
   for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
   amax = __builtin_fmaxf(amax, __shfl_xor(amax, 1, 4));
   amax = __builtin_fmaxf(amax, __shfl_xor(amax, 2, 4));
-  uint32_t s;
-  float y[8];
-  if (RULE == kRpUe8m0) {
-    // min(max(v * inverse, -448), 448): no NaN is left for the conversion
-    s = e8m0_rp(amax);
-    const float inv = e8m0_rp_inverse(s);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = __builtin_fminf(__builtin_fmaxf(v[i] * inv, -448.0f), 448.0f);
-    packed[0] = e4m3x4_raw(y[0], y[1], y[2], y[3]);
-    packed[1] = e4m3x4_raw(y[4], y[5], y[6], y[7]);
-    return s;
-  }
-  if (RULE == kFloorCarry175) {
-    s = scale_floor_carry175(f2u(amax) >> 16);
-    const int e2 = 127 - (int)s;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = __builtin_ldexpf(v[i], e2);
-  } else {
-    const uint32_t bits = pow2_ceil_div448(amax);
-    s = bits >> 23;
-    const float mul = 1.0f / u2f(bits);
-    if (NAN_ANY && bits == 0x7F800000u) {
-      // an infinite amax: mul = 0 and inf * 0 makes a NaN of the multiply's own sign,
-      // coded by f32_to_e4m3 from the product of the canonical values
-#pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = (v[i] != v[i] ? u2f(0x7FC00000u) : v[i]) * mul;
-      packed[0] = f32_to_e4m3(y[0]) | f32_to_e4m3(y[1]) << 8 | f32_to_e4m3(y[2]) << 16 | f32_to_e4m3(y[3]) << 24;
-      packed[1] = f32_to_e4m3(y[4]) | f32_to_e4m3(y[5]) << 8 | f32_to_e4m3(y[6]) << 16 | f32_to_e4m3(y[7]) << 24;
-      return s;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = v[i] * mul;
-  }
-  if (NAN_ANY) {
-    // every NaN (and every value from 480 up) -> 480 -> 0x7F
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = __builtin_fminf(y[i], 480.0f);
-    packed[0] = e4m3x4_raw(y[0], y[1], y[2], y[3]);
-    packed[1] = e4m3x4_raw(y[4], y[5], y[6], y[7]);
-  } else {
-    packed[0] = e4m3x4(y[0], y[1], y[2], y[3]);
-    packed[1] = e4m3x4(y[4], y[5], y[6], y[7]);
-  }
-  return s;
+  return quant_block_codes<RULE, NAN_ANY, 8>(v, amax, packed);
 }
 
 // Unpack 8 bf16 from a 16-byte vector into floats

@@ -251,13 +251,13 @@ std::tuple<at::Tensor, at::Tensor> quantize_logical(const at::Tensor& x, int rul
   return {codes, scales};
 }
 
-// One bf16 row quantized inside the weight-streaming GEMM (one launch, the same bits as
-// quantize + GEMM); nullopt for shapes that take the two calls (more rows: the one-launch
-// handoff measured slower than the two launches).
+// Up to 16 bf16 rows quantized inside the weight-streaming GEMM's own wavefronts (one
+// launch, the same bits as quantize + GEMM); nullopt for shapes that take the two calls
+// (the one-launch handoff measured slower than the two launches).
 std::optional<at::Tensor> quant_row(const at::Tensor& x, const Tiled& t, int fmt, int64_t N, int64_t K,
                                     const mxl_gemm_options& o, hipStream_t s) {
   const int64_t M = x.size(0);
-  if (M != 1 || !mxl_producer_gemm_supported(1, M, K, kFloorCarry175, fmt) ||
+  if (M < 1 || M > 16 || !mxl_producer_gemm_supported(3, M, K, kFloorCarry175, fmt) ||
       x.scalar_type() != at::kBFloat16 || !x.is_cuda())
     return {};
   at::Tensor xc = x.contiguous();

@@ -477,6 +477,13 @@ def quant_row_fusable(m: int, k: int, rule: int, w_fmt: int = E4M3) -> bool:
     return 1 <= m <= 16 and bool(query("mxl_producer_gemm_supported", 1, m, k, rule, w_fmt))
 
 
+def quant_rows_inreg(m: int, k: int, rule: int, w_fmt: int = E4M3) -> bool:
+    """Shapes whose MXFP8 quantization ``mxl_quant_mx_gemm`` runs inside the GEMM's own
+    wavefronts (one row; or up to 16 rows at K <= 4096), the one-launch scheme that measured
+    faster than the quantizer and GEMM as two launches."""
+    return 1 <= m <= 16 and bool(query("mxl_producer_gemm_supported", 3, m, k, rule, w_fmt))
+
+
 def block_row_fusable(m: int, k: int) -> bool:
     """Shapes ``mxl_block_fp8_quant_gemm`` runs in one launch (M <= 16 rows)."""
     return 1 <= m <= 16 and bool(query("mxl_producer_gemm_supported", 2, m, k, 0, E4M3))
@@ -630,12 +637,13 @@ def mx_gemm_from_float(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: in
     """Quantize bf16 activations to MXFP8 and run the MX GEMM.
 
     Replaces ``mxfp8_sm120::gemm_from_float`` / ``mxfp6::gemm_from_float``
-    (src/vllm_mach/mxfp6/dense_mxfp8.py:96, src/vllm_mach/mxfp6/dense.py:122-129).  One
-    One row runs as one launch (``quant_mx_gemm``, the same bits: every wavefront
-    recomputes the row's codes); more rows take the quantizer and the GEMM, which measured
-    faster than the one-launch handoff that ``quant_mx_gemm`` offers up to 16 rows.
+    (src/vllm_mach/mxfp6/dense_mxfp8.py:96, src/vllm_mach/mxfp6/dense.py:122-129).  Where
+    the GEMM's own wavefronts can quantize (one row, or up to 16 rows at K <= 4096) it runs
+    as one launch (``quant_mx_gemm``, the same bits); other shapes take the quantizer and
+    the GEMM, which measured faster than the one-launch handoff ``quant_mx_gemm`` offers
+    there.
     """
-    if x.shape[0] == 1 and quant_row_fusable(1, x.shape[1], rule, w_fmt):
+    if quant_rows_inreg(x.shape[0], x.shape[1], rule, w_fmt):
         return torch.ops.mach_amd.quant_mx_gemm(x, w, sw, n, w_fmt, rule, bias)
     a, sa = torch.ops.mach_amd.quantize_mxfp8(x, rule)
     return torch.ops.mach_amd.mx_gemm(a, sa, w, sw, n, x.shape[1], w_fmt, bias)
