@@ -153,6 +153,16 @@ def _dense_plan(M, N, K, fmt, block=False) -> str:
     return _lib.plan_name("mxl_gemm_plan_name", M, N, K, fmt, int(block))
 
 
+def _row_plan(M, K, fmt, rowp) -> str:
+    """The weight-streaming kernel a one-launch producer + GEMM runs (launch_row_fmt in
+    csrc/gemm_stream.hip): ROWP = rule (SwiGLU row), 4 + rule (one quantized row) or
+    8 + rule (up to 16 rows quantized in the fragment registers, one super-tile per wave);
+    the row producers take two super-tiles per wave past 16 waves."""
+    kt = -(-K // 512)
+    run = 1 if rowp >= 8 or kt <= 16 else 2
+    return f"gemm_stream_kernel<{fmt},{run},{'true' if run == 1 else 'false'},false,{rowp},-1>"
+
+
 class SwigluDown(Workload):
     """c2: SwiGLU -> MXFP8 producer + MXFP8 down projection."""
     name, describe = "c2", "c2: SwiGLU->MXFP8 producer + MXFP8 down projection N=2560 K=9216"
@@ -179,6 +189,8 @@ class SwigluDown(Workload):
         return 2.0 * M * self.N * self.K
 
     def plan(self, kname, M):
+        if "one launch" in kname:
+            return _row_plan(M, self.K, self.ops.E4M3, self.ops.CEIL_DIV448)
         return _dense_plan(M, self.N, self.K, self.ops.E4M3)
 
     def kernels(self, M):
@@ -238,6 +250,8 @@ class MxLinear(Workload):
         return 2.0 * M * self.N * self.K
 
     def plan(self, kname, M):
+        if "one launch" in kname:
+            return _row_plan(M, self.K, self.fmt, (4 if M == 1 else 8) + self.ops.FLOOR_CARRY175)
         return _dense_plan(M, self.N, self.K, self.fmt)
 
     def kernels(self, M):

@@ -74,6 +74,14 @@ def test_quant_one_launch_bit_identical(pkg, oracle_mod, dev, fmt, rule, M, N, K
     special[M - 1, 40] = float("nan")
     special[0, 70] = -float("inf")
     special[M - 1, 100] = 1e-40
+    # a block below 2^-119 (rule 0's E8M0 code wraps to 255), a zero block, a negative NaN
+    # and a signalling NaN: the in-register quantizer's binary32 branch and its scaled
+    # conversions' block conditions
+    if K >= 192:
+        special[(M - 1) // 2, 128:160] = torch.linspace(-3e-37, 3e-37, 32)
+        special[(M - 1) // 2, 160:192] = 0.0
+    special[0, 200 % K] = torch.tensor([-64], dtype=torch.int16).view(torch.bfloat16)  # 0xFFC0
+    special[M - 1, 250 % K] = torch.tensor([0x7F81], dtype=torch.int16).view(torch.bfloat16)
     inreg = ops.quant_rows_inreg(M, K, rule, fmt)
     for rows in (x, special):
         xd = rows.to(dev)

@@ -489,41 +489,102 @@ void gemm_stream_kernel(GemmParams p) {
     }
   } else if constexpr (QROWS) {
     // The MXFP8 quantizer of up to 16 rows in the fragment registers (the standalone
-    // kernel's quiet8 + quant8x4 arithmetic): lane (q, r)'s two 16-value pieces of slice j
-    // are halves of blocks q / 2 and 2 + q / 2 of the slice, whose other halves lane q ^ 1
-    // (lane xor 16, the same row) holds, so one shuffle completes each block amax; the
-    // MFMA takes lane (q, r)'s scale for block q, which lane q = 2 (block 1) or q = 0
-    // (block 2) computed, or the lane itself (blocks 0 and 3).
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // slice j's raw values "depend" on slice j - 1's result (an empty asm), so the
-      // compiler converts one slice at a time instead of hoisting every slice's 32 floats
-      if (j > 0) {
-#pragma unroll
-        for (int h = 0; h < 4; ++h)
-          asm volatile("" : "+v"(qr_raw[j][h].x), "+v"(qr_raw[j][h].y), "+v"(qr_raw[j][h].z), "+v"(qr_raw[j][h].w)
-                       : "v"(sraw[0][j > 0 ? j - 1 : 0]));
-      }
-      uint32_t c[2][4], sc[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {  // one piece (half a block) at a time: 16 values live
-        float v[16];
-        bf16x8_to_f32(qr_raw[j][2 * h], v);
-        bf16x8_to_f32(qr_raw[j][2 * h + 1], v + 8);
-        quiet8(v);
-        quiet8(v + 8);
-        float m = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
-        m = __builtin_fmaxf(m, __shfl_xor(m, 16));
-        sc[h] = quant_block_codes<RRULE, false, 16>(v, m, c[h]);
-      }
+    // kernel's arithmetic): lane (q, r)'s two 16-value pieces of slice j are halves of
+    // blocks q / 2 and 2 + q / 2 of the slice, whose other halves lane q ^ 1 (lane xor 16,
+    // the same row) holds, so one row swap completes each block amax; the MFMA takes lane
+    // (q, r)'s scale for block q, which lane q = 3 (block 1) or q = 0 (block 2) computed,
+    // or the lane itself (blocks 0 and 3).  Both exchanges are VALU lane swaps
+    // (v_permlane16_swap / v_permlane32_swap), not LDS round trips: with one wave per
+    // SIMD nothing else hides their latency.
+    auto piece = [&](int j, int h, uint32_t* d) {
+      d[0] = qr_raw[j][2 * h].x;     d[1] = qr_raw[j][2 * h].y;     d[2] = qr_raw[j][2 * h].z;
+      d[3] = qr_raw[j][2 * h].w;     d[4] = qr_raw[j][2 * h + 1].x; d[5] = qr_raw[j][2 * h + 1].y;
+      d[6] = qr_raw[j][2 * h + 1].z; d[7] = qr_raw[j][2 * h + 1].w;
+    };
+    auto place = [&](int j, const uint32_t (*c)[4], const uint32_t* sc) {
       a[0][j] = v8i{(int)c[0][0], (int)c[0][1], (int)c[0][2], (int)c[0][3],
                     (int)c[1][0], (int)c[1][1], (int)c[1][2], (int)c[1][3]};
-      const uint32_t b1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (r + 32), (int)sc[0]);
-      const uint32_t b2 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * r, (int)sc[1]);
-      const uint32_t sb = q == 0 ? sc[0] : q == 1 ? b1 : q == 2 ? b2 : sc[1];
-      sraw[0][j] = sb << (8 * q);
+      // x = rows (sc0.0, sc0.1, sc1.0, sc1.1), y = rows (sc0.2, sc0.3, sc1.2, sc1.3): even
+      // q takes x (its own block 0, or lane q = 0's block 2), odd q takes y (lane q = 3's
+      // block 1, or its own block 3)
+      const auto xy = __builtin_amdgcn_permlane32_swap(sc[0], sc[1], false, false);
+      sraw[0][j] = ((q & 1) ? xy[1] : xy[0]) << (8 * q);
+    };
+    // Every block amax as bf16 magnitude bits, NaNs included (above 0x7F80 when one is
+    // present); rows {0, 1} and {2, 3} side by side, so the max is the xor-16 max.  With
+    // power-of-two scales, no NaN in the wave's blocks and no E8M0 code 255 (rule 0 wraps
+    // there for amax below 2^-119, rule 1 at an infinite amax) the scaled conversion codes
+    // straight from bf16, one branch for the wave; otherwise each block whose scale or
+    // values need it takes the standalone quantizer's binary32 arithmetic.
+    uint32_t sfs[4][2];
+    bool fast = RRULE != kRpUe8m0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t d[8];
+        piece(j, h, d);
+        uint32_t mb = amax_bf16_bits<8, false>(d);
+        const auto mm = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+        mb = mm[0] > mm[1] ? mm[0] : mm[1];
+        uint32_t sf = 255u;
+        if constexpr (RRULE == kFloorCarry175) sf = scale_floor_carry175(mb);
+        if constexpr (RRULE == kCeilDiv448) sf = pow2_ceil_div448(u2f(mb << 16)) >> 23;
+        sfs[j][h] = sf;
+        fast = fast && mb <= 0x7F80u && sf < 255u;
+      }
+    if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t c[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint32_t d[8];
+          piece(j, h, d);
+          codes_bf16_scaled<4, false>(d, sfs[j][h], c[h]);
+        }
+        place(j, c, sfs[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // slice j's raw values "depend" on slice j - 1's result (an empty asm), so the
+        // compiler converts one slice at a time instead of hoisting every slice's floats
+        if (j > 0) {
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+            asm volatile("" : "+v"(qr_raw[j][h].x), "+v"(qr_raw[j][h].y), "+v"(qr_raw[j][h].z), "+v"(qr_raw[j][h].w)
+                         : "v"(sraw[0][j > 0 ? j - 1 : 0]));
+        }
+        uint32_t c[2][4], sc[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint32_t d[8];
+          piece(j, h, d);
+          const uint32_t mb = amax_bf16_bits<8, false>(d);
+          const auto mm = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+          const bool blk_fast = RRULE != kRpUe8m0 && (mm[0] > mm[1] ? mm[0] : mm[1]) <= 0x7F80u && sfs[j][h] < 255u;
+          float m = 0.0f;
+          float v[16];
+          if (!blk_fast) {
+            bf16x8_to_f32(qr_raw[j][2 * h], v);
+            bf16x8_to_f32(qr_raw[j][2 * h + 1], v + 8);
+            quiet8(v);
+            quiet8(v + 8);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+          }
+          // (outside the branch, whose condition the two lanes of a block share)
+          const auto ms = __builtin_amdgcn_permlane16_swap(f2u(m), f2u(m), false, false);
+          if (blk_fast) {
+            codes_bf16_scaled<4, false>(d, sfs[j][h], c[h]);
+            sc[h] = sfs[j][h];
+          } else {
+            sc[h] = quant_block_codes<RRULE, false, 16>(v, __builtin_fmaxf(u2f(ms[0]), u2f(ms[1])), c[h]);
+          }
+        }
+        place(j, c, sc);
+      }
     }
   } else if constexpr (FUSED) {
     // the scratch holds the codes in fragment order (stream_produce): slice s's 32 bytes

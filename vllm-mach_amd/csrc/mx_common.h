@@ -58,9 +58,11 @@ __device__ __forceinline__ void bf16_round2_nan_any(float& lo, float& hi) {
 
 // Four binary32 values -> four E4M3 codes (byte i = value i), equal to f32_to_e4m3 on
 // every input: a positive NaN, which the instruction would code 0xFF, is first replaced
-// by 480 (code 0x7F).
-__device__ __forceinline__ float e4m3_pos_nan_to_480(float y) {
-  return (int32_t)f2u(y) > (int32_t)0x7F800000 ? 480.0f : y;
+// by +inf (code 0x7F, as 480 and above): as signed integers positive NaNs are exactly
+// the values above +inf's bits, so one integer min does it.
+__device__ __forceinline__ float e4m3_pos_nan_to_inf(float y) {
+  const int32_t b = (int32_t)f2u(y);
+  return u2f((uint32_t)(b < (int32_t)0x7F800000 ? b : (int32_t)0x7F800000));
 }
 // (exact unless an input is a positive NaN)
 __device__ __forceinline__ uint32_t e4m3x4_raw(float a, float b, float c, float d) {
@@ -68,8 +70,8 @@ __device__ __forceinline__ uint32_t e4m3x4_raw(float a, float b, float c, float 
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
-  return e4m3x4_raw(e4m3_pos_nan_to_480(a), e4m3_pos_nan_to_480(b), e4m3_pos_nan_to_480(c),
-                    e4m3_pos_nan_to_480(d));
+  return e4m3x4_raw(e4m3_pos_nan_to_inf(a), e4m3_pos_nan_to_inf(b), e4m3_pos_nan_to_inf(c),
+                    e4m3_pos_nan_to_inf(d));
 }
 
 // binary32 -> E4M3 ("fn") with torch's cast semantics: RNE onto the E4M3
@@ -233,6 +235,50 @@ __device__ __forceinline__ uint32_t quant_block_codes(const float* v, float amax
     for (int i = 0; i < N / 4; ++i) packed[i] = e4m3x4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
   }
   return s;
+}
+
+// The bf16 magnitude bits of the largest |x| over N raw bf16 pairs.  SKIP_NAN: of the
+// largest non-NaN |x| (0 when all are NaN), equal to the bf16 bits of the quieted-float
+// amax -- per 16-bit half, |x| + 0x7F keeps every non-NaN magnitude (at most +inf's
+// 0x7F80) below 0x8000 and moves every NaN magnitude (0x7F81 .. 0x7FFF) to 0x8000 and
+// above, negative as a signed half, so a signed packed max skips the NaNs (the halves
+// never carry into each other).  Otherwise NaNs count, so a result above 0x7F80 says
+// that a NaN is present.
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
+template <int N, bool SKIP_NAN>
+__device__ __forceinline__ uint32_t amax_bf16_bits(const uint32_t* d) {
+  const uint32_t bias = SKIP_NAN ? 0x007F007Fu : 0u;
+  i16x2_t m = __builtin_bit_cast(i16x2_t, bias);
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(i16x2_t, (d[i] & 0x7FFF7FFFu) + bias));
+  return (uint32_t)((m[0] > m[1] ? m[0] : m[1]) - (int)(bias & 0xFFu));
+}
+
+// 4 N raw bf16 values (2 N pairs) -> N dwords of E4M3 codes divided by 2^(s - 127),
+// s < 255: v_cvt_scalef32_pk_fp8_bf16 divides by the power of two its scale operand's
+// exponent field names and rounds once, which equals f32_to_e4m3(ldexpf(x, 127 - s)) for
+// every bf16 x and s < 255 (checked on the device for all 65536 x 255 pairs) except
+// positive NaNs, which it codes 0xFF.  NAN_FIX turns those into +inf first (code 0x7F),
+// the signed packed min with +inf's bits doing for both halves what e4m3_pos_nan_to_inf
+// does; without it the caller guarantees that no input is a NaN.
+template <int N, bool NAN_FIX>
+__device__ __forceinline__ void codes_bf16_scaled(const uint32_t* d, uint32_t s, uint32_t* packed) {
+  const float scale = u2f(s << 23);
+  const i16x2_t inf2 = __builtin_bit_cast(i16x2_t, 0x7F807F80u);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    i16x2_t lo = __builtin_bit_cast(i16x2_t, d[2 * i]), hi = __builtin_bit_cast(i16x2_t, d[2 * i + 1]);
+    if (NAN_FIX) {
+      lo = __builtin_elementwise_min(lo, inf2);
+      hi = __builtin_elementwise_min(hi, inf2);
+    }
+    // both 16-bit halves of the result are written, so the first conversion's "old"
+    // operand is any register: its own source
+    i16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(lo, __builtin_bit_cast(bf16x2_t, lo), scale, false);
+    c = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(c, __builtin_bit_cast(bf16x2_t, hi), scale, true);
+    packed[i] = __builtin_bit_cast(uint32_t, c);
+  }
 }
 
 // Quantize one 32-element block held by 4 consecutive lanes (8 values each,
