@@ -269,9 +269,7 @@ __device__ __forceinline__ void stream_produce(const GemmParams& p, int lane, in
           swiglu8<RULE>(gt, up, v);
           s = quant8x4<RULE, true>(v, pk);
         } else {
-          bf16x8_to_f32(raw[u][0], v);
-          quiet8(v);
-          s = quant8x4<RULE>(v, pk);
+          s = quant8x4_bf16<RULE>(raw[u][0], pk);
         }
         if (live[u] && (lane & 3) == 0) {
           // block b of the row: super-tile b / 16, slice (b % 16) / 4, lane group b % 4
@@ -471,9 +469,7 @@ void gemm_stream_kernel(GemmParams p) {
         swiglu8<RRULE>(g, up, v);
         sc = quant8x4<RRULE, true>(v, pk);
       } else {
-        bf16x8_to_f32(gu_raw[u][0], v);
-        quiet8(v);
-        sc = quant8x4<RRULE>(v, pk);
+        sc = quant8x4_bf16<RRULE>(gu_raw[u][0], pk);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -758,9 +754,7 @@ __device__ __forceinline__ void produce_store(const GemmParams& p, int c, bool l
   float v[8];
   uint32_t packed[2], sc;
   if constexpr (PRODUCER == 1) {
-    bf16x8_to_f32(in.x, v);
-    quiet8(v);
-    sc = quant8x4<RULE>(v, packed);
+    sc = quant8x4_bf16<RULE>(in.x, packed);
   } else {
     float g[8], u[8];
     bf16x8_to_f32(in.x, g);

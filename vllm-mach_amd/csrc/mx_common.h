@@ -317,6 +317,31 @@ __device__ __forceinline__ void quiet8(float* f) {
   for (int i = 0; i < 8; ++i) f[i] = __builtin_canonicalizef(f[i]);
 }
 
+// quant8x4 of 8 raw bf16 values (one 16-byte load; four lanes per block, lane (tid & 3)
+// owning elements [8 (tid & 3), +8)), equal to bf16x8_to_f32 + quiet8 + quant8x4<RULE>:
+// where the block's scale is a power of two (rules 0 and 1) below E8M0 code 255 and no
+// value of the block is a NaN, the codes come straight from the bf16 pairs
+// (amax_bf16_bits, codes_bf16_scaled); other blocks take the binary32 arithmetic.  The
+// condition is the block's, so the four lanes of a block take the same path.
+template <int RULE>
+__device__ __forceinline__ uint32_t quant8x4_bf16(uint4 raw, uint32_t* packed) {
+  if constexpr (RULE != kRpUe8m0) {
+    const uint32_t d[4] = {raw.x, raw.y, raw.z, raw.w};
+    uint32_t mb = amax_bf16_bits<4, false>(d);
+    mb = __builtin_elementwise_max(mb, (uint32_t)__shfl_xor((int)mb, 1, 4));
+    mb = __builtin_elementwise_max(mb, (uint32_t)__shfl_xor((int)mb, 2, 4));
+    const uint32_t sf = RULE == kFloorCarry175 ? scale_floor_carry175(mb) : pow2_ceil_div448(u2f(mb << 16)) >> 23;
+    if (mb <= 0x7F80u && sf < 255u) {
+      codes_bf16_scaled<2, false>(d, sf, packed);
+      return sf;
+    }
+  }
+  float v[8];
+  bf16x8_to_f32(raw, v);
+  quiet8(v);
+  return quant8x4<RULE>(v, packed);
+}
+
 // Block-FP8 activation quantization of one 128-element group held by 16 consecutive
 // lanes (8 quieted values each; fp8/_quantize_kernel.py:7-18): the group amax by an
 // xor-shuffle max (order-free), floored at 1e-10, scale = amax / 448, codes =

@@ -49,11 +49,8 @@ __global__ __launch_bounds__(256) void quant_mxfp8_kernel(const uint16_t* __rest
   const int sub = bl.sub;
   const bool live = bl.live;
   const int64_t row = bl.row, blk = bl.blk;
-  float v[8];
-  bf16x8_to_f32(*reinterpret_cast<const uint4*>(x + row * ldx + blk * 32 + sub * 8), v);
-  quiet8(v);
   uint32_t packed[2];
-  const uint32_t s = quant8x4<RULE>(v, packed);
+  const uint32_t s = quant8x4_bf16<RULE>(*reinterpret_cast<const uint4*>(x + row * ldx + blk * 32 + sub * 8), packed);
   if (!live) return;
   *reinterpret_cast<uint2*>(codes + row * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
   if (sub == 0) scales[SWIZZLED ? swizzle_offset(row, blk, K) : row * blocks_per_row + blk] = (uint8_t)s;
