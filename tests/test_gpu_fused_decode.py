@@ -117,6 +117,31 @@ def test_quant_one_launch_bit_identical(pkg, oracle_mod, dev, fmt, rule, M, N, K
         _check(y.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("rule", [0, 1, 2])
+def test_quant_rows_inreg_every_value_at_every_scale(pkg, dev, rule):
+    # the in-register quantizer against quantizer + GEMM on every (bf16 value, E8M0
+    # scale) pair: an identity weight makes each output element one activation code times
+    # its scale, so a code that differs shows (outputs below bf16's subnormal range
+    # aside, which both paths flush alike)
+    from test_gpu_quant import _every_value_at_every_scale
+    ops = pkg.ops
+    K = N = 4096
+    x = _every_value_at_every_scale().reshape(-1)
+    x = torch.cat([x, torch.zeros((-x.numel()) % (16 * K), dtype=torch.bfloat16)]).reshape(-1, K)
+    assert ops.quant_rows_inreg(16, K, rule, ops.E4M3)
+    eye = torch.zeros(N, K, dtype=torch.uint8)
+    eye[torch.arange(N), torch.arange(K)] = 0x38  # E4M3 1.0
+    tiled, tiled_s = ops.pack_weight(eye.to(dev), torch.full((N, K // 32), 127, dtype=torch.uint8, device=dev),
+                                     ops.E4M3)
+    xd = x.to(dev)
+    for r0 in range(0, xd.shape[0], 16):
+        rows = xd[r0:r0 + 16]
+        a, sa = torch.ops.mach_amd.quantize_mxfp8(rows, rule)
+        y_ref = torch.ops.mach_amd.mx_gemm(a, sa, tiled, tiled_s, N, K, ops.E4M3, None)
+        y = torch.ops.mach_amd.quant_mx_gemm(rows, tiled, tiled_s, N, ops.E4M3, rule, None)
+        assert _eq(y, y_ref), r0
+
+
 def _block_weights(N, K, seed):
     g = torch.Generator().manual_seed(seed)
     w = torch.randn(N, K, generator=g) * 0.02

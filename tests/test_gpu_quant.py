@@ -135,6 +135,38 @@ def test_quantize_mxfp8_every_bf16(pkg, oracle_mod, dev, rule, seed):
         assert np.array_equal(_u8(got), want)
 
 
+def _every_value_at_every_scale():
+    """Blocks that put every bf16 value x with |x| <= A beside a block maximum A, for one
+    A per exponent field 0..254 (mantissa 0x5F: the largest before rule 0's carry; the
+    sign alternating by exponent): every (value, E8M0 scale) pair the blocks' amax
+    reaches, both signs, subnormals and zeros, including the tiny maxima whose rule-0
+    scale wraps to 255.  [8411, 1024] bf16."""
+    blocks = []
+    for e in range(255):
+        a = (e << 7) | 0x5F
+        mags = np.arange(a + 1, dtype=np.uint32)
+        xs = np.concatenate([mags, mags | 0x8000]).astype(np.uint16)
+        xs = np.concatenate([xs, np.zeros((-len(xs)) % 31, np.uint16)]).reshape(-1, 31)
+        lead = np.full((len(xs), 1), a | ((e & 1) << 15), np.uint16)
+        blocks.append(np.concatenate([lead, xs], axis=1))
+    b = np.concatenate(blocks)
+    b = np.concatenate([b, np.zeros(((-len(b)) % 32, 32), np.uint16)])
+    return torch.from_numpy(b.reshape(-1, 1024).view(np.int16).copy()).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rule", [0, 1, 2])
+def test_quantize_mxfp8_every_value_at_every_scale(pkg, oracle_mod, dev, rule):
+    # the quantizer codes power-of-two-scaled blocks straight from the bf16 pairs (one
+    # scaled conversion per pair) and the others with binary32 arithmetic: both against
+    # the oracle on every (value, scale) pair
+    x = _every_value_at_every_scale()
+    codes, scales = torch.ops.mach_amd.quantize_mxfp8(x.to(dev), rule)
+    rc, rs = oracle_mod.quant_mxfp8(x, rule)
+    assert np.array_equal(_u8(scales), rs)
+    assert np.array_equal(_u8(codes), rc)
+    assert len(np.unique(rs)) >= (200 if rule == 0 else 100)
+
+
 @pytest.mark.parametrize("rule", [0, 1, 2])
 @pytest.mark.parametrize("seed", [None, 12])
 def test_swiglu_mxfp8_every_bf16(pkg, oracle_mod, dev, rule, seed):
