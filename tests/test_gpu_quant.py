@@ -180,6 +180,30 @@ def test_swiglu_mxfp8_every_bf16(pkg, oracle_mod, dev, rule, seed):
         assert np.array_equal(_u8(codes), rc)
 
 
+@pytest.mark.parametrize("rule", [0, 1])
+def test_swiglu_mxfp8_table_every_gate(pkg, oracle_mod, dev, rule):
+    """Launches large enough for the producer's SiLU table (2^-24 <= |g| < 256, both signs;
+    512 items per CU and up), with only such gates: every one of them in every row, up values
+    random, with outliers, infinities and NaNs, so the table path and its quantization
+    fallbacks both run; then the same rows with one out-of-range gate per row, which sends
+    those waves to the arithmetic."""
+    lo, span = 103 << 7, 32 << 7
+    gates = np.concatenate([np.arange(lo, lo + span), np.arange(lo, lo + span) | 0x8000]).astype(np.uint16)
+    rows = 128
+    g = np.stack([np.roll(gates, 97 * r) for r in range(rows)])
+    gate = torch.from_numpy(g.view(np.int16).copy()).view(torch.bfloat16)
+    up = _inputs(rows, gates.size, 1.0, 77, outliers=True)
+    up[1, 5] = float("inf")
+    up[2, 9] = float("nan")
+    up[3, :32] = 0.0
+    for gu in (torch.cat([gate, up], dim=1), torch.cat([gate.clone().index_fill_(1, torch.tensor([300]), 0.0), up], dim=1)):
+        assert gu.shape[0] * gu.shape[1] // 2 // 8 >= 512 * 256
+        codes, scales = torch.ops.mach_amd.swiglu_mxfp8(gu.to(dev), rule, False)
+        rc, rs = oracle_mod.swiglu_mxfp8(gu, rule)
+        assert np.array_equal(_u8(scales), rs)
+        assert np.array_equal(_u8(codes), rc)
+
+
 @pytest.mark.parametrize("seed", [None, 13])
 def test_block_fp8_producers_every_bf16(pkg, oracle_mod, dev, seed):
     x = _every_bf16(8, 8192, seed)

@@ -63,7 +63,7 @@ def parse_resource_remarks(text: str) -> dict[str, dict[str, int]]:
 
 def _compile(src: Path) -> tuple[Path, dict[str, dict[str, int]]]:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-Rpass-analysis=kernel-resource-usage",
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), f"-I{BUILD}", "-Rpass-analysis=kernel-resource-usage",
            "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -99,8 +99,29 @@ def build_torch_ops(verbose: bool = False) -> Path:
     return TORCH_OPS_OUT
 
 
+SILU_GEN = CSRC / "silu_table_gen.cpp"
+
+
+def generate_silu_table() -> Path:
+    """Compile and run the host generator of the SwiGLU activation table: it evaluates
+    the device's binary32 SiLU (csrc/silu_math.h) for every bf16 gate of the table's
+    range and writes ``_build/silu_table.h``, which the device code includes."""
+    exe = BUILD / "silu_table_gen"
+    out = BUILD / "silu_table.h"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-ffp-contract=off", "-Wall", f"-I{CSRC}",
+           str(SILU_GEN), "-o", str(exe)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"silu_table_gen build failed:\n{r.stdout}\n{r.stderr}")
+    r = subprocess.run([str(exe), str(out)], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"silu_table_gen failed:\n{r.stdout}\n{r.stderr}")
+    return out
+
+
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
+    generate_silu_table()
     sources = sorted(CSRC.glob("*.hip"))
     jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:

@@ -10,6 +10,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "silu_math.h"
+#include "silu_table.h"  // generated at build time (silu_table_gen.cpp)
+
 namespace mxl {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -145,28 +148,6 @@ __device__ __forceinline__ float e8m0_rp_inverse(uint32_t s) {
   return (s == 0u || s == 254u) ? 0.0f : u2f((254u - s) << 23);
 }
 
-// exp() with a fixed binary32 operation sequence: Cody-Waite reduction by ln2
-// and the Cephes expf minimax polynomial (S. L. Moshier), explicit FMAs.
-__device__ __forceinline__ float mx_exp(float x) {
-  // branch-free: the range limits select the result; the exponent is clamped before
-  // the integer conversion so that it is defined for every x (NaN included)
-  const float n = __builtin_rintf(x * 1.44269504088896341f);
-  float r = __builtin_fmaf(n, -0.693359375f, x);
-  r = __builtin_fmaf(n, 2.12194440e-4f, r);
-  float p = 1.9875691500e-4f;
-  p = __builtin_fmaf(p, r, 1.3981999507e-3f);
-  p = __builtin_fmaf(p, r, 8.3334519073e-3f);
-  p = __builtin_fmaf(p, r, 4.1665795894e-2f);
-  p = __builtin_fmaf(p, r, 1.6666665459e-1f);
-  p = __builtin_fmaf(p, r, 5.0000001201e-1f);
-  const float r2 = r * r;
-  const float y = __builtin_fmaf(p, r2, r) + 1.0f;
-  const float nc = __builtin_fminf(__builtin_fmaxf(n, -300.0f), 300.0f);
-  float e = __builtin_ldexpf(y, (int)nc);
-  e = x < -87.0f ? 0.0f : e;
-  return x > 88.0f ? __builtin_inff() : e;
-}
-
 // SwiGLU of eight (gate, up) pairs: act = bf16(g / (1 + exp(-g))) and v = bf16(act * u)
 // (mxfp8_mlp.py:96-97), or for the rp_ue8m0 rule v = bf16((g / (1 + exp(-g))) * u)
 // (swiglu_quant.py:56-57).  A NaN act makes a NaN v, and quant8x4<RULE, true> codes every
@@ -175,7 +156,7 @@ template <int RULE, int N = 8>
 __device__ __forceinline__ void swiglu8(const float* g, const float* u, float* v) {
 #pragma unroll
   for (int i = 0; i < N; i += 2) {
-    float a0 = g[i] / (1.0f + mx_exp(-g[i])), a1 = g[i + 1] / (1.0f + mx_exp(-g[i + 1]));
+    float a0 = mx_silu(g[i]), a1 = mx_silu(g[i + 1]);
     if (RULE != kRpUe8m0) bf16_round2_nan_any(a0, a1);
     v[i] = a0 * u[i];
     v[i + 1] = a1 * u[i + 1];
@@ -340,6 +321,58 @@ __device__ __forceinline__ uint32_t quant8x4_bf16(uint4 raw, uint32_t* packed) {
   bf16x8_to_f32(raw, v);
   quiet8(v);
   return quant8x4<RULE>(v, packed);
+}
+
+// SwiGLU activations from the table: per 16-bit half of a gate dword, (g & 0x7FFF) -
+// (kSiluELo << 7) is the table offset when below kSiluSpan (gates under the range wrap
+// around to large offsets), and bit 15 moved to bit 12 adds kSiluSpan (4096) for a
+// negative gate.  silu_offsets returns the pair of offsets; the lane's gates all lie in
+// the table when the largest offset of its dwords is below kSiluSpan.
+static_assert(kSiluSpan == 4096, "the sign bit selects the negative half by one shift");
+__device__ __forceinline__ uint32_t silu_offsets(uint32_t d) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 lo = __builtin_bit_cast(u16x2, (kSiluELo << 7) | (kSiluELo << 23));
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, d & 0x7FFF7FFFu) - lo);
+}
+__device__ __forceinline__ bool silu_in_table(uint4 graw) {
+  const uint32_t o[4] = {silu_offsets(graw.x), silu_offsets(graw.y), silu_offsets(graw.z), silu_offsets(graw.w)};
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = __builtin_elementwise_max(m, (o[i] & 0xFFFFu)), m = __builtin_elementwise_max(m, o[i] >> 16);
+  return m < kSiluSpan;
+}
+
+// bf16x8_to_f32 + swiglu8<RULE> + quant8x4<RULE, true> of a lane's 8 (gate, up) pairs for
+// rules 0 and 1, with each activation bf16(mx_silu(g)) read from the table staged in LDS
+// (tab) -- the caller has checked silu_in_table for the four lanes of the block -- and
+// the codes of power-of-two-scaled NaN-free blocks straight from the bf16 products
+// (amax_bf16_bits, codes_bf16_scaled); other blocks take the binary32 arithmetic.
+template <int RULE>
+__device__ __forceinline__ uint32_t swiglu_quant8_table(uint4 graw, uint4 uraw, const uint16_t* tab, uint32_t* packed) {
+  static_assert(RULE == kFloorCarry175 || RULE == kCeilDiv448, "the table holds the bf16-rounded activation");
+  const uint32_t gd[4] = {graw.x, graw.y, graw.z, graw.w}, ud[4] = {uraw.x, uraw.y, uraw.z, uraw.w};
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t o = silu_offsets(gd[i]) + ((gd[i] >> 3) & 0x10001000u);
+    const float a0 = u2f((uint32_t)tab[o & 0xFFFFu] << 16), a1 = u2f((uint32_t)tab[o >> 16] << 16);
+    w[i] = cvt_pk_bf16(a0 * u2f(ud[i] << 16), a1 * u2f(ud[i] & 0xFFFF0000u));
+  }
+  uint32_t mb = amax_bf16_bits<4, false>(w);
+  mb = __builtin_elementwise_max(mb, (uint32_t)__shfl_xor((int)mb, 1, 4));
+  mb = __builtin_elementwise_max(mb, (uint32_t)__shfl_xor((int)mb, 2, 4));
+  const uint32_t sf = RULE == kFloorCarry175 ? scale_floor_carry175(mb) : pow2_ceil_div448(u2f(mb << 16)) >> 23;
+  if (mb <= 0x7F80u && sf < 255u) {
+    codes_bf16_scaled<2, false>(w, sf, packed);
+    return sf;
+  }
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = u2f(w[i] << 16);
+    v[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
+  }
+  return quant8x4<RULE, true>(v, packed);
 }
 
 // Block-FP8 activation quantization of one 128-element group held by 16 consecutive

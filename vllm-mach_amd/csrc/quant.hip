@@ -10,6 +10,8 @@
 // from one 16-byte load; the amax is an xor-shuffle max inside the group.  Loads and
 // stores are 16-byte vectors; consecutive threads walk consecutive blocks of
 // a row so every wavefront access is one contiguous span.
+#include <algorithm>
+
 #include "mx_common.h"
 
 namespace mxl {
@@ -139,30 +141,66 @@ __device__ __forceinline__ int64_t swizzle_offset(int64_t r, int64_t g, int64_t 
   return (((r / 128 * T + g / 4) * 32 + r % 32) * 4 + (r % 128) / 32) * 4 + g % 4;
 }
 
-template <int RULE, bool SWIZZLED>
-__global__ __launch_bounds__(256) void swiglu_mxfp8_kernel(const uint16_t* __restrict__ gate_up,
-                                                           uint8_t* __restrict__ codes,
-                                                           uint8_t* __restrict__ scales, int64_t M,
-                                                           int64_t K) {
-  const int64_t blocks_per_row = K / 32;
-  const BlockLane<4> bl((uint32_t)blocks_per_row, (uint32_t)(M * blocks_per_row));
-  const int sub = bl.sub;
-  const bool live = bl.live;
-  const int64_t row = bl.row, blk = bl.blk;
-  const int64_t off = row * 2 * K + blk * 32 + sub * 8;
-  float g[8], u[8], v[8];
-  bf16x8_to_f32(*reinterpret_cast<const uint4*>(gate_up + off), g);
-  bf16x8_to_f32(*reinterpret_cast<const uint4*>(gate_up + off + K), u);
-  swiglu8<RULE>(g, u, v);
-  uint32_t packed[2];
-  const uint32_t s = quant8x4<RULE, true>(v, packed);
-  if (!live) return;
-  *reinterpret_cast<uint2*>(codes + row * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
-  if (sub == 0) {
-    if (SWIZZLED)
-      scales[swizzle_offset(row, blk, K)] = (uint8_t)s;
-    else
-      scales[row * blocks_per_row + blk] = (uint8_t)s;
+// The workgroup's threads stride over the items (four lanes per 32-block, 8 values
+// each).  TABLE (rules 0 and 1, 1024 threads): the workgroup first stages the SiLU table
+// (16 KiB) in LDS, and a wave whose gates all lie in it reads the activations from it
+// instead of evaluating exp and the division.  Without it (small launches, where the
+// staging costs more than it saves, and rule 2) 256 threads, one item each.
+constexpr int kSwigluThreads = 1024;
+// the table pays from about half a 1024-thread workgroup's items per CU
+constexpr int64_t kSwigluTableItemsPerCu = 512;
+int cu_count();  // compute units of the current device (gemm_stream.hip)
+template <int RULE, bool SWIZZLED, bool TABLE>
+__global__ __launch_bounds__(TABLE ? kSwigluThreads : 256) void swiglu_mxfp8_kernel(const uint16_t* __restrict__ gate_up,
+                                                                                    uint8_t* __restrict__ codes,
+                                                                                    uint8_t* __restrict__ scales,
+                                                                                    int64_t M, int64_t K) {
+  static_assert(!TABLE || RULE != kRpUe8m0, "the table holds the bf16-rounded activation of rules 0 and 1");
+  constexpr bool TAB = TABLE;
+  __shared__ __attribute__((aligned(16))) uint16_t tab[TAB ? kSiluEntries : 8];
+  if constexpr (TAB) {
+    for (uint32_t i = threadIdx.x; i < kSiluEntries / 8; i += blockDim.x)
+      reinterpret_cast<uint4*>(tab)[i] = reinterpret_cast<const uint4*>(kSiluAct)[i];
+    __syncthreads();
+  }
+  // lanes are indexed in 32 bits (the host bounds the item count)
+  const uint32_t blocks_per_row = (uint32_t)(K / 32), items = (uint32_t)M * blocks_per_row * 4;
+  // the same trip count for every thread of the workgroup; items past the end redo the
+  // last block without storing, so the four lanes of a block stay together
+  for (uint32_t base = blockIdx.x * blockDim.x; base < items; base += gridDim.x * blockDim.x) {
+    const uint32_t t = base + threadIdx.x;
+    const bool live = t < items;
+    const uint32_t it = live ? t : items - 4 + (t & 3);
+    const int sub = (int)(it & 3);
+    const uint32_t id = it >> 2;
+    const int64_t row = id / blocks_per_row, blk = id - (uint32_t)row * blocks_per_row;
+    const int64_t off = row * 2 * K + blk * 32 + sub * 8;
+    const uint4 graw = *reinterpret_cast<const uint4*>(gate_up + off);
+    const uint4 uraw = *reinterpret_cast<const uint4*>(gate_up + off + K);
+    uint32_t packed[2], s = 0;
+    bool done = false;
+    if constexpr (TAB) {
+      if (__builtin_amdgcn_ballot_w64(!silu_in_table(graw)) == 0) {
+        s = swiglu_quant8_table<RULE>(graw, uraw, tab, packed);
+        done = true;
+      }
+    }
+    if (!done) {
+      float g[8], u[8], v[8];
+      bf16x8_to_f32(graw, g);
+      bf16x8_to_f32(uraw, u);
+      swiglu8<RULE>(g, u, v);
+      s = quant8x4<RULE, true>(v, packed);
+    }
+    if (live) {
+      *reinterpret_cast<uint2*>(codes + row * K + blk * 32 + sub * 8) = make_uint2(packed[0], packed[1]);
+      if (sub == 0) {
+        if (SWIZZLED)
+          scales[swizzle_offset(row, blk, K)] = (uint8_t)s;
+        else
+          scales[row * blocks_per_row + blk] = (uint8_t)s;
+      }
+    }
   }
 }
 
@@ -460,6 +498,23 @@ extern "C" int mxl_swizzle_scales(const void* logical, int64_t R, int64_t K, voi
   return MXL_OK;
 }
 
+namespace {
+template <bool SWIZZLED>
+void launch_swiglu(int rule, bool table, dim3 grid, int threads, hipStream_t s, const uint16_t* in, uint8_t* c,
+                   uint8_t* sc, int64_t M, int64_t K) {
+  if (table && rule == kFloorCarry175)
+    swiglu_mxfp8_kernel<kFloorCarry175, SWIZZLED, true><<<grid, threads, 0, s>>>(in, c, sc, M, K);
+  else if (table)
+    swiglu_mxfp8_kernel<kCeilDiv448, SWIZZLED, true><<<grid, threads, 0, s>>>(in, c, sc, M, K);
+  else if (rule == kFloorCarry175)
+    swiglu_mxfp8_kernel<kFloorCarry175, SWIZZLED, false><<<grid, threads, 0, s>>>(in, c, sc, M, K);
+  else if (rule == kCeilDiv448)
+    swiglu_mxfp8_kernel<kCeilDiv448, SWIZZLED, false><<<grid, threads, 0, s>>>(in, c, sc, M, K);
+  else
+    swiglu_mxfp8_kernel<kRpUe8m0, SWIZZLED, false><<<grid, threads, 0, s>>>(in, c, sc, M, K);
+}
+}  // namespace
+
 extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int rule, int swizzled,
                                 void* codes, void* scales, void* stream) {
   MXL_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0, "mxl_swiglu_mxfp8: need K > 0, K %% 32 == 0 (K=%lld)", (long long)K);
@@ -468,7 +523,12 @@ extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int r
   MXL_CHECK_ARG(lanes_fit(M * (K / 32) * 4), "mxl_swiglu_mxfp8: too large (M=%lld, K=%lld)", (long long)M, (long long)K);
   if (M == 0) return MXL_OK;
   const int64_t n = M * (K / 32) * 4;
-  dim3 grid((unsigned)((n + 255) / 256));
+  // with the table at most two workgroups per CU (each stages the 16 KiB table once),
+  // striding over the items
+  const bool table = rule != kRpUe8m0 && n >= kSwigluTableItemsPerCu * cu_count();
+  const int threads = table ? kSwigluThreads : 256;
+  dim3 grid((unsigned)(table ? std::min<int64_t>((n + threads - 1) / threads, 2 * (int64_t)cu_count())
+                             : (n + threads - 1) / threads));
   hipStream_t s = (hipStream_t)stream;
   const uint16_t* in = (const uint16_t*)gate_up;
   uint8_t* c = (uint8_t*)codes;
@@ -478,13 +538,9 @@ extern "C" int mxl_swiglu_mxfp8(const void* gate_up, int64_t M, int64_t K, int r
       const int64_t total = mxl_swizzled_scale_bytes(M, K);
       swizzle_pad_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, s>>>(sc, M, K, total);
     }
-    if (rule == kFloorCarry175) swiglu_mxfp8_kernel<kFloorCarry175, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
-    else if (rule == kCeilDiv448) swiglu_mxfp8_kernel<kCeilDiv448, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
-    else swiglu_mxfp8_kernel<kRpUe8m0, true><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+    launch_swiglu<true>(rule, table, grid, threads, s, in, c, sc, M, K);
   } else {
-    if (rule == kFloorCarry175) swiglu_mxfp8_kernel<kFloorCarry175, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
-    else if (rule == kCeilDiv448) swiglu_mxfp8_kernel<kCeilDiv448, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
-    else swiglu_mxfp8_kernel<kRpUe8m0, false><<<grid, 256, 0, s>>>(in, c, sc, M, K);
+    launch_swiglu<false>(rule, table, grid, threads, s, in, c, sc, M, K);
   }
   MXL_CHECK_LAUNCH("mxl_swiglu_mxfp8");
   return MXL_OK;
