@@ -279,7 +279,7 @@ int mxl_swiglu_mx_gemm_ex(const void* gate_up, int64_t M, int64_t K, int rule, c
 /* MXFP8 quantization -> MX GEMM for M <= 16 bf16 activation rows x [M, K] in one launch,
  * bit-identical to mxl_quantize_mxfp8 (rule 0, 1 or 2) followed by mxl_mx_gemm.  Two
  * schemes: the GEMM's own wavefronts quantize (M = 1: each wavefront its super-tiles' row
- * values; 2 <= M <= 16 with K <= 4096: each MFMA fragment lane the two 16-value pieces of
+ * values; 2 <= M <= 16 with K <= 6144: each MFMA fragment lane the two 16-value pieces of
  * its row it multiplies, the block amax completed with the lane holding the blocks' other
  * halves; no scratch and no synchronisation beyond the workgroup), or the producer waves,
  * scratch slots, handoff and shapes of mxl_swiglu_mx_gemm.  Replaces

@@ -104,8 +104,8 @@ def test_quant_one_launch_bit_identical(pkg, oracle_mod, dev, fmt, rule, M, N, K
             assert kernel == 0 or inreg
             assert _eq(y_k, y_ref), kernel
     # the layer path takes one launch where the GEMM's wavefronts quantize (one row, or up
-    # to 16 rows at K <= 4096), else the two launches (faster than the handoff)
-    assert inreg == (M == 1 or K <= 4096)
+    # to 16 rows at K <= 6144), else the two launches (faster than the handoff)
+    assert inreg == (M == 1 or K <= 6144)
     before = dict(ops._COUNTS)
     y_layer = ops.mx_gemm_from_float(x.to(dev), tiled, tiled_s, N, fmt, rule)
     assert ops._COUNTS.get("quant_mx_gemm", 0) == before.get("quant_mx_gemm", 0) + int(inreg)
@@ -118,14 +118,15 @@ def test_quant_one_launch_bit_identical(pkg, oracle_mod, dev, fmt, rule, M, N, K
 
 
 @pytest.mark.parametrize("rule", [0, 1, 2])
-def test_quant_rows_inreg_every_value_at_every_scale(pkg, dev, rule):
+@pytest.mark.parametrize("K", [4096, 6144])  # the wave-wide and the slice-by-slice forms
+def test_quant_rows_inreg_every_value_at_every_scale(pkg, dev, rule, K):
     # the in-register quantizer against quantizer + GEMM on every (bf16 value, E8M0
     # scale) pair: an identity weight makes each output element one activation code times
     # its scale, so a code that differs shows (outputs below bf16's subnormal range
     # aside, which both paths flush alike)
     from test_gpu_quant import _every_value_at_every_scale
     ops = pkg.ops
-    K = N = 4096
+    N = K
     x = _every_value_at_every_scale().reshape(-1)
     x = torch.cat([x, torch.zeros((-x.numel()) % (16 * K), dtype=torch.bfloat16)]).reshape(-1, K)
     assert ops.quant_rows_inreg(16, K, rule, ops.E4M3)

@@ -53,7 +53,7 @@ def test_swiglu_mxfp8_bit_exact(pkg, oracle_mod, dev, M, K):
         assert np.array_equal(_u8(scales), rs), magnitude
 
 
-@pytest.mark.parametrize("M,K", [(1, 9216), (130, 6144), (200, 128)])
+@pytest.mark.parametrize("M,K", [(1, 9216), (130, 6144), (200, 128), (600, 6144)])  # 600: the table path
 def test_swiglu_mxfp8_swizzled_layout(pkg, oracle_mod, dev, M, K):
     gu = _inputs(M, 2 * K, 1.0, 5, outliers=False)
     codes, scales = torch.ops.mach_amd.swiglu_mxfp8(gu.to(dev), 1, True)

@@ -909,7 +909,7 @@ static int quant_row_common(const void* x, int64_t M, int64_t K, int rule, const
   const bool qrows = stream_quant_rows_eligible(M, K, rule);
   // The producer inside the GEMM's own wavefronts (options.kernel 3, automatic where it
   // runs): for one row every wavefront quantizes its super-tiles' row values; for up to 16
-  // rows (K <= 4096) every fragment lane its own pieces, once per workgroup.  Both measured
+  // rows (K <= 6144) every fragment lane its own pieces, once per workgroup.  Both measured
   // faster than the producer waves' grid-wide handoff (options.kernel 0), whose
   // synchronisation costs more than the launch it saves.
   const bool inreg = M == 1 ? rowwise : qrows;
@@ -917,7 +917,7 @@ static int quant_row_common(const void* x, int64_t M, int64_t K, int rule, const
   if (use_inreg ? !inreg : (!handoff || (o.kernel != kAuto && o.kernel != kStream))) {
     set_error("mxl_quant_mx_gemm: unsupported (M <= 16, K %% 128 == 0, K <= 12288 except 7680 < K <= 8192 and "
               "K > 11264 for M > 1, rule 0, 1 or 2; options.kernel -1, 0 or 3 (3: M = 1, or M <= 16 with "
-              "K <= 4096); M=%lld K=%lld rule=%d kernel=%d)", (long long)M, (long long)K, rule, o.kernel);
+              "K <= 6144); M=%lld K=%lld rule=%d kernel=%d)", (long long)M, (long long)K, rule, o.kernel);
     return MXL_EUNSUPPORTED;
   }
   if (M == 0) return MXL_OK;

@@ -41,6 +41,9 @@ constexpr int kStreamMaxWaves = 16;
 // per wave, two waves per SIMD), so the raw rows' registers fit beside the weights
 // (K <= 4096; at ten waves the 168-register budget spilled)
 constexpr int kStreamQuantRowsMaxKT = 8;
+// the slice-by-slice form of it (ROWP = 12 + rule): fewer registers (156), so up to
+// twelve waves (K <= 6144, three per SIMD)
+constexpr int kStreamQuantRowsSliceMaxKT = 12;
 constexpr int64_t kStreamMaxK = 12288;  // two super-tiles per wave, at most twelve waves
 // block-FP8 keeps four fp32 activation scales per slice in registers: at most eight
 // waves (two per SIMD, 256 registers each), one super-tile each up to K = 4096, two up to 8192
@@ -325,7 +328,7 @@ __device__ __forceinline__ void stream_produce(const GemmParams& p, int lane, in
 // then read the codes (device-coherent loads, sc1) as the two-launch path's GEMM does,
 // with the same MFMA chain and sums.
 template <int FMT, int RUN, bool DB, bool BLOCK, int ROWP = -1, int FPROD = -1>
-__global__ __launch_bounds__(BLOCK ? 512 : (ROWP >= 8 ? 64 * kStreamQuantRowsMaxKT : (RUN == 1 ? 1024 : 768)))
+__global__ __launch_bounds__(BLOCK ? 512 : (ROWP >= 12 ? 64 * kStreamQuantRowsSliceMaxKT : ROWP >= 8 ? 64 * kStreamQuantRowsMaxKT : (RUN == 1 ? 1024 : 768)))
 void gemm_stream_kernel(GemmParams p) {
   static_assert(!BLOCK || FMT == kE4M3, "block-FP8 weights are E4M3");
   static_assert(ROWP < 0 || !BLOCK, "the fused producer row feeds MX GEMMs");
@@ -333,7 +336,7 @@ void gemm_stream_kernel(GemmParams p) {
   static_assert(FPROD < 0 || (FPROD == 8) == BLOCK, "block-FP8 GEMMs take the block-FP8 quantizer");
   static_assert(ROWP < 8 || RUN == 1, "the in-register quantizer takes one super-tile per wave");
   constexpr bool ROW = ROWP >= 0 && ROWP < 8, SWI = ROWP >= 0 && ROWP < 4;
-  constexpr bool QROWS = ROWP >= 8;
+  constexpr bool QROWS = ROWP >= 8, QSLICE = ROWP >= 12;
   constexpr bool FUSED = FPROD >= 0;
   constexpr int RRULE = ROWP & 3;
   __shared__ float red[2][kStreamMaxWaves][4][64];
@@ -506,46 +509,12 @@ void gemm_stream_kernel(GemmParams p) {
       const auto xy = __builtin_amdgcn_permlane32_swap(sc[0], sc[1], false, false);
       sraw[0][j] = ((q & 1) ? xy[1] : xy[0]) << (8 * q);
     };
-    // Every block amax as bf16 magnitude bits, NaNs included (above 0x7F80 when one is
-    // present); rows {0, 1} and {2, 3} side by side, so the max is the xor-16 max.  With
-    // power-of-two scales, no NaN in the wave's blocks and no E8M0 code 255 (rule 0 wraps
-    // there for amax below 2^-119, rule 1 at an infinite amax) the scaled conversion codes
-    // straight from bf16, one branch for the wave; otherwise each block whose scale or
-    // values need it takes the standalone quantizer's binary32 arithmetic.
-    uint32_t sfs[4][2];
-    bool fast = RRULE != kRpUe8m0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        uint32_t d[8];
-        piece(j, h, d);
-        uint32_t mb = amax_bf16_bits<8, false>(d);
-        const auto mm = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
-        mb = mm[0] > mm[1] ? mm[0] : mm[1];
-        uint32_t sf = 255u;
-        if constexpr (RRULE == kFloorCarry175) sf = scale_floor_carry175(mb);
-        if constexpr (RRULE == kCeilDiv448) sf = pow2_ceil_div448(u2f(mb << 16)) >> 23;
-        sfs[j][h] = sf;
-        fast = fast && mb <= 0x7F80u && sf < 255u;
-      }
-    if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+    if constexpr (QSLICE) {
+      // Slice by slice (an empty asm chains each slice's raw values to the previous
+      // slice's scale, so the compiler does not hoist every slice's work: 156 registers),
+      // one wave-uniform branch per slice; otherwise as below.
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint32_t c[2][4];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          uint32_t d[8];
-          piece(j, h, d);
-          codes_bf16_scaled<4, false>(d, sfs[j][h], c[h]);
-        }
-        place(j, c, sfs[j]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // slice j's raw values "depend" on slice j - 1's result (an empty asm), so the
-        // compiler converts one slice at a time instead of hoisting every slice's floats
         if (j > 0) {
 #pragma unroll
           for (int h = 0; h < 4; ++h)
@@ -553,33 +522,128 @@ void gemm_stream_kernel(GemmParams p) {
                          : "v"(sraw[0][j > 0 ? j - 1 : 0]));
         }
         uint32_t c[2][4], sc[2];
+        bool fast[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           uint32_t d[8];
           piece(j, h, d);
-          const uint32_t mb = amax_bf16_bits<8, false>(d);
+          uint32_t mb = amax_bf16_bits<8, false>(d);
           const auto mm = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
-          const bool blk_fast = RRULE != kRpUe8m0 && (mm[0] > mm[1] ? mm[0] : mm[1]) <= 0x7F80u && sfs[j][h] < 255u;
-          float m = 0.0f;
-          float v[16];
-          if (!blk_fast) {
-            bf16x8_to_f32(qr_raw[j][2 * h], v);
-            bf16x8_to_f32(qr_raw[j][2 * h + 1], v + 8);
-            quiet8(v);
-            quiet8(v + 8);
+          mb = mm[0] > mm[1] ? mm[0] : mm[1];
+          sc[h] = 255u;
+          if constexpr (RRULE == kFloorCarry175) sc[h] = scale_floor_carry175(mb);
+          if constexpr (RRULE == kCeilDiv448) sc[h] = pow2_ceil_div448(u2f(mb << 16)) >> 23;
+          fast[h] = RRULE != kRpUe8m0 && mb <= 0x7F80u && sc[h] < 255u;
+        }
+        if (__builtin_amdgcn_ballot_w64(!(fast[0] && fast[1])) == 0) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+          for (int h = 0; h < 2; ++h) {
+            uint32_t d[8];
+            piece(j, h, d);
+            codes_bf16_scaled<4, false>(d, sc[h], c[h]);
           }
-          // (outside the branch, whose condition the two lanes of a block share)
-          const auto ms = __builtin_amdgcn_permlane16_swap(f2u(m), f2u(m), false, false);
-          if (blk_fast) {
-            codes_bf16_scaled<4, false>(d, sfs[j][h], c[h]);
-            sc[h] = sfs[j][h];
-          } else {
-            sc[h] = quant_block_codes<RRULE, false, 16>(v, __builtin_fmaxf(u2f(ms[0]), u2f(ms[1])), c[h]);
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            float m = 0.0f;
+            float v[16];
+            if (!fast[h]) {
+              bf16x8_to_f32(qr_raw[j][2 * h], v);
+              bf16x8_to_f32(qr_raw[j][2 * h + 1], v + 8);
+              quiet8(v);
+              quiet8(v + 8);
+#pragma unroll
+              for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+            }
+            // (outside the branch, whose condition the two lanes of a block share)
+            const auto ms = __builtin_amdgcn_permlane16_swap(f2u(m), f2u(m), false, false);
+            if (fast[h]) {
+              uint32_t d[8];
+              piece(j, h, d);
+              codes_bf16_scaled<4, false>(d, sc[h], c[h]);
+            } else {
+              sc[h] = quant_block_codes<RRULE, false, 16>(v, __builtin_fmaxf(u2f(ms[0]), u2f(ms[1])), c[h]);
+            }
           }
         }
         place(j, c, sc);
+      }
+    } else {
+      // Every block amax as bf16 magnitude bits, NaNs included (above 0x7F80 when one is
+      // present); rows {0, 1} and {2, 3} side by side, so the max is the xor-16 max.  With
+      // power-of-two scales, no NaN in the wave's blocks and no E8M0 code 255 (rule 0 wraps
+      // there for amax below 2^-119, rule 1 at an infinite amax) the scaled conversion codes
+      // straight from bf16, one branch for the wave; otherwise each block whose scale or
+      // values need it takes the standalone quantizer's binary32 arithmetic.
+      uint32_t sfs[4][2];
+      bool fast = RRULE != kRpUe8m0;
+  #pragma unroll
+      for (int j = 0; j < 4; ++j)
+  #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint32_t d[8];
+          piece(j, h, d);
+          uint32_t mb = amax_bf16_bits<8, false>(d);
+          const auto mm = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+          mb = mm[0] > mm[1] ? mm[0] : mm[1];
+          uint32_t sf = 255u;
+          if constexpr (RRULE == kFloorCarry175) sf = scale_floor_carry175(mb);
+          if constexpr (RRULE == kCeilDiv448) sf = pow2_ceil_div448(u2f(mb << 16)) >> 23;
+          sfs[j][h] = sf;
+          fast = fast && mb <= 0x7F80u && sf < 255u;
+        }
+      if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint32_t c[2][4];
+  #pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            uint32_t d[8];
+            piece(j, h, d);
+            codes_bf16_scaled<4, false>(d, sfs[j][h], c[h]);
+          }
+          place(j, c, sfs[j]);
+        }
+      } else {
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // slice j's raw values "depend" on slice j - 1's result (an empty asm), so the
+          // compiler converts one slice at a time instead of hoisting every slice's floats
+          if (j > 0) {
+  #pragma unroll
+            for (int h = 0; h < 4; ++h)
+              asm volatile("" : "+v"(qr_raw[j][h].x), "+v"(qr_raw[j][h].y), "+v"(qr_raw[j][h].z), "+v"(qr_raw[j][h].w)
+                           : "v"(sraw[0][j > 0 ? j - 1 : 0]));
+          }
+          uint32_t c[2][4], sc[2];
+  #pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            uint32_t d[8];
+            piece(j, h, d);
+            const uint32_t mb = amax_bf16_bits<8, false>(d);
+            const auto mm = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+            const bool blk_fast = RRULE != kRpUe8m0 && (mm[0] > mm[1] ? mm[0] : mm[1]) <= 0x7F80u && sfs[j][h] < 255u;
+            float m = 0.0f;
+            float v[16];
+            if (!blk_fast) {
+              bf16x8_to_f32(qr_raw[j][2 * h], v);
+              bf16x8_to_f32(qr_raw[j][2 * h + 1], v + 8);
+              quiet8(v);
+              quiet8(v + 8);
+  #pragma unroll
+              for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+            }
+            // (outside the branch, whose condition the two lanes of a block share)
+            const auto ms = __builtin_amdgcn_permlane16_swap(f2u(m), f2u(m), false, false);
+            if (blk_fast) {
+              codes_bf16_scaled<4, false>(d, sfs[j][h], c[h]);
+              sc[h] = sfs[j][h];
+            } else {
+              sc[h] = quant_block_codes<RRULE, false, 16>(v, __builtin_fmaxf(u2f(ms[0]), u2f(ms[1])), c[h]);
+            }
+          }
+          place(j, c, sc);
+        }
       }
     }
   } else if constexpr (FUSED) {
@@ -1231,7 +1295,8 @@ namespace {
 template <int FMT, int ROWP>
 hipError_t launch_row_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
   if constexpr (ROWP >= 8) {  // the in-register quantizer: one super-tile per wave
-    if (p.KT > kStreamQuantRowsMaxKT || p.M > 16) return hipErrorInvalidValue;
+    if (p.KT > (ROWP >= 12 ? kStreamQuantRowsSliceMaxKT : kStreamQuantRowsMaxKT) || p.M > 16)
+      return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, false, ROWP>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
   } else if (p.KT <= kStreamMaxWaves) {
     hipLaunchKernelGGL((gemm_stream_kernel<FMT, 1, true, false, ROWP>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
@@ -1276,14 +1341,22 @@ hipError_t launch_gemm_stream_quant_row(int fmt, int rule, const GemmParams& p, 
 }
 
 bool stream_quant_rows_eligible(int64_t M, int64_t K, int rule) {
-  return M >= 1 && M <= 16 && stream_gemm_eligible(M, K, false) && (K + kTileK - 1) / kTileK <= kStreamQuantRowsMaxKT &&
-         rule >= kFloorCarry175 && rule <= kRpUe8m0;
+  return M >= 1 && M <= 16 && stream_gemm_eligible(M, K, false) &&
+         (K + kTileK - 1) / kTileK <= kStreamQuantRowsSliceMaxKT && rule >= kFloorCarry175 && rule <= kRpUe8m0;
 }
 
 hipError_t launch_gemm_stream_quant_rows(int fmt, int rule, const GemmParams& p, hipStream_t s) {
-  if (rule == kFloorCarry175) return launch_row<8 + kFloorCarry175>(fmt, p, row_grid(p), s);
-  if (rule == kCeilDiv448) return launch_row<8 + kCeilDiv448>(fmt, p, row_grid(p), s);
-  if (rule == kRpUe8m0) return launch_row<8 + kRpUe8m0>(fmt, p, row_grid(p), s);
+  // the wave-wide branch up to eight waves (measured faster at c1), the slice-by-slice
+  // form past them
+  if (p.KT <= kStreamQuantRowsMaxKT) {
+    if (rule == kFloorCarry175) return launch_row<8 + kFloorCarry175>(fmt, p, row_grid(p), s);
+    if (rule == kCeilDiv448) return launch_row<8 + kCeilDiv448>(fmt, p, row_grid(p), s);
+    if (rule == kRpUe8m0) return launch_row<8 + kRpUe8m0>(fmt, p, row_grid(p), s);
+  } else {
+    if (rule == kFloorCarry175) return launch_row<12 + kFloorCarry175>(fmt, p, row_grid(p), s);
+    if (rule == kCeilDiv448) return launch_row<12 + kCeilDiv448>(fmt, p, row_grid(p), s);
+    if (rule == kRpUe8m0) return launch_row<12 + kRpUe8m0>(fmt, p, row_grid(p), s);
+  }
   return hipErrorInvalidValue;
 }
 

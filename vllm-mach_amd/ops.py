@@ -479,7 +479,7 @@ def quant_row_fusable(m: int, k: int, rule: int, w_fmt: int = E4M3) -> bool:
 
 def quant_rows_inreg(m: int, k: int, rule: int, w_fmt: int = E4M3) -> bool:
     """Shapes whose MXFP8 quantization ``mxl_quant_mx_gemm`` runs inside the GEMM's own
-    wavefronts (one row; or up to 16 rows at K <= 4096), the one-launch scheme that measured
+    wavefronts (one row; or up to 16 rows at K <= 6144), the one-launch scheme that measured
     faster than the quantizer and GEMM as two launches."""
     return 1 <= m <= 16 and bool(query("mxl_producer_gemm_supported", 3, m, k, rule, w_fmt))
 
@@ -638,7 +638,7 @@ def mx_gemm_from_float(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: in
 
     Replaces ``mxfp8_sm120::gemm_from_float`` / ``mxfp6::gemm_from_float``
     (src/vllm_mach/mxfp6/dense_mxfp8.py:96, src/vllm_mach/mxfp6/dense.py:122-129).  Where
-    the GEMM's own wavefronts can quantize (one row, or up to 16 rows at K <= 4096) it runs
+    the GEMM's own wavefronts can quantize (one row, or up to 16 rows at K <= 6144) it runs
     as one launch (``quant_mx_gemm``, the same bits); other shapes take the quantizer and
     the GEMM, which measured faster than the one-launch handoff ``quant_mx_gemm`` offers
     there.
