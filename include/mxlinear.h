@@ -297,24 +297,27 @@ int mxl_quant_mx_gemm_ex(const void* x, int64_t M, int64_t K, int rule, const vo
                          const mxl_gemm_options* options, void* stream);
 
 /* Block-FP8 activation quantization -> block-FP8 GEMM for M <= 16 bf16 rows x [M, K] in
- * one launch, bit-identical to mxl_quantize_block_fp8 followed by mxl_block_fp8_gemm (the
- * producer waves, scratch slots and handoff of mxl_swiglu_mx_gemm); K % 128 == 0, K <= 3584
- * or 4096 < K <= 7168.  Replaces the per-token-group quantization + block-FP8 GEMM pair
+ * one launch, bit-identical to mxl_quantize_block_fp8 followed by mxl_block_fp8_gemm.  One
+ * row (K <= 8192): every wavefront of the GEMM quantizes its own super-tiles of it; more
+ * rows: the producer waves, scratch slots and handoff of mxl_swiglu_mx_gemm, K % 128 == 0,
+ * K <= 3584 or 4096 < K <= 7168.  Replaces the per-token-group quantization + block-FP8 GEMM pair
  * of the patched CutlassFp8BlockScaledMMKernel at decode sizes
  * (src/vllm_mach/fp8/linear.py:65-81,157-216). */
 int mxl_block_fp8_quant_gemm(const void* x, int64_t M, int64_t K, const void* w_tiled, const void* sb, int64_t N,
                              const void* bias, void* out, int64_t ldc, void* stream);
 
 /* mxl_block_fp8_quant_gemm with the output format and scale of `options`
- * (options->kernel -1 or 0). */
+ * (options->kernel -1 automatic, 0 the handoff, 3 the wavefronts' own quantization of one
+ * row). */
 int mxl_block_fp8_quant_gemm_ex(const void* x, int64_t M, int64_t K, const void* w_tiled, const void* sb, int64_t N,
                                 const void* bias, void* out, int64_t ldc, const mxl_gemm_options* options,
                                 void* stream);
 
 /* 1 when the one-launch producer + GEMM runs (kind 0 mxl_swiglu_mx_gemm, 1
- * mxl_quant_mx_gemm, 2 mxl_block_fp8_quant_gemm; 3 mxl_quant_mx_gemm with the
- * quantization in the GEMM's own wavefronts, the scheme that measured faster than two
- * launches) for M rows, K, scale rule and weight format, else 0.  No counterpart in the reference (its fused rows are fixed,
+ * mxl_quant_mx_gemm, 2 mxl_block_fp8_quant_gemm; 3 mxl_quant_mx_gemm and 4
+ * mxl_block_fp8_quant_gemm with the quantization in the GEMM's own wavefronts, the
+ * scheme that measured faster than two launches) for M rows, K, scale rule and weight
+ * format, else 0.  No counterpart in the reference (its fused rows are fixed,
  * src/vllm_mach/mxfp6/fused_mlp.py:13-19); for callers choosing between one launch and
  * two. */
 int mxl_producer_gemm_supported(int kind, int64_t M, int64_t K, int rule, int w_fmt);

@@ -143,6 +143,33 @@ def test_quant_rows_inreg_every_value_at_every_scale(pkg, dev, rule, K):
         assert _eq(y, y_ref), r0
 
 
+@pytest.mark.parametrize("K", [640, 2176, 2560, 8192])
+def test_block_fp8_row_inreg_part_supertile(pkg, dev, K):
+    # one row quantized by the GEMM's wavefronts where the last super-tile is partly past K
+    # (640, 2176: slices past K take the last slice's scale, as the clamped two-launch load
+    # does -- an infinity in the last group makes both outputs NaN alike) and at the two
+    # super-tiles per wave of K = 8192
+    ops = pkg.ops
+    N = 256
+    wq, sb = _block_weights(N, K, 900 + K)
+    tiled, _ = ops.pack_weight(wq.to(dev), None, 0)
+    sbd = sb.to(dev)
+    assert ops.block_row_inreg(1, K)
+    g = torch.Generator().manual_seed(901 + K)
+    for case in range(3):
+        x = torch.randn(1, K, generator=g).bfloat16()
+        if case == 1:
+            x[0, K - 100] = float("inf")
+        if case == 2:
+            x[0, K - 128:] = 0.0
+            x[0, 3] = float("nan")
+        xd = x.to(dev)
+        q, s = torch.ops.mach_amd.quantize_block_fp8(xd)
+        y_ref = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sbd, N, K, None)
+        y = torch.ops.mach_amd.block_fp8_quant_gemm(xd, tiled, sbd, N, None)
+        assert _eq(y, y_ref), case
+
+
 def _block_weights(N, K, seed):
     g = torch.Generator().manual_seed(seed)
     w = torch.randn(N, K, generator=g) * 0.02
@@ -167,14 +194,32 @@ def test_block_fp8_one_launch_bit_identical(pkg, oracle_mod, dev, M, N, K):
     special[M - 1, 200] = float("inf")
     special[0, 300] = 0.0
     special[M - 1, : min(K, 128)] = 0.0  # an all-zero group: the 1e-10 floor
+    inreg = ops.block_row_inreg(M, K)
+    assert inreg == (M == 1)
+    from vllm_mach_amd import _lib
     for rows in (x, special):
         xd = rows.to(dev)
         q, s = torch.ops.mach_amd.quantize_block_fp8(xd)
         y_ref = torch.ops.mach_amd.block_fp8_gemm(q, s, tiled, sbd, N, K, bias)
         y = torch.ops.mach_amd.block_fp8_quant_gemm(xd, tiled, sbd, N, bias)
         assert _eq(y, y_ref)
-    # the layer path takes the two launches (faster), with the same bits
+        # each scheme by name: 0 the producer waves and handoff, 3 the GEMM's own wavefronts
+        for kernel in (0, 3):
+            y_k = torch.empty_like(y_ref)
+            try:
+                _lib.call("mxl_block_fp8_quant_gemm_ex", xd.data_ptr(), M, K, tiled.data_ptr(), sbd.data_ptr(), N,
+                          bias.data_ptr() if bias is not None else None, y_k.data_ptr(), N,
+                          _lib.options_ptr(_lib.GemmOptions(kernel=kernel)), torch.cuda.current_stream(dev).cuda_stream)
+            except _lib.MxlError as e:
+                assert "unsupported" in str(e) and (kernel == 0 or not inreg), (kernel, str(e))
+                continue
+            assert kernel == 0 or inreg
+            assert _eq(y_k, y_ref), kernel
+    # the layer path: one launch for one row (the wavefronts' own quantization), else the
+    # two launches (faster than the handoff), with the same bits
+    before = dict(ops._COUNTS)
     y = ops.block_fp8_from_float(x.to(dev), tiled, sbd, N)
+    assert ops._COUNTS.get("block_fp8_quant_gemm", 0) == before.get("block_fp8_quant_gemm", 0) + int(inreg)
     assert _eq(y, torch.ops.mach_amd.block_fp8_quant_gemm(x.to(dev), tiled, sbd, N, None))
     if M * N >= 2048 and N * K <= 2_500_000:
         rq, rs = oracle_mod.quant_block_fp8(x)

@@ -965,7 +965,9 @@ extern "C" int mxl_producer_gemm_supported(int kind, int64_t M, int64_t K, int r
              (stream_fused_eligible(m, K, false, w_fmt) || stream_quant_row_eligible(m, K, rule) ||
               stream_quant_rows_eligible(m, K, rule));
     case 2:  // block-FP8 quantization -> block-FP8 GEMM
-      return stream_fused_eligible(m, K, true, kE4M3);
+      return stream_fused_eligible(m, K, true, kE4M3) || stream_block_row_eligible(m, K);
+    case 4:  // block-FP8 quantization inside the GEMM's own wavefronts (one row)
+      return stream_block_row_eligible(m, K);
     case 3:  // MXFP8 quantization inside the GEMM's own wavefronts (no handoff)
       return valid_wfmt(w_fmt) && (m == 1 ? stream_quant_row_eligible(1, K, rule) : stream_quant_rows_eligible(m, K, rule));
     default:
@@ -982,9 +984,15 @@ static int block_quant_common(const void* x, int64_t M, int64_t K, const void* w
                 (double)o.alpha);
   MXL_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)w_tiled & 15) == 0,
                 "mxl_block_fp8_quant_gemm: x and w must be 16-byte aligned");
-  if (!stream_fused_eligible(M > 0 ? M : 1, K, true, kE4M3) || (o.kernel != kAuto && o.kernel != kStream)) {
+  // one row: every wavefront quantizes it (options.kernel 3, automatic where it runs);
+  // more rows: the producer waves' grid handoff (options.kernel 0)
+  const bool inreg = stream_block_row_eligible(M, K);
+  const bool handoff = stream_fused_eligible(M > 0 ? M : 1, K, true, kE4M3);
+  const bool use_inreg = o.kernel == kStreamWide || (o.kernel == kAuto && inreg);
+  if (use_inreg ? !inreg : (!handoff || (o.kernel != kAuto && o.kernel != kStream))) {
     set_error("mxl_block_fp8_quant_gemm: unsupported (M <= 16, K %% 128 == 0, K <= 3584 or 4096 < K <= 7168; "
-              "options.kernel -1 or 0; M=%lld K=%lld)", (long long)M, (long long)K);
+              "options.kernel -1, 0 or 3 (3: M = 1, K <= 8192); M=%lld K=%lld kernel=%d)", (long long)M, (long long)K,
+              o.kernel);
     return MXL_EUNSUPPORTED;
   }
   if (M == 0) return MXL_OK;
@@ -993,6 +1001,16 @@ static int block_quant_common(const void* x, int64_t M, int64_t K, const void* w
   p.ldc = ldc; p.M = M; p.N = N; p.K = K; p.KT = (K + kTileK - 1) / kTileK; p.a_rows = M;
   p.row_div = 1; p.S = 1;
   p.alpha = o.alpha; p.out_f16 = o.out_dtype == kOutF16;
+  if (use_inreg) {
+    p.a = (const uint8_t*)x;
+    p.lda = K;
+    const hipError_t e = launch_gemm_stream_block_row(p, (hipStream_t)stream);
+    if (e != hipSuccess) {
+      set_error("mxl_block_fp8_quant_gemm: launch failed: %s", hipGetErrorString(e));
+      return MXL_EHIP;
+    }
+    return MXL_OK;
+  }
   p.fsrc = (const uint16_t*)x;
   p.fsrc_ld = K;
   return launch_gemm_stream_fused(kE4M3, kFusedBlockFp8, p, (hipStream_t)stream, "mxl_block_fp8_quant_gemm");

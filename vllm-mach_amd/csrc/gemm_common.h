@@ -311,6 +311,10 @@ bool stream_quant_row_eligible(int64_t M, int64_t K, int rule);
 hipError_t launch_gemm_stream_quant_row(int fmt, int rule, const GemmParams& p, hipStream_t s);
 // MXFP8 quantization of up to 16 bf16 rows inside the weight-streaming GEMM, each fragment
 // lane quantizing its own pieces (K <= 4096)
+// One bf16 row block-FP8 quantized inside the block-FP8 weight-streaming GEMM by every
+// wavefront (M = 1, the stream path's K range), bit-identical to the quantizer + GEMM.
+bool stream_block_row_eligible(int64_t M, int64_t K);
+hipError_t launch_gemm_stream_block_row(const GemmParams& p, hipStream_t s);
 bool stream_quant_rows_eligible(int64_t M, int64_t K, int rule);
 hipError_t launch_gemm_stream_quant_rows(int fmt, int rule, const GemmParams& p, hipStream_t s);
 // Producer + weight-streaming GEMM in one launch (M <= 16): prod 1 / 2 = SwiGLU ->

@@ -331,12 +331,13 @@ template <int FMT, int RUN, bool DB, bool BLOCK, int ROWP = -1, int FPROD = -1>
 __global__ __launch_bounds__(BLOCK ? 512 : (ROWP >= 12 ? 64 * kStreamQuantRowsSliceMaxKT : ROWP >= 8 ? 64 * kStreamQuantRowsMaxKT : (RUN == 1 ? 1024 : 768)))
 void gemm_stream_kernel(GemmParams p) {
   static_assert(!BLOCK || FMT == kE4M3, "block-FP8 weights are E4M3");
-  static_assert(ROWP < 0 || !BLOCK, "the fused producer row feeds MX GEMMs");
+  static_assert(ROWP < 0 || BLOCK == (ROWP == 16), "ROWP 16 is the block-FP8 row, the others feed MX GEMMs");
   static_assert(ROWP < 0 || FPROD < 0, "one producer scheme per launch");
   static_assert(FPROD < 0 || (FPROD == 8) == BLOCK, "block-FP8 GEMMs take the block-FP8 quantizer");
-  static_assert(ROWP < 8 || RUN == 1, "the in-register quantizer takes one super-tile per wave");
+  static_assert(ROWP < 8 || ROWP == 16 || RUN == 1, "the in-register quantizer takes one super-tile per wave");
   constexpr bool ROW = ROWP >= 0 && ROWP < 8, SWI = ROWP >= 0 && ROWP < 4;
-  constexpr bool QROWS = ROWP >= 8, QSLICE = ROWP >= 12;
+  constexpr bool QROWS = ROWP >= 8 && ROWP < 16, QSLICE = ROWP >= 12 && ROWP < 16;
+  constexpr bool BROW = ROWP == 16;  // one bf16 row, block-FP8 quantized by every wavefront
   constexpr bool FUSED = FPROD >= 0;
   constexpr int RRULE = ROWP & 3;
   __shared__ float red[2][kStreamMaxWaves][4][64];
@@ -372,8 +373,8 @@ void gemm_stream_kernel(GemmParams p) {
   // The fused row's bf16 pieces (gate and up for SwiGLU) are requested before the weights:
   // vector loads complete in issue order, so the producer arithmetic then waits for these
   // loads only and runs while the weights stream in.
-  uint4 gu_raw[ROW ? RUN : 1][SWI ? 2 : 1];
-  if constexpr (ROW) {
+  uint4 gu_raw[ROW || BROW ? RUN : 1][SWI ? 2 : 1];
+  if constexpr (ROW || BROW) {
     const uint16_t* gu = reinterpret_cast<const uint16_t*>(p.a);
 #pragma unroll
     for (int u = 0; u < RUN; ++u) {
@@ -437,7 +438,7 @@ void gemm_stream_kernel(GemmParams p) {
   v8i a[RUN][4];
   uint32_t sraw[RUN][4];
   float4 s4[BLOCK ? RUN : 1][4];  // block-FP8: fp32 scales of the lane's output rows 4 q .. 4 q + 3, slice j
-  if constexpr (BLOCK) {
+  if constexpr (BLOCK && !BROW) {
     const float* sa = static_cast<const float*>(p.sa);  // column-major [K/128, M]
     const int64_t G = p.K / 128;
     int64_t rows[4];
@@ -644,6 +645,37 @@ void gemm_stream_kernel(GemmParams p) {
           }
           place(j, c, sc);
         }
+      }
+    }
+  } else if constexpr (BROW) {
+    // The block-FP8 quantizer of the row (the standalone kernel's quiet8 +
+    // block_fp8_quant8: lanes 16 j .. 16 j + 15 hold slice j's 128 values, 8 each, the
+    // group's amax by xor-shuffles over them), every wavefront its own super-tiles.  The
+    // codes reach the fragment lanes as in the MX row above (lane l holds values 8 l ..
+    // 8 l + 7 of the super-tile); every output row of the lane is row 0 (M = 1), so its
+    // four activation scales are the slice's.  A slice past K (a part super-tile) takes
+    // the last slice's scale, as the two-launch path's clamped scale load does; its
+    // weights are zero.
+#pragma unroll
+    for (int u = 0; u < RUN; ++u) {
+      float v[8];
+      uint32_t pk[2];
+      bf16x8_to_f32(gu_raw[u][0], v);
+      quiet8(v);
+      const float scale = block_fp8_quant8(v, pk);
+      const int64_t last = (p.K / 128 - 1) - kt[u] * 4;  // the super-tile's last slice inside K
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int b = 4 * j + 2 * (e >> 2) + (q >> 1);
+          y[e] = __builtin_amdgcn_ds_bpermute(4 * (4 * b + 2 * (q & 1) + ((e & 3) >> 1)), (int)pk[e & 1]);
+        }
+        a[u][j] = v8i{y[0], y[1], y[2], y[3], y[4], y[5], y[6], y[7]};
+        const int js = j <= last ? j : (int)last;
+        const float sj = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * 16 * js, __builtin_bit_cast(int, scale)));
+        s4[u][j] = float4{sj, sj, sj, sj};
       }
     }
   } else if constexpr (FUSED) {
@@ -1338,6 +1370,21 @@ hipError_t launch_gemm_stream_quant_row(int fmt, int rule, const GemmParams& p, 
   if (rule == kCeilDiv448) return launch_row<4 + kCeilDiv448>(fmt, p, row_grid(p), s);
   if (rule == kRpUe8m0) return launch_row<4 + kRpUe8m0>(fmt, p, row_grid(p), s);
   return hipErrorInvalidValue;
+}
+
+bool stream_block_row_eligible(int64_t M, int64_t K) { return M == 1 && stream_gemm_eligible(1, K, true); }
+
+hipError_t launch_gemm_stream_block_row(const GemmParams& p, hipStream_t s) {
+  // ROWP 16: the block-FP8 row quantized by every wavefront (E4M3 weights); the waves
+  // and super-tiles of the two-launch path's block-FP8 GEMM
+  if (p.M != 1) return hipErrorInvalidValue;
+  const dim3 grid = row_grid(p);
+  if (p.KT <= kStreamBlockMaxWaves)
+    hipLaunchKernelGGL((gemm_stream_kernel<kE4M3, 1, true, true, 16>), grid, dim3((unsigned)(p.KT * 64)), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_stream_kernel<kE4M3, 2, false, true, 16>), grid, dim3((unsigned)((p.KT + 1) / 2 * 64)), 0,
+                       s, p);
+  return hipGetLastError();
 }
 
 bool stream_quant_rows_eligible(int64_t M, int64_t K, int rule) {

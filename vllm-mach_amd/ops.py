@@ -489,6 +489,13 @@ def block_row_fusable(m: int, k: int) -> bool:
     return 1 <= m <= 16 and bool(query("mxl_producer_gemm_supported", 2, m, k, 0, E4M3))
 
 
+def block_row_inreg(m: int, k: int) -> bool:
+    """Shapes whose block-FP8 quantization ``mxl_block_fp8_quant_gemm`` runs inside the
+    GEMM's own wavefronts (one row), the one-launch scheme that measured faster than the
+    quantizer and GEMM as two launches."""
+    return m == 1 and bool(query("mxl_producer_gemm_supported", 4, m, k, 0, E4M3))
+
+
 @torch.library.custom_op("mach_amd::quant_mx_gemm", mutates_args=())
 def quant_mx_gemm(x: torch.Tensor, w: torch.Tensor, sw: torch.Tensor, n: int, w_fmt: int,
                   rule: int = FLOOR_CARRY175, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -718,8 +725,12 @@ def block_fp8_from_float(x: torch.Tensor, w: torch.Tensor, sb: torch.Tensor, n: 
                          bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Quantize bf16 activations to block-FP8 (fp32 scale per row per 128) and run the
     block-FP8 GEMM (the patched ``CutlassFp8BlockScaledMMKernel.apply_weights`` pair,
-    src/vllm_mach/fp8/linear.py:157-216), as two launches: they measured faster than the
-    one-launch handoff ``block_fp8_quant_gemm`` offers up to 16 rows."""
+    src/vllm_mach/fp8/linear.py:157-216).  One row runs as one launch (every wavefront of
+    the GEMM quantizes its own part of the row, the same bits); more rows take the two
+    launches, which measured faster than the one-launch handoff ``block_fp8_quant_gemm``
+    offers up to 16 rows."""
+    if x.dtype == torch.bfloat16 and block_row_inreg(x.shape[0], x.shape[1]):
+        return torch.ops.mach_amd.block_fp8_quant_gemm(x, w, sb, n, bias)
     q, s = torch.ops.mach_amd.quantize_block_fp8(x)
     return torch.ops.mach_amd.block_fp8_gemm(q, s, w, sb, n, x.shape[1], bias)
 
