@@ -444,15 +444,22 @@ void gemm_stream_kernel(GemmParams p) {
     int64_t rows[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) rows[i] = 4 * q + i < p.M ? 4 * q + i : p.M - 1;
+    // the lane's four rows are consecutive floats of the group's column: one 16-byte
+    // load where they all lie inside M and the column keeps 16-byte alignment
+    bool vec4 = false;
+    if constexpr (!FUSED) vec4 = p.M % 4 == 0 && (reinterpret_cast<uintptr_t>(sa) & 15) == 0 && 4 * q + 3 < p.M;
 #pragma unroll
     for (int u = 0; u < RUN; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int64_t gi = kt[u] * 4 + j < G ? kt[u] * 4 + j : G - 1;
-        s4[u][j] = float4{__builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[0])),
-                          __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[1])),
-                          __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[2])),
-                          __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[3]))};
+        if (vec4)
+          s4[u][j] = *reinterpret_cast<const float4*>(sa + gi * p.M + 4 * q);
+        else
+          s4[u][j] = float4{__builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[0])),
+                            __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[1])),
+                            __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[2])),
+                            __builtin_bit_cast(float, load_s32(sa + gi * p.M + rows[3]))};
       }
   }
   if constexpr (ROW) {
