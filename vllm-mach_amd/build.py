@@ -36,6 +36,9 @@ FLAGS = [
 # per-source additions to FLAGS
 FILE_FLAGS: dict[str, list[str]] = {
     "gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # the one-row SwiGLU launch: its SiLU arithmetic ahead of the weight stream schedules
+    # better for instruction-level parallelism
+    "gemm_stream_swiglu.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
 }
 
 

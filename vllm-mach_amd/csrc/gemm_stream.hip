@@ -1294,6 +1294,10 @@ __global__ __launch_bounds__((64 * stream_grouped_waves<FMT, MT>())) void gemm_s
 
 // ------------------------------------------------------------ configuration
 
+// The host side.  gemm_stream_swiglu.hip compiles this file again with
+// MXL_STREAM_SWIGLU_ONLY for the one-row SwiGLU launch alone (its own scheduling
+// flags); this translation unit holds everything else.
+#ifndef MXL_STREAM_SWIGLU_ONLY
 // MX: one super-tile per wave (double-buffered) up to 16 super-tiles (K <= 8192);
 // two per wave, single-buffered, up to 24 (K <= 12288, twelve waves of at most
 // 168 registers).  A super-tile costs 32 + 4 VGPRs of activations and 32 (24
@@ -1328,6 +1332,8 @@ hipError_t launch_stream_fmt(const GemmParams& p, dim3 grid, hipStream_t s) {
 }
 }  // namespace
 
+#endif  // MXL_STREAM_SWIGLU_ONLY
+
 namespace {
 // ROWP: the row producer of gemm_stream_kernel (rule of the SwiGLU row, or 4 + rule of
 // the quantized row)
@@ -1358,6 +1364,7 @@ dim3 row_grid(const GemmParams& p) {
 }
 }  // namespace
 
+#ifdef MXL_STREAM_SWIGLU_ONLY
 bool stream_swiglu_eligible(int64_t M, int64_t K, int rule) {
   return M == 1 && stream_gemm_eligible(1, K, false) && (rule == kCeilDiv448 || rule == kRpUe8m0);
 }
@@ -1367,6 +1374,8 @@ hipError_t launch_gemm_stream_swiglu(int fmt, int rule, const GemmParams& p, hip
   if (rule == kRpUe8m0) return launch_row<kRpUe8m0>(fmt, p, row_grid(p), s);
   return hipErrorInvalidValue;
 }
+
+#else
 
 bool stream_quant_row_eligible(int64_t M, int64_t K, int rule) {
   return M == 1 && stream_gemm_eligible(1, K, false) && rule >= kFloorCarry175 && rule <= kRpUe8m0;
@@ -1640,5 +1649,7 @@ hipError_t launch_gemm_stream(int fmt, bool block, const GemmParams& p, hipStrea
   if (fmt == kE3M2) return launch_stream_fmt<kE3M2, false>(p, grid, s);
   return hipErrorInvalidValue;
 }
+
+#endif  // MXL_STREAM_SWIGLU_ONLY
 
 }  // namespace mxl
