@@ -36,6 +36,8 @@ FLAGS = [
 # per-source additions to FLAGS
 FILE_FLAGS: dict[str, list[str]] = {
     "gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # the dense MX wide launches: the iterative ILP schedule
+    "gemm_wide_mx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     # the one-row SwiGLU launch: its SiLU arithmetic ahead of the weight stream schedules
     # better for instruction-level parallelism
     "gemm_stream_swiglu.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],

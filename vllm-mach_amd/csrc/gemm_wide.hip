@@ -734,6 +734,7 @@ __global__ __launch_bounds__(256 * WM, GROUPED ? 2 : 1) void gemm_wide_kernel(Ge
 // 4 q .. 4 q + 3 of column r.  One thread per (tile, fragment, lane): its S float4 loads
 // are contiguous across the wave, and each of its four rows gets one 2-byte store (sixteen
 // lanes cover 32 contiguous bytes of a row).
+#ifndef MXL_WIDE_MX_DENSE_ONLY
 __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __restrict__ partial,
                                                                const uint16_t* __restrict__ bias,
                                                                uint16_t* __restrict__ out, int64_t M, int64_t N,
@@ -770,7 +771,9 @@ __global__ __launch_bounds__(256) void wide_tile_reduce_kernel(const float* __re
   for (int e = 0; e < 4; ++e)
     if (row0 + e < M) out[(row0 + e) * ldc + col] = out_bits(a4[e], alpha, f16, b, bv);
 }
+#endif  // MXL_WIDE_MX_DENSE_ONLY
 
+#ifndef MXL_WIDE_MX_DENSE_ONLY
 // ------------------------------------------------------------ configuration
 
 namespace {
@@ -888,6 +891,8 @@ int64_t wide_workspace_bytes(const WideConfig& c, int64_t M, int64_t N) {
 
 bool wide_gemm_eligible(int64_t M, int64_t K) { return M >= 64 && K % 256 == 0 && M * K < (int64_t(1) << 32); }
 
+#endif  // MXL_WIDE_MX_DENSE_ONLY
+
 template <int FMT, int MT, bool BLOCK, bool GROUPED>
 static hipError_t launch_wide_mt(const WideConfig& c, const GemmParams& p, const WideGrid& g, int64_t grid,
                                  hipStream_t s) {
@@ -933,6 +938,21 @@ static hipError_t launch_wide_fmt(const WideConfig& c, const GemmParams& p, cons
   return hipErrorInvalidValue;
 }
 
+// The dense MX launches (gemm_wide_mx.hip compiles this file again with
+// MXL_WIDE_MX_DENSE_ONLY for them alone, under its own scheduling flags; the block-FP8
+// and grouped launches stay in this translation unit).
+hipError_t launch_wide_mx_dense(int fmt, const WideConfig& c, const GemmParams& q, const WideGrid& gg, int64_t n,
+                                hipStream_t s)
+#ifdef MXL_WIDE_MX_DENSE_ONLY
+{
+  if (fmt == kE4M3) return launch_wide_fmt<kE4M3, false, false>(c, q, gg, n, s);
+  if (fmt == kE2M3) return launch_wide_fmt<kE2M3, false, false>(c, q, gg, n, s);
+  if (fmt == kE3M2) return launch_wide_fmt<kE3M2, false, false>(c, q, gg, n, s);
+  return hipErrorInvalidValue;
+}
+#else
+;
+
 hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const GemmParams& p, int64_t num_experts,
                             hipStream_t s) {
   const int64_t bm = 16 * c.MT;
@@ -956,10 +976,7 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
   g.tiles = g.mblocks * g.nblocks;
   auto dense = [&](const GemmParams& q, const WideGrid& gg, int64_t n) -> hipError_t {
     if (block) return fmt == kE4M3 ? launch_wide_fmt<kE4M3, true, false>(c, q, gg, n, s) : hipErrorInvalidValue;
-    if (fmt == kE4M3) return launch_wide_fmt<kE4M3, false, false>(c, q, gg, n, s);
-    if (fmt == kE2M3) return launch_wide_fmt<kE2M3, false, false>(c, q, gg, n, s);
-    if (fmt == kE3M2) return launch_wide_fmt<kE3M2, false, false>(c, q, gg, n, s);
-    return hipErrorInvalidValue;
+    return launch_wide_mx_dense(fmt, c, q, gg, n, s);
   };
   const int64_t tw = 64 * c.NT;
   auto tile_reduce = [&](int64_t tile0, int64_t tiles, int S) -> hipError_t {
@@ -991,5 +1008,7 @@ hipError_t launch_gemm_wide(int fmt, bool block, const WideConfig& c, const Gemm
   if (e != hipSuccess) return e;
   return tile_reduce(gd.rem_tile0, gd.rem_tiles, c.S2);
 }
+
+#endif  // MXL_WIDE_MX_DENSE_ONLY
 
 }  // namespace mxl
